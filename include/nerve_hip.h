@@ -1,0 +1,239 @@
+/*
+ * nerve_hip.h -- C ABI of the MI355X (gfx950) backend for NERVE's
+ * quantized-matmul hot path.
+ *
+ * Conventions
+ *   - Every device buffer is owned by the caller and passed as a raw device
+ *     pointer; sizes are element counts given by the shape arguments.
+ *   - Every operation enqueues on the caller's `stream` (a hipStream_t passed
+ *     as void*; NULL = the default stream) and returns without synchronizing.
+ *   - Host-side validation failures (bad specialization string, shape,
+ *     alignment, NULL pointer) return a nonzero nerve_hip_status and set a
+ *     thread-local message readable through nerve_hip_last_error().  This
+ *     mirrors the reference's Result<_, String> error style
+ *     (execution-contracts/src/lib.rs:8-17).
+ *   - Device-side conditions fail closed exactly as the reference shaders do:
+ *     an out-of-range expert id, an unbound parameter slot, a non-resident or
+ *     too-short address record makes the affected route write nothing
+ *     (runtime-rs/shaders/independent_sparse_moe_gate_up_batch1_mxfp4.
+ *     comp.template:135-228).
+ *   - A context is bound to one device.  Calls on one context must be
+ *     externally serialized (the reference runs its tests and queues
+ *     single-threaded: runtime-rs/.cargo/config.toml, AGENTS.md:3-9).  The
+ *     context owns a device workspace that calls reuse; two calls on one
+ *     context must not overlap on different streams.
+ *
+ * Buffer encodings are the compiled package's, unchanged:
+ *   bf16 tensors       uint16 bit patterns, row-major ("words" of two, low half
+ *                      = even element, as the templates read them)
+ *   MXFP4 weight       u8 [rows, K/2], low nibble first along K
+ *                      (nerve/quantized_layouts.py:4-7)
+ *   MXFP4 scale        e8m0 u8 [rows, K/32]
+ *   route word         (bf16(weight) << 16) | expert
+ *   intermediates      u32 frames [B][k*I/2 + k]: bf16 h, then k route-map words
+ *   BatchControl       u32[7] {batch_width, expert_start, expert_count,
+ *                      owned_route_count, dispatch_x, dispatch_y, dispatch_z}
+ *   address record     u32[8] {addr_lo, addr_hi, bytes_lo, bytes_hi, gen_lo,
+ *                      gen_hi, resident(==1), representation}
+ *
+ * Shape extension: the reference compiler requires hidden/intermediate/K to
+ * be multiples of 128 (nerve/model_package_shader_templates.py:4805-4807,
+ * 2437-2440).  This library also accepts multiples of 32 and treats the last
+ * 128-column activation block as zero-padded (its amax is taken over the real
+ * columns), which is the reference's result on zero-padded K.
+ */
+#ifndef NERVE_HIP_H
+#define NERVE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NERVE_HIP_ABI_VERSION 1
+
+typedef struct nerve_hip_ctx nerve_hip_ctx;
+
+typedef enum {
+    NERVE_HIP_OK = 0,
+    NERVE_HIP_INVALID_ARGUMENT = 1,
+    NERVE_HIP_INVALID_SPEC = 2,
+    NERVE_HIP_UNSUPPORTED = 3,
+    NERVE_HIP_DEVICE_ERROR = 4,
+    NERVE_HIP_OUT_OF_MEMORY = 5
+} nerve_hip_status;
+
+/* ---- lifecycle --------------------------------------------------------- */
+
+/* ABI version of the loaded library (NERVE_HIP_ABI_VERSION it was built with). */
+int nerve_hip_abi_version(void);
+
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char* nerve_hip_last_error(void);
+
+/* Opens a context on a HIP device ordinal.  Replaces the Vulkan device handle
+ * the reference mounts kernels on (runtime-rs/src/vulkan_compute/
+ * compute_device_dispatch.rs:2-249). */
+nerve_hip_status nerve_hip_open(int device_ordinal, nerve_hip_ctx** out);
+
+/* Releases the context and its workspace.  NULL is accepted. */
+void nerve_hip_close(nerve_hip_ctx* ctx);
+
+/* ---- a2: activation block quantization -------------------------------- */
+
+/* Replaces quantize_fp8_e4m3[_spow2]_b128_h{N}.comp
+ * (runtime-rs/shaders/quantize_fp8_e4m3.comp.template:41-59; specialization
+ * nerve/model_package_shader_templates.py:1513-1545), batched over `rows`.
+ * x: bf16 [rows, N]; q: e4m3 [rows, N]; scales: f32 [rows, ceil(N/128)].
+ * "_spow2" uses the power-of-two scale of the MXFP4 expert kernels
+ * (…gate_up_batch1_mxfp4.comp.template:357-363), otherwise amax/448. */
+nerve_hip_status nerve_hip_quantize_fp8_e4m3(nerve_hip_ctx* ctx, const char* spec,
+                                             const void* x_bf16, uint32_t rows,
+                                             void* q_e4m3, void* scales_f32, void* stream);
+
+/* ---- raw MXFP4 GEMV (config-0 entry; parity and measurement) ----------- */
+
+/* y[m, n] = sum_k e4m3(x)[m,k] * sx[m,k/128] * e2m1(W)[n,k] * e8m0(S)[n,k/32]
+ * in f32, for pre-quantized activations (the a2 output).  This is the
+ * accumulation of …gate_up_batch1_mxfp4.comp.template:759-787 without the
+ * SwiGLU epilogue.  q: e4m3 [M, K]; sx: f32 [M, ceil(K/128)]; W: u8 [N, K/2];
+ * S: u8 [N, K/32]; y: f32 [M, N].  M <= 64. */
+nerve_hip_status nerve_hip_mxfp4_gemv(nerve_hip_ctx* ctx, const void* q_e4m3,
+                                      const void* scales_f32, uint32_t M, uint32_t K,
+                                      const void* weight, const void* weight_scale,
+                                      uint32_t N, void* y_f32, void* stream);
+
+/* ---- a5: router projection --------------------------------------------- */
+
+/* Replaces linear_bf16.comp.template:40-98 for the router node
+ * (nerve/circuit_lowering_sparse_experts.py:82-88), batched:
+ * logits[b, e] = bf16(sum_k x[b,k] * W[e,k]).  x: bf16 [B, H]; W: bf16 [E, H];
+ * logits: bf16 [B, E]. */
+nerve_hip_status nerve_hip_router_linear_bf16(nerve_hip_ctx* ctx, const void* x_bf16,
+                                              const void* weight_bf16, void* logits_bf16,
+                                              uint32_t batch_width, uint32_t hidden,
+                                              uint32_t experts, void* stream);
+
+/* ---- a6: top-k routing -------------------------------------------------- */
+
+/* Replaces moe_topk[_batch1]_{sigmoid|softmax}_bf16_e{E}_k{k}_norm{0|1}_cap{c}_
+ * {nobias|biasf32|biasbf16}.comp (moe_topk_routed_batch1_bf16.comp.template:
+ * 71-182) and moe_router[_batch1]_score_topk_{sigmoid|softmax|sqrtsoftplus}_
+ * bf16_r{E}_k{k}_a{A}w{w}_norm{0|1}_scale{s}_bias{f32|bf16}.comp
+ * (moe_router_score_topk_batch1_bf16.comp.template:109-219); grammar in
+ * nerve/model_package_shader_templates.py:4850-5060.
+ * logits: bf16 [B, E]; bias: f32 [E] or bf16 [E] per spec, or NULL for
+ * "nobias"; routes: u32 [B, k(+A)]; telemetry: u32 [T + T(T-1)/2] counters
+ * (T = E(+A)), incremented atomically, or NULL to skip them. */
+nerve_hip_status nerve_hip_moe_router_topk(nerve_hip_ctx* ctx, const char* spec,
+                                           const void* logits_bf16, const void* bias,
+                                           void* routes_u32, void* telemetry_u32,
+                                           uint32_t batch_width, void* stream);
+
+/* ---- a7: expert-sorted route permutation -------------------------------- */
+
+/* Replaces moe_route_compact_batch1 (moe_route_compact_batch1.comp.template:
+ * 26-106) and, when `intermediates` is NULL, moe_route_count_batch1
+ * (moe_route_count_batch1.comp.template:21-58).  `spec` is the consuming
+ * projection's specialization (it fixes I, k and the tile count per route).
+ * control: device BatchControl; fields 0..2 are read, 3..6 are written.
+ * The route map goes to the tail k words of each intermediate frame.  With
+ * expert_count == 0 the map is the stable sort of routes by expert; otherwise
+ * it lists the routes of experts in [expert_start, expert_start+expert_count)
+ * in source order. */
+nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spec,
+                                             const void* routes_u32, void* intermediates,
+                                             void* control_u32, uint32_t batch_width,
+                                             void* stream);
+
+/* ---- a2+a3: MXFP4 gate/up + SwiGLU -------------------------------------- */
+
+/* Replaces independent_sparse_moe_gate_up[_batch1][_prequant]_mxfp4_e2m1_g32_
+ * h{H}_i{I}_e{E}_k{k}_limit{L}.comp (…gate_up_batch1_mxfp4.comp.template:
+ * 643-802; grammar nerve/model_package_shader_templates.py:4773-4846).
+ * Inputs follow the template's bindings: hidden bf16 [B, H] (or, for
+ * "_prequant", hidden = e4m3 [B, H] and hidden_scales = f32 [B, H/128]),
+ * routes u32 [B, k], intermediates (frames, map read from the tails),
+ * addresses u32 [8 * address_records], param_slots u32 [4 * E]
+ * (gate_w, gate_s, up_w, up_s).  control: device BatchControl (batch_width
+ * given on the host; expert_count and owned_route_count read on the device).
+ * The grid is sized for batch_width * k routes; routes past the owned count
+ * exit on the device, which replaces the reference's indirect dispatch. */
+nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spec,
+                                             const void* hidden, const void* hidden_scales,
+                                             const void* routes_u32, void* intermediates,
+                                             const void* addresses_u32, uint32_t address_records,
+                                             const void* param_slots_u32, uint32_t param_slot_words,
+                                             const void* control_u32, uint32_t batch_width,
+                                             void* stream);
+
+/* ---- a2+a4: MXFP4 down + route weight ----------------------------------- */
+
+/* Replaces independent_sparse_moe_down[_batch1]_mxfp4_e2m1_g32_h{H}_i{I}_e{E}_
+ * k{k}.comp (…down_batch1_mxfp4.comp.template:507-610).  Reads h from the
+ * intermediate frames (map in the tails), writes expert_outputs bf16
+ * [B, k, H] = bf16(y * route_weight); param_slots u32 [2 * E]
+ * (down_w, down_s). */
+nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec,
+                                          const void* intermediates, const void* routes_u32,
+                                          void* expert_outputs,
+                                          const void* addresses_u32, uint32_t address_records,
+                                          const void* param_slots_u32, uint32_t param_slot_words,
+                                          const void* control_u32, uint32_t batch_width,
+                                          void* stream);
+
+/* ---- a8: weighted combine ----------------------------------------------- */
+
+/* Replaces moe_reduce[_batch1]_bf16 (moe_reduce_batch1_bf16.comp.template:
+ * 29-54): out[b, j] = bf16(bf16-sequential-sum_r expert_outputs[b, r, j] *
+ * routed_scale).  expert_outputs bf16 [B, k, H]; out bf16 [B, H]. */
+nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_outputs,
+                                      void* out_bf16, uint32_t batch_width, uint32_t hidden,
+                                      uint32_t experts_per_token, float routed_scale,
+                                      void* stream);
+
+/* ---- a9: group-scaled INT4 linear --------------------------------------- */
+
+/* Replaces {linear|linear_bias|linear_residual}[_batch{T}]_int4_{gptq|ct}_
+ * s{f16|bf16}_g{G}_{K}x{N}.comp (linear_int4_gptq.comp.template:47-135,
+ * linear_int4_ct.comp.template:49-150; replacements nerve/model_package_
+ * shader_selection.py:2469-2549).  x: bf16 [B, K]; qweight: u32 [K/8, N]
+ * (gptq) or [N, K/8] (ct); scales: f16/bf16 [K/G, N] (gptq) or [N, K/G]
+ * (ct); zeros: NULL for the reference's symmetric code-8 ABI, or (gptq only,
+ * an extension outside the reference ABI) AutoGPTQ qzeros u32 [K/G, N/8];
+ * aux: bias bf16 [N] (linear_bias) or residual bf16 [B, N] (linear_residual),
+ * else NULL; y: bf16 [B, N]. */
+nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char* spec,
+                                       const void* x_bf16, const void* qweight,
+                                       const void* scales, const void* zeros,
+                                       const void* aux_bf16, void* y_bf16,
+                                       uint32_t batch_width, void* stream);
+
+/* ---- a10+a11: FP8 output projection + fused argmax ----------------------- */
+
+/* Replaces tied_output_projection[_batch{T}]_fp8_e4m3_b{BR}x128_{N}x{K}_
+ * scale{S}_to_f32.comp (tied_output_projection_fp8_e4m3.comp.template:87-144,
+ * …_batch_fp8_e4m3.comp.template:94-186) followed by greedy_sampler_f32
+ * (greedy_sampler_f32.comp.template:25-109) / argmax_candidate_reduce.
+ * x: bf16 [B, K]; weight: e4m3 [N, K]; scale_inv: bf16 [ceil(N/BR), K/128];
+ * logits_f32: f32 [B, N] (the reference's output) or NULL; logits_bf16:
+ * bf16 [B, N] or NULL; argmax: u32 [B] (ties -> lower id, on the f32 logits)
+ * or NULL. */
+nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char* spec,
+                                                 const void* x_bf16, const void* weight_e4m3,
+                                                 const void* scale_inv_bf16, void* logits_f32,
+                                                 void* logits_bf16, void* argmax_u32,
+                                                 uint32_t batch_width, void* stream);
+
+/* Standalone greedy argmax over f32 logits [B, N] (greedy_sampler_f32.comp.
+ * template:25-109 without its stream-control bookkeeping). */
+nerve_hip_status nerve_hip_argmax_f32(nerve_hip_ctx* ctx, const void* logits_f32,
+                                      uint32_t batch_width, uint32_t vocab, void* argmax_u32,
+                                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NERVE_HIP_H */

@@ -1,0 +1,166 @@
+// Shared device numerics and host plumbing for libnerve_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/nerve_hip.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// Device numerics.  Each helper restates one rounding rule of the reference
+// shaders bit for bit.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float((h & 0xffffu) << 16); }
+
+// bf16 round-to-nearest-even as the templates do it
+// (independent_sparse_moe_gate_up_batch1_mxfp4.comp.template:92-96).
+__device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+    uint32_t b = __float_as_uint(v);
+    return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// f32 -> OCP e4m3 with round-to-nearest-even and saturation at +-448: the
+// GLSL fe4m3vec4(x) conversion of the activation quantizers
+// (…gate_up_batch1_mxfp4.comp.template:380).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+    uint32_t b = __float_as_uint(x);
+    uint32_t sign = (b >> 24) & 0x80u;
+    uint32_t a = b & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7fu;
+    if (a < 0x3c800000u) {  // below 2^-6: subnormal grid of 2^-9
+        float y = __uint_as_float(a) * 512.0f;
+        return sign | (uint32_t)__builtin_rintf(y);
+    }
+    uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    int e4 = (int)(r >> 23) - 120;
+    uint32_t m = (r >> 20) & 7u;
+    if (e4 > 15 || (e4 == 15 && m == 7u)) return sign | 0x7eu;
+    return sign | ((uint32_t)e4 << 3) | m;
+}
+
+// rounded_fp8_scale (…gate_up_batch1_mxfp4.comp.template:357-363).
+__device__ __forceinline__ float pow2_fp8_scale(float block_max) {
+    float ratio = fmaxf(block_max, 1e-4f) / 448.0f;
+    uint32_t bits = __float_as_uint(ratio);
+    int exponent = (int)((bits >> 23) & 0xffu) - 127;
+    if ((bits & 0x7fffffu) != 0u) exponent++;
+    return __uint_as_float((uint32_t)(exponent + 127) << 23);
+}
+
+// amax/448 scale (tied_output_projection_fp8_e4m3.comp.template:99).
+__device__ __forceinline__ float amax_fp8_scale(float block_max) {
+    return block_max > 0.0f ? block_max / 448.0f : 1.0f;
+}
+
+// e8m0 byte of a power-of-two f32 scale (its biased exponent field).
+__device__ __forceinline__ uint32_t pow2_to_e8m0(float s) { return (__float_as_uint(s) >> 23) & 0xffu; }
+
+__device__ __forceinline__ float wave_max32(float v) {
+    // Reduction inside each 32-lane half of the wave (subgroupClusteredMax(v, 32)).
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 8));
+    v = fmaxf(v, __shfl_xor(v, 4));
+    v = fmaxf(v, __shfl_xor(v, 2));
+    v = fmaxf(v, __shfl_xor(v, 1));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Host side: context, errors, workspace.
+// ---------------------------------------------------------------------------
+
+struct nerve_hip_ctx {
+    int device;
+    int cu_count;
+    void* workspace;
+    size_t workspace_bytes;
+};
+
+namespace nh {
+
+nerve_hip_status fail(nerve_hip_status code, const std::string& msg);
+nerve_hip_status ok();
+// Makes ctx's device current and validates ctx itself.
+nerve_hip_status enter(nerve_hip_ctx* ctx);
+// Grows the context workspace to at least `bytes` (may synchronize the device
+// when it has to grow).  Returns the device pointer through `out`.
+nerve_hip_status workspace(nerve_hip_ctx* ctx, size_t bytes, void** out);
+// Checks the launch status of the last kernel.
+nerve_hip_status check_launch(const char* what);
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves aligned sub-buffers out of one workspace allocation.
+struct Carver {
+    size_t offset = 0;
+    template <typename T>
+    size_t take(size_t count) {
+        offset = align_up(offset, 256);
+        size_t at = offset;
+        offset += count * sizeof(T);
+        return at;
+    }
+};
+
+// ---- specialization strings (reference grammar, nerve/model_package_shader_templates.py) ----
+
+struct MoeSpec {
+    bool gate_up = false;       // gate_up vs down
+    bool batch1 = false;
+    bool tensor_parallel = false;
+    bool prequant = false;
+    bool input_block_major = false;
+    int weight_repr = 0;        // 0 compact, 1 resident_fp8_e4m3, 2 adaptive_fp8_e4m3
+    int native_fp8_start = -1;
+    uint32_t hidden = 0, inter = 0, experts = 0, k = 0;
+    bool has_limit = false;
+    float limit = 0.0f;
+};
+nerve_hip_status parse_moe_spec(const char* spec, MoeSpec* out);
+
+struct TopkSpec {
+    int mode = 0;               // 0 moe_topk, 1 moe_router_score_topk
+    int activation = 0;         // mode 0: 1 = sigmoid; mode 1: 0 sigmoid, 1 softmax, 2 sqrtsoftplus
+    uint32_t experts = 0, k = 0, always_count = 0;
+    float always_weight = 0.0f;
+    int normalize = 0;
+    float softcap = 0.0f;
+    float routed_scale = 1.0f;
+    int bias = 0;               // 0 none, 1 f32, 2 bf16
+};
+nerve_hip_status parse_topk_spec(const char* spec, TopkSpec* out);
+
+struct Int4Spec {
+    int op = 0;                 // 0 linear, 1 linear_bias, 2 linear_residual
+    int batch_tile = 0;         // 0 = unbatched form
+    int layout = 0;             // 0 gptq, 1 ct
+    int scale_bf16 = 0;
+    uint32_t group = 0, in = 0, out = 0;
+};
+nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out);
+
+struct Fp8HeadSpec {
+    int batch_tile = 0;
+    uint32_t block_rows = 0, block_cols = 0, vocab = 0, in = 0;
+    float output_scale = 1.0f;
+};
+nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out);
+
+struct QuantSpec {
+    int batch_tile = 0;
+    bool pow2 = false;
+    uint32_t block = 0, elements = 0;
+};
+nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out);
+
+}  // namespace nh

@@ -1,0 +1,262 @@
+// Context lifecycle, thread-local errors, workspace and specialization-string
+// parsing for libnerve_hip.
+#include <cstdarg>
+#include <cstdlib>
+#include <regex>
+#include <string>
+
+#include "common.h"
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+namespace nh {
+
+nerve_hip_status fail(nerve_hip_status code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+nerve_hip_status ok() { return NERVE_HIP_OK; }
+
+nerve_hip_status enter(nerve_hip_ctx* ctx) {
+    if (!ctx) return fail(NERVE_HIP_INVALID_ARGUMENT, "null nerve_hip_ctx");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail(NERVE_HIP_DEVICE_ERROR, std::string("hipSetDevice: ") + hipGetErrorString(e));
+    return NERVE_HIP_OK;
+}
+
+nerve_hip_status workspace(nerve_hip_ctx* ctx, size_t bytes, void** out) {
+    if (bytes == 0) bytes = 256;
+    if (ctx->workspace_bytes < bytes) {
+        if (ctx->workspace) {
+            // hipFree waits for work that may still use the old allocation.
+            (void)hipDeviceSynchronize();
+            (void)hipFree(ctx->workspace);
+            ctx->workspace = nullptr;
+            ctx->workspace_bytes = 0;
+        }
+        size_t grow = align_up(bytes + bytes / 4, 1 << 20);
+        hipError_t e = hipMalloc(&ctx->workspace, grow);
+        if (e != hipSuccess) {
+            ctx->workspace = nullptr;
+            return fail(NERVE_HIP_OUT_OF_MEMORY, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+        }
+        ctx->workspace_bytes = grow;
+    }
+    *out = ctx->workspace;
+    return NERVE_HIP_OK;
+}
+
+nerve_hip_status check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(NERVE_HIP_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+    return NERVE_HIP_OK;
+}
+
+static bool parse_float(const std::string& s, float* out) {
+    char* end = nullptr;
+    float v = strtof(s.c_str(), &end);
+    if (!end || *end != '\0' || s.empty()) return false;
+    *out = v;
+    return true;
+}
+
+static bool parse_u32(const std::string& s, uint32_t* out) {
+    if (s.empty() || s.size() > 9) return false;
+    *out = (uint32_t)strtoul(s.c_str(), nullptr, 10);
+    return true;
+}
+
+// nerve/model_package_shader_templates.py:4773-4846
+nerve_hip_status parse_moe_spec(const char* spec, MoeSpec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex re(
+        "independent_sparse_moe_(gate_up|down)(?:_(batch1))?"
+        "(?:_(tensor_parallel))?"
+        "(?:_(prequant))?_"
+        "(?:(input_block_major_b128)_)?"
+        "mxfp4_e2m1(?:_(resident_fp8_e4m3|adaptive_fp8_e4m3))?_g32"
+        "(?:_native_fp8_e4m3_se8m0_b128_nf(\\d+))?_"
+        "h(\\d+)_i(\\d+)_e(\\d+)_k(\\d+)"
+        "(?:_limit([0-9eE+.-]+))?\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re)) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an MXFP4 expert kernel: ") + spec);
+    MoeSpec s;
+    s.gate_up = m[1].str() == "gate_up";
+    s.batch1 = m[2].matched;
+    s.tensor_parallel = m[3].matched;
+    s.prequant = m[4].matched;
+    s.input_block_major = m[5].matched;
+    s.weight_repr = !m[6].matched ? 0 : (m[6].str() == "resident_fp8_e4m3" ? 1 : 2);
+    uint32_t nf = 0;
+    if (m[7].matched) { parse_u32(m[7].str(), &nf); s.native_fp8_start = (int)nf; }
+    if (!parse_u32(m[8].str(), &s.hidden) || !parse_u32(m[9].str(), &s.inter) ||
+        !parse_u32(m[10].str(), &s.experts) || !parse_u32(m[11].str(), &s.k))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("bad shape in ") + spec);
+    s.has_limit = m[12].matched;
+    if (s.has_limit && !parse_float(m[12].str(), &s.limit)) return fail(NERVE_HIP_INVALID_SPEC, std::string("bad limit in ") + spec);
+    // Reference validation, with the 128-multiple rule relaxed to 32 (the
+    // MX group) under zero-padded tail-block semantics.
+    if (s.hidden == 0 || s.hidden % 32 || s.inter == 0 || s.inter % 32 || !(0 < s.k && s.k <= s.experts) ||
+        s.gate_up != s.has_limit || s.experts > 65536)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid demand-addressed MXFP4 expert kernel ") + spec);
+    if (s.tensor_parallel) return fail(NERVE_HIP_UNSUPPORTED, "tensor-parallel expert partials are a multi-GPU path; this backend is single-GPU");
+    if (s.weight_repr != 0 || s.native_fp8_start >= 0)
+        return fail(NERVE_HIP_UNSUPPORTED, "resident/adaptive FP8 and native-FP8 expert banks are not implemented yet");
+    if (s.input_block_major) return fail(NERVE_HIP_UNSUPPORTED, "input_block_major_b128 layout is not implemented yet");
+    if (s.prequant && !s.gate_up) return fail(NERVE_HIP_INVALID_SPEC, "prequant applies to gate_up only");
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
+// nerve/model_package_shader_templates.py:4850-4915 and :5003-5060
+nerve_hip_status parse_topk_spec(const char* spec, TopkSpec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex topk(
+        "moe_topk(?:_batch(\\d+))?_(sigmoid|softmax)_bf16_e(\\d+)_k(\\d+)_"
+        "norm([01])_cap([0-9eE+.-]+)_(biasf32|biasbf16|nobias)\\.comp");
+    static const std::regex score(
+        "moe_router(?:_(batch1))?_score_topk_(sigmoid|softmax|sqrtsoftplus)_bf16_r(\\d+)_k(\\d+)_"
+        "a(\\d+)w([0-9eE+.-]+)_norm([01])_scale([0-9eE+.-]+)_bias(f32|bf16)\\.comp");
+    std::cmatch m;
+    TopkSpec s;
+    if (std::regex_match(spec, m, topk)) {
+        if (m[1].matched && m[1].str() != "1") return fail(NERVE_HIP_INVALID_SPEC, "sparse routing supports only frame-parallel batch tiles");
+        s.mode = 0;
+        s.activation = m[2].str() == "sigmoid" ? 1 : 0;
+        parse_u32(m[3].str(), &s.experts);
+        parse_u32(m[4].str(), &s.k);
+        s.normalize = m[5].str() == "1";
+        if (!parse_float(m[6].str(), &s.softcap)) return fail(NERVE_HIP_INVALID_SPEC, "bad softcap");
+        std::string b = m[7].str();
+        s.bias = b == "nobias" ? 0 : (b == "biasf32" ? 1 : 2);
+    } else if (std::regex_match(spec, m, score)) {
+        s.mode = 1;
+        std::string a = m[2].str();
+        s.activation = a == "sigmoid" ? 0 : (a == "softmax" ? 1 : 2);
+        parse_u32(m[3].str(), &s.experts);
+        parse_u32(m[4].str(), &s.k);
+        parse_u32(m[5].str(), &s.always_count);
+        if (!parse_float(m[6].str(), &s.always_weight)) return fail(NERVE_HIP_INVALID_SPEC, "bad always-selected weight");
+        s.normalize = m[7].str() == "1";
+        if (!parse_float(m[8].str(), &s.routed_scale)) return fail(NERVE_HIP_INVALID_SPEC, "bad routed scale");
+        s.bias = m[9].str() == "f32" ? 1 : 2;
+    } else {
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("not a top-k routing kernel: ") + spec);
+    }
+    if (!(0 < s.k && s.k <= s.experts && s.experts <= 4096) || s.experts + s.always_count > 4096 || s.k + s.always_count > 64)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid sparse expert routing ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
+// nerve/model_package_shader_templates.py:3219-3276
+nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex re(
+        "(linear|linear_bias|linear_residual)(?:_batch(\\d+))?_int4_(gptq|ct)_s(f16|bf16)_g(\\d+)_(\\d+)x(\\d+)\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re)) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an INT4 linear kernel: ") + spec);
+    Int4Spec s;
+    std::string op = m[1].str();
+    s.op = op == "linear" ? 0 : (op == "linear_bias" ? 1 : 2);
+    uint32_t bt = 0;
+    if (m[2].matched) parse_u32(m[2].str(), &bt);
+    s.batch_tile = (int)bt;
+    s.layout = m[3].str() == "gptq" ? 0 : 1;
+    s.scale_bf16 = m[4].str() == "bf16";
+    parse_u32(m[5].str(), &s.group);
+    parse_u32(m[6].str(), &s.in);
+    parse_u32(m[7].str(), &s.out);
+    if (s.group == 0 || s.group % 32 || s.in == 0 || s.in % s.group || s.out == 0 || s.out % 2 ||
+        (m[2].matched && bt == 0))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid native INT4 shape ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
+// nerve/model_package_shader_templates.py:2419-2465 (the output-scale token is
+// accepted as any float literal: the manifest writes it with format ".9g",
+// nerve/model_package_manifest.py:530-545).
+nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex re(
+        "tied_output_projection(?:_batch(\\d+))?_fp8_e4m3_b(\\d+)x(\\d+)_(\\d+)x(\\d+)_scale([0-9eE+.-]+)_to_f32\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re)) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an FP8 output projection: ") + spec);
+    Fp8HeadSpec s;
+    uint32_t bt = 0;
+    if (m[1].matched) parse_u32(m[1].str(), &bt);
+    s.batch_tile = (int)bt;
+    parse_u32(m[2].str(), &s.block_rows);
+    parse_u32(m[3].str(), &s.block_cols);
+    parse_u32(m[4].str(), &s.vocab);
+    parse_u32(m[5].str(), &s.in);
+    if (!parse_float(m[6].str(), &s.output_scale)) return fail(NERVE_HIP_INVALID_SPEC, "bad output scale");
+    if ((m[1].matched && bt == 0) || s.block_rows == 0 || s.block_cols != 128 || s.in == 0 || s.in % 32 || s.vocab == 0)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid FP8 output projection shader shape ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
+// nerve/model_package_shader_templates.py:1513-1545
+nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex re("quantize(?:_batch(\\d+))?_fp8_e4m3(?:_(spow2))?_b(\\d+)_h(\\d+)\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re)) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an FP8 activation quantizer: ") + spec);
+    QuantSpec s;
+    uint32_t bt = 0;
+    if (m[1].matched) parse_u32(m[1].str(), &bt);
+    s.batch_tile = (int)bt;
+    s.pow2 = m[2].matched;
+    parse_u32(m[3].str(), &s.block);
+    parse_u32(m[4].str(), &s.elements);
+    if ((m[1].matched && bt == 0) || s.block != 128 || s.elements == 0 || s.elements % 32)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid FP8 activation-quantizer shape ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
+}  // namespace nh
+
+extern "C" {
+
+int nerve_hip_abi_version(void) { return NERVE_HIP_ABI_VERSION; }
+
+const char* nerve_hip_last_error(void) { return g_last_error.c_str(); }
+
+nerve_hip_status nerve_hip_open(int device_ordinal, nerve_hip_ctx** out) {
+    if (!out) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return nh::fail(NERVE_HIP_DEVICE_ERROR, "no HIP device available");
+    if (device_ordinal < 0 || device_ordinal >= count) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "device ordinal out of range");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device_ordinal);
+    if (e != hipSuccess) return nh::fail(NERVE_HIP_DEVICE_ERROR, std::string("hipGetDeviceProperties: ") + hipGetErrorString(e));
+    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+        return nh::fail(NERVE_HIP_UNSUPPORTED, std::string("libnerve_hip is built for gfx950, device is ") + prop.gcnArchName);
+    nerve_hip_ctx* ctx = new nerve_hip_ctx();
+    ctx->device = device_ordinal;
+    ctx->cu_count = prop.multiProcessorCount;
+    ctx->workspace = nullptr;
+    ctx->workspace_bytes = 0;
+    *out = ctx;
+    return NERVE_HIP_OK;
+}
+
+void nerve_hip_close(nerve_hip_ctx* ctx) {
+    if (!ctx) return;
+    if (ctx->workspace) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ctx->workspace);
+    }
+    delete ctx;
+}
+
+}  // extern "C"

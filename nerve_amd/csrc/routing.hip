@@ -1,0 +1,406 @@
+// MoE routing on gfx950: router projection (a5), top-k (a6), expert-sorted
+// route compaction (a7) and the weighted combine (a8).
+#include <cmath>
+
+#include "common.h"
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// a5: logits[b, e] = bf16(sum_k x[b,k] W[e,k]) (linear_bf16.comp.template:
+// 40-98).  One block = 16 tokens x 16 experts; its 8 waves split K and reduce
+// through LDS.  Each wave issues v_mfma_f32_16x16x32_bf16 with both operands
+// loaded in the same per-lane k order (8 contiguous values per lane), so the
+// pairing of A and B elements is the identity whatever the hardware's k
+// numbering is.
+// ---------------------------------------------------------------------------
+constexpr int RL_WAVES = 8;
+
+__global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ W, uint32_t B,
+                                                                       uint32_t H, uint32_t E,
+                                                                       uint16_t* __restrict__ logits) {
+    __shared__ v4f part[RL_WAVES][64];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t b0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+    const uint32_t tok = b0 + rr, ex = e0 + rr;
+    const uint32_t nsteps = (H + 31) / 32;
+    const uint32_t per = (nsteps + RL_WAVES - 1) / RL_WAVES;
+    const uint32_t s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+    const bool H8 = (H % 8) == 0;
+    for (uint32_t s = s0; s < s1; s++) {
+        const uint32_t k0 = s * 32 + g * 8;
+        v4i av = v4i{0, 0, 0, 0}, bv = v4i{0, 0, 0, 0};
+        if (H8) {
+            if (tok < B && k0 < H) av = *reinterpret_cast<const v4i*>(x + (uint64_t)tok * H + k0);
+            if (ex < E && k0 < H) bv = *reinterpret_cast<const v4i*>(W + (uint64_t)ex * H + k0);
+        } else {
+            uint16_t at[8], bt[8];
+            for (int j = 0; j < 8; j++) {
+                at[j] = (tok < B && k0 + j < H) ? x[(uint64_t)tok * H + k0 + j] : 0;
+                bt[j] = (ex < E && k0 + j < H) ? W[(uint64_t)ex * H + k0 + j] : 0;
+            }
+            av = *reinterpret_cast<v4i*>(at);
+            bv = *reinterpret_cast<v4i*>(bt);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bv), acc,
+                                                      0, 0, 0);
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        v4f t = part[0][lane];
+#pragma unroll
+        for (int w = 1; w < RL_WAVES; w++) t += part[w][lane];
+        // Result lane (g, rr) holds D[token 4g+i][expert rr].
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t bt = b0 + 4 * g + i;
+            if (bt < B && ex < E) logits[(uint64_t)bt * E + ex] = (uint16_t)f32_to_bf16(t[i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// a6: top-k.  One wave per token.
+// ---------------------------------------------------------------------------
+struct TopkParams {
+    uint32_t E, k, always_count;
+    int mode, activation, normalize, bias;
+    float softcap, routed_scale, always_weight;
+};
+
+__device__ __forceinline__ bool better(float s, uint32_t i, float bs, uint32_t bi) {
+    return s > bs || (s == bs && i < bi);
+}
+
+__device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ logits, const void* __restrict__ bias,
+                                                  uint32_t* __restrict__ routes, uint32_t* __restrict__ telemetry,
+                                                  uint32_t B, TopkParams P) {
+    extern __shared__ float sh[];
+    float* raw = sh;                 // [E] router values (after softcap / activation)
+    uint32_t* sel = reinterpret_cast<uint32_t*>(sh + P.E);  // [E]
+    __shared__ uint32_t top[128];
+    __shared__ float wts[128];
+    __shared__ float smax_sh, sden_sh;
+    const uint32_t b = blockIdx.x;
+    if (b >= B) return;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t E = P.E;
+    for (uint32_t e = lane; e < E; e += 64) {
+        float v = bf16_to_f32(logits[(uint64_t)b * E + e]);
+        if (P.mode == 0 && P.softcap > 0.0f) v = tanhf(v / P.softcap) * P.softcap;
+        raw[e] = v;
+        sel[e] = 0;
+    }
+    __syncthreads();
+    if (P.mode == 1) {
+        // initialize_softmax + activate_router_value
+        // (moe_router_score_topk_batch1_bf16.comp.template:62-107).
+        if (P.activation == 1) {
+            float m = -INFINITY;
+            for (uint32_t e = lane; e < E; e += 64) m = fmaxf(m, raw[e]);
+            for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+            float s = 0.0f;
+            for (uint32_t e = lane; e < E; e += 64) s += expf(raw[e] - m);
+            for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d);
+            if (lane == 0) { smax_sh = m; sden_sh = s; }
+        }
+        __syncthreads();
+        for (uint32_t e = lane; e < E; e += 64) {
+            float v = raw[e];
+            if (P.activation == 0) v = sigmoidf_(v);
+            else if (P.activation == 1) v = expf(v - smax_sh) / sden_sh;
+            else v = sqrtf(fmaxf(v, 0.0f) + logf(1.0f + expf(-fabsf(v))));
+            raw[e] = v;
+        }
+        __syncthreads();
+    }
+    for (uint32_t r = 0; r < P.k; r++) {
+        float best = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (uint32_t e = lane; e < E; e += 64) {
+            float s = (P.mode == 0 && P.activation) ? sigmoidf_(raw[e]) : raw[e];
+            if (P.bias == 1) s = s + static_cast<const float*>(bias)[e];
+            else if (P.bias == 2) s = s + bf16_to_f32(static_cast<const uint16_t*>(bias)[e]);
+            if (!sel[e] && better(s, e, best, bi)) { best = s; bi = e; }
+        }
+        for (int d = 32; d > 0; d >>= 1) {
+            float os = __shfl_xor(best, d);
+            uint32_t oi = __shfl_xor(bi, d);
+            if (better(os, oi, best, bi)) { best = os; bi = oi; }
+        }
+        if (lane == 0) {
+            top[r] = bi;
+            if (bi < E) sel[bi] = 1;
+        }
+        __syncthreads();
+    }
+    if (lane != 0) return;
+    // All-NaN rows leave no selectable expert; index 0 keeps every LDS read in
+    // bounds (the reference shader would read past its array there).
+    for (uint32_t r = 0; r < P.k; r++)
+        if (top[r] >= E) top[r] = 0;
+    const uint32_t ks = P.k;
+    uint32_t total_sel = ks, total_res = E;
+    if (P.mode == 0) {
+        // moe_topk_routed_batch1_bf16.comp.template:133-167
+        const bool sig = P.activation != 0;
+        float maximum = raw[top[0]];
+        float den = 0.0f;
+        if (P.normalize) {
+            for (uint32_t r = 0; r < ks; r++) {
+                float l = raw[top[r]];
+                den += sig ? sigmoidf_(l) : expf(l - maximum);
+            }
+        } else if (!sig) {
+            maximum = -INFINITY;
+            for (uint32_t e = 0; e < E; e++) maximum = fmaxf(maximum, raw[e]);
+            for (uint32_t e = 0; e < E; e++) den += expf(raw[e] - maximum);
+        }
+        for (uint32_t r = 1; r < ks; r++) {
+            uint32_t ex = top[r];
+            uint32_t ins = r;
+            while (ins > 0 && top[ins - 1] > ex) { top[ins] = top[ins - 1]; ins--; }
+            top[ins] = ex;
+        }
+        for (uint32_t r = 0; r < ks; r++) {
+            float l = raw[top[r]];
+            float w = sig ? sigmoidf_(l) : expf(l - maximum);
+            if (P.normalize || !sig) w /= den;
+            wts[r] = w;
+        }
+    } else {
+        // moe_router_score_topk_batch1_bf16.comp.template:169-205
+        total_sel = ks + P.always_count;
+        total_res = E + P.always_count;
+        float den = 0.0f;
+        if (P.normalize) for (uint32_t r = 0; r < ks; r++) den += raw[top[r]];
+        for (uint32_t r = 0; r < ks; r++) {
+            float w = raw[top[r]];
+            wts[r] = P.normalize ? w / den * P.routed_scale : w * P.routed_scale;
+        }
+        for (uint32_t a = 0; a < P.always_count; a++) {
+            top[ks + a] = E + a;
+            wts[ks + a] = P.always_weight;
+        }
+        for (uint32_t r = 1; r < total_sel; r++) {
+            uint32_t ex = top[r];
+            float w = wts[r];
+            uint32_t ins = r;
+            while (ins > 0 && top[ins - 1] > ex) {
+                top[ins] = top[ins - 1];
+                wts[ins] = wts[ins - 1];
+                ins--;
+            }
+            top[ins] = ex;
+            wts[ins] = w;
+        }
+    }
+    for (uint32_t r = 0; r < total_sel; r++) {
+        routes[(uint64_t)b * total_sel + r] = (f32_to_bf16(wts[r]) << 16) | top[r];
+        if (telemetry) atomicAdd(&telemetry[top[r]], 1u);
+    }
+    if (telemetry) {
+        for (uint32_t l = 0; l < total_sel; l++)
+            for (uint32_t r = l + 1; r < total_sel; r++) {
+                uint32_t left = top[l], right = top[r];
+                if (left < right) {
+                    uint32_t preceding = left * (2u * total_res - left - 1u) / 2u;
+                    atomicAdd(&telemetry[total_res + preceding + right - left - 1u], 1u);
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// a7: route compaction (moe_route_compact_batch1.comp.template:26-106).
+// ---------------------------------------------------------------------------
+constexpr uint32_t COMPACT_LDS_ROUTES = 16384;
+
+__global__ __launch_bounds__(256) void compact_sorted_guarded_kernel(const uint32_t* __restrict__ routes, uint32_t n,
+                                                                      uint32_t k, uint32_t* __restrict__ frames,
+                                                                      uint64_t frame_words, uint32_t data_words,
+                                                                      uint32_t* __restrict__ control,
+                                                                      uint32_t tiles_per_route) {
+    if (control[2] != 0u) return;  // partitioned: compact_owned_kernel handles it
+    __shared__ uint16_t ex[COMPACT_LDS_ROUTES];
+    const bool staged = n <= COMPACT_LDS_ROUTES;
+    if (staged)
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ex[i] = (uint16_t)(routes[i] & 0xffffu);
+    __syncthreads();
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        control[3] = n;
+        control[4] = k * tiles_per_route;
+        control[5] = control[0];
+        control[6] = 1;
+    }
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n || !frames) return;
+    const uint32_t e = staged ? ex[i] : (routes[i] & 0xffffu);
+    uint32_t rank = 0;
+    for (uint32_t c = 0; c < n; c++) {
+        uint32_t ce = staged ? ex[c] : (routes[c] & 0xffffu);
+        rank += (ce < e || (ce == e && c < i)) ? 1u : 0u;
+    }
+    frames[(uint64_t)(rank / k) * frame_words + data_words + rank % k] = i;
+}
+
+__global__ __launch_bounds__(1024) void compact_owned_guarded_kernel(const uint32_t* __restrict__ routes, uint32_t n,
+                                                                      uint32_t k, uint32_t* __restrict__ frames,
+                                                                      uint64_t frame_words, uint32_t data_words,
+                                                                      uint32_t* __restrict__ control,
+                                                                      uint32_t tiles_per_route) {
+    if (control[2] == 0u) return;
+    __shared__ uint32_t wave_tot[16];
+    __shared__ uint32_t base_sh;
+    const uint32_t start = control[1], end = control[1] + control[2];
+    if (threadIdx.x == 0) base_sh = 0;
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    for (uint32_t c0 = 0; c0 < n; c0 += blockDim.x) {
+        const uint32_t i = c0 + threadIdx.x;
+        uint32_t flag = 0;
+        if (i < n) {
+            uint32_t e = routes[i] & 0xffffu;
+            flag = (e >= start && e < end) ? 1u : 0u;
+        }
+        uint32_t inc = flag;
+        for (int d = 1; d < 64; d <<= 1) {
+            uint32_t t = __shfl_up(inc, d);
+            if (lane >= (uint32_t)d) inc += t;
+        }
+        if (lane == 63) wave_tot[wave] = inc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t run = 0;
+            for (uint32_t w = 0; w < nwave; w++) {
+                uint32_t t = wave_tot[w];
+                wave_tot[w] = run;
+                run += t;
+            }
+        }
+        __syncthreads();
+        const uint32_t pos = base_sh + wave_tot[wave] + inc - flag;
+        if (flag && frames) frames[(uint64_t)(pos / k) * frame_words + data_words + pos % k] = i;
+        __syncthreads();
+        if (threadIdx.x == blockDim.x - 1) base_sh = pos + flag;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        control[3] = base_sh;
+        control[4] = base_sh * tiles_per_route;
+        control[5] = 1;
+        control[6] = 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// a8: weighted combine (moe_reduce_batch1_bf16.comp.template:29-54).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* __restrict__ eo, uint16_t* __restrict__ out,
+                                                     uint32_t B, uint32_t H, uint32_t k, float routed_scale) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)B * H) return;
+    const uint32_t b = (uint32_t)(idx / H), j = (uint32_t)(idx % H);
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < k; r++) acc = round_bf16(acc + bf16_to_f32(eo[((uint64_t)b * k + r) * H + j]));
+    out[idx] = (uint16_t)f32_to_bf16(acc * routed_scale);
+}
+
+}  // namespace
+
+extern "C" {
+
+nerve_hip_status nerve_hip_router_linear_bf16(nerve_hip_ctx* ctx, const void* x_bf16, const void* weight_bf16,
+                                              void* logits_bf16, uint32_t batch_width, uint32_t hidden,
+                                              uint32_t experts, void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    if (!x_bf16 || !weight_bf16 || !logits_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (hidden == 0 || experts == 0) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "empty router shape");
+    if (batch_width == 0) return nh::ok();
+    if (hidden % 8 == 0 && (((uintptr_t)x_bf16 | (uintptr_t)weight_bf16) & 15))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "router buffers must be 16-byte aligned");
+    dim3 grid((batch_width + 15) / 16, (experts + 15) / 16);
+    router_linear_kernel<<<grid, 64 * RL_WAVES, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(x_bf16), static_cast<const uint16_t*>(weight_bf16), batch_width, hidden, experts,
+        static_cast<uint16_t*>(logits_bf16));
+    return nh::check_launch("router_linear_bf16");
+}
+
+nerve_hip_status nerve_hip_moe_router_topk(nerve_hip_ctx* ctx, const char* spec, const void* logits_bf16,
+                                           const void* bias, void* routes_u32, void* telemetry_u32,
+                                           uint32_t batch_width, void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::TopkSpec ts;
+    if ((st = nh::parse_topk_spec(spec, &ts))) return st;
+    if (!logits_bf16 || !routes_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (ts.bias != 0 && !bias) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "specialization requires a selection bias");
+    if (batch_width == 0) return nh::ok();
+    TopkParams P;
+    P.E = ts.experts;
+    P.k = ts.k;
+    P.always_count = ts.always_count;
+    P.mode = ts.mode;
+    P.activation = ts.activation;
+    P.normalize = ts.normalize;
+    P.bias = ts.bias;
+    P.softcap = ts.softcap;
+    P.routed_scale = ts.routed_scale;
+    P.always_weight = ts.always_weight;
+    size_t lds = (size_t)ts.experts * 8;
+    topk_kernel<<<batch_width, 64, lds, (hipStream_t)stream>>>(static_cast<const uint16_t*>(logits_bf16), bias,
+                                                               static_cast<uint32_t*>(routes_u32),
+                                                               static_cast<uint32_t*>(telemetry_u32), batch_width, P);
+    return nh::check_launch("moe_router_topk");
+}
+
+nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spec, const void* routes_u32,
+                                             void* intermediates, void* control_u32, uint32_t batch_width,
+                                             void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::MoeSpec ms;
+    if ((st = nh::parse_moe_spec(spec, &ms))) return st;
+    if (!routes_u32 || !control_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    const uint32_t n = batch_width * ms.k;
+    // TILES_PER_ROUTE of the consuming projection: 32-row gate_up tiles,
+    // 64-row down tiles (nerve/model_package_shader_templates.py:4836).
+    const uint32_t tiles = ms.gate_up ? (ms.inter + 31) / 32 : (ms.hidden + 63) / 64;
+    const uint64_t frame_words = (uint64_t)ms.k * ms.inter / 2 + ms.k;
+    const uint32_t data_words = ms.k * ms.inter / 2;
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* frames = static_cast<uint32_t*>(intermediates);
+    const uint32_t* routes = static_cast<const uint32_t*>(routes_u32);
+    uint32_t* control = static_cast<uint32_t*>(control_u32);
+    uint32_t blocks = n == 0 ? 1 : (n + 255) / 256;
+    compact_sorted_guarded_kernel<<<blocks, 256, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control, tiles);
+    if ((st = nh::check_launch("moe_route_compact"))) return st;
+    compact_owned_guarded_kernel<<<1, 1024, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control, tiles);
+    return nh::check_launch("moe_route_compact_owned");
+}
+
+nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_outputs, void* out_bf16,
+                                      uint32_t batch_width, uint32_t hidden, uint32_t experts_per_token,
+                                      float routed_scale, void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    if (!expert_outputs || !out_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (experts_per_token == 0) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "experts_per_token must be positive");
+    const uint64_t total = (uint64_t)batch_width * hidden;
+    if (total == 0) return nh::ok();
+    reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(expert_outputs), static_cast<uint16_t*>(out_bf16), batch_width, hidden,
+        experts_per_token, routed_scale);
+    return nh::check_launch("moe_reduce");
+}
+
+}  // extern "C"

@@ -1,0 +1,221 @@
+"""GPU parity: activation quantization (a2), raw MXFP4 GEMV, MXFP4 expert
+gate_up/down (a3/a4), route compaction (a7), combine (a8), all through the
+C ABI, against the CPU oracle."""
+import numpy as np
+import pytest
+
+import oracle
+from nerve_amd import workloads as wl
+from nerve_amd.moe import ExpertBank, address_record, down_spec, gate_up_spec, u32_tensor
+
+from helpers import bf16_close, rel_err_normwise, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+@pytest.mark.parametrize("cols", [128, 2880, 4096, 96])
+@pytest.mark.parametrize("pow2", [True, False])
+def test_quantize_bit_exact(ctx, dev, cols, pow2):
+    torch = _torch()
+    rng = np.random.default_rng(cols + pow2)
+    rows = 7
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * rng.uniform(1e-3, 50, (rows, 1)).astype(np.float32)
+    x[0, :40] = 0.0  # zero-amax block edge
+    x[1, 5] = 3e4
+    xb = wl.f32_to_bf16_bits(x)
+    xb[2, :] = 0  # all-zero row -> floor scale
+    nblk = (cols + 127) // 128
+    q = torch.zeros(rows, cols, dtype=torch.uint8, device=dev)
+    s = torch.zeros(rows, nblk, dtype=torch.float32, device=dev)
+    spec = f"quantize_fp8_e4m3{'_spow2' if pow2 else ''}_b128_h{cols}.comp"
+    ctx.quantize_fp8_e4m3(spec, to_dev(xb, dev), rows, q, s)
+    qr, sr = oracle.quantize_blocks(xb, pow2)
+    assert np.array_equal(to_np(q, np.uint8), qr)
+    assert np.array_equal(to_np(s, np.float32).view(np.uint32), sr.view(np.uint32))
+
+
+def _gemv(ctx, dev, q, s, W, S):
+    torch = _torch()
+    M, K = q.shape
+    N = W.shape[0]
+    y = torch.zeros(M, N, dtype=torch.float32, device=dev)
+    ctx.mxfp4_gemv(to_dev(q, dev), to_dev(s, dev), M, K, to_dev(W, dev), to_dev(S, dev), N, y)
+    return to_np(y, np.float32)
+
+
+def test_gemv_config0_parity(ctx, dev):
+    d = wl.config0()
+    q, s = oracle.quantize_blocks(d["x_bf16"], pow2=True)
+    y = _gemv(ctx, dev, q, s, d["W"], d["S"])
+    ref = oracle.mxfp4_gemv(q, s, d["W"], d["S"])
+    assert rel_err_normwise(y, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 16), (4, 256, 64), (16, 2880, 256), (33, 4096, 128), (64, 160, 32)])
+def test_gemv_shapes(ctx, dev, M, K, N):
+    rng = np.random.default_rng(M * K + N)
+    W, S = wl.mxfp4_matrix(rng, N, K, 118, 130)
+    x = wl.bf16_normal(rng, (M, K))
+    q, s = oracle.quantize_blocks(x, pow2=True)
+    y = _gemv(ctx, dev, q, s, W, S)
+    ideal = oracle.mxfp4_gemv_f64(q, s, W, S)
+    ref = oracle.mxfp4_gemv(q, s, W, S)
+    assert rel_err_normwise(y, ref) <= 1e-3
+    assert rel_err_normwise(y, ideal) <= 1e-3
+
+
+# --------------------------------------------------------------------------
+# MoE chain helpers
+# --------------------------------------------------------------------------
+
+class MoeRig:
+    """Device buffers of one gate_up -> down -> reduce run in package layouts."""
+
+    def __init__(self, dev, d, routes_np):
+        torch = _torch()
+        self.dev = dev
+        self.B, self.k = routes_np.shape
+        self.E, self.I, _ = d["gate_w"].shape
+        self.H = d["down_w"].shape[1]
+        self.d = d
+        self.bank = ExpertBank(*(to_dev(d[n], dev) for n in ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")))
+        self.routes = to_dev(routes_np.astype(np.uint32), dev)
+        self.frame_words = self.k * self.I // 2 + self.k
+        self.inter = torch.zeros(self.B * self.frame_words, dtype=torch.int32, device=dev)
+        self.control = to_dev(np.array([self.B, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev)
+        self.expert_out = torch.zeros(self.B, self.k, self.H, dtype=torch.int16, device=dev)
+        self.out = torch.zeros(self.B, self.H, dtype=torch.int16, device=dev)
+        self.gu = gate_up_spec(self.H, self.I, self.E, self.k, d.get("limit", 7.0))
+        self.dn = down_spec(self.H, self.I, self.E, self.k)
+
+    def frames_np(self):
+        return to_np(self.inter, np.uint32).reshape(self.B, self.frame_words)
+
+    def h_np(self):
+        fr = self.frames_np()[:, : self.k * self.I // 2].copy()
+        return fr.view(np.uint16).reshape(self.B, self.k, self.I)
+
+    def map_np(self):
+        return self.frames_np()[:, self.k * self.I // 2:].reshape(-1)
+
+    def run(self, ctx, hidden_np, addresses=None, gate_slots=None, down_slots=None):
+        hidden = to_dev(hidden_np, self.dev)
+        bank = self.bank
+        ctx.moe_route_compact(self.gu, self.routes, self.inter, self.control, self.B)
+        ctx.mxfp4_moe_gate_up(self.gu, hidden, None, self.routes, self.inter,
+                              bank.addresses if addresses is None else addresses,
+                              bank.gate_slots if gate_slots is None else gate_slots, self.control, self.B)
+        ctx.moe_route_compact(self.dn, self.routes, None, self.control, self.B)
+        ctx.mxfp4_moe_down(self.dn, self.inter, self.routes, self.expert_out,
+                           bank.addresses if addresses is None else addresses,
+                           bank.down_slots if down_slots is None else down_slots, self.control, self.B)
+        ctx.moe_reduce(self.expert_out, self.out, self.B, self.H, self.k, 1.0)
+
+
+def _route_words(experts: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    return ((wl.f32_to_bf16_bits(weights).astype(np.uint32) << np.uint32(16)) | experts.astype(np.uint32))
+
+
+def test_known_answers_mxfp4_tests_rs(ctx, dev):
+    """runtime-rs/src/vulkan_compute/mxfp4_tests.rs:67-216: H = I = 128, all
+    nibbles 0x22 (1.0), scale byte 120 (2^-7), hidden 1.0, route weight 1.0."""
+    torch = _torch()
+    W = 128
+    d = dict(gate_w=np.full((1, W, W // 2), 0x22, np.uint8), gate_s=np.full((1, W, W // 32), 120, np.uint8),
+             up_w=np.full((1, W, W // 2), 0x22, np.uint8), up_s=np.full((1, W, W // 32), 120, np.uint8),
+             down_w=np.full((1, W, W // 2), 0x22, np.uint8), down_s=np.full((1, W, W // 32), 120, np.uint8),
+             limit=10.0)
+    routes = _route_words(np.zeros((1, 1)), np.ones((1, 1), np.float32))
+    rig = MoeRig(dev, d, routes)
+    hidden = np.full((1, W), 0x3F80, np.uint16)
+    rig.run(ctx, hidden)
+    expected = int(wl.f32_to_bf16_bits(np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(-1.0)))))
+    assert expected == 0x3F3B
+    assert np.all(rig.h_np() == expected)
+    # down with intermediate 1.0 -> 1.0 per code; every e2m1 code reproduces its value
+    fr = rig.frames_np()
+    fr[:, : W // 2] = 0x3F803F80
+    values = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, 0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    for nib, val in enumerate(values):
+        rig.bank.down_w.fill_(nib | (nib << 4))
+        rig.inter.copy_(to_dev(fr.reshape(-1), dev))
+        ctx.moe_route_compact(rig.dn, rig.routes, None, rig.control, 1)
+        ctx.mxfp4_moe_down(rig.dn, rig.inter, rig.routes, rig.expert_out, rig.bank.addresses, rig.bank.down_slots,
+                           rig.control, 1)
+        got = to_np(rig.expert_out, np.uint16)
+        assert np.all(got == wl.f32_to_bf16_bits(np.float32(val))), (nib, got[0, 0, :4])
+
+
+def _moe_case(E, k, B, H, I, seed):
+    rng = np.random.default_rng(seed)
+    d = wl.moe_experts(rng, E, H, I)
+    d["limit"] = 7.0
+    logits = wl.bf16_normal(rng, (B, E))
+    routes, _ = oracle.topk(logits, k)
+    hidden = wl.bf16_normal(rng, (B, H))
+    return d, routes, hidden
+
+
+@pytest.mark.parametrize("E,k,B,H,I", [(8, 2, 4, 256, 256), (4, 4, 3, 160, 96), (32, 4, 16, 2880, 2880),
+                                       (16, 1, 40, 512, 384)])
+def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
+    d, routes, hidden = _moe_case(E, k, B, H, I, seed=E * 100 + B)
+    rig = MoeRig(dev, d, routes)
+    rig.run(ctx, hidden)
+    cmap, ctl = oracle.route_compact(routes, k, (I + 31) // 32, B)
+    assert np.array_equal(rig.map_np(), cmap)
+    ctl_gpu = to_np(rig.control, np.uint32)[:7]
+    # after the down-stage count the dispatch geometry is the down projection's
+    _, ctl_down = oracle.route_compact(routes, k, (H + 63) // 64, B)
+    assert np.array_equal(ctl_gpu, ctl_down)
+    h_ref = oracle.moe_gate_up(hidden, routes, cmap, B * k, k, d["gate_w"], d["gate_s"], d["up_w"], d["up_s"], 7.0)
+    ok, worst, exact = bf16_close(rig.h_np(), h_ref)
+    assert ok and exact > 0.9, (worst, exact)
+    # down on the GPU's own h (isolates a4 from a3 rounding differences)
+    eo_ref = oracle.moe_down(rig.h_np(), routes, cmap, B * k, d["down_w"], d["down_s"])
+    ok, worst, exact = bf16_close(to_np(rig.expert_out, np.uint16), eo_ref)
+    assert ok and exact > 0.9, (worst, exact)
+    out_ref = oracle.moe_reduce(to_np(rig.expert_out, np.uint16), 1.0)
+    assert np.array_equal(to_np(rig.out, np.uint16), out_ref)
+    # end to end against the oracle chain
+    eo_chain = oracle.moe_down(h_ref, routes, cmap, B * k, d["down_w"], d["down_s"])
+    ok, worst, _ = bf16_close(to_np(rig.out, np.uint16), oracle.moe_reduce(eo_chain, 1.0))
+    assert ok, worst
+
+
+def test_fail_closed_invalid_metadata(ctx, dev):
+    """mxfp4_tests.rs:218-315: invalid expert ids, unbound slots, non-resident
+    records, zero generation and short byte counts write nothing."""
+    torch = _torch()
+    E, k, B, H, I = 4, 2, 2, 128, 128
+    d, _, hidden = _moe_case(E, k, B, H, I, seed=7)
+    # token 0: expert 0 (valid) and expert 9 (>= E); token 1: expert 1 (to be
+    # invalidated) and expert 2 (valid)
+    routes = _route_words(np.array([[0, 9], [1, 2]]), np.full((2, 2), 0.5, np.float32))
+    rig = MoeRig(dev, d, routes)
+    bad = np.array(rig.bank.records, np.uint64).reshape(-1, 8)
+    e_bad = 1
+    gslots = to_np(rig.bank.gate_slots, np.uint32).copy()
+    dslots = to_np(rig.bank.down_slots, np.uint32).copy()
+    cases = []
+    r1 = bad.copy(); r1[gslots[e_bad * 4 + 0], 6] = 0; cases.append(("non-resident", r1, gslots, dslots))
+    r2 = bad.copy(); r2[gslots[e_bad * 4 + 1], 4:6] = 0; cases.append(("zero generation", r2, gslots, dslots))
+    r3 = bad.copy(); r3[gslots[e_bad * 4 + 2], 2] -= 1; cases.append(("short byte count", r3, gslots, dslots))
+    g4 = gslots.copy(); g4[e_bad * 4 + 3] = 0xFFFFFFFF; cases.append(("unbound slot", bad, g4, dslots))
+    g5 = gslots.copy(); g5[e_bad * 4 + 0] = 10_000; cases.append(("slot out of table", bad, g5, dslots))
+    for name, rec, gs_, ds_ in cases:
+        rig.inter.fill_(0x7F7F7F7F)  # sentinel bf16 pair
+        rig.run(ctx, hidden, addresses=u32_tensor(rec.reshape(-1), dev), gate_slots=u32_tensor(gs_, dev),
+                down_slots=u32_tensor(ds_, dev))
+        h = rig.h_np()
+        sentinel = np.uint16(0x7F7F)
+        assert np.all(h[0, 1] == sentinel), name           # invalid expert id
+        assert np.all(h[1, 0] == sentinel), name           # invalidated expert record
+        assert not np.any(h[0, 0] == sentinel), name       # valid routes still computed
+        assert not np.any(h[1, 1] == sentinel), name

@@ -130,7 +130,8 @@ class MoEBlock:
                 routes=torch.empty(B, k, dtype=torch.int32, device=dev),
                 telemetry=torch.zeros(T, dtype=torch.int32, device=dev),
                 inter=torch.zeros(B * frame_words, dtype=torch.int32, device=dev),
-                control=torch.zeros(8, dtype=torch.int32, device=dev),
+                # BatchControl {batch_width, expert_start=0, expert_count=0, ...}
+                control=torch.tensor([B, 0, 0, 0, 0, 0, 0, 0], dtype=torch.int32, device=dev),
                 expert_out=torch.empty(B, k, H, dtype=torch.int16, device=dev),
                 out=torch.empty(B, H, dtype=torch.int16, device=dev),
             )
@@ -142,8 +143,6 @@ class MoEBlock:
         c = self.ctx
         b = self.buffers(B)
         bank = self.bank
-        # BatchControl {batch_width, expert_start=0, expert_count=0, ...}
-        b["control"][0] = B
         c.router_linear_bf16(hidden, self.router_w, b["logits"], B, self.H, self.E, stream)
         c.moe_router_topk(self.topk, b["logits"], None, b["routes"], b["telemetry"], B, stream)
         c.moe_route_compact(self.gate_up, b["routes"], b["inter"], b["control"], B, stream)

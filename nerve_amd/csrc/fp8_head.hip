@@ -1,13 +1,264 @@
-// FP8 output projection + argmax (a10, a11).
+// FP8 e4m3 output projection (a10) with fused greedy argmax (a11).
+//
+// Reference: tied_output_projection_fp8_e4m3.comp.template:87-144 (and the
+// _batch twin :94-186): the bf16 input is quantized per 128-column block with
+// s = amax/448 (not a power of two), and
+//   logit[n] = OUTPUT_SCALE * sum_b fma(dot(qx_b, W[n]_b), s_x[b] * s_w[n/BR, b])
+// Here each 128-column block is one v_mfma_scale_f32_16x16x128_f8f6f4 with
+// unit scales (e8m0 127); its f32 result is multiplied by s_x * s_w and
+// accumulated, which is the same contraction with a different summation order.
+// fp8 x fp8 operand pairing is the identity (both operands use the same lane
+// layout), so each lane loads 32 contiguous bytes of its row for both.
+//
+// Argmax follows greedy_sampler_f32.comp.template:25-109: larger f32 logit
+// wins, ties go to the lower token id.
+#include <cfloat>
+
 #include "common.h"
-extern "C" nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*, const void*, const void*,
-                                                            const void*, void*, void*, void*, uint32_t, void*) {
+
+namespace nh {
+nerve_hip_status quantize_rows(const uint16_t* x, uint32_t cols, uint32_t rows, bool pow2, uint8_t* q, float* s,
+                               hipStream_t st);
+}
+
+namespace {
+
+constexpr int HEAD_WAVES = 8;     // 8 waves x 16 columns = 128 columns per block
+constexpr int HEAD_MT = 4;        // token sub-tiles (of 16) per wave
+
+struct HeadArgs {
+    const uint8_t* xq;            // e4m3 [M, K]
+    const float* xs;              // f32 [M, nblk]
+    const uint8_t* W;             // e4m3 [N, K]
+    const uint16_t* scale_inv;    // bf16 [ceil(N/BR), nblk]
+    uint32_t M, K, N, BR;
+    float out_scale;
+    float* logits_f32;            // [M, N] or null
+    uint16_t* logits_bf16;        // [M, N] or null
+    float* part_val;              // [M, nblocks] or null
+    uint32_t* part_idx;
+    uint32_t nblocks;
+};
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(64 * HEAD_WAVES) void fp8_head_kernel(HeadArgs A) {
+    __shared__ float red_v[HEAD_WAVES][HEAD_MT * 16];
+    __shared__ uint32_t red_i[HEAD_WAVES][HEAD_MT * 16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t col = blockIdx.x * (16 * HEAD_WAVES) + wave * 16 + rr;
+    const bool cv = col < A.N;
+    const uint32_t m_base = blockIdx.y * (16 * HEAD_MT);
+    const uint32_t K = A.K, nblk = (K + 127) / 128;
+    const uint8_t* wrow = A.W + (uint64_t)(cv ? col : 0) * K;
+    const uint16_t* srow = A.scale_inv + (uint64_t)((cv ? col : 0) / A.BR) * nblk;
+    const uint8_t* arow[HEAD_MT];
+    bool av[HEAD_MT];
+#pragma unroll
+    for (int mt = 0; mt < HEAD_MT; mt++) {
+        uint32_t t = m_base + mt * 16 + rr;
+        av[mt] = t < A.M;
+        arow[mt] = A.xq + (uint64_t)(av[mt] ? t : 0) * K;
+    }
+    v4f acc[HEAD_MT];
+#pragma unroll
+    for (int mt = 0; mt < HEAD_MT; mt++) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = 0; c < nblk; c++) {
+        const uint32_t k0 = c * 128 + 32 * g;
+        const bool kv = k0 < K;
+        v4i b0 = v4i{0, 0, 0, 0}, b1 = v4i{0, 0, 0, 0};
+        if (cv && kv) {
+            b0 = *reinterpret_cast<const v4i*>(wrow + k0);
+            b1 = *reinterpret_cast<const v4i*>(wrow + k0 + 16);
+        }
+        v8i b = v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        const float sw = cv ? bf16_to_f32(srow[c]) : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < HEAD_MT; mt++) {
+            if (m_base + mt * 16 >= A.M) break;
+            v4i a0 = v4i{0, 0, 0, 0}, a1 = v4i{0, 0, 0, 0};
+            if (av[mt] && kv) {
+                a0 = *reinterpret_cast<const v4i*>(arow[mt] + k0);
+                a1 = *reinterpret_cast<const v4i*>(arow[mt] + k0 + 16);
+            }
+            v8i a = v8i{a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0,
+                                                                     127);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t t = m_base + mt * 16 + 4 * g + i;
+                float sx = t < A.M ? A.xs[(uint64_t)t * nblk + c] : 0.0f;
+                acc[mt][i] = fmaf(p[i], sx * sw, acc[mt][i]);
+            }
+        }
+    }
+    // Epilogue: logits and per-block argmax partials.
+#pragma unroll
+    for (int mt = 0; mt < HEAD_MT; mt++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t tl = mt * 16 + 4 * g + i;
+            const uint32_t t = m_base + tl;
+            const float v = acc[mt][i] * A.out_scale;
+            if (t < A.M && cv) {
+                if (A.logits_f32) A.logits_f32[(uint64_t)t * A.N + col] = v;
+                if (A.logits_bf16) A.logits_bf16[(uint64_t)t * A.N + col] = (uint16_t)f32_to_bf16(v);
+            }
+            if (A.part_val) {
+                float bv = cv ? v : -INFINITY;
+                uint32_t bi = cv ? col : 0xffffffffu;
+#pragma unroll
+                for (int d = 1; d < 16; d <<= 1) {
+                    float ov = __shfl_xor(bv, d);
+                    uint32_t oi = __shfl_xor(bi, d);
+                    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                }
+                if (rr == 0) {
+                    red_v[wave][tl] = bv;
+                    red_i[wave][tl] = bi;
+                }
+            }
+        }
+    }
+    if (!A.part_val) return;
+    __syncthreads();
+    if (threadIdx.x < HEAD_MT * 16) {
+        const uint32_t tl = threadIdx.x, t = m_base + tl;
+        if (t < A.M) {
+            float bv = red_v[0][tl];
+            uint32_t bi = red_i[0][tl];
+            for (int w = 1; w < HEAD_WAVES; w++)
+                if (better(red_v[w][tl], red_i[w][tl], bv, bi)) { bv = red_v[w][tl]; bi = red_i[w][tl]; }
+            A.part_val[(uint64_t)t * A.nblocks + blockIdx.x] = bv;
+            A.part_idx[(uint64_t)t * A.nblocks + blockIdx.x] = bi;
+        }
+    }
+}
+
+// Second pass: one block per row over the partials (argmax_candidate_reduce.
+// comp.template:10-37).
+__global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                              uint32_t n, uint32_t* __restrict__ out) {
+    __shared__ float sv[256];
+    __shared__ uint32_t si[256];
+    const uint32_t row = blockIdx.x;
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t j = threadIdx.x; j < n; j += 256) {
+        float v = pv[(uint64_t)row * n + j];
+        uint32_t i = pi[(uint64_t)row * n + j];
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s && better(sv[threadIdx.x + s], si[threadIdx.x + s], sv[threadIdx.x], si[threadIdx.x])) {
+            sv[threadIdx.x] = sv[threadIdx.x + s];
+            si[threadIdx.x] = si[threadIdx.x + s];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[row] = si[0];
+}
+
+// Standalone greedy argmax over f32 logits: each lane starts from its own
+// logit as the shader does, then strided candidates and a block reduction.
+__global__ __launch_bounds__(1024) void argmax_f32_kernel(const float* __restrict__ logits, uint32_t vocab,
+                                                          uint32_t* __restrict__ out) {
+    __shared__ float sv[1024];
+    __shared__ uint32_t si[1024];
+    const uint32_t row = blockIdx.x, lane = threadIdx.x;
+    const float* lg = logits + (uint64_t)row * vocab;
+    uint32_t bi = lane;
+    float bv = lane < vocab ? lg[lane] : -FLT_MAX;
+    for (uint32_t t = lane + 1024; t < vocab; t += 1024) {
+        float v = lg[t];
+        if (better(v, t, bv, bi)) { bv = v; bi = t; }
+    }
+    sv[lane] = bv;
+    si[lane] = bi;
+    __syncthreads();
+    for (uint32_t s = 512; s > 0; s >>= 1) {
+        if (lane < s && better(sv[lane + s], si[lane + s], sv[lane], si[lane])) {
+            sv[lane] = sv[lane + s];
+            si[lane] = si[lane + s];
+        }
+        __syncthreads();
+    }
+    if (lane == 0) out[row] = si[0];
+}
+
+}  // namespace
+
+extern "C" {
+
+nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
+                                                 const void* weight_e4m3, const void* scale_inv_bf16, void* logits_f32,
+                                                 void* logits_bf16, void* argmax_u32, uint32_t batch_width,
+                                                 void* stream) {
     nerve_hip_status st = nh::enter(ctx);
     if (st) return st;
-    return nh::fail(NERVE_HIP_UNSUPPORTED, "fp8_output_projection: not built yet");
+    nh::Fp8HeadSpec s;
+    if ((st = nh::parse_fp8_head_spec(spec, &s))) return st;
+    if (!x_bf16 || !weight_e4m3 || !scale_inv_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (!logits_f32 && !logits_bf16 && !argmax_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "no output requested");
+    if (s.batch_tile == 0 && batch_width > 1)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "unbatched FP8 projection takes batch_width 1");
+    if (batch_width == 0) return nh::ok();
+    if ((uintptr_t)weight_e4m3 & 15) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "weight must be 16-byte aligned");
+    const uint32_t M = batch_width, K = s.in, N = s.vocab, nblk = (K + 127) / 128;
+    const uint32_t nblocks = (N + 16 * HEAD_WAVES - 1) / (16 * HEAD_WAVES);
+    nh::Carver cv;
+    size_t o_q = cv.take<uint8_t>((size_t)M * K);
+    size_t o_s = cv.take<float>((size_t)M * nblk);
+    size_t o_pv = cv.take<float>(argmax_u32 ? (size_t)M * nblocks : 0);
+    size_t o_pi = cv.take<uint32_t>(argmax_u32 ? (size_t)M * nblocks : 0);
+    void* ws = nullptr;
+    if ((st = nh::workspace(ctx, cv.offset, &ws))) return st;
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    hipStream_t strm = (hipStream_t)stream;
+    HeadArgs A;
+    A.xq = base + o_q;
+    A.xs = reinterpret_cast<float*>(base + o_s);
+    if ((st = nh::quantize_rows(static_cast<const uint16_t*>(x_bf16), K, M, false, const_cast<uint8_t*>(A.xq),
+                                const_cast<float*>(A.xs), strm)))
+        return st;
+    A.W = static_cast<const uint8_t*>(weight_e4m3);
+    A.scale_inv = static_cast<const uint16_t*>(scale_inv_bf16);
+    A.M = M;
+    A.K = K;
+    A.N = N;
+    A.BR = s.block_rows;
+    A.out_scale = s.output_scale;
+    A.logits_f32 = static_cast<float*>(logits_f32);
+    A.logits_bf16 = static_cast<uint16_t*>(logits_bf16);
+    A.part_val = argmax_u32 ? reinterpret_cast<float*>(base + o_pv) : nullptr;
+    A.part_idx = argmax_u32 ? reinterpret_cast<uint32_t*>(base + o_pi) : nullptr;
+    A.nblocks = nblocks;
+    dim3 grid(nblocks, (M + 16 * HEAD_MT - 1) / (16 * HEAD_MT));
+    fp8_head_kernel<<<grid, 64 * HEAD_WAVES, 0, strm>>>(A);
+    if ((st = nh::check_launch("fp8_output_projection"))) return st;
+    if (argmax_u32) {
+        argmax_partials_kernel<<<M, 256, 0, strm>>>(A.part_val, A.part_idx, nblocks, static_cast<uint32_t*>(argmax_u32));
+        return nh::check_launch("fp8_output_projection_argmax");
+    }
+    return nh::ok();
 }
-extern "C" nerve_hip_status nerve_hip_argmax_f32(nerve_hip_ctx* ctx, const void*, uint32_t, uint32_t, void*, void*) {
+
+nerve_hip_status nerve_hip_argmax_f32(nerve_hip_ctx* ctx, const void* logits_f32, uint32_t batch_width, uint32_t vocab,
+                                      void* argmax_u32, void* stream) {
     nerve_hip_status st = nh::enter(ctx);
     if (st) return st;
-    return nh::fail(NERVE_HIP_UNSUPPORTED, "argmax_f32: not built yet");
+    if (!logits_f32 || !argmax_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (vocab == 0) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "empty vocabulary");
+    if (batch_width == 0) return nh::ok();
+    argmax_f32_kernel<<<batch_width, 1024, 0, (hipStream_t)stream>>>(static_cast<const float*>(logits_f32), vocab,
+                                                                    static_cast<uint32_t*>(argmax_u32));
+    return nh::check_launch("argmax_f32");
 }
+
+}  // extern "C"

@@ -1,0 +1,124 @@
+"""GPU parity: router projection (a5), top-k (a6) and route compaction (a7),
+through the C ABI, against the CPU oracle.  Expert indices and permutations
+are compared bit for bit; route weights within bf16 tolerance."""
+import numpy as np
+import pytest
+
+import oracle
+from nerve_amd import workloads as wl
+from nerve_amd.moe import gate_up_spec, topk_spec
+
+from helpers import to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+@pytest.mark.parametrize("B,H,E", [(16, 2880, 32), (2048, 2880, 128), (3, 100, 5)])
+def test_router_linear(ctx, dev, B, H, E):
+    torch = _torch()
+    rng = np.random.default_rng(B + E)
+    x = wl.bf16_normal(rng, (B, H))
+    w = wl.bf16_normal(rng, (E, H), 0.02)
+    out = torch.zeros(B, E, dtype=torch.int16, device=dev)
+    ctx.router_linear_bf16(to_dev(x, dev), to_dev(w, dev), out, B, H, E)
+    got = wl.bf16_bits_to_f32(to_np(out, np.uint16)).astype(np.float64)
+    ref = wl.bf16_bits_to_f32(oracle.router_linear(x, w)).astype(np.float64)
+    ideal = wl.bf16_bits_to_f32(x).astype(np.float64) @ wl.bf16_bits_to_f32(w).astype(np.float64).T
+    # bf16 outputs: within one bf16 ulp of the oracle (and of the f64 ideal)
+    ulp = np.maximum(np.abs(ref), 1e-30) * 2.0 ** -7
+    assert np.all(np.abs(got - ref) <= ulp + 1e-6)
+    assert np.all(np.abs(got - ideal) <= 2 * ulp + 1e-5)
+
+
+def _route_split(routes):
+    r = np.asarray(routes, np.uint32)
+    return r & 0xFFFF, wl.bf16_bits_to_f32((r >> 16).astype(np.uint16))
+
+
+@pytest.mark.parametrize("B,E,k,sigmoid,normalize,softcap,bias", [
+    (16, 32, 4, False, True, 0.0, "nobias"),
+    (64, 128, 8, False, True, 0.0, "biasf32"),
+    (9, 256, 6, True, True, 0.0, "biasbf16"),
+    (5, 64, 2, False, False, 30.0, "nobias"),
+    (7, 16, 3, True, False, 0.0, "nobias"),
+])
+def test_topk_routed(ctx, dev, B, E, k, sigmoid, normalize, softcap, bias):
+    torch = _torch()
+    rng = np.random.default_rng(E + k)
+    logits = wl.bf16_normal(rng, (B, E), 2.0)
+    logits[0, 3] = logits[0, 7] = logits[0, 11] = wl.f32_to_bf16_bits(np.float32(9.0))  # ties -> lower index
+    b = None
+    bias_np = None
+    if bias == "biasf32":
+        bias_np = rng.standard_normal(E).astype(np.float32) * np.float32(0.1)
+        b = to_dev(bias_np, dev)
+    elif bias == "biasbf16":
+        bb = wl.bf16_normal(rng, (E,), 0.1)
+        bias_np = wl.bf16_bits_to_f32(bb)
+        b = to_dev(bb, dev)
+    spec = topk_spec(E, k, sigmoid=sigmoid, normalize=normalize, softcap=softcap, bias=bias)
+    T = E + E * (E - 1) // 2
+    routes = torch.zeros(B, k, dtype=torch.int32, device=dev)
+    tel = torch.zeros(T, dtype=torch.int32, device=dev)
+    ctx.moe_router_topk(spec, to_dev(logits, dev), b, routes, tel, B)
+    ref, ref_tel = oracle.topk(logits, k, mode=0, activation=int(sigmoid), normalize=int(normalize),
+                               softcap=softcap, bias=bias_np)
+    got = to_np(routes, np.uint32)
+    gi, gw = _route_split(got)
+    ri, rw = _route_split(ref)
+    assert np.array_equal(gi, ri)                        # indices bit-exact
+    assert np.all(np.diff(gi.astype(np.int64), axis=1) > 0)   # ascending
+    assert np.allclose(gw, rw, rtol=2e-2, atol=1e-6)     # weights in bf16 tolerance
+    assert np.array_equal(to_np(tel, np.uint32), ref_tel)  # telemetry counts exact
+
+
+@pytest.mark.parametrize("act", ["sigmoid", "softmax", "sqrtsoftplus"])
+def test_score_router(ctx, dev, act):
+    torch = _torch()
+    B, E, k, A = 11, 64, 4, 2
+    rng = np.random.default_rng(len(act))
+    logits = wl.bf16_normal(rng, (B, E), 1.5)
+    bias = rng.standard_normal(E).astype(np.float32) * np.float32(0.01)
+    spec = f"moe_router_batch1_score_topk_{act}_bf16_r{E}_k{k}_a{A}w0.5_norm1_scale2.5_biasf32.comp"
+    T = E + A
+    routes = torch.zeros(B, k + A, dtype=torch.int32, device=dev)
+    tel = torch.zeros(T + T * (T - 1) // 2, dtype=torch.int32, device=dev)
+    ctx.moe_router_topk(spec, to_dev(logits, dev), to_dev(bias, dev), routes, tel, B)
+    ref, ref_tel = oracle.topk(logits, k, mode=1, activation=["sigmoid", "softmax", "sqrtsoftplus"].index(act),
+                               normalize=1, routed_scale=2.5, always_count=A, always_weight=0.5, bias=bias)
+    gi, gw = _route_split(to_np(routes, np.uint32))
+    ri, rw = _route_split(ref)
+    assert np.array_equal(gi, ri)
+    assert np.allclose(gw, rw, rtol=2e-2, atol=1e-6)
+    assert np.array_equal(to_np(tel, np.uint32), ref_tel)
+
+
+@pytest.mark.parametrize("B,k,E", [(16, 4, 32), (2048, 4, 128), (1, 1, 8), (300, 6, 64)])
+@pytest.mark.parametrize("partition", [None, (8, 20)])
+def test_route_compact(ctx, dev, B, k, E, partition):
+    torch = _torch()
+    rng = np.random.default_rng(B * k + E)
+    logits = wl.bf16_normal(rng, (B, E))
+    routes, _ = oracle.topk(logits, k, telemetry=False)
+    I, H = 256, 128
+    spec = gate_up_spec(H, I, E, k, 7.0)
+    frame_words = k * I // 2 + k
+    inter = torch.zeros(B * frame_words, dtype=torch.int32, device=dev)
+    start, count = partition or (0, 0)
+    control = to_dev(np.array([B, start, count, 0, 0, 0, 0, 0], np.uint32), dev)
+    ctx.moe_route_compact(spec, to_dev(routes, dev), inter, control, B)
+    fr = to_np(inter, np.uint32).reshape(B, frame_words)[:, k * I // 2:].reshape(-1)
+    cmap, ctl = oracle.route_compact(routes, k, (I + 31) // 32, B, start, count)
+    got_ctl = to_np(control, np.uint32)[:7]
+    assert np.array_equal(got_ctl, ctl)
+    n = int(ctl[3])
+    assert np.array_equal(fr[:n], cmap[:n])
+    if partition is None:
+        # closed form: the stable argsort of the expert ids
+        assert np.array_equal(fr, np.argsort(routes.reshape(-1) & 0xFFFF, kind="stable"))

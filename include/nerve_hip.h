@@ -80,6 +80,14 @@ nerve_hip_status nerve_hip_open(int device_ordinal, nerve_hip_ctx** out);
 /* Releases the context and its workspace.  NULL is accepted. */
 void nerve_hip_close(nerve_hip_ctx* ctx);
 
+/* Validates a specialization string on the host, without a device: returns
+ * NERVE_HIP_OK when some entry point of this library accepts it, else the
+ * status that entry point would return (message via nerve_hip_last_error).
+ * This is the check the reference compiler performs when it renders a
+ * template (nerve/model_package_shader_templates.py:4773-5060, 2419-2465,
+ * 3219-3276, 1513-1545), extended to shapes that are multiples of 32. */
+nerve_hip_status nerve_hip_check_specialization(const char* spec);
+
 /* ---- a2: activation block quantization -------------------------------- */
 
 /* Replaces quantize_fp8_e4m3[_spow2]_b128_h{N}.comp

@@ -249,6 +249,38 @@ nerve_hip_status nerve_hip_open(int device_ordinal, nerve_hip_ctx** out) {
     return NERVE_HIP_OK;
 }
 
+nerve_hip_status nerve_hip_check_specialization(const char* spec) {
+    if (!spec) return nh::fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    std::string s(spec);
+    if (s.rfind("independent_sparse_moe_", 0) == 0) {
+        nh::MoeSpec m;
+        return nh::parse_moe_spec(spec, &m);
+    }
+    if (s.rfind("moe_topk", 0) == 0 || s.rfind("moe_router", 0) == 0) {
+        nh::TopkSpec t;
+        return nh::parse_topk_spec(spec, &t);
+    }
+    if (s.rfind("tied_output_projection", 0) == 0) {
+        nh::Fp8HeadSpec f;
+        return nh::parse_fp8_head_spec(spec, &f);
+    }
+    if (s.rfind("quantize", 0) == 0) {
+        nh::QuantSpec q;
+        return nh::parse_quant_spec(spec, &q);
+    }
+    if (s.rfind("linear", 0) == 0) {
+        nh::Int4Spec i;
+        nerve_hip_status st = nh::parse_int4_spec(spec, &i);
+        if (st) return st;
+        if (i.layout == 1 && i.group % 128)
+            return nh::fail(NERVE_HIP_UNSUPPORTED, "CT INT4 kernel needs group % 128 == 0");
+        if (i.layout == 0 && i.out % 64) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 64 == 0");
+        if (i.layout == 1 && i.out % 16) return nh::fail(NERVE_HIP_UNSUPPORTED, "CT INT4 kernel needs N % 16 == 0");
+        return NERVE_HIP_OK;
+    }
+    return nh::fail(NERVE_HIP_INVALID_SPEC, std::string("no kernel family matches ") + spec);
+}
+
 void nerve_hip_close(nerve_hip_ctx* ctx) {
     if (!ctx) return;
     if (ctx->workspace) {

@@ -19,6 +19,7 @@ EXPORTS = (
     "nerve_hip_last_error",
     "nerve_hip_open",
     "nerve_hip_close",
+    "nerve_hip_check_specialization",
     "nerve_hip_quantize_fp8_e4m3",
     "nerve_hip_mxfp4_gemv",
     "nerve_hip_router_linear_bf16",
@@ -67,6 +68,7 @@ def _declare(lib) -> None:
         "nerve_hip_last_error": (ctypes.c_char_p, []),
         "nerve_hip_open": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(P)]),
         "nerve_hip_close": (None, [P]),
+        "nerve_hip_check_specialization": (ctypes.c_int, [S]),
         "nerve_hip_quantize_fp8_e4m3": (ctypes.c_int, [P, S, P, U32, P, P, P]),
         "nerve_hip_mxfp4_gemv": (ctypes.c_int, [P, P, P, U32, U32, P, P, U32, P, P]),
         "nerve_hip_router_linear_bf16": (ctypes.c_int, [P, P, P, P, U32, U32, U32, P]),
@@ -104,6 +106,11 @@ def load():
 
 def last_error() -> str:
     return load().nerve_hip_last_error().decode()
+
+
+def check_specialization(spec: str) -> int:
+    """Host-only validation of a specialization string (0 = accepted)."""
+    return load().nerve_hip_check_specialization(spec.encode())
 
 
 def _check(status: int) -> None:

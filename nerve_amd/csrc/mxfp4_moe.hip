@@ -421,6 +421,174 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs A) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Prefill-shaped grouped GEMM: one block = (expert tile of <= 64 routes,
+// 128 weight rows).  For gate_up the 128 rows are 64 gate and 64 up rows of
+// the same channels; for down they are 128 output rows.  Every 128-k chunk
+// of activations (64 x 128 B e4m3) and weights (128 x 64 B e2m1) is staged in
+// LDS, double-buffered: the next chunk's global loads are in flight while the
+// MFMAs consume the current one.  Wave (wm, wn) of the 2 x 2 wave grid owns
+// tokens [32 wm, 32 wm + 32) and a quarter of the weight rows.
+// ---------------------------------------------------------------------------
+constexpr int GT_M = 64;
+constexpr int GT_ROWS = 128;
+constexpr int A_STRIDE = 144;   // 128-byte token chunk + 16 bytes of bank padding
+constexpr int B_STRIDE = 80;    // 64-byte weight-row chunk + 16 bytes of bank padding
+
+template <int NMAT>
+__global__ __launch_bounds__(256) void moe_grouped_kernel(ExpertArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][GT_M * A_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][GT_ROWS * B_STRIDE];
+    __shared__ uint32_t lds_sb[2][GT_ROWS];
+    __shared__ uint32_t lds_sa[2][GT_M];
+    __shared__ uint32_t tok_route[GT_M];
+    const uint32_t tile = blockIdx.x;
+    if (tile >= *A.n_tiles) return;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t e = A.tile_expert[tile], begin = A.tile_begin[tile], cnt = A.tile_count[tile];
+    const uint32_t K = A.K, N = A.N, nch = (K + 127) / 128, nblk = nch;
+    const uint32_t rows_per_mat = GT_ROWS / NMAT;
+    const uint32_t row0 = blockIdx.y * rows_per_mat;
+    if (tid < GT_M) tok_route[tid] = tid < cnt ? A.seg_list[begin + tid] : 0xffffffffu;
+    __syncthreads();
+
+    // loader roles
+    const uint32_t ta = tid >> 2, apart = tid & 3;
+    const uint8_t* a_src = nullptr;
+    if (ta < cnt) a_src = A.aq + (uint64_t)(tok_route[ta] / A.a_row_div) * K;
+    const uint32_t rb = tid >> 1, bhalf = tid & 1;
+    const uint32_t mat = rb / rows_per_mat, lrow = rb % rows_per_mat;
+    const uint32_t n = row0 + lrow;
+    const uint8_t* w_src = nullptr;
+    const uint8_t* s_src = nullptr;
+    if (n < N) {
+        const uint8_t* wbase = param_ptr(A.addr, A.slots, e * A.P + 2 * mat);
+        const uint8_t* sbase = param_ptr(A.addr, A.slots, e * A.P + 2 * mat + 1);
+        w_src = wbase + (uint64_t)n * (K / 2);
+        s_src = sbase + (uint64_t)n * (K / 32);
+    }
+
+    v4i ra0, ra1, rb0, rb1;
+    uint32_t rsb = 0, rsa = 127;
+    auto load = [&](uint32_t c) {
+        const uint32_t ka = c * 128 + apart * 32;
+        ra0 = v4i{0, 0, 0, 0};
+        ra1 = v4i{0, 0, 0, 0};
+        if (a_src && ka < K) {
+            ra0 = *reinterpret_cast<const v4i*>(a_src + ka);
+            ra1 = *reinterpret_cast<const v4i*>(a_src + ka + 16);
+        }
+        const uint32_t kb = c * 128 + bhalf * 64;
+        rb0 = v4i{0, 0, 0, 0};
+        rb1 = v4i{0, 0, 0, 0};
+        if (w_src && kb < K) {
+            rb0 = *reinterpret_cast<const v4i*>(w_src + kb / 2);
+            rb1 = *reinterpret_cast<const v4i*>(w_src + kb / 2 + 16);
+        }
+        if (bhalf == 0) {
+            rsb = 0x7f7f7f7fu;
+            if (s_src) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t blk = c * 4 + j;
+                    v |= (blk * 32 < K ? (uint32_t)s_src[blk] : 127u) << (8 * j);
+                }
+                rsb = v;
+            }
+        }
+        if (tid < GT_M) rsa = (tid < cnt) ? pow2_to_e8m0(A.as[(uint64_t)(tok_route[tid] / A.a_row_div) * nblk + c]) : 127u;
+    };
+    auto store = [&](uint32_t buf) {
+        uint8_t* pa = &lds_a[buf][ta * A_STRIDE + apart * 32];
+        *reinterpret_cast<v4i*>(pa) = ra0;
+        *reinterpret_cast<v4i*>(pa + 16) = ra1;
+        uint8_t* pb = &lds_b[buf][rb * B_STRIDE + bhalf * 32];
+        *reinterpret_cast<v4i*>(pb) = rb0;
+        *reinterpret_cast<v4i*>(pb + 16) = rb1;
+        if (bhalf == 0) lds_sb[buf][rb] = rsb;
+        if (tid < GT_M) lds_sa[buf][tid] = rsa;
+    };
+
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    // B sub-tile row bases (LDS rows) of this wave: 4 sub-tiles of 16 rows.
+    uint32_t brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (NMAT == 2) brow[j] = (j >> 1) * 64 + wn * 32 + (j & 1) * 16;   // gate0, gate1, up0, up1
+        else brow[j] = wn * 64 + j * 16;
+    }
+    v4f acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint32_t buf = c & 1;
+        if (c + 1 < nch) load(c + 1);
+        v8i av[2];
+        uint32_t sa[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+            const uint32_t t = wm * 32 + a * 16 + rr;
+            const uint8_t* p = &lds_a[buf][t * A_STRIDE + 16 * g];
+            v4i lo = *reinterpret_cast<const v4i*>(p);
+            v4i hi = *reinterpret_cast<const v4i*>(p + 64);
+            av[a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            sa[a] = lds_sa[buf][t];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t r = brow[j] + rr;
+            v4i w = *reinterpret_cast<const v4i*>(&lds_b[buf][r * B_STRIDE + 16 * g]);
+            uint32_t sw = (lds_sb[buf][r] >> (8 * g)) & 0xffu;
+#pragma unroll
+            for (int a = 0; a < 2; a++) acc[a][j] = mfma_fp8_fp4(av[a], w, sa[a], sw, acc[a][j]);
+        }
+        if (c + 1 < nch) store(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t t = wm * 32 + a * 16 + 4 * g + i;
+            if (t >= cnt) continue;
+            const uint32_t r = tok_route[t];
+            if (NMAT == 2) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; h2++) {
+                    const uint32_t ch = row0 + wn * 32 + h2 * 16 + rr;
+                    if (ch >= N) continue;
+                    float gv = round_bf16(acc[a][h2][i]);
+                    float uv = round_bf16(acc[a][2 + h2][i]);
+                    if (A.limit > 0.0f) {
+                        gv = fminf(gv, A.limit);
+                        uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                    }
+                    float h = (gv / (1.0f + expf(-gv))) * uv;
+                    const uint32_t b = r / A.k, route = r % A.k;
+                    A.out[(uint64_t)b * A.frame_elems + (uint64_t)route * N + ch] = (uint16_t)f32_to_bf16(h);
+                }
+            } else {
+                const float wr = bf16_to_f32(A.routes[r] >> 16);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t row = row0 + brow[j] + rr;
+                    if (row < N) A.out[(uint64_t)r * N + row] = (uint16_t)f32_to_bf16(acc[a][j][i] * wr);
+                }
+            }
+        }
+    }
+}
+
 nerve_hip_status launch_quant(const uint16_t* x, uint32_t k, uint64_t frame_elems, uint64_t seg_elems, uint32_t cols,
                               uint32_t rows, bool pow2, uint8_t* q, float* s, hipStream_t st) {
     if (rows == 0) return nh::ok();
@@ -486,7 +654,11 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     const uint32_t N = gate_up ? I : H;       // output rows per matrix
     const uint32_t nblk = (K + 127) / 128;
     const uint32_t arows = gate_up ? batch_width : cap;
-    const uint32_t TM = 16;
+    // Decode-shaped batches stream each expert's weights once per <= 16
+    // routes; prefill-shaped batches use the LDS-staged grouped GEMM with
+    // 64-route tiles.
+    const bool grouped = cap >= 512;
+    const uint32_t TM = grouped ? 64 : 16;
     const uint32_t max_tiles = (cap + TM - 1) / TM + (E < cap ? E : cap);
     nh::Carver cv;
     size_t o_aq = cv.take<uint8_t>((size_t)arows * K);
@@ -562,6 +734,18 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ea.n_tiles = ta.n_tiles;
     ea.frame_elems = frame_words * 2;
     ea.limit = ms.limit;
+    if (grouped) {
+        const uint32_t rows_per_block = gate_up ? 64 : 128;
+        dim3 ggrid(max_tiles, (N + rows_per_block - 1) / rows_per_block);
+        if (gate_up) {
+            ea.out = static_cast<uint16_t*>(intermediates);
+            moe_grouped_kernel<2><<<ggrid, 256, 0, stream>>>(ea);
+            return nh::check_launch("moe_gate_up_grouped");
+        }
+        ea.out = static_cast<uint16_t*>(expert_outputs);
+        moe_grouped_kernel<1><<<ggrid, 256, 0, stream>>>(ea);
+        return nh::check_launch("moe_down_grouped");
+    }
     dim3 grid(max_tiles, (N + 63) / 64);
     if (gate_up) {
         ea.out = static_cast<uint16_t*>(intermediates);

@@ -252,6 +252,103 @@ __global__ __launch_bounds__(256) void compact_sorted_guarded_kernel(const uint3
     frames[(uint64_t)(rank / k) * frame_words + data_words + rank % k] = i;
 }
 
+
+// Stable counting sort for large route counts (O(n) work): wave w owns a
+// contiguous segment of the routes; per-wave expert histograms give every
+// (expert, wave) pair its output offset, and each wave then places its
+// routes in source order, ranking equal experts inside a 64-lane group with
+// shuffles.  Same result as the rank loop (key = (expert, source index)).
+constexpr uint32_t COUNT_MAX_EXPERTS = 512;
+
+__global__ __launch_bounds__(1024) void compact_sorted_counting_kernel(const uint32_t* __restrict__ routes, uint32_t n,
+                                                                       uint32_t k, uint32_t E,
+                                                                       uint32_t* __restrict__ frames,
+                                                                       uint64_t frame_words, uint32_t data_words,
+                                                                       uint32_t* __restrict__ control,
+                                                                       uint32_t tiles_per_route) {
+    if (control[2] != 0u) return;
+    __shared__ uint32_t cnt[16 * COUNT_MAX_EXPERTS];
+    __shared__ uint32_t wave_tot[16];
+    __shared__ uint32_t out_of_range;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) {
+        control[3] = n;
+        control[4] = k * tiles_per_route;
+        control[5] = control[0];
+        control[6] = 1;
+        out_of_range = 0;
+    }
+    for (uint32_t i = tid; i < 16 * E; i += blockDim.x) cnt[i] = 0;
+    __syncthreads();
+    const uint32_t seg = (n + 15) / 16;
+    const uint32_t s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
+    for (uint32_t i = s0 + lane; i < s1; i += 64) {
+        uint32_t e = routes[i] & 0xffffu;
+        if (e < E) atomicAdd(&cnt[wave * E + e], 1u);
+        else out_of_range = 1;
+    }
+    __syncthreads();
+    if (out_of_range) {
+        // Expert ids beyond the specialization: rank by the full 16-bit key.
+        for (uint32_t i = tid; i < n && frames; i += blockDim.x) {
+            const uint32_t e = routes[i] & 0xffffu;
+            uint32_t rank = 0;
+            for (uint32_t c = 0; c < n; c++) {
+                uint32_t ce = routes[c] & 0xffffu;
+                rank += (ce < e || (ce == e && c < i)) ? 1u : 0u;
+            }
+            frames[(uint64_t)(rank / k) * frame_words + data_words + rank % k] = i;
+        }
+        return;
+    }
+    uint32_t t = 0;
+    if (tid < E)
+        for (uint32_t w = 0; w < 16; w++) t += cnt[w * E + tid];
+    // exclusive scan of per-expert totals over the block
+    uint32_t inc = t;
+    for (int d = 1; d < 64; d <<= 1) {
+        uint32_t u = __shfl_up(inc, d);
+        if (lane >= (uint32_t)d) inc += u;
+    }
+    if (lane == 63) wave_tot[wave] = inc;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t run = 0;
+        for (uint32_t w = 0; w < blockDim.x / 64; w++) {
+            uint32_t u = wave_tot[w];
+            wave_tot[w] = run;
+            run += u;
+        }
+    }
+    __syncthreads();
+    if (tid < E) {
+        uint32_t run = wave_tot[wave] + inc - t;
+        for (uint32_t w = 0; w < 16; w++) {
+            uint32_t c = cnt[w * E + tid];
+            cnt[w * E + tid] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    if (!frames) return;
+    for (uint32_t base = s0; base < s1; base += 64) {
+        const uint32_t i = base + lane;
+        const bool valid = i < s1;
+        const uint32_t e = valid ? (routes[i] & 0xffffu) : 0xffffffffu;
+        uint32_t before = 0, after = 0;
+        for (uint32_t j = 0; j < 64; j++) {
+            uint32_t ej = __shfl(e, j);
+            before += (j < lane && ej == e) ? 1u : 0u;
+            after += (j > lane && ej == e) ? 1u : 0u;
+        }
+        uint32_t pos = valid ? cnt[wave * E + e] + before : 0;
+        if (valid) {
+            frames[(uint64_t)(pos / k) * frame_words + data_words + pos % k] = i;
+            if (after == 0) cnt[wave * E + e] = pos + 1;
+        }
+    }
+}
+
 __global__ __launch_bounds__(1024) void compact_owned_guarded_kernel(const uint32_t* __restrict__ routes, uint32_t n,
                                                                       uint32_t k, uint32_t* __restrict__ frames,
                                                                       uint64_t frame_words, uint32_t data_words,
@@ -381,8 +478,14 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
     uint32_t* frames = static_cast<uint32_t*>(intermediates);
     const uint32_t* routes = static_cast<const uint32_t*>(routes_u32);
     uint32_t* control = static_cast<uint32_t*>(control_u32);
-    uint32_t blocks = n == 0 ? 1 : (n + 255) / 256;
-    compact_sorted_guarded_kernel<<<blocks, 256, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control, tiles);
+    if (n > 1024 && ms.experts <= COUNT_MAX_EXPERTS) {
+        compact_sorted_counting_kernel<<<1, 1024, 0, s>>>(routes, n, ms.k, ms.experts, frames, frame_words, data_words,
+                                                          control, tiles);
+    } else {
+        uint32_t blocks = n == 0 ? 1 : (n + 255) / 256;
+        compact_sorted_guarded_kernel<<<blocks, 256, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control,
+                                                             tiles);
+    }
     if ((st = nh::check_launch("moe_route_compact"))) return st;
     compact_owned_guarded_kernel<<<1, 1024, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control, tiles);
     return nh::check_launch("moe_route_compact_owned");

@@ -163,7 +163,9 @@ def _moe_case(E, k, B, H, I, seed):
 
 
 @pytest.mark.parametrize("E,k,B,H,I", [(8, 2, 4, 256, 256), (4, 4, 3, 160, 96), (32, 4, 16, 2880, 2880),
-                                       (16, 1, 40, 512, 384)])
+                                       (16, 1, 40, 512, 384),
+                                       # >= 512 routes: the LDS-staged grouped GEMM path
+                                       (16, 4, 160, 512, 384), (8, 2, 300, 2880, 160), (64, 8, 70, 224, 288)])
 def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
     d, routes, hidden = _moe_case(E, k, B, H, I, seed=E * 100 + B)
     rig = MoeRig(dev, d, routes)
@@ -183,10 +185,13 @@ def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
     assert ok and exact > 0.9, (worst, exact)
     out_ref = oracle.moe_reduce(to_np(rig.expert_out, np.uint16), 1.0)
     assert np.array_equal(to_np(rig.out, np.uint16), out_ref)
-    # end to end against the oracle chain
+    # End to end against the oracle chain.  A one-ulp bf16 difference in h can
+    # move its e4m3 re-quantization in the down stage by one e4m3 step (~6%),
+    # so the composed chain is held to the bf16 tolerance normwise; each stage
+    # above is held to it elementwise.
     eo_chain = oracle.moe_down(h_ref, routes, cmap, B * k, d["down_w"], d["down_s"])
-    ok, worst, _ = bf16_close(to_np(rig.out, np.uint16), oracle.moe_reduce(eo_chain, 1.0))
-    assert ok, worst
+    out_chain = wl.bf16_bits_to_f32(oracle.moe_reduce(eo_chain, 1.0))
+    assert rel_err_normwise(wl.bf16_bits_to_f32(to_np(rig.out, np.uint16)), out_chain) <= 2e-2
 
 
 def test_fail_closed_invalid_metadata(ctx, dev):
@@ -219,3 +224,28 @@ def test_fail_closed_invalid_metadata(ctx, dev):
         assert np.all(h[1, 0] == sentinel), name           # invalidated expert record
         assert not np.any(h[0, 0] == sentinel), name       # valid routes still computed
         assert not np.any(h[1, 1] == sentinel), name
+
+
+def test_moe_prefill_config3_subset(ctx, dev):
+    """Config 3 (2048 tokens, 128 Zipf-loaded experts, H = I = 2880) on the GPU;
+    24 tokens re-computed by the oracle (each token's result depends only on
+    its own row and routes)."""
+    torch = _torch()
+    d = wl.config3()
+    B, E, k, H, I = d["B"], d["E"], d["k"], d["H"], d["I"]
+    routes, _ = oracle.topk(d["logits"], k, telemetry=False)
+    rig = MoeRig(dev, d, routes)
+    rig.run(ctx, d["hidden"])
+    counts = np.bincount((routes & 0xFFFF).ravel(), minlength=E)
+    assert counts.max() > 256 and (counts > 0).sum() > 100      # Zipf skew is present
+    sel = np.random.default_rng(0).choice(B, 24, replace=False)
+    rs, hs = routes[sel], d["hidden"][sel]
+    cm, _ = oracle.route_compact(rs, k, (I + 31) // 32, 24)
+    h_ref = oracle.moe_gate_up(hs, rs, cm, 24 * k, k, d["gate_w"], d["gate_s"], d["up_w"], d["up_s"], 7.0)
+    h = rig.h_np()[sel]
+    ok, worst, exact = bf16_close(h, h_ref)
+    assert ok and exact > 0.9, (worst, exact)
+    eo_ref = oracle.moe_down(h, rs, cm, 24 * k, d["down_w"], d["down_s"])
+    ok, worst, exact = bf16_close(to_np(rig.expert_out, np.uint16)[sel], eo_ref)
+    assert ok and exact > 0.9, (worst, exact)
+    assert np.array_equal(to_np(rig.out, np.uint16)[sel], oracle.moe_reduce(to_np(rig.expert_out, np.uint16)[sel], 1.0))

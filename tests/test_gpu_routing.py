@@ -122,3 +122,22 @@ def test_route_compact(ctx, dev, B, k, E, partition):
     if partition is None:
         # closed form: the stable argsort of the expert ids
         assert np.array_equal(fr, np.argsort(routes.reshape(-1) & 0xFFFF, kind="stable"))
+
+
+def test_route_compact_expert_ids_beyond_spec(ctx, dev):
+    """Garbage expert ids (>= E) still sort by the full 16-bit key, as the
+    reference's rank loop does."""
+    torch = _torch()
+    B, k, E, I, H = 400, 4, 32, 64, 64
+    rng = np.random.default_rng(11)
+    ex = rng.integers(0, E, size=(B, k)).astype(np.uint32)
+    ex[3, 1] = 200
+    ex[17, 0] = 65535
+    routes = ex | (np.uint32(0x3F80) << np.uint32(16))
+    spec = gate_up_spec(H, I, E, k, 7.0)
+    frame_words = k * I // 2 + k
+    inter = torch.zeros(B * frame_words, dtype=torch.int32, device=dev)
+    control = to_dev(np.array([B, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev)
+    ctx.moe_route_compact(spec, to_dev(routes, dev), inter, control, B)
+    fr = to_np(inter, np.uint32).reshape(B, frame_words)[:, k * I // 2:].reshape(-1)
+    assert np.array_equal(fr, np.argsort(ex.reshape(-1), kind="stable"))

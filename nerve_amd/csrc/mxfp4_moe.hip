@@ -30,34 +30,49 @@ constexpr uint32_t UNBOUND_SLOT = 0xffffffffu;
 // the intermediate frames.  One 32-lane cluster per 128-column block, as in
 // quantize_hidden (…gate_up_batch1_mxfp4.comp.template:366-382).
 // ---------------------------------------------------------------------------
+struct QuantArgs {
+    const uint16_t* x;
+    uint32_t k;              // rows are grouped k per frame
+    uint64_t frame_elems;    // elements per frame
+    uint64_t seg_elems;      // elements between rows of one frame
+    uint32_t cols, rows;
+    uint8_t* q;              // e4m3 [rows, cols]
+    float* s;                // f32 [rows, ceil(cols/128)]
+};
+
+// One 32-lane cluster quantizes one (row, 128-column block) unit.  All 32
+// lanes of the cluster must call it (the amax is a cluster reduction).
 template <bool POW2>
-__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x, uint32_t k,
-                                                          uint64_t frame_elems, uint64_t seg_elems,
-                                                          uint32_t cols, uint32_t rows,
-                                                          uint8_t* __restrict__ q, float* __restrict__ s) {
-    const uint32_t row = blockIdx.y;
-    if (row >= rows) return;
-    const uint32_t nblk = (cols + 127) / 128;
-    const uint32_t blk = blockIdx.x * 8 + (threadIdx.x >> 5);
-    const uint32_t cl = threadIdx.x & 31;
+__device__ __forceinline__ void quant_unit(const QuantArgs& Q, uint32_t unit, uint32_t cl) {
+    const uint32_t nblk = (Q.cols + 127) / 128;
+    const uint32_t row = unit / nblk, blk = unit % nblk;
+    const bool unit_ok = row < Q.rows;
     const uint32_t col = blk * 128 + cl * 4;
-    const bool valid = blk < nblk && col < cols;
-    const uint16_t* xr = x + (uint64_t)(row / k) * frame_elems + (uint64_t)(row % k) * seg_elems;
+    const bool valid = unit_ok && col < Q.cols;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (valid) {
+        const uint16_t* xr = Q.x + (uint64_t)(row / Q.k) * Q.frame_elems + (uint64_t)(row % Q.k) * Q.seg_elems;
         const uint32_t* p = reinterpret_cast<const uint32_t*>(xr + col);
-        uint32_t w0 = p[0], w1 = p[1];
+        const uint32_t w0 = p[0], w1 = p[1];
         v[0] = bf16_to_f32(w0); v[1] = bf16_to_f32(w0 >> 16);
         v[2] = bf16_to_f32(w1); v[3] = bf16_to_f32(w1 >> 16);
     }
     float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     m = wave_max32(m);
     if (!valid) return;
-    float sc = POW2 ? pow2_fp8_scale(m) : amax_fp8_scale(m);
-    if (cl == 0) s[(uint64_t)row * nblk + blk] = sc;
-    uint32_t packed = f32_to_e4m3(v[0] / sc) | (f32_to_e4m3(v[1] / sc) << 8) |
-                      (f32_to_e4m3(v[2] / sc) << 16) | (f32_to_e4m3(v[3] / sc) << 24);
-    *reinterpret_cast<uint32_t*>(q + (uint64_t)row * cols + col) = packed;
+    const float sc = POW2 ? pow2_fp8_scale(m) : amax_fp8_scale(m);
+    if (cl == 0) Q.s[(uint64_t)row * nblk + blk] = sc;
+    const uint32_t packed = f32_to_e4m3(v[0] / sc) | (f32_to_e4m3(v[1] / sc) << 8) |
+                            (f32_to_e4m3(v[2] / sc) << 16) | (f32_to_e4m3(v[3] / sc) << 24);
+    *reinterpret_cast<uint32_t*>(Q.q + (uint64_t)row * Q.cols + col) = packed;
+}
+
+// a2 standalone: blockwise e4m3 quantization of bf16 rows (quantize_hidden,
+// …gate_up_batch1_mxfp4.comp.template:366-382; quantize_fp8_e4m3.comp.
+// template:41-59).  8 clusters of 32 lanes per 256-thread block.
+template <bool POW2>
+__global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs Q) {
+    quant_unit<POW2>(Q, blockIdx.x * 8 + (threadIdx.x >> 5), threadIdx.x & 31);
 }
 
 // ---------------------------------------------------------------------------
@@ -228,6 +243,16 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tot, uint32_
     return r;
 }
 
+// One unit of expert work: up to TM routes of one expert, with the expert's
+// weight/scale pointers already resolved through the address table, so a
+// consuming block needs a single round of independent loads to start
+// streaming.
+struct TileRec {
+    uint32_t expert, begin, count, pad;
+    const uint8_t* w[2];
+    const uint8_t* s[2];
+};
+
 struct TileArgs {
     const uint32_t* frames;     // intermediate frames (u32 words)
     uint64_t frame_words;       // k*I/2 + k
@@ -242,13 +267,11 @@ struct TileArgs {
     uint64_t req_w, req_s;
     uint32_t TM, max_tiles;
     uint32_t* seg_list;
-    uint32_t* tile_expert;
-    uint32_t* tile_begin;
-    uint32_t* tile_count;
+    TileRec* recs;
     uint32_t* n_tiles;
 };
 
-__global__ __launch_bounds__(1024) void moe_build_tiles_kernel(TileArgs A) {
+__device__ void build_tiles(const TileArgs& A) {
     __shared__ uint32_t cnt[MAX_EXPERTS];
     __shared__ uint32_t cur[MAX_EXPERTS];
     __shared__ uint32_t tst[MAX_EXPERTS];
@@ -300,9 +323,17 @@ __global__ __launch_bounds__(1024) void moe_build_tiles_kernel(TileArgs A) {
         for (uint32_t t = 0; t < nte; t++) {
             uint32_t idx = tst[e] + t;
             if (idx < A.max_tiles) {
-                A.tile_expert[idx] = e;
-                A.tile_begin[idx] = cur[e] + t * A.TM;
-                A.tile_count[idx] = min(A.TM, cnt[e] - t * A.TM);
+                TileRec rec;
+                rec.expert = e;
+                rec.begin = cur[e] + t * A.TM;
+                rec.count = min(A.TM, cnt[e] - t * A.TM);
+                rec.pad = 0;
+                for (uint32_t m = 0; m < 2; m++) {
+                    const bool has = 2 * m < A.P;
+                    rec.w[m] = has ? param_ptr(A.addr, A.slots, e * A.P + 2 * m) : nullptr;
+                    rec.s[m] = has ? param_ptr(A.addr, A.slots, e * A.P + 2 * m + 1) : nullptr;
+                }
+                A.recs[idx] = rec;
             }
         }
     }
@@ -319,9 +350,19 @@ __global__ __launch_bounds__(1024) void moe_build_tiles_kernel(TileArgs A) {
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
 }
 
+// Preparation launch of one MoE projection: block 0 turns the route map into
+// tile records while the other blocks quantize the activation rows (32
+// (row, 128-column) units per block).
+__global__ __launch_bounds__(1024) void moe_prep_kernel(TileArgs T, QuantArgs Q) {
+    if (blockIdx.x == 0) {
+        build_tiles(T);
+        return;
+    }
+    quant_unit<true>(Q, (blockIdx.x - 1) * 32 + (threadIdx.x >> 5), threadIdx.x & 31);
+}
+
 // ---------------------------------------------------------------------------
-// Decode-shaped expert projections: one block = (expert tile of <= 16 routes,
-// 64 output rows); wave w owns rows [16w, 16w+16).
+// Arguments shared by the grouped (prefill-shaped) kernels.
 // ---------------------------------------------------------------------------
 struct ExpertArgs {
     const uint8_t* aq;          // e4m3 activations, row stride K
@@ -334,93 +375,14 @@ struct ExpertArgs {
     uint32_t P;
     const uint32_t* routes;
     const uint32_t* seg_list;
-    const uint32_t* tile_expert;
-    const uint32_t* tile_begin;
-    const uint32_t* tile_count;
+    const TileRec* recs;
     const uint32_t* n_tiles;
+    uint32_t max_tiles;         // tile slots in the grid
+    uint32_t work_items;        // max_tiles x row blocks (grouped kernels)
     uint16_t* out;              // gate_up: frames as u16; down: expert_outputs
     uint64_t frame_elems;       // gate_up only
     float limit;
 };
-
-__global__ __launch_bounds__(256) void moe_gate_up_kernel(ExpertArgs A) {
-    const uint32_t tile = blockIdx.x;
-    if (tile >= *A.n_tiles) return;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t g = lane >> 4, rr = lane & 15;
-    const uint32_t n0 = blockIdx.y * 64 + wave * 16;
-    if (n0 >= A.N) return;
-    const uint32_t e = A.tile_expert[tile], begin = A.tile_begin[tile], cnt = A.tile_count[tile];
-    const uint32_t K = A.K, nblk = (K + 127) / 128;
-    const uint8_t* gw = param_ptr(A.addr, A.slots, e * 4 + 0);
-    const uint8_t* gs = param_ptr(A.addr, A.slots, e * 4 + 1);
-    const uint8_t* uw = param_ptr(A.addr, A.slots, e * 4 + 2);
-    const uint8_t* us = param_ptr(A.addr, A.slots, e * 4 + 3);
-    const uint8_t* wrow[2] = {gw + (uint64_t)(n0 + rr) * (K / 2), uw + (uint64_t)(n0 + rr) * (K / 2)};
-    const uint8_t* srow[2] = {gs + (uint64_t)(n0 + rr) * (K / 32), us + (uint64_t)(n0 + rr) * (K / 32)};
-    const uint8_t* arow = nullptr;
-    const float* ascale = A.as;
-    if (rr < cnt) {
-        uint32_t row = A.seg_list[begin + rr] / A.a_row_div;
-        arow = A.aq + (uint64_t)row * K;
-        ascale = A.as + (uint64_t)row * nblk;
-    }
-    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
-    mx_tile_loop<2>(arow, ascale, wrow, srow, K, 0, nblk, g, acc);
-    // SwiGLU epilogue, …gate_up_batch1_mxfp4.comp.template:776-786.
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        uint32_t t = 4 * g + i;
-        if (t < cnt) {
-            uint32_t r = A.seg_list[begin + t];
-            uint32_t b = r / A.k, route = r % A.k;
-            float gv = round_bf16(acc[0][i]);
-            float uv = round_bf16(acc[1][i]);
-            if (A.limit > 0.0f) {
-                gv = fminf(gv, A.limit);
-                uv = fminf(fmaxf(uv, -A.limit), A.limit);
-            }
-            float h = (gv / (1.0f + expf(-gv))) * uv;
-            A.out[(uint64_t)b * A.frame_elems + (uint64_t)route * A.N + n0 + rr] = (uint16_t)f32_to_bf16(h);
-        }
-    }
-}
-
-__global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs A) {
-    const uint32_t tile = blockIdx.x;
-    if (tile >= *A.n_tiles) return;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t g = lane >> 4, rr = lane & 15;
-    const uint32_t n0 = blockIdx.y * 64 + wave * 16;
-    if (n0 >= A.N) return;
-    const uint32_t e = A.tile_expert[tile], begin = A.tile_begin[tile], cnt = A.tile_count[tile];
-    const uint32_t K = A.K, nblk = (K + 127) / 128;
-    const uint8_t* dw = param_ptr(A.addr, A.slots, e * 2 + 0);
-    const uint8_t* ds = param_ptr(A.addr, A.slots, e * 2 + 1);
-    const uint8_t* wrow[1] = {dw + (uint64_t)(n0 + rr) * (K / 2)};
-    const uint8_t* srow[1] = {ds + (uint64_t)(n0 + rr) * (K / 32)};
-    const uint8_t* arow = nullptr;
-    const float* ascale = A.as;
-    if (rr < cnt) {
-        uint32_t row = A.seg_list[begin + rr] / A.a_row_div;
-        arow = A.aq + (uint64_t)row * K;
-        ascale = A.as + (uint64_t)row * nblk;
-    }
-    v4f acc[1] = {v4f{0.f, 0.f, 0.f, 0.f}};
-    mx_tile_loop<1>(arow, ascale, wrow, srow, K, 0, nblk, g, acc);
-    // Route weight applied once before the bf16 boundary,
-    // …down_batch1_mxfp4.comp.template:588-607.
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        uint32_t t = 4 * g + i;
-        if (t < cnt) {
-            uint32_t r = A.seg_list[begin + t];
-            float wr = bf16_to_f32(A.routes[r] >> 16);
-            A.out[(uint64_t)r * A.N + n0 + rr] = (uint16_t)f32_to_bf16(acc[0][i] * wr);
-        }
-    }
-}
-
 
 // ---------------------------------------------------------------------------
 // Prefill-shaped grouped GEMM: one block = (expert tile of <= 64 routes,
@@ -444,10 +406,12 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(ExpertArgs A) {
     __shared__ uint32_t lds_sa[2][GT_M];
     __shared__ uint32_t tok_route[GT_M];
     const uint32_t tile = blockIdx.x;
-    if (tile >= *A.n_tiles) return;
+    const uint32_t n_tiles = *A.n_tiles;
+    const TileRec rec = A.recs[tile];
+    if (tile >= n_tiles) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t g = lane >> 4, rr = lane & 15;
-    const uint32_t e = A.tile_expert[tile], begin = A.tile_begin[tile], cnt = A.tile_count[tile];
+    const uint32_t begin = rec.begin, cnt = rec.count;
     const uint32_t K = A.K, N = A.N, nch = (K + 127) / 128, nblk = nch;
     const uint32_t rows_per_mat = GT_ROWS / NMAT;
     const uint32_t row0 = blockIdx.y * rows_per_mat;
@@ -464,10 +428,8 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(ExpertArgs A) {
     const uint8_t* w_src = nullptr;
     const uint8_t* s_src = nullptr;
     if (n < N) {
-        const uint8_t* wbase = param_ptr(A.addr, A.slots, e * A.P + 2 * mat);
-        const uint8_t* sbase = param_ptr(A.addr, A.slots, e * A.P + 2 * mat + 1);
-        w_src = wbase + (uint64_t)n * (K / 2);
-        s_src = sbase + (uint64_t)n * (K / 32);
+        w_src = rec.w[mat] + (uint64_t)n * (K / 2);
+        s_src = rec.s[mat] + (uint64_t)n * (K / 32);
     }
 
     v4i ra0, ra1, rb0, rb1;
@@ -589,16 +551,460 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(ExpertArgs A) {
     }
 }
 
-nerve_hip_status launch_quant(const uint16_t* x, uint32_t k, uint64_t frame_elems, uint64_t seg_elems, uint32_t cols,
-                              uint32_t rows, bool pow2, uint8_t* q, float* s, hipStream_t st) {
-    if (rows == 0) return nh::ok();
-    const uint32_t nblk = (cols + 127) / 128;
-    dim3 grid((nblk + 7) / 8, rows);
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM with an asynchronous LDS pipeline.  Same tile as
+// moe_grouped_kernel (64 routes x 128 weight rows, 2 x 2 waves), but every
+// chunk is copied global -> LDS with global_load_lds_dwordx4 (no register
+// staging) into a ring of GS_STAGES buffers, so GS_STAGES - 1 chunks are in
+// flight while one is consumed.  The block's e8m0 weight scales and the
+// activation block scales are staged in LDS once per tile.  Rows are stored
+// with an XOR swizzle of their 16-byte pieces so the MFMA operand reads
+// spread over the LDS banks: 16 lanes reading one operand touch 16
+// distinct 16-byte bank groups.  Synchronization is s_barrier plus explicit
+// vmcnt waits (a fenced __syncthreads would drain the pipeline).
+// ---------------------------------------------------------------------------
+constexpr uint32_t GS_MAX_K = 4096;
+
+__device__ __attribute__((aligned(16))) const uint8_t kZero16[16] = {0};
+
+__device__ __forceinline__ void wait_vm(uint32_t outstanding) {
+    // s_waitcnt vmcnt(n) with expcnt / lgkmcnt left at their maxima.
+    switch (outstanding) {
+        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+        case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
+
+// LDS reads of pipeline stages are issued as inline ds_read_b128 so the
+// compiler does not pair them with the asynchronous copies (its waitcnt
+// insertion would otherwise drain every copy in flight before each read);
+// lds_wait() then orders the reads' results before their use.
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+
+__device__ __forceinline__ v4i lds_read16(const uint8_t* p) {
+    v4i r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+__device__ __forceinline__ void lds_wait(v4i& a0, v4i& a1, v4i& a2, v4i& a3, v4i& b0, v4i& b1, v4i& b2, v4i& b3) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3));
+}
+
+template <int NMAT>
+__global__ __launch_bounds__(256) void moe_grouped_async_kernel(ExpertArgs A) {
+    // One LDS object per pipeline stage: the compiler tracks asynchronous LDS
+    // writes per object, so reads of the current stage wait only for the
+    // copies into that stage.
+    __shared__ __attribute__((aligned(16))) uint8_t st_a0[GT_M * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t st_a1[GT_M * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t st_a2[GT_M * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t st_b0[GT_ROWS * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t st_b1[GT_ROWS * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t st_b2[GT_ROWS * 64];
+    __shared__ uint8_t sc_b[GT_ROWS * (GS_MAX_K / 32)];
+    __shared__ uint8_t sc_a[GT_M * (GS_MAX_K / 128)];
+    __shared__ uint32_t tok_route[GT_M];
+    // XCD-aware work order: the hardware deals consecutive workgroups to the
+    // 8 XCDs in turn; remap so that each XCD walks a contiguous range of
+    // (tile, row-block) work with tiles fastest.  Tiles of one expert at one
+    // row block then run back to back on one XCD and share its L2 copy of
+    // the weight rows.
+    const uint32_t per_xcd = gridDim.x / 8;   // the grid is a multiple of 8
+    const uint32_t w = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (w >= A.work_items) return;
+    const uint32_t tile = w % A.max_tiles;
+    const uint32_t n_tiles = *A.n_tiles;
+    const TileRec rec = A.recs[tile];
+    if (tile >= n_tiles) return;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t begin = rec.begin, cnt = rec.count;
+    const uint32_t K = A.K, N = A.N, nch = (K + 127) / 128, nmx = K / 32;
+    const uint32_t rows_per_mat = GT_ROWS / NMAT;
+    const uint32_t row0 = (w / A.max_tiles) * rows_per_mat;
+    if (tid < GT_M) tok_route[tid] = tid < cnt ? A.seg_list[begin + tid] : 0xffffffffu;
+    __syncthreads();
+
+    const uint8_t* wbase[NMAT];
+    const uint8_t* sbase[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        wbase[m] = rec.w[m];
+        sbase[m] = rec.s[m];
+    }
+    // Stage all scales of the tile.
+    for (uint32_t i = tid; i < GT_ROWS * nmx; i += blockDim.x) {
+        const uint32_t r = i / nmx, b = i % nmx;
+        const uint32_t m = r / rows_per_mat, n = row0 + r % rows_per_mat;
+        sc_b[r * nmx + b] = n < N ? sbase[m][(uint64_t)n * nmx + b] : 127;
+    }
+    for (uint32_t i = tid; i < GT_M * nch; i += blockDim.x) {
+        const uint32_t t = i / nch, c = i % nch;
+        sc_a[t * nch + c] =
+            t < cnt ? (uint8_t)pow2_to_e8m0(A.as[(uint64_t)(tok_route[t] / A.a_row_div) * nch + c]) : 127;
+    }
+
+    // Per-lane source rows of the two A and two B copy instructions.  Copy
+    // instruction q of a stage fills LDS bytes [q*1024, q*1024+1024): for A
+    // the 128-byte chunks of tokens 8q..8q+7, for B the 64-byte chunks of
+    // rows 16q..16q+15, each lane one 16-byte piece (XOR-swizzled slot).
+    const uint8_t* a_row[2];
+    uint32_t a_piece[2];
+    const uint8_t* b_row[2];
+    uint32_t b_piece[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t q = wave * 2 + j;
+        const uint32_t t = 8 * q + (lane >> 3);
+        const uint32_t tt = t < cnt ? t : 0;
+        a_row[j] = A.aq + (uint64_t)(tok_route[tt] / A.a_row_div) * K;
+        a_piece[j] = (lane & 7) ^ ((t ^ (t >> 3)) & 7);
+        const uint32_t r = 16 * q + (lane >> 2);
+        const uint32_t m = r / rows_per_mat, n = row0 + r % rows_per_mat;
+        b_row[j] = wbase[m] + (uint64_t)(n < N ? n : 0) * (K / 2);
+        b_piece[j] = (lane & 3) ^ ((r ^ (r >> 2)) & 3);
+    }
+    auto issue = [&](uint32_t c, uint8_t* sa, uint8_t* sb) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t q = wave * 2 + j;
+            const uint32_t ka = c * 128 + a_piece[j] * 16;
+            const uint8_t* src = ka < K ? a_row[j] + ka : kZero16;
+            __builtin_amdgcn_global_load_lds(src, sa + q * 1024, 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t q = wave * 2 + j;
+            const uint32_t kb = c * 128 + b_piece[j] * 32;
+            const uint8_t* src = kb < K ? b_row[j] + kb / 2 : kZero16;
+            __builtin_amdgcn_global_load_lds(src, sb + q * 1024, 16, 0, 0);
+        }
+    };
+
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    uint32_t brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (NMAT == 2) brow[j] = (j >> 1) * 64 + wn * 32 + (j & 1) * 16;
+        else brow[j] = wn * 64 + j * 16;
+    }
+    v4f acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](uint32_t c, const uint8_t* sa_lds, const uint8_t* sb_lds) {
+        const uint32_t t0 = wm * 32 + rr, t1 = t0 + 16;
+        const uint32_t f0 = (t0 ^ (t0 >> 3)) & 7, f1 = (t1 ^ (t1 >> 3)) & 7;
+        v4i lo0 = lds_read16(sa_lds + t0 * 128 + ((g ^ f0) * 16));
+        v4i hi0 = lds_read16(sa_lds + t0 * 128 + (((g + 4) ^ f0) * 16));
+        v4i lo1 = lds_read16(sa_lds + t1 * 128 + ((g ^ f1) * 16));
+        v4i hi1 = lds_read16(sa_lds + t1 * 128 + (((g + 4) ^ f1) * 16));
+        v4i w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t r = brow[j] + rr;
+            w[j] = lds_read16(sb_lds + r * 64 + ((g ^ ((r ^ (r >> 2)) & 3)) * 16));
+        }
+        lds_wait(lo0, hi0, lo1, hi1, w[0], w[1], w[2], w[3]);
+        const v8i av[2] = {v8i{lo0.x, lo0.y, lo0.z, lo0.w, hi0.x, hi0.y, hi0.z, hi0.w},
+                           v8i{lo1.x, lo1.y, lo1.z, lo1.w, hi1.x, hi1.y, hi1.z, hi1.w}};
+        const uint32_t sa[2] = {sc_a[t0 * nch + c], sc_a[t1 * nch + c]};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t r = brow[j] + rr;
+            const uint32_t blk = c * 4 + g;
+            uint32_t sw = blk < nmx ? sc_b[r * nmx + blk] : 127u;
+#pragma unroll
+            for (int a = 0; a < 2; a++) acc[a][j] = mfma_fp8_fp4(av[a], w[j], sa[a], sw, acc[a][j]);
+        }
+    };
+    // One pipeline step: refill the stage freed last step with chunk c + 2,
+    // wait for chunk c, consume it.
+    auto step = [&](uint32_t c, const uint8_t* ca, const uint8_t* cb, uint8_t* na, uint8_t* nb) {
+        __builtin_amdgcn_s_barrier();
+        if (c + 2 < nch) {
+            issue(c + 2, na, nb);
+            wait_vm(8);
+        } else if (c + 1 < nch) {
+            wait_vm(4);
+        } else {
+            wait_vm(0);
+        }
+        __builtin_amdgcn_s_barrier();
+        compute(c, ca, cb);
+    };
+
+    __syncthreads();  // scales staged; nothing asynchronous is in flight yet
+    issue(0, st_a0, st_b0);
+    if (1 < nch) issue(1, st_a1, st_b1);
+    for (uint32_t c = 0; c < nch; c += 3) {
+        step(c, st_a0, st_b0, st_a2, st_b2);
+        if (c + 1 < nch) step(c + 1, st_a1, st_b1, st_a0, st_b0);
+        if (c + 2 < nch) step(c + 2, st_a2, st_b2, st_a1, st_b1);
+    }
+
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t t = wm * 32 + a * 16 + 4 * g + i;
+            if (t >= cnt) continue;
+            const uint32_t r = tok_route[t];
+            if (NMAT == 2) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; h2++) {
+                    const uint32_t ch = row0 + wn * 32 + h2 * 16 + rr;
+                    if (ch >= N) continue;
+                    float gv = round_bf16(acc[a][h2][i]);
+                    float uv = round_bf16(acc[a][2 + h2][i]);
+                    if (A.limit > 0.0f) {
+                        gv = fminf(gv, A.limit);
+                        uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                    }
+                    float h = (gv / (1.0f + expf(-gv))) * uv;
+                    const uint32_t b = r / A.k, route = r % A.k;
+                    A.out[(uint64_t)b * A.frame_elems + (uint64_t)route * N + ch] = (uint16_t)f32_to_bf16(h);
+                }
+            } else {
+                const float wr = bf16_to_f32(A.routes[r] >> 16);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t row = row0 + brow[j] + rr;
+                    if (row < N) A.out[(uint64_t)r * N + row] = (uint16_t)f32_to_bf16(acc[a][j][i] * wr);
+                }
+            }
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// Span-streaming expert GEMV (decode-shaped batches and the raw GEMV).
+//
+// A block owns 16*NSUB consecutive rows of NMAT weight matrices of one expert
+// and <= 16 routes.  Those rows are contiguous in the package layout
+// ([rows, K/2] bytes), so the block copies each matrix's row span and its
+// e8m0 scale span straight into LDS with global_load_lds (1 KB per wave
+// instruction, all issued up front), while each lane also prefetches its
+// activation operands.  DRAM therefore sees long sequential runs instead of
+// one 64-byte stream per weight row.  After a single wait the 4 waves split
+// the K chunks, contract from LDS on the scaled MFMA, and reduce through LDS.
+// ---------------------------------------------------------------------------
+enum SpanMode { SPAN_RAW = 0, SPAN_GATE_UP = 1, SPAN_DOWN = 2 };
+constexpr uint32_t SPAN_MAX_CHUNKS_PER_WAVE = 8;   // K <= 4096
+
+struct SpanArgs {
+    const uint8_t* aq;
+    const float* as;
+    uint32_t a_row_div;
+    uint32_t K, N, k, M;
+    const uint8_t* w_direct;    // raw mode
+    const uint8_t* s_direct;
+    const uint32_t* addr;
+    const uint32_t* slots;
+    uint32_t P;
+    const uint32_t* routes;
+    const uint32_t* seg_list;
+    const TileRec* recs;
+    const uint32_t* n_tiles;
+    uint16_t* out16;
+    float* out32;
+    uint64_t frame_elems;
+    float limit;
+    uint32_t w_region, s_region;   // LDS bytes per matrix (padded)
+};
+
+__host__ __device__ inline uint32_t span_w_region(uint32_t rows, uint32_t K) { return (rows * (K / 2) + 1023) / 1024 * 1024; }
+__host__ __device__ inline uint32_t span_s_region(uint32_t rows, uint32_t K) { return (rows * (K / 32) + 255) / 256 * 256; }
+
+template <int MODE, int NMAT, int NSUB>
+__global__ __launch_bounds__(256) void mx_span_kernel(SpanArgs A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t span_lds[];
+    constexpr uint32_t R = 16 * NSUB;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
+    const uint32_t n0 = blockIdx.x * R;
+    if (n0 >= N) return;
+    uint32_t cnt, begin = 0;
+    TileRec rec;
+    if (MODE == SPAN_RAW) {
+        cnt = min(16u, A.M - blockIdx.y * 16);
+        rec.w[0] = A.w_direct;
+        rec.s[0] = A.s_direct;
+        rec.w[1] = rec.s[1] = nullptr;
+    } else {
+        const uint32_t tile = blockIdx.y;
+        const uint32_t n_tiles = *A.n_tiles;   // independent of the record load
+        rec = A.recs[tile];
+        if (tile >= n_tiles) return;
+        begin = rec.begin;
+        cnt = rec.count;
+    }
+    // ---- asynchronous copies of the weight and scale spans
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        const uint8_t* wb = rec.w[m];
+        const uint8_t* sb = rec.s[m];
+        const uint32_t rows = min(R, N - n0);
+        const uint8_t* wsrc = wb + (uint64_t)n0 * RB;
+        const uint32_t wbytes = rows * RB;
+        uint8_t* wdst = span_lds + m * A.w_region;
+        for (uint32_t pc = wave; pc * 1024 < wbytes; pc += 4) {
+            uint32_t off = pc * 1024 + lane * 16;
+            __builtin_amdgcn_global_load_lds(wsrc + (off < wbytes ? off : 0), wdst + pc * 1024, 16, 0, 0);
+        }
+        const uint8_t* ssrc = sb + (uint64_t)n0 * SB;
+        const uint32_t sbytes = rows * SB;
+        uint8_t* sdst = span_lds + NMAT * A.w_region + m * A.s_region;
+        for (uint32_t pc = wave; pc * 256 < sbytes; pc += 4) {
+            uint32_t off = pc * 256 + lane * 4;
+            __builtin_amdgcn_global_load_lds(ssrc + (off < sbytes ? off : 0), sdst + pc * 256, 4, 0, 0);
+        }
+    }
+    // ---- activation operands of this wave's chunks, prefetched to registers
+    const uint32_t per = (nch + 3) / 4;
+    const uint32_t c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
+    const uint8_t* arow = nullptr;
+    const float* ascale = nullptr;
+    if (rr < cnt) {
+        uint32_t row;
+        if (MODE == SPAN_RAW) row = blockIdx.y * 16 + rr;
+        else row = A.seg_list[begin + rr] / A.a_row_div;
+        arow = A.aq + (uint64_t)row * K;
+        ascale = A.as + (uint64_t)row * nch;
+    }
+    v8i av[SPAN_MAX_CHUNKS_PER_WAVE];
+    uint32_t sa[SPAN_MAX_CHUNKS_PER_WAVE];
+#pragma unroll
+    for (uint32_t i = 0; i < SPAN_MAX_CHUNKS_PER_WAVE; i++) {
+        if (c0 + i < c1) load_a(arow, ascale, K, c0 + i, g, av[i], sa[i]);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): spans and operands have landed
+    __syncthreads();
+
+    v4f acc[NMAT][NSUB];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int j = 0; j < NSUB; j++) acc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t i = 0; i < SPAN_MAX_CHUNKS_PER_WAVE; i++) {
+        const uint32_t c = c0 + i;
+        if (c >= c1) break;
+        const uint32_t kb = c * 128 + g * 32;
+        const bool kv = kb < K;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+#pragma unroll
+            for (int j = 0; j < NSUB; j++) {
+                const uint32_t row = j * 16 + rr;
+                v4i w = v4i{0, 0, 0, 0};
+                uint32_t sw = 127;
+                if (kv) {
+                    w = *reinterpret_cast<const v4i*>(span_lds + m * A.w_region + row * RB + kb / 2);
+                    sw = span_lds[NMAT * A.w_region + m * A.s_region + row * SB + kb / 32];
+                }
+                acc[m][j] = mfma_fp8_fp4(av[i], w, sa[i], sw, acc[m][j]);
+            }
+        }
+    }
+    // ---- cross-wave reduction through LDS (the span region is free now)
+    __syncthreads();
+    v4f* red = reinterpret_cast<v4f*>(span_lds);
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int j = 0; j < NSUB; j++) red[((wave * NMAT + m) * NSUB + j) * 64 + lane] = acc[m][j];
+    __syncthreads();
+    // Wave w finalizes the sub-tiles j with j % 4 == w (all matrices).
+#pragma unroll
+    for (int j = 0; j < NSUB; j++) {
+        if ((uint32_t)(j % 4) != wave) continue;
+        v4f t[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            t[m] = red[((0 * NMAT + m) * NSUB + j) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < 4; w++) t[m] += red[((w * NMAT + m) * NSUB + j) * 64 + lane];
+        }
+        const uint32_t n = n0 + j * 16 + rr;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t tl = 4 * g + i;
+            if (tl >= cnt) continue;
+            if (MODE == SPAN_RAW) {
+                A.out32[(uint64_t)(blockIdx.y * 16 + tl) * N + n] = t[0][i];
+            } else if (MODE == SPAN_GATE_UP) {
+                const uint32_t r = A.seg_list[begin + tl];
+                float gv = round_bf16(t[0][i]);
+                float uv = round_bf16(t[NMAT - 1][i]);
+                if (A.limit > 0.0f) {
+                    gv = fminf(gv, A.limit);
+                    uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                }
+                float h = (gv / (1.0f + expf(-gv))) * uv;
+                A.out16[(uint64_t)(r / A.k) * A.frame_elems + (uint64_t)(r % A.k) * N + n] = (uint16_t)f32_to_bf16(h);
+            } else {
+                const uint32_t r = A.seg_list[begin + tl];
+                const float wr = bf16_to_f32(A.routes[r] >> 16);
+                A.out16[(uint64_t)r * N + n] = (uint16_t)f32_to_bf16(t[0][i] * wr);
+            }
+        }
+    }
+}
+
+template <int MODE, int NMAT, int NSUB>
+nerve_hip_status launch_span(SpanArgs A, uint32_t tiles, hipStream_t st) {
+    constexpr uint32_t R = 16 * NSUB;
+    A.w_region = span_w_region(R, A.K);
+    A.s_region = span_s_region(R, A.K);
+    size_t lds = (size_t)NMAT * (A.w_region + A.s_region);
+    size_t red = (size_t)4 * NMAT * NSUB * 64 * sizeof(v4f);
+    if (red > lds) lds = red;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)mx_span_kernel<MODE, NMAT, NSUB>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr_set = true;
+    }
+    dim3 grid((A.N + R - 1) / R, tiles);
+    mx_span_kernel<MODE, NMAT, NSUB><<<grid, 256, lds, st>>>(A);
+    return nh::check_launch("mx_span_kernel");
+}
+
+nerve_hip_status launch_quant(const QuantArgs& Q, bool pow2, hipStream_t st) {
+    if (Q.rows == 0) return nh::ok();
+    const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
+    const uint32_t blocks = (uint32_t)((units + 7) / 8);
     if (pow2)
-        quant_rows_kernel<true><<<grid, 256, 0, st>>>(x, k, frame_elems, seg_elems, cols, rows, q, s);
+        quant_rows_kernel<true><<<blocks, 256, 0, st>>>(Q);
     else
-        quant_rows_kernel<false><<<grid, 256, 0, st>>>(x, k, frame_elems, seg_elems, cols, rows, q, s);
+        quant_rows_kernel<false><<<blocks, 256, 0, st>>>(Q);
     return nh::check_launch("quantize_fp8_e4m3");
+}
+
+QuantArgs plain_rows(const uint16_t* x, uint32_t cols, uint32_t rows, uint8_t* q, float* s) {
+    QuantArgs Q;
+    Q.x = x;
+    Q.k = 1;
+    Q.frame_elems = cols;
+    Q.seg_elems = cols;
+    Q.cols = cols;
+    Q.rows = rows;
+    Q.q = q;
+    Q.s = s;
+    return Q;
 }
 
 }  // namespace
@@ -606,7 +1012,7 @@ nerve_hip_status launch_quant(const uint16_t* x, uint32_t k, uint64_t frame_elem
 namespace nh {
 nerve_hip_status quantize_rows(const uint16_t* x, uint32_t cols, uint32_t rows, bool pow2, uint8_t* q, float* s,
                                hipStream_t st) {
-    return launch_quant(x, 1, cols, cols, cols, rows, pow2, q, s, st);
+    return launch_quant(plain_rows(x, cols, rows, q, s), pow2, st);
 }
 }  // namespace nh
 
@@ -622,8 +1028,9 @@ nerve_hip_status nerve_hip_quantize_fp8_e4m3(nerve_hip_ctx* ctx, const char* spe
     nh::QuantSpec qs;
     if ((st = nh::parse_quant_spec(spec, &qs))) return st;
     if (!x_bf16 || !q_e4m3 || !scales_f32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
-    return launch_quant(static_cast<const uint16_t*>(x_bf16), 1, qs.elements, qs.elements, qs.elements, rows, qs.pow2,
-                        static_cast<uint8_t*>(q_e4m3), static_cast<float*>(scales_f32), (hipStream_t)stream);
+    return launch_quant(plain_rows(static_cast<const uint16_t*>(x_bf16), qs.elements, rows, static_cast<uint8_t*>(q_e4m3),
+                                   static_cast<float*>(scales_f32)),
+                        qs.pow2, (hipStream_t)stream);
 }
 
 nerve_hip_status nerve_hip_mxfp4_gemv(nerve_hip_ctx* ctx, const void* q_e4m3, const void* scales_f32, uint32_t M,
@@ -636,6 +1043,20 @@ nerve_hip_status nerve_hip_mxfp4_gemv(nerve_hip_ctx* ctx, const void* q_e4m3, co
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "mxfp4_gemv needs 1 <= M <= 64, K % 32 == 0, N % 16 == 0");
     if (((uintptr_t)weight & 15) || ((uintptr_t)q_e4m3 & 15))
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "weight and activation buffers must be 16-byte aligned");
+    if (K <= 4096 && ((uintptr_t)weight_scale & 3) == 0) {
+        SpanArgs sa{};
+        sa.aq = static_cast<const uint8_t*>(q_e4m3);
+        sa.as = static_cast<const float*>(scales_f32);
+        sa.a_row_div = 1;
+        sa.K = K;
+        sa.N = N;
+        sa.k = 1;
+        sa.M = M;
+        sa.w_direct = static_cast<const uint8_t*>(weight);
+        sa.s_direct = static_cast<const uint8_t*>(weight_scale);
+        sa.out32 = static_cast<float*>(y_f32);
+        return launch_span<SPAN_RAW, 1, 1>(sa, (M + 15) / 16, (hipStream_t)stream);
+    }
     mxfp4_gemv_kernel<8><<<N / 16, 512, 0, (hipStream_t)stream>>>(
         static_cast<const uint8_t*>(q_e4m3), static_cast<const float*>(scales_f32), M, K,
         static_cast<const uint8_t*>(weight), static_cast<const uint8_t*>(weight_scale), N, static_cast<float*>(y_f32));
@@ -657,16 +1078,14 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     // Decode-shaped batches stream each expert's weights once per <= 16
     // routes; prefill-shaped batches use the LDS-staged grouped GEMM with
     // 64-route tiles.
-    const bool grouped = cap >= 512;
+    const bool grouped = cap >= 512 || K > 4096;
     const uint32_t TM = grouped ? 64 : 16;
     const uint32_t max_tiles = (cap + TM - 1) / TM + (E < cap ? E : cap);
     nh::Carver cv;
     size_t o_aq = cv.take<uint8_t>((size_t)arows * K);
     size_t o_as = cv.take<float>((size_t)arows * nblk);
     size_t o_seg = cv.take<uint32_t>(cap);
-    size_t o_te = cv.take<uint32_t>(max_tiles);
-    size_t o_tb = cv.take<uint32_t>(max_tiles);
-    size_t o_tc = cv.take<uint32_t>(max_tiles);
+    size_t o_rec = cv.take<TileRec>(max_tiles);
     size_t o_nt = cv.take<uint32_t>(1);
     void* ws = nullptr;
     nerve_hip_status st = nh::workspace(ctx, cv.offset, &ws);
@@ -677,18 +1096,27 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     const uint64_t frame_words = (uint64_t)k * I / 2 + k;
     const uint16_t* frames16 = static_cast<const uint16_t*>(intermediates);
 
+    // Activation rows to quantize in the preparation launch: the hidden rows
+    // for gate_up (quantize_hidden, …gate_up_batch1_mxfp4.comp.template:
+    // 366-382), every route slice of the intermediate frames for down
+    // (quantize_intermediate, …down_batch1_mxfp4.comp.template:332-353).
+    QuantArgs Q;
     if (gate_up) {
+        Q = plain_rows(static_cast<const uint16_t*>(act_bf16), H, batch_width, aq, as);
         if (ms.prequant) {
             aq = const_cast<uint8_t*>(static_cast<const uint8_t*>(pre_q));
             as = const_cast<float*>(static_cast<const float*>(pre_s));
-        } else {
-            st = launch_quant(static_cast<const uint16_t*>(act_bf16), 1, H, H, H, batch_width, true, aq, as, stream);
-            if (st) return st;
+            Q.rows = 0;
         }
     } else {
-        // quantize_intermediate (…down_batch1_mxfp4.comp.template:332-353) for every route slice.
-        st = launch_quant(frames16, k, frame_words * 2, I, I, cap, true, aq, as, stream);
-        if (st) return st;
+        Q.x = frames16;
+        Q.k = k;
+        Q.frame_elems = frame_words * 2;
+        Q.seg_elems = I;
+        Q.cols = I;
+        Q.rows = cap;
+        Q.q = aq;
+        Q.s = as;
     }
     TileArgs ta;
     ta.frames = static_cast<const uint32_t*>(intermediates);
@@ -709,12 +1137,11 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.TM = TM;
     ta.max_tiles = max_tiles;
     ta.seg_list = reinterpret_cast<uint32_t*>(base + o_seg);
-    ta.tile_expert = reinterpret_cast<uint32_t*>(base + o_te);
-    ta.tile_begin = reinterpret_cast<uint32_t*>(base + o_tb);
-    ta.tile_count = reinterpret_cast<uint32_t*>(base + o_tc);
+    ta.recs = reinterpret_cast<TileRec*>(base + o_rec);
     ta.n_tiles = reinterpret_cast<uint32_t*>(base + o_nt);
-    moe_build_tiles_kernel<<<1, 1024, 0, stream>>>(ta);
-    if ((st = nh::check_launch("moe_build_tiles"))) return st;
+    const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
+    moe_prep_kernel<<<1 + (uint32_t)((units + 31) / 32), 1024, 0, stream>>>(ta, Q);
+    if ((st = nh::check_launch("moe_prep"))) return st;
 
     ExpertArgs ea;
     ea.aq = aq;
@@ -728,33 +1155,53 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ea.P = ta.P;
     ea.routes = ta.routes;
     ea.seg_list = ta.seg_list;
-    ea.tile_expert = ta.tile_expert;
-    ea.tile_begin = ta.tile_begin;
-    ea.tile_count = ta.tile_count;
+    ea.recs = ta.recs;
     ea.n_tiles = ta.n_tiles;
     ea.frame_elems = frame_words * 2;
     ea.limit = ms.limit;
     if (grouped) {
         const uint32_t rows_per_block = gate_up ? 64 : 128;
         dim3 ggrid(max_tiles, (N + rows_per_block - 1) / rows_per_block);
+        const bool async_ok = K <= GS_MAX_K && K % 32 == 0;
+        ea.max_tiles = max_tiles;
+        ea.work_items = ggrid.x * ggrid.y;
+        const uint32_t flat = (ea.work_items + 7) / 8 * 8;
         if (gate_up) {
             ea.out = static_cast<uint16_t*>(intermediates);
-            moe_grouped_kernel<2><<<ggrid, 256, 0, stream>>>(ea);
+            if (async_ok) moe_grouped_async_kernel<2><<<flat, 256, 0, stream>>>(ea);
+            else moe_grouped_kernel<2><<<ggrid, 256, 0, stream>>>(ea);
             return nh::check_launch("moe_gate_up_grouped");
         }
         ea.out = static_cast<uint16_t*>(expert_outputs);
-        moe_grouped_kernel<1><<<ggrid, 256, 0, stream>>>(ea);
+        if (async_ok) moe_grouped_async_kernel<1><<<flat, 256, 0, stream>>>(ea);
+        else moe_grouped_kernel<1><<<ggrid, 256, 0, stream>>>(ea);
         return nh::check_launch("moe_down_grouped");
     }
-    dim3 grid(max_tiles, (N + 63) / 64);
-    if (gate_up) {
-        ea.out = static_cast<uint16_t*>(intermediates);
-        moe_gate_up_kernel<<<grid, 256, 0, stream>>>(ea);
-        return nh::check_launch("moe_gate_up");
+    {
+        SpanArgs sa{};
+        sa.aq = aq;
+        sa.as = as;
+        sa.a_row_div = ea.a_row_div;
+        sa.K = K;
+        sa.N = N;
+        sa.k = k;
+        sa.addr = ea.addr;
+        sa.slots = ea.slots;
+        sa.P = ea.P;
+        sa.routes = ea.routes;
+        sa.seg_list = ea.seg_list;
+        sa.recs = ea.recs;
+        sa.n_tiles = ea.n_tiles;
+        sa.frame_elems = ea.frame_elems;
+        sa.limit = ea.limit;
+        if (gate_up) {
+            sa.out16 = static_cast<uint16_t*>(intermediates);
+            return launch_span<SPAN_GATE_UP, 2, 1>(sa, max_tiles, stream);
+        }
+        sa.out16 = static_cast<uint16_t*>(expert_outputs);
+        return launch_span<SPAN_DOWN, 1, 2>(sa, max_tiles, stream);
     }
-    ea.out = static_cast<uint16_t*>(expert_outputs);
-    moe_down_kernel<<<grid, 256, 0, stream>>>(ea);
-    return nh::check_launch("moe_down");
+    return nh::fail(NERVE_HIP_UNSUPPORTED, "no MXFP4 expert kernel for this shape");
 }
 
 nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spec, const void* hidden,

@@ -220,102 +220,80 @@ __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ l
 }
 
 // ---------------------------------------------------------------------------
-// a7: route compaction (moe_route_compact_batch1.comp.template:26-106).
+// a7: route compaction (moe_route_compact_batch1.comp.template:26-106,
+// moe_route_count_batch1.comp.template:21-58) in one 1024-thread block.
+// With expert_count == 0 the map is the stable sort of the routes by expert
+// (key = (expert, source index)); otherwise it lists the owned experts'
+// routes in source order.  The control words are written either way.
 // ---------------------------------------------------------------------------
-constexpr uint32_t COMPACT_LDS_ROUTES = 16384;
-
-__global__ __launch_bounds__(256) void compact_sorted_guarded_kernel(const uint32_t* __restrict__ routes, uint32_t n,
-                                                                      uint32_t k, uint32_t* __restrict__ frames,
-                                                                      uint64_t frame_words, uint32_t data_words,
-                                                                      uint32_t* __restrict__ control,
-                                                                      uint32_t tiles_per_route) {
-    if (control[2] != 0u) return;  // partitioned: compact_owned_kernel handles it
-    __shared__ uint16_t ex[COMPACT_LDS_ROUTES];
-    const bool staged = n <= COMPACT_LDS_ROUTES;
-    if (staged)
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ex[i] = (uint16_t)(routes[i] & 0xffffu);
-    __syncthreads();
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        control[3] = n;
-        control[4] = k * tiles_per_route;
-        control[5] = control[0];
-        control[6] = 1;
-    }
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n || !frames) return;
-    const uint32_t e = staged ? ex[i] : (routes[i] & 0xffffu);
-    uint32_t rank = 0;
-    for (uint32_t c = 0; c < n; c++) {
-        uint32_t ce = staged ? ex[c] : (routes[c] & 0xffffu);
-        rank += (ce < e || (ce == e && c < i)) ? 1u : 0u;
-    }
-    frames[(uint64_t)(rank / k) * frame_words + data_words + rank % k] = i;
-}
-
-
-// Stable counting sort for large route counts (O(n) work): wave w owns a
-// contiguous segment of the routes; per-wave expert histograms give every
-// (expert, wave) pair its output offset, and each wave then places its
-// routes in source order, ranking equal experts inside a 64-lane group with
-// shuffles.  Same result as the rank loop (key = (expert, source index)).
+constexpr uint32_t COMPACT_LDS_ROUTES = 8192;
 constexpr uint32_t COUNT_MAX_EXPERTS = 512;
 
-__global__ __launch_bounds__(1024) void compact_sorted_counting_kernel(const uint32_t* __restrict__ routes, uint32_t n,
-                                                                       uint32_t k, uint32_t E,
-                                                                       uint32_t* __restrict__ frames,
-                                                                       uint64_t frame_words, uint32_t data_words,
-                                                                       uint32_t* __restrict__ control,
-                                                                       uint32_t tiles_per_route) {
-    if (control[2] != 0u) return;
-    __shared__ uint32_t cnt[16 * COUNT_MAX_EXPERTS];
-    __shared__ uint32_t wave_tot[16];
-    __shared__ uint32_t out_of_range;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (tid == 0) {
-        control[3] = n;
-        control[4] = k * tiles_per_route;
-        control[5] = control[0];
-        control[6] = 1;
-        out_of_range = 0;
-    }
-    for (uint32_t i = tid; i < 16 * E; i += blockDim.x) cnt[i] = 0;
+struct CompactArgs {
+    const uint32_t* routes;
+    uint32_t n, k, E;
+    uint32_t* frames;        // may be null (count-only form)
+    uint64_t frame_words;
+    uint32_t data_words;
+    uint32_t* control;
+    uint32_t tiles_per_route;
+};
+
+__device__ __forceinline__ void put_map(const CompactArgs& A, uint32_t pos, uint32_t src) {
+    A.frames[(uint64_t)(pos / A.k) * A.frame_words + A.data_words + pos % A.k] = src;
+}
+
+// Rank of each route by the full 16-bit key: O(n) per route from LDS.
+__device__ void compact_rank_loop(const CompactArgs& A, uint16_t* ex) {
+    const bool staged = A.n <= COMPACT_LDS_ROUTES;
+    if (staged)
+        for (uint32_t i = threadIdx.x; i < A.n; i += blockDim.x) ex[i] = (uint16_t)(A.routes[i] & 0xffffu);
     __syncthreads();
-    const uint32_t seg = (n + 15) / 16;
+    for (uint32_t i = threadIdx.x; i < A.n; i += blockDim.x) {
+        const uint32_t e = staged ? ex[i] : (A.routes[i] & 0xffffu);
+        uint32_t rank = 0;
+        for (uint32_t c = 0; c < A.n; c++) {
+            const uint32_t ce = staged ? ex[c] : (A.routes[c] & 0xffffu);
+            rank += (ce < e || (ce == e && c < i)) ? 1u : 0u;
+        }
+        put_map(A, rank, i);
+    }
+}
+
+// Stable counting sort for large n: wave w owns a contiguous segment; per-
+// wave expert histograms give each (expert, wave) its output offset, then
+// each wave places its routes in order, ranking equal experts inside a
+// 64-lane group with shuffles.  Returns false (nothing written) if an
+// expert id is outside [0, E).
+__device__ bool compact_counting(const CompactArgs& A, uint32_t* cnt, uint32_t* wave_tot, uint32_t* flag) {
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+    const uint32_t E = A.E, n = A.n;
+    if (tid == 0) *flag = 0;
+    for (uint32_t i = tid; i < nw * E; i += blockDim.x) cnt[i] = 0;
+    __syncthreads();
+    const uint32_t seg = (n + nw - 1) / nw;
     const uint32_t s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
     for (uint32_t i = s0 + lane; i < s1; i += 64) {
-        uint32_t e = routes[i] & 0xffffu;
+        const uint32_t e = A.routes[i] & 0xffffu;
         if (e < E) atomicAdd(&cnt[wave * E + e], 1u);
-        else out_of_range = 1;
+        else *flag = 1;
     }
     __syncthreads();
-    if (out_of_range) {
-        // Expert ids beyond the specialization: rank by the full 16-bit key.
-        for (uint32_t i = tid; i < n && frames; i += blockDim.x) {
-            const uint32_t e = routes[i] & 0xffffu;
-            uint32_t rank = 0;
-            for (uint32_t c = 0; c < n; c++) {
-                uint32_t ce = routes[c] & 0xffffu;
-                rank += (ce < e || (ce == e && c < i)) ? 1u : 0u;
-            }
-            frames[(uint64_t)(rank / k) * frame_words + data_words + rank % k] = i;
-        }
-        return;
-    }
+    if (*flag) return false;
     uint32_t t = 0;
     if (tid < E)
-        for (uint32_t w = 0; w < 16; w++) t += cnt[w * E + tid];
-    // exclusive scan of per-expert totals over the block
+        for (uint32_t w = 0; w < nw; w++) t += cnt[w * E + tid];
     uint32_t inc = t;
     for (int d = 1; d < 64; d <<= 1) {
-        uint32_t u = __shfl_up(inc, d);
+        const uint32_t u = __shfl_up(inc, d);
         if (lane >= (uint32_t)d) inc += u;
     }
     if (lane == 63) wave_tot[wave] = inc;
     __syncthreads();
     if (tid == 0) {
         uint32_t run = 0;
-        for (uint32_t w = 0; w < blockDim.x / 64; w++) {
-            uint32_t u = wave_tot[w];
+        for (uint32_t w = 0; w < nw; w++) {
+            const uint32_t u = wave_tot[w];
             wave_tot[w] = run;
             run += u;
         }
@@ -323,79 +301,97 @@ __global__ __launch_bounds__(1024) void compact_sorted_counting_kernel(const uin
     __syncthreads();
     if (tid < E) {
         uint32_t run = wave_tot[wave] + inc - t;
-        for (uint32_t w = 0; w < 16; w++) {
-            uint32_t c = cnt[w * E + tid];
+        for (uint32_t w = 0; w < nw; w++) {
+            const uint32_t c = cnt[w * E + tid];
             cnt[w * E + tid] = run;
             run += c;
         }
     }
     __syncthreads();
-    if (!frames) return;
     for (uint32_t base = s0; base < s1; base += 64) {
         const uint32_t i = base + lane;
         const bool valid = i < s1;
-        const uint32_t e = valid ? (routes[i] & 0xffffu) : 0xffffffffu;
+        const uint32_t e = valid ? (A.routes[i] & 0xffffu) : 0xffffffffu;
         uint32_t before = 0, after = 0;
         for (uint32_t j = 0; j < 64; j++) {
-            uint32_t ej = __shfl(e, j);
+            const uint32_t ej = __shfl(e, j);
             before += (j < lane && ej == e) ? 1u : 0u;
             after += (j > lane && ej == e) ? 1u : 0u;
         }
-        uint32_t pos = valid ? cnt[wave * E + e] + before : 0;
         if (valid) {
-            frames[(uint64_t)(pos / k) * frame_words + data_words + pos % k] = i;
+            const uint32_t pos = cnt[wave * E + e] + before;
+            put_map(A, pos, i);
             if (after == 0) cnt[wave * E + e] = pos + 1;
         }
     }
+    return true;
 }
 
-__global__ __launch_bounds__(1024) void compact_owned_guarded_kernel(const uint32_t* __restrict__ routes, uint32_t n,
-                                                                      uint32_t k, uint32_t* __restrict__ frames,
-                                                                      uint64_t frame_words, uint32_t data_words,
-                                                                      uint32_t* __restrict__ control,
-                                                                      uint32_t tiles_per_route) {
-    if (control[2] == 0u) return;
-    __shared__ uint32_t wave_tot[16];
-    __shared__ uint32_t base_sh;
-    const uint32_t start = control[1], end = control[1] + control[2];
-    if (threadIdx.x == 0) base_sh = 0;
+// Partitioned form: owned routes in source order (block-wide prefix sums).
+__device__ uint32_t compact_owned(const CompactArgs& A, uint32_t* wave_tot, uint32_t* base_sh) {
+    const uint32_t start = A.control[1], end = A.control[1] + A.control[2];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (threadIdx.x == 0) *base_sh = 0;
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    for (uint32_t c0 = 0; c0 < n; c0 += blockDim.x) {
+    for (uint32_t c0 = 0; c0 < A.n; c0 += blockDim.x) {
         const uint32_t i = c0 + threadIdx.x;
         uint32_t flag = 0;
-        if (i < n) {
-            uint32_t e = routes[i] & 0xffffu;
+        if (i < A.n) {
+            const uint32_t e = A.routes[i] & 0xffffu;
             flag = (e >= start && e < end) ? 1u : 0u;
         }
         uint32_t inc = flag;
         for (int d = 1; d < 64; d <<= 1) {
-            uint32_t t = __shfl_up(inc, d);
+            const uint32_t t = __shfl_up(inc, d);
             if (lane >= (uint32_t)d) inc += t;
         }
         if (lane == 63) wave_tot[wave] = inc;
         __syncthreads();
         if (threadIdx.x == 0) {
             uint32_t run = 0;
-            for (uint32_t w = 0; w < nwave; w++) {
-                uint32_t t = wave_tot[w];
+            for (uint32_t w = 0; w < nw; w++) {
+                const uint32_t t = wave_tot[w];
                 wave_tot[w] = run;
                 run += t;
             }
         }
         __syncthreads();
-        const uint32_t pos = base_sh + wave_tot[wave] + inc - flag;
-        if (flag && frames) frames[(uint64_t)(pos / k) * frame_words + data_words + pos % k] = i;
+        const uint32_t pos = *base_sh + wave_tot[wave] + inc - flag;
+        if (flag && A.frames) put_map(A, pos, i);
         __syncthreads();
-        if (threadIdx.x == blockDim.x - 1) base_sh = pos + flag;
+        if (threadIdx.x == blockDim.x - 1) *base_sh = pos + flag;
         __syncthreads();
+    }
+    return *base_sh;
+}
+
+__global__ __launch_bounds__(1024) void compact_kernel(CompactArgs A) {
+    __shared__ uint32_t scratch[16 * COUNT_MAX_EXPERTS];
+    __shared__ uint32_t wave_tot[16];
+    __shared__ uint32_t misc[2];
+    uint32_t* control = A.control;
+    if (control[2] != 0u) {
+        const uint32_t owned = compact_owned(A, wave_tot, &misc[0]);
+        if (threadIdx.x == 0) {
+            control[3] = owned;
+            control[4] = owned * A.tiles_per_route;
+            control[5] = 1;
+            control[6] = 1;
+        }
+        return;
     }
     if (threadIdx.x == 0) {
-        control[3] = base_sh;
-        control[4] = base_sh * tiles_per_route;
-        control[5] = 1;
+        control[3] = A.n;
+        control[4] = A.k * A.tiles_per_route;
+        control[5] = control[0];
         control[6] = 1;
     }
+    if (!A.frames || A.n == 0) return;
+    if (A.n > blockDim.x && A.E <= COUNT_MAX_EXPERTS) {
+        if (compact_counting(A, scratch, wave_tot, &misc[1])) return;
+        __syncthreads();
+    }
+    compact_rank_loop(A, reinterpret_cast<uint16_t*>(scratch));
 }
 
 // ---------------------------------------------------------------------------
@@ -474,21 +470,18 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
     const uint32_t tiles = ms.gate_up ? (ms.inter + 31) / 32 : (ms.hidden + 63) / 64;
     const uint64_t frame_words = (uint64_t)ms.k * ms.inter / 2 + ms.k;
     const uint32_t data_words = ms.k * ms.inter / 2;
-    hipStream_t s = (hipStream_t)stream;
-    uint32_t* frames = static_cast<uint32_t*>(intermediates);
-    const uint32_t* routes = static_cast<const uint32_t*>(routes_u32);
-    uint32_t* control = static_cast<uint32_t*>(control_u32);
-    if (n > 1024 && ms.experts <= COUNT_MAX_EXPERTS) {
-        compact_sorted_counting_kernel<<<1, 1024, 0, s>>>(routes, n, ms.k, ms.experts, frames, frame_words, data_words,
-                                                          control, tiles);
-    } else {
-        uint32_t blocks = n == 0 ? 1 : (n + 255) / 256;
-        compact_sorted_guarded_kernel<<<blocks, 256, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control,
-                                                             tiles);
-    }
-    if ((st = nh::check_launch("moe_route_compact"))) return st;
-    compact_owned_guarded_kernel<<<1, 1024, 0, s>>>(routes, n, ms.k, frames, frame_words, data_words, control, tiles);
-    return nh::check_launch("moe_route_compact_owned");
+    CompactArgs A;
+    A.routes = static_cast<const uint32_t*>(routes_u32);
+    A.n = n;
+    A.k = ms.k;
+    A.E = ms.experts;
+    A.frames = static_cast<uint32_t*>(intermediates);
+    A.frame_words = frame_words;
+    A.data_words = data_words;
+    A.control = static_cast<uint32_t*>(control_u32);
+    A.tiles_per_route = tiles;
+    compact_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(A);
+    return nh::check_launch("moe_route_compact");
 }
 
 nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_outputs, void* out_bf16,

@@ -1,13 +1,18 @@
-"""Benchmark of the MXFP4 routed-MoE hot path on one MI355X.
+"""Benchmarks of NERVE's quantized-matmul hot path on one MI355X.
 
-Workload: one MoE decode block, 32 experts, top-4,
-hidden = intermediate = 2880, 16 bf16 tokens, MXFP4 gate/up/down experts,
-SwiGLU limit 7.  A step is one full pass of the reference node chain
-(router linear -> top-k -> compact -> gate_up -> count -> down -> reduce)
-through libnerve_hip's C ABI, inputs resident in HBM.
+Default workload (the metric's MoE decode block):
+32 experts, top-4, hidden = intermediate = 2880, 16 bf16 tokens, MXFP4
+gate/up/down experts, SwiGLU limit 7.  One step is one full pass of the
+reference node chain (router linear -> top-k -> compact -> gate_up -> count
+-> down -> reduce) through libnerve_hip's C ABI with inputs resident in HBM.
+Steps alternate between two MoE layers with distinct weights (2 x 423 MB,
+beyond the 256 MB Infinity Cache), so weights stream from HBM as they do
+when a model runs consecutive layers.
 
-Prints one JSON line.  `value` = routed (token, expert) pairs processed per
-second (16 tokens x 4 experts per step).
+`value` = routed (token, expert) pairs per second.  The line also carries the
+prefill block as a sub-object, since the metric names prefill
+MXFP4 TFLOPS.  Other workloads (--workload) report their own rate with the
+same JSON shape.
 """
 from __future__ import annotations
 
@@ -24,6 +29,9 @@ sys.path.insert(0, HERE)
 
 METRIC = "MoE expert tokens/s; decode HBM GB/s + prefill MXFP4 TFLOPS as % of peak"
 HBM_PEAK_GBS = 8000.0
+MXFP4_PEAK_TFLOPS = 10100.0
+FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -31,7 +39,11 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default="moe_decode",
+                   choices=["moe_decode", "moe_prefill", "mxfp4_gemv", "int4_gemv", "fp8_head"])
+    p.add_argument("--m", type=int, default=1, help="batch rows for int4_gemv / fp8_head")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
 
@@ -40,98 +52,271 @@ def to_dev(a, dev):
     import torch
 
     a = np.ascontiguousarray(a)
-    view = {np.dtype(np.uint8): np.uint8, np.dtype(np.uint16): np.int16, np.dtype(np.uint32): np.int32}[a.dtype]
+    view = {np.dtype(np.uint8): np.uint8, np.dtype(np.uint16): np.int16, np.dtype(np.uint32): np.int32,
+            np.dtype(np.float16): np.int16, np.dtype(np.float32): np.float32}[a.dtype]
     return torch.from_numpy(a.view(view).copy()).to(dev)
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
-              file=sys.stderr)
-        sys.exit(2)
+def event_ms(fn, n, stream):
+    """Median duration (ms) of fn() over n calls, each bracketed by HIP events
+    on `stream` (the stream the kernels are launched on)."""
+    import torch
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record(stream)
+        fn(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in ev]))
+
+
+def wall_ms(fn, steps, warmup):
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def base_line(args, value, unit, ms, dtype, config, higher=True):
+    return {"metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": higher, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+            "data": "synthetic (seeded, package layouts, random-init weights)", "config": config}
+
+
+# --------------------------------------------------------------------------
+# MoE decode (default)
+# --------------------------------------------------------------------------
+
+def moe_decode(args, ctx, dev):
     import torch
 
     from nerve_amd import workloads as wl
-    from nerve_amd.hip import Context
     from nerve_amd.moe import ExpertBank, MoEBlock
 
-    dev = torch.device("cuda:0")
-    d = wl.config2()
+    layers, hidden, data = [], [], []
+    for layer in range(2):
+        d = wl.config2(layer=layer)
+        bank = ExpertBank(*(to_dev(d[n], dev) for n in ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")))
+        layers.append(MoEBlock(ctx, to_dev(d["router_w"], dev), bank, d["k"], limit=d["limit"]))
+        hidden.append(to_dev(d["hidden"], dev))
+        data.append(d)
+    d = data[0]
     B, E, k, H, I = d["B"], d["E"], d["k"], d["H"], d["I"]
-    ctx = Context(0)
-    bank = ExpertBank(*(to_dev(d[n], dev) for n in ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")))
-    block = MoEBlock(ctx, to_dev(d["router_w"], dev), bank, k, limit=d["limit"])
-    hidden = to_dev(d["hidden"], dev)
     stream = torch.cuda.current_stream()
+    U = []
+    for L in range(2):
+        layers[L].forward(hidden[L])
+        torch.cuda.synchronize()
+        r = layers[L].buffers(B)["routes"].cpu().numpy().view(np.uint32)
+        U.append(len(np.unique(r & 0xFFFF)))
+    mat = I * H // 2 + I * H // 32                 # one MXFP4 matrix + scales
+    gate_up_bytes = [u * 2 * mat + B * H * 2 + B * k * I * 2 for u in U]
+    down_bytes = [u * mat + B * k * I * 2 + B * k * H * 2 for u in U]
+    step_bytes = float(np.mean([g + dn + E * H * 2 + 2 * B * H * 2 + B * k * H * 2
+                                for g, dn in zip(gate_up_bytes, down_bytes)]))
 
-    # Routing of this seeded batch (distinct experts U fixes the algorithmic bytes).
-    block.forward(hidden)
+    ms = wall_ms(lambda i: layers[i % 2].forward(hidden[i % 2]), args.steps, args.warmup)
+
+    def gate_up(i):
+        L = layers[i % 2]
+        b = L.buffers(B)
+        ctx.mxfp4_moe_gate_up(L.gate_up, hidden[i % 2], None, b["routes"], b["inter"], L.bank.addresses,
+                              L.bank.gate_slots, b["control"], B, stream)
+
+    # routes / maps of both layers are in their own buffers already
+    gu_ms = event_ms(gate_up, max(100, args.steps), stream)
+    achieved = float(np.mean(gate_up_bytes)) / (gu_ms * 1e-3) / 1e9
+    out = base_line(args, B * k / (ms * 1e-3), "expert-tokens/s", ms, "e4m3xe2m1->f32",
+                    {"workload": "moe_decode_e32_k4_h2880_i2880_b16", "experts": E, "top_k": k, "hidden": H,
+                     "intermediate": I, "batch_tokens": B, "layers_rotated": 2, "distinct_experts": U})
+    out["tokens_per_s"] = B / (ms * 1e-3)
+    out["step_hbm_gbs"] = step_bytes / (ms * 1e-3) / 1e9
+    out["step_hbm_frac"] = out["step_hbm_gbs"] / HBM_PEAK_GBS
+    out["roofline"] = {"bound": "hbm", "kernel": "mxfp4_moe_gate_up (moe_prep_kernel + mx_span_kernel<1,2,1>)",
+                       "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                       "traffic": None, "algorithmic_bytes_per_launch": float(np.mean(gate_up_bytes)),
+                       "launch_ms": gu_ms}
+    return out, data[0]
+
+
+# --------------------------------------------------------------------------
+# MoE prefill (configs[3])
+# --------------------------------------------------------------------------
+
+class Prefill:
+    def __init__(self, ctx, dev):
+        import torch
+
+        from nerve_amd import workloads as wl
+        from nerve_amd.moe import ExpertBank, down_spec, gate_up_spec, topk_spec
+
+        d = wl.config3()
+        self.d = d
+        B, E, k, H, I = d["B"], d["E"], d["k"], d["H"], d["I"]
+        self.ctx = ctx
+        self.bank = ExpertBank(*(to_dev(d[n], dev) for n in ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")))
+        self.logits = to_dev(d["logits"], dev)
+        self.hidden = to_dev(d["hidden"], dev)
+        self.routes = torch.zeros(B, k, dtype=torch.int32, device=dev)
+        self.inter = torch.zeros(B * (k * I // 2 + k), dtype=torch.int32, device=dev)
+        self.control = torch.tensor([B, 0, 0, 0, 0, 0, 0, 0], dtype=torch.int32, device=dev)
+        self.eo = torch.zeros(B, k, H, dtype=torch.int16, device=dev)
+        self.out = torch.zeros(B, H, dtype=torch.int16, device=dev)
+        self.gu, self.dn, self.tk = gate_up_spec(H, I, E, k, 7.0), down_spec(H, I, E, k), topk_spec(E, k)
+
+    def step(self, _i=0, stream=None):
+        c, d = self.ctx, self.d
+        B, k, H = d["B"], d["k"], d["H"]
+        c.moe_router_topk(self.tk, self.logits, None, self.routes, None, B, stream)
+        c.moe_route_compact(self.gu, self.routes, self.inter, self.control, B, stream)
+        c.mxfp4_moe_gate_up(self.gu, self.hidden, None, self.routes, self.inter, self.bank.addresses,
+                            self.bank.gate_slots, self.control, B, stream)
+        c.moe_route_compact(self.dn, self.routes, None, self.control, B, stream)
+        c.mxfp4_moe_down(self.dn, self.inter, self.routes, self.eo, self.bank.addresses, self.bank.down_slots,
+                         self.control, B, stream)
+        c.moe_reduce(self.eo, self.out, B, H, k, 1.0, stream)
+
+    def figures(self, ms):
+        d = self.d
+        B, E, k, H, I = d["B"], d["E"], d["k"], d["H"], d["I"]
+        flop = 2.0 * B * k * 3 * H * I
+        mat = I * H // 2 + I * H // 32
+        hbm = 3 * E * mat + B * H * 2 + 2 * B * k * I * 2 + 2 * B * k * H * 2 + B * H * 2
+        tf = flop / (ms * 1e-3) / 1e12
+        return {"workload": "moe_prefill_e128_k4_b2048_zipf1.1", "ms": ms, "tflops": tf,
+                "mxfp4_peak_frac": tf / MXFP4_PEAK_TFLOPS, "fp8_peak_frac": tf / FP8_PEAK_TFLOPS,
+                "hbm_gbs": hbm / (ms * 1e-3) / 1e9, "hbm_frac": hbm / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "algorithmic_flop": flop, "algorithmic_bytes": hbm,
+                "note": "HBM-bound shape: ~240 FLOP/B is below the MXFP4 ridge, so the MFMA fraction is capped "
+                        "near 19% of the MXFP4 peak"}
+
+
+def prefill_sub(ctx, dev, n=10):
+    import torch
+
+    pf = Prefill(ctx, dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        pf.step()
     torch.cuda.synchronize()
-    bufs = block.buffers(B)
-    routes = bufs["routes"].cpu().numpy().view(np.uint32)
-    U = len(np.unique(routes & 0xFFFF))
-    expert_bytes = I * H // 2 + I * H // 32            # one MXFP4 matrix + its scales
-    gate_up_bytes = U * 2 * expert_bytes + B * H * 2 + B * k * I * 2
-    down_bytes = U * expert_bytes + B * k * I * 2 + B * k * H * 2
-    step_bytes = gate_up_bytes + down_bytes + E * H * 2 + B * H * 2 * 2 + B * k * H * 2
+    ms = event_ms(lambda i: pf.step(i, stream), n, stream)
+    return pf.figures(ms)
 
-    for _ in range(args.warmup):
-        block.forward(hidden)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        block.forward(hidden)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
 
-    # Dominant kernel: the gate_up entry (act quant + tile build + MFMA GEMV),
-    # timed with HIP events on the stream it is launched on.
-    c = bufs["control"]
-    n_ev = max(50, args.steps)
-    ev0 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    ev1 = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    for i in range(n_ev):
-        ev0[i].record(stream)
-        ctx.mxfp4_moe_gate_up(block.gate_up, hidden, None, bufs["routes"], bufs["inter"], bank.addresses,
-                              bank.gate_slots, c, B, stream)
-        ev1[i].record(stream)
-    torch.cuda.synchronize()
-    gu_ms = float(np.median([a.elapsed_time(b) for a, b in zip(ev0, ev1)]))
-    achieved = gate_up_bytes / (gu_ms * 1e-3) / 1e9
+# --------------------------------------------------------------------------
+# single-kernel workloads (configs 0, 1, 4)
+# --------------------------------------------------------------------------
 
-    result = {
-        "metric": METRIC,
-        "value": B * k / (ms_per_step * 1e-3),
-        "unit": "expert-tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "e4m3xe2m1->f32",
-        "data": "synthetic (seeded, package layouts, random-init MXFP4 experts)",
-        "config": {"workload": "moe_decode_e32_k4_h2880_i2880_b16", "experts": E, "top_k": k, "hidden": H,
-                   "intermediate": I, "batch_tokens": B, "distinct_experts": U},
-        "tokens_per_s": B / (ms_per_step * 1e-3),
-        "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
-        "roofline": {"bound": "hbm", "kernel": "mxfp4_moe_gate_up", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes": gate_up_bytes, "launch_ms": gu_ms},
-    }
+def mxfp4_gemv(args, ctx, dev):
+    import torch
 
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(d, args.cpu_seconds)
-    print(json.dumps(result))
+    from nerve_amd import workloads as wl
+
+    d = wl.config0()
+    K, N = 2880, 5760
+    nbytes = N * K // 2 + N * K // 32
+    copies = -(-512 * 2 ** 20 // nbytes) + 1   # rotate past the Infinity Cache
+    W = to_dev(np.tile(d["W"], (copies, 1)), dev).view(copies, N, K // 2)
+    S = to_dev(np.tile(d["S"], (copies, 1)), dev).view(copies, N, K // 32)
+    x = to_dev(d["x_bf16"], dev)
+    q = torch.zeros(1, K, dtype=torch.uint8, device=dev)
+    s = torch.zeros(1, (K + 127) // 128, dtype=torch.float32, device=dev)
+    y = torch.zeros(1, N, dtype=torch.float32, device=dev)
+    ctx.quantize_fp8_e4m3(f"quantize_fp8_e4m3_spow2_b128_h{K}.comp", x, 1, q, s)
+    stream = torch.cuda.current_stream()
+    fn = lambda i: ctx.mxfp4_gemv(q, s, 1, K, W[i % copies], S[i % copies], N, y, stream)
+    ms = wall_ms(fn, args.steps, args.warmup)
+    kms = event_ms(fn, max(200, args.steps), stream)
+    alg = nbytes + K + 4 * 23 + N * 4
+    gbs = alg / (kms * 1e-3) / 1e9
+    out = base_line(args, gbs, "GB/s", ms, "e4m3xe2m1->f32",
+                    {"workload": "mxfp4_gemv_m1_k2880_n5760", "weight_copies_rotated": copies})
+    out["roofline"] = {"bound": "hbm", "kernel": "mx_span_kernel<0,1,1>", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                       "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
+    return out
+
+
+def int4_gemv(args, ctx, dev):
+    import torch
+
+    from nerve_amd import workloads as wl
+
+    M = args.m
+    d = wl.config1(M=M)
+    K, N, G = d["K"], d["N"], d["group"]
+    nbytes = K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2
+    copies = -(-512 * 2 ** 20 // nbytes) + 1
+    qw = to_dev(np.tile(d["qweight"], (copies, 1)), dev).view(copies, K // 8, N)
+    sc = to_dev(np.tile(d["scales"], (copies, 1)), dev).view(copies, K // G, N)
+    qz = to_dev(np.tile(d["qzeros"], (copies, 1)), dev).view(copies, K // G, N // 8)
+    x = to_dev(d["x"], dev)
+    y = torch.zeros(M, N, dtype=torch.int16, device=dev)
+    spec = f"linear_batch16_int4_gptq_sf16_g{G}_{K}x{N}.comp"
+    stream = torch.cuda.current_stream()
+    fn = lambda i: ctx.int4_linear(spec, x, qw[i % copies], sc[i % copies], qz[i % copies], None, y, M, stream)
+    ms = wall_ms(fn, args.steps, args.warmup)
+    kms = event_ms(fn, max(200, args.steps), stream)
+    alg = nbytes + M * K * 2 + M * N * 2
+    gbs = alg / (kms * 1e-3) / 1e9
+    out = base_line(args, gbs, "GB/s", ms, "bf16xint4->f32",
+                    {"workload": f"int4_gptq_g128_asym_m{M}_k4096_n14336", "weight_copies_rotated": copies})
+    out["roofline"] = {"bound": "hbm", "kernel": "int4_gptq_kernel<8>", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                       "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
+    return out
+
+
+def fp8_head(args, ctx, dev):
+    """Weights are drawn on the GPU (N(0,0.02), per-row bf16 amax/448 scale,
+    torch's e4m3fn cast): 579 MB exceeds the Infinity Cache on its own."""
+    import torch
+
+    M, K, N = args.m, 2880, 201088
+    g = torch.Generator(device=dev).manual_seed(20260004)
+    W = torch.empty(N, K, dtype=torch.uint8, device=dev)
+    sc = torch.empty(N, dtype=torch.float32, device=dev)
+    for r0 in range(0, N, 16384):
+        wf = torch.randn(min(16384, N - r0), K, generator=g, device=dev) * 0.02
+        s = (wf.abs().amax(dim=1) / 448.0).to(torch.bfloat16).float()
+        sc[r0:r0 + wf.shape[0]] = s
+        W[r0:r0 + wf.shape[0]] = (wf / s[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    nblk = (K + 127) // 128
+    grid = sc.to(torch.bfloat16).view(torch.int16)[:, None].repeat(1, nblk).contiguous()
+    x = (torch.randn(M, K, generator=g, device=dev)).to(torch.bfloat16).view(torch.int16)
+    lb = torch.zeros(M, N, dtype=torch.int16, device=dev)
+    am = torch.zeros(M, dtype=torch.int32, device=dev)
+    spec = f"tied_output_projection_batch4_fp8_e4m3_b1x128_{N}x{K}_scale1_to_f32.comp"
+    stream = torch.cuda.current_stream()
+    fn = lambda i: ctx.fp8_output_projection(spec, x, W, grid, None, lb, am, M, stream)
+    ms = wall_ms(fn, args.steps, args.warmup)
+    kms = event_ms(fn, max(50, args.steps), stream)
+    alg = N * K + N * nblk * 2 + M * K * 2 + M * N * 2 + M * 4
+    flop = 2.0 * M * N * K
+    gbs = alg / (kms * 1e-3) / 1e9
+    tf = flop / (kms * 1e-3) / 1e12
+    out = base_line(args, M / (kms * 1e-3), "tokens/s", ms, "e4m3xe4m3->f32",
+                    {"workload": f"fp8_lm_head_m{M}_k2880_n201088_argmax"})
+    mfma_bound = M >= 512
+    out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": "fp8_head_kernel",
+                       "achieved": tf if mfma_bound else gbs, "peak": FP8_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
+                       "unit": "TFLOP/s" if mfma_bound else "GB/s",
+                       "frac": (tf / FP8_PEAK_TFLOPS) if mfma_bound else (gbs / HBM_PEAK_GBS), "traffic": None,
+                       "hbm_gbs": gbs, "tflops": tf, "launch_ms": kms}
+    return out
 
 
 def cpu_baseline(d, budget_s):
-    """The C oracle (a scalar-per-lane restatement of the reference shaders,
-    OpenMP over rows) timed on this host on the same workload: whole MoE
-    blocks of 16 tokens, repeated until `budget_s` elapses."""
+    """The C oracle (a per-lane restatement of the reference shaders, OpenMP
+    over rows) timed on this host's cores on the same workload: whole MoE
+    decode blocks of 16 tokens, repeated until `budget_s` elapses."""
     import oracle
 
     B, k = d["B"], d["k"]
@@ -152,6 +337,44 @@ def cpu_baseline(d, budget_s):
     el = time.perf_counter() - t0
     return {"value": done * B * k / el, "unit": "expert-tokens/s", "cores": threads, "kind": "port",
             "sample": f"{done} full MoE decode block(s) of {B} tokens x top-{k} in {el:.1f} s (C oracle, OpenMP)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from nerve_amd.hip import Context
+
+    dev = torch.device("cuda:0")
+    ctx = Context(0)
+    if args.workload == "moe_decode":
+        out, d0 = moe_decode(args, ctx, dev)
+        if not args.no_prefill:
+            out["prefill"] = prefill_sub(ctx, dev)
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline(d0, args.cpu_seconds)
+    elif args.workload == "moe_prefill":
+        pf = Prefill(ctx, dev)
+        stream = torch.cuda.current_stream()
+        ms = wall_ms(pf.step, args.steps, args.warmup)
+        kms = event_ms(lambda i: pf.step(i, stream), max(20, args.steps), stream)
+        fig = pf.figures(kms)
+        out = base_line(args, pf.d["B"] * pf.d["k"] / (kms * 1e-3), "expert-tokens/s", ms, "e4m3xe2m1->f32",
+                        {"workload": fig["workload"]})
+        out["roofline"] = {"bound": "hbm", "kernel": "MoE prefill block", "achieved": fig["hbm_gbs"],
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": fig["hbm_frac"], "traffic": None,
+                           "tflops": fig["tflops"], "mxfp4_peak_frac": fig["mxfp4_peak_frac"]}
+    elif args.workload == "mxfp4_gemv":
+        out = mxfp4_gemv(args, ctx, dev)
+    elif args.workload == "int4_gemv":
+        out = int4_gemv(args, ctx, dev)
+    else:
+        out = fp8_head(args, ctx, dev)
+    print(json.dumps(out))
 
 
 if __name__ == "__main__":

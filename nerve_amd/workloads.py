@@ -60,9 +60,10 @@ def moe_experts(rng: np.random.Generator, E: int, H: int, I: int):
     return dict(gate_w=gw, gate_s=gs, up_w=uw, up_s=us, down_w=dw, down_s=ds)
 
 
-def config2(B: int = 16, E: int = 32, k: int = 4, H: int = 2880, I: int = 2880):
-    """MoE decode block: bf16 router N(0, 0.02), tokens N(0, 1), MXFP4 experts."""
-    rng = rng_for(2)
+def config2(B: int = 16, E: int = 32, k: int = 4, H: int = 2880, I: int = 2880, layer: int = 0):
+    """MoE decode block: bf16 router N(0, 0.02), tokens N(0, 1), MXFP4 experts.
+    `layer` > 0 draws another layer's router, experts and input tokens."""
+    rng = rng_for(2, salt=layer)
     router = bf16_normal(rng, (E, H), 0.02)
     tokens = bf16_normal(rng, (B, H), 1.0)
     d = dict(router_w=router, hidden=tokens, B=B, E=E, k=k, H=H, I=I, limit=7.0)

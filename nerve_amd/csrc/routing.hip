@@ -32,9 +32,10 @@ __global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint
     const uint32_t s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
     const bool H8 = (H % 8) == 0;
-    for (uint32_t s = s0; s < s1; s++) {
+    auto operands = [&](uint32_t s, v4i& av, v4i& bv) {
         const uint32_t k0 = s * 32 + g * 8;
-        v4i av = v4i{0, 0, 0, 0}, bv = v4i{0, 0, 0, 0};
+        av = v4i{0, 0, 0, 0};
+        bv = v4i{0, 0, 0, 0};
         if (H8) {
             if (tok < B && k0 < H) av = *reinterpret_cast<const v4i*>(x + (uint64_t)tok * H + k0);
             if (ex < E && k0 < H) bv = *reinterpret_cast<const v4i*>(W + (uint64_t)ex * H + k0);
@@ -47,8 +48,21 @@ __global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint
             av = *reinterpret_cast<v4i*>(at);
             bv = *reinterpret_cast<v4i*>(bt);
         }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bv), acc,
-                                                      0, 0, 0);
+    };
+    // Eight steps of operands are loaded before any of them is consumed, so a
+    // wave waits for memory once per eight MFMAs.
+    constexpr uint32_t U = 8;
+    for (uint32_t s = s0; s < s1; s += U) {
+        v4i av[U], bv[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++) {
+            if (s + u < s1) operands(s + u, av[u], bv[u]);
+            else av[u] = bv[u] = v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av[u]),
+                                                          __builtin_bit_cast(v8bf, bv[u]), acc, 0, 0, 0);
     }
     part[wave][lane] = acc;
     __syncthreads();
@@ -80,6 +94,34 @@ __device__ __forceinline__ bool better(float s, uint32_t i, float bs, uint32_t b
 
 __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); }
 
+// Route words and telemetry (…topk_routed_batch1_bf16.comp.template:168-179),
+// spread over the wave: lane r writes route r, lanes take one counter each.
+__device__ __forceinline__ void topk_publish(uint32_t b, uint32_t lane, const uint32_t* top, const float* wts,
+                                             uint32_t total_sel, uint32_t total_res, uint32_t* routes,
+                                             uint32_t* telemetry) {
+    if (lane < total_sel) {
+        routes[(uint64_t)b * total_sel + lane] = (f32_to_bf16(wts[lane]) << 16) | top[lane];
+        if (telemetry) __hip_atomic_fetch_add(&telemetry[top[lane]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!telemetry) return;
+    const uint32_t pairs = total_sel * (total_sel - 1) / 2;
+    for (uint32_t p = lane; p < pairs; p += 64) {
+        // p -> (l, r), l < r, in row-major order of the upper triangle
+        uint32_t l = 0, rem = p;
+        while (rem >= total_sel - 1 - l) {
+            rem -= total_sel - 1 - l;
+            l++;
+        }
+        const uint32_t r = l + 1 + rem;
+        const uint32_t left = top[l], right = top[r];
+        if (left < right) {
+            const uint32_t preceding = left * (2u * total_res - left - 1u) / 2u;
+            __hip_atomic_fetch_add(&telemetry[total_res + preceding + right - left - 1u], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ logits, const void* __restrict__ bias,
                                                   uint32_t* __restrict__ routes, uint32_t* __restrict__ telemetry,
                                                   uint32_t B, TopkParams P) {
@@ -89,6 +131,7 @@ __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ l
     __shared__ uint32_t top[128];
     __shared__ float wts[128];
     __shared__ float smax_sh, sden_sh;
+    __shared__ uint32_t sel_total, res_total;
     const uint32_t b = blockIdx.x;
     if (b >= B) return;
     const uint32_t lane = threadIdx.x;
@@ -142,82 +185,74 @@ __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ l
         }
         __syncthreads();
     }
-    if (lane != 0) return;
-    // All-NaN rows leave no selectable expert; index 0 keeps every LDS read in
-    // bounds (the reference shader would read past its array there).
-    for (uint32_t r = 0; r < P.k; r++)
-        if (top[r] >= E) top[r] = 0;
-    const uint32_t ks = P.k;
-    uint32_t total_sel = ks, total_res = E;
-    if (P.mode == 0) {
-        // moe_topk_routed_batch1_bf16.comp.template:133-167
-        const bool sig = P.activation != 0;
-        float maximum = raw[top[0]];
-        float den = 0.0f;
-        if (P.normalize) {
+    if (lane == 0) {
+        // All-NaN rows leave no selectable expert; index 0 keeps every LDS read in
+        // bounds (the reference shader would read past its array there).
+        for (uint32_t r = 0; r < P.k; r++)
+            if (top[r] >= E) top[r] = 0;
+        const uint32_t ks = P.k;
+        uint32_t total_sel = ks, total_res = E;
+        if (P.mode == 0) {
+            // moe_topk_routed_batch1_bf16.comp.template:133-167
+            const bool sig = P.activation != 0;
+            float maximum = raw[top[0]];
+            float den = 0.0f;
+            if (P.normalize) {
+                for (uint32_t r = 0; r < ks; r++) {
+                    float l = raw[top[r]];
+                    den += sig ? sigmoidf_(l) : expf(l - maximum);
+                }
+            } else if (!sig) {
+                maximum = -INFINITY;
+                for (uint32_t e = 0; e < E; e++) maximum = fmaxf(maximum, raw[e]);
+                for (uint32_t e = 0; e < E; e++) den += expf(raw[e] - maximum);
+            }
+            for (uint32_t r = 1; r < ks; r++) {
+                uint32_t ex = top[r];
+                uint32_t ins = r;
+                while (ins > 0 && top[ins - 1] > ex) { top[ins] = top[ins - 1]; ins--; }
+                top[ins] = ex;
+            }
             for (uint32_t r = 0; r < ks; r++) {
                 float l = raw[top[r]];
-                den += sig ? sigmoidf_(l) : expf(l - maximum);
+                float w = sig ? sigmoidf_(l) : expf(l - maximum);
+                if (P.normalize || !sig) w /= den;
+                wts[r] = w;
             }
-        } else if (!sig) {
-            maximum = -INFINITY;
-            for (uint32_t e = 0; e < E; e++) maximum = fmaxf(maximum, raw[e]);
-            for (uint32_t e = 0; e < E; e++) den += expf(raw[e] - maximum);
-        }
-        for (uint32_t r = 1; r < ks; r++) {
-            uint32_t ex = top[r];
-            uint32_t ins = r;
-            while (ins > 0 && top[ins - 1] > ex) { top[ins] = top[ins - 1]; ins--; }
-            top[ins] = ex;
-        }
-        for (uint32_t r = 0; r < ks; r++) {
-            float l = raw[top[r]];
-            float w = sig ? sigmoidf_(l) : expf(l - maximum);
-            if (P.normalize || !sig) w /= den;
-            wts[r] = w;
-        }
-    } else {
-        // moe_router_score_topk_batch1_bf16.comp.template:169-205
-        total_sel = ks + P.always_count;
-        total_res = E + P.always_count;
-        float den = 0.0f;
-        if (P.normalize) for (uint32_t r = 0; r < ks; r++) den += raw[top[r]];
-        for (uint32_t r = 0; r < ks; r++) {
-            float w = raw[top[r]];
-            wts[r] = P.normalize ? w / den * P.routed_scale : w * P.routed_scale;
-        }
-        for (uint32_t a = 0; a < P.always_count; a++) {
-            top[ks + a] = E + a;
-            wts[ks + a] = P.always_weight;
-        }
-        for (uint32_t r = 1; r < total_sel; r++) {
-            uint32_t ex = top[r];
-            float w = wts[r];
-            uint32_t ins = r;
-            while (ins > 0 && top[ins - 1] > ex) {
-                top[ins] = top[ins - 1];
-                wts[ins] = wts[ins - 1];
-                ins--;
+        } else {
+            // moe_router_score_topk_batch1_bf16.comp.template:169-205
+            total_sel = ks + P.always_count;
+            total_res = E + P.always_count;
+            float den = 0.0f;
+            if (P.normalize) for (uint32_t r = 0; r < ks; r++) den += raw[top[r]];
+            for (uint32_t r = 0; r < ks; r++) {
+                float w = raw[top[r]];
+                wts[r] = P.normalize ? w / den * P.routed_scale : w * P.routed_scale;
             }
-            top[ins] = ex;
-            wts[ins] = w;
-        }
-    }
-    for (uint32_t r = 0; r < total_sel; r++) {
-        routes[(uint64_t)b * total_sel + r] = (f32_to_bf16(wts[r]) << 16) | top[r];
-        if (telemetry) atomicAdd(&telemetry[top[r]], 1u);
-    }
-    if (telemetry) {
-        for (uint32_t l = 0; l < total_sel; l++)
-            for (uint32_t r = l + 1; r < total_sel; r++) {
-                uint32_t left = top[l], right = top[r];
-                if (left < right) {
-                    uint32_t preceding = left * (2u * total_res - left - 1u) / 2u;
-                    atomicAdd(&telemetry[total_res + preceding + right - left - 1u], 1u);
+            for (uint32_t a = 0; a < P.always_count; a++) {
+                top[ks + a] = E + a;
+                wts[ks + a] = P.always_weight;
+            }
+            for (uint32_t r = 1; r < total_sel; r++) {
+                uint32_t ex = top[r];
+                float w = wts[r];
+                uint32_t ins = r;
+                while (ins > 0 && top[ins - 1] > ex) {
+                    top[ins] = top[ins - 1];
+                    wts[ins] = wts[ins - 1];
+                    ins--;
                 }
+                top[ins] = ex;
+                wts[ins] = w;
             }
+        }
+        sel_total = total_sel;
+        res_total = total_res;
     }
+    __syncthreads();
+    topk_publish(b, lane, top, wts, sel_total, res_total, routes, telemetry);
 }
+
 
 // ---------------------------------------------------------------------------
 // a7: route compaction (moe_route_compact_batch1.comp.template:26-106,

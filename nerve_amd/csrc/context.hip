@@ -4,6 +4,7 @@
 #include <cstdlib>
 #include <regex>
 #include <string>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -70,7 +71,7 @@ static bool parse_u32(const std::string& s, uint32_t* out) {
 }
 
 // nerve/model_package_shader_templates.py:4773-4846
-nerve_hip_status parse_moe_spec(const char* spec, MoeSpec* out) {
+static nerve_hip_status parse_moe_spec_uncached(const char* spec, MoeSpec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re(
         "independent_sparse_moe_(gate_up|down)(?:_(batch1))?"
@@ -112,7 +113,7 @@ nerve_hip_status parse_moe_spec(const char* spec, MoeSpec* out) {
 }
 
 // nerve/model_package_shader_templates.py:4850-4915 and :5003-5060
-nerve_hip_status parse_topk_spec(const char* spec, TopkSpec* out) {
+static nerve_hip_status parse_topk_spec_uncached(const char* spec, TopkSpec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex topk(
         "moe_topk(?:_batch(\\d+))?_(sigmoid|softmax)_bf16_e(\\d+)_k(\\d+)_"
@@ -153,7 +154,7 @@ nerve_hip_status parse_topk_spec(const char* spec, TopkSpec* out) {
 }
 
 // nerve/model_package_shader_templates.py:3219-3276
-nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out) {
+static nerve_hip_status parse_int4_spec_uncached(const char* spec, Int4Spec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re(
         "(linear|linear_bias|linear_residual)(?:_batch(\\d+))?_int4_(gptq|ct)_s(f16|bf16)_g(\\d+)_(\\d+)x(\\d+)\\.comp");
@@ -180,7 +181,7 @@ nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out) {
 // nerve/model_package_shader_templates.py:2419-2465 (the output-scale token is
 // accepted as any float literal: the manifest writes it with format ".9g",
 // nerve/model_package_manifest.py:530-545).
-nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out) {
+static nerve_hip_status parse_fp8_head_spec_uncached(const char* spec, Fp8HeadSpec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re(
         "tied_output_projection(?:_batch(\\d+))?_fp8_e4m3_b(\\d+)x(\\d+)_(\\d+)x(\\d+)_scale([0-9eE+.-]+)_to_f32\\.comp");
@@ -202,7 +203,7 @@ nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out) {
 }
 
 // nerve/model_package_shader_templates.py:1513-1545
-nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out) {
+static nerve_hip_status parse_quant_spec_uncached(const char* spec, QuantSpec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re("quantize(?:_batch(\\d+))?_fp8_e4m3(?:_(spow2))?_b(\\d+)_h(\\d+)\\.comp");
     std::cmatch m;
@@ -218,6 +219,45 @@ nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out) {
         return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid FP8 activation-quantizer shape ") + spec);
     *out = s;
     return NERVE_HIP_OK;
+}
+
+
+// Specialization strings are parsed once per thread: a dispatch looks its
+// string up here (a hash of ~60 bytes) instead of running the grammar again,
+// which costs more host time than a decode-sized kernel takes on the device.
+// Only accepted strings are cached, so rejections keep their messages.
+template <class S, nerve_hip_status (*Parse)(const char*, S*)>
+static nerve_hip_status parse_cached(const char* spec, S* out) {
+    if (!spec) return Parse(spec, out);
+    thread_local std::unordered_map<std::string, S> cache;
+    std::string key(spec);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+        *out = it->second;
+        return NERVE_HIP_OK;
+    }
+    nerve_hip_status st = Parse(spec, out);
+    if (st == NERVE_HIP_OK) {
+        if (cache.size() >= 4096) cache.clear();
+        cache.emplace(std::move(key), *out);
+    }
+    return st;
+}
+
+nerve_hip_status parse_moe_spec(const char* spec, MoeSpec* out) {
+    return parse_cached<MoeSpec, parse_moe_spec_uncached>(spec, out);
+}
+nerve_hip_status parse_topk_spec(const char* spec, TopkSpec* out) {
+    return parse_cached<TopkSpec, parse_topk_spec_uncached>(spec, out);
+}
+nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out) {
+    return parse_cached<Int4Spec, parse_int4_spec_uncached>(spec, out);
+}
+nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out) {
+    return parse_cached<Fp8HeadSpec, parse_fp8_head_spec_uncached>(spec, out);
+}
+nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out) {
+    return parse_cached<QuantSpec, parse_quant_spec_uncached>(spec, out);
 }
 
 }  // namespace nh
@@ -274,7 +314,7 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
         if (st) return st;
         if (i.layout == 1 && i.group % 128)
             return nh::fail(NERVE_HIP_UNSUPPORTED, "CT INT4 kernel needs group % 128 == 0");
-        if (i.layout == 0 && i.out % 64) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 64 == 0");
+        if (i.layout == 0 && i.out % 16) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 16 == 0");
         if (i.layout == 1 && i.out % 16) return nh::fail(NERVE_HIP_UNSUPPORTED, "CT INT4 kernel needs N % 16 == 0");
         return NERVE_HIP_OK;
     }

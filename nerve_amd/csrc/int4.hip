@@ -39,11 +39,12 @@ __device__ __forceinline__ v4i permute_act(v4i a) {
                (int)((d1 & 0xFFFFu) | (d3 << 16)), (int)((d1 >> 16) | (d3 & 0xFFFF0000u))};
 }
 
-__device__ __forceinline__ float load_scale(const uint16_t* p, bool bf16) {
-    uint16_t v = *p;
+__device__ __forceinline__ float decode_scale(uint16_t v, bool bf16) {
     if (bf16) return bf16_to_f32(v);
     return (float)__builtin_bit_cast(_Float16, v);
 }
+
+__device__ __forceinline__ float load_scale(const uint16_t* p, bool bf16) { return decode_scale(*p, bf16); }
 
 constexpr uint32_t ONES_BF16 = 0x3F803F80u;
 
@@ -66,55 +67,102 @@ __device__ __forceinline__ void finalize_store(const Int4Args& A, uint32_t t, ui
     A.y[(uint64_t)t * A.N + n] = (uint16_t)f32_to_bf16(v);
 }
 
-// GPTQ layout: qweight [K/8, N].  A wave owns 64 columns (4 MFMA column tiles,
-// lane r takes columns n0 + 4r .. n0 + 4r + 3 so one 16-byte load feeds all
-// four) and 16 tokens; the block's KS waves split the groups.
-template <int KS>
+// J consecutive packed words of one qweight row (J = 1, 2 or 4).
+template <int J>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&w)[J]) {
+    if constexpr (J == 4) {
+        v4i v = *reinterpret_cast<const v4i*>(p);
+        w[0] = (uint32_t)v.x; w[1] = (uint32_t)v.y; w[2] = (uint32_t)v.z; w[3] = (uint32_t)v.w;
+    } else if constexpr (J == 2) {
+        v2i v = *reinterpret_cast<const v2i*>(p);
+        w[0] = (uint32_t)v.x; w[1] = (uint32_t)v.y;
+    } else {
+        w[0] = *p;
+    }
+}
+
+// GPTQ layout: qweight [K/8, N].  A wave owns 16 J columns (J MFMA column
+// tiles; lane r takes columns n0 + J r .. n0 + J r + J - 1 so one load feeds
+// all J) and 16 tokens; the block's KS waves split the groups.
+template <int KS, int J, uint32_t GQ_BATCH>
 __global__ __launch_bounds__(64 * KS) void int4_gptq_kernel(Int4Args A) {
-    __shared__ v4f part[KS][4][64];
+    __shared__ v4f part[KS][J][64];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t g = lane >> 4, rr = lane & 15;
-    const uint32_t n0 = blockIdx.x * 64;
+    // XCD-aware order: the hardware deals consecutive workgroups to the 8
+    // XCDs in turn; remapping gives each XCD a contiguous run of column tiles
+    // so partial cache lines shared by neighbouring tiles hit its L2.  The
+    // grid is padded to a multiple of 8; padding blocks exit.
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const uint32_t n0 = tile * (16 * J);
+    if (n0 >= A.N) return;
     const uint32_t m0 = blockIdx.y * 16;
     const uint32_t tok = m0 + rr;
     const uint32_t ngroups = A.K / A.G, steps = A.G / 32;
     const uint32_t per = (ngroups + KS - 1) / KS;
     const uint32_t g0 = min(ngroups, wave * per), g1 = min(ngroups, g0 + per);
-    const uint32_t col = n0 + 4 * rr;
+    const uint32_t col = n0 + J * rr;
     const bool tv = tok < A.B;
     const uint16_t* xrow = A.x + (uint64_t)(tv ? tok : 0) * A.K;
-    v4f acc[4] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
-    for (uint32_t grp = g0; grp < g1; grp++) {
-        v4f ag[4] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
-        v4f as = v4f{0.f, 0.f, 0.f, 0.f};
-        for (uint32_t s = 0; s < steps; s++) {
-            const uint32_t kb = grp * A.G + 32 * s;
+    v4f acc[J], ag[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) acc[j] = ag[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f as = v4f{0.f, 0.f, 0.f, 0.f};
+    // The wave's 32-k steps run in batches of GQ_BATCH: every weight and
+    // activation load of a batch is issued before its first MFMA, so the wave
+    // waits for memory once per batch.  A group's partial sums are scaled and
+    // folded into acc when its last step has been contracted.
+    const uint32_t first = g0 * steps, last = g1 * steps;
+    for (uint32_t base = first; base < last; base += GQ_BATCH) {
+        uint32_t wbuf[GQ_BATCH][J], zbuf[GQ_BATCH];
+        uint16_t sbuf[GQ_BATCH][J];
+        v4i abuf[GQ_BATCH];
+#pragma clang loop unroll(full)
+        for (uint32_t u = 0; u < GQ_BATCH; u++) {
+            const uint32_t i = min(base + u, last - 1);
+            const uint32_t kb = i * 32;
             const uint32_t p = kb / 8 + g;
-            v4i wv = *reinterpret_cast<const v4i*>(A.qw + (uint64_t)p * A.N + col);
-            v4i av = tv ? *reinterpret_cast<const v4i*>(xrow + kb + 8 * g) : v4i{0, 0, 0, 0};
-            v4i ap = permute_act(av);
-            ag[0] = mfma_bf16(ap, dequant_word((uint32_t)wv.x), ag[0]);
-            ag[1] = mfma_bf16(ap, dequant_word((uint32_t)wv.y), ag[1]);
-            ag[2] = mfma_bf16(ap, dequant_word((uint32_t)wv.z), ag[2]);
-            ag[3] = mfma_bf16(ap, dequant_word((uint32_t)wv.w), ag[3]);
-            as = mfma_bf16(ap, v4i{(int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16}, as);
+            load_words<J>(A.qw + (uint64_t)p * A.N + col, wbuf[u]);
+            abuf[u] = tv ? *reinterpret_cast<const v4i*>(xrow + kb + 8 * g) : v4i{0, 0, 0, 0};
+            // The group's scales and zero codes ride with its last step, so
+            // the fold below does not wait on a dependent load.
+            if ((i + 1) % steps == 0) {
+                const uint32_t grp = i / steps;
+                const uint16_t* sp = A.scales + (uint64_t)grp * A.N + col;
+#pragma unroll
+                for (int j = 0; j < J; j++) sbuf[u][j] = sp[j];
+                zbuf[u] = A.qzeros ? A.qzeros[(uint64_t)grp * (A.N / 8) + col / 8] >> (4 * (col % 8)) : 0x8888u;
+            }
         }
-        const uint16_t* sp = A.scales + (uint64_t)grp * A.N + col;
-        uint32_t zw = A.qzeros ? A.qzeros[(uint64_t)grp * (A.N / 8) + col / 8] >> (4 * (col % 8)) : 0x8888u;
+#pragma clang loop unroll(full)
+        for (uint32_t u = 0; u < GQ_BATCH; u++) {
+            const uint32_t i = base + u;
+            if (i >= last) continue;
+            v4i ap = permute_act(abuf[u]);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float sc = load_scale(sp + j, A.scale_bf16);
-            float off = 128.0f + (float)((zw >> (4 * j)) & 15u);
+            for (int j = 0; j < J; j++) ag[j] = mfma_bf16(ap, dequant_word(wbuf[u][j]), ag[j]);
+            as = mfma_bf16(ap, v4i{(int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16}, as);
+            if ((i + 1) % steps == 0) {
+                const uint32_t zw = zbuf[u];
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[j][i] = fmaf(sc, ag[j][i] - off * as[i], acc[j][i]);
+                for (int j = 0; j < J; j++) {
+                    float sc = decode_scale(sbuf[u][j], A.scale_bf16);
+                    float off = 128.0f + (float)((zw >> (4 * j)) & 15u);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) acc[j][q] = fmaf(sc, ag[j][q] - off * as[q], acc[j][q]);
+                    ag[j] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+                as = v4f{0.f, 0.f, 0.f, 0.f};
+            }
         }
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++) part[wave][j][lane] = acc[j];
+    for (int j = 0; j < J; j++) part[wave][j][lane] = acc[j];
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < J; j++) {
         v4f t = part[0][j][lane];
 #pragma unroll
         for (int w = 1; w < KS; w++) t += part[w][j][lane];
@@ -123,6 +171,232 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_kernel(Int4Args A) {
             uint32_t tt = m0 + 4 * g + i;
             if (tt < A.B) finalize_store(A, tt, col + j, t[i]);
         }
+    }
+}
+
+// GPTQ layout with the group length fixed at compile time (STEPS = G / 32).
+// Same tile and lane mapping as int4_gptq_kernel; a load batch holds GPB whole
+// groups (GPB * STEPS 32-k steps), so the per-group fold needs no per-step
+// test, and the wave's group range is derived from a scalar wave index so
+// that all step and group addressing stays on the scalar unit.
+template <int KS, int J, int STEPS>
+__global__ __launch_bounds__(64 * KS) void int4_gptq_fixed_kernel(Int4Args A) {
+    constexpr int GPB = STEPS >= 8 ? 1 : 8 / STEPS;
+    __shared__ v4f part[KS][J][64];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const uint32_t n0 = tile * (16 * J);
+    if (n0 >= A.N) return;
+    const uint32_t m0 = blockIdx.y * 16;
+    const uint32_t tok = m0 + rr;
+    const uint32_t N = A.N;
+    const uint32_t ngroups = A.K / (32 * STEPS);
+    const uint32_t per = (ngroups + KS - 1) / KS;
+    const uint32_t g0 = min(ngroups, wave * per), g1 = min(ngroups, g0 + per);
+    const uint32_t col = n0 + J * rr;
+    const bool tv = tok < A.B;
+    // Lane bases: packed row 4 i + g of step i is wq + i * 4 N; activations
+    // of step i start at xq + 32 i.
+    const uint32_t* wq = A.qw + (uint64_t)g * N + col;
+    const uint16_t* xq = A.x + (uint64_t)(tv ? tok : 0) * A.K + 8 * g;
+    const uint16_t* sq = A.scales + col;
+    const uint32_t* zq = A.qzeros ? A.qzeros + col / 8 : nullptr;
+    const uint32_t zshift = 4 * (col % 8);
+    v4f acc[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    const v4i ones = v4i{(int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16};
+    for (uint32_t grp = g0; grp < g1; grp += GPB) {
+        uint32_t wbuf[GPB][STEPS][J], zbuf[GPB];
+        uint16_t sbuf[GPB][J];
+        v4i abuf[GPB][STEPS];
+#pragma unroll
+        for (int gb = 0; gb < GPB; gb++) {
+            const uint32_t gi = min(grp + gb, g1 - 1);
+#pragma unroll
+            for (int st = 0; st < STEPS; st++) {
+                const uint32_t i = gi * STEPS + st;
+                load_words<J>(wq + (uint64_t)i * 4 * N, wbuf[gb][st]);
+                abuf[gb][st] = tv ? *reinterpret_cast<const v4i*>(xq + 32 * i) : v4i{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int j = 0; j < J; j++) sbuf[gb][j] = sq[(uint64_t)gi * N + j];
+            zbuf[gb] = zq ? zq[(uint64_t)gi * (N / 8)] >> zshift : 0x8888u;
+        }
+#pragma unroll
+        for (int gb = 0; gb < GPB; gb++) {
+            if (grp + gb >= g1) continue;
+            v4f ag[J], as = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < J; j++) ag[j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < STEPS; st++) {
+                v4i ap = permute_act(abuf[gb][st]);
+#pragma unroll
+                for (int j = 0; j < J; j++) ag[j] = mfma_bf16(ap, dequant_word(wbuf[gb][st][j]), ag[j]);
+                as = mfma_bf16(ap, ones, as);
+            }
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const float sc = decode_scale(sbuf[gb][j], A.scale_bf16);
+                const float off = 128.0f + (float)((zbuf[gb] >> (4 * j)) & 15u);
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[j][q] = fmaf(sc, ag[j][q] - off * as[q], acc[j][q]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) part[wave][j][lane] = acc[j];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        v4f t = part[0][j][lane];
+#pragma unroll
+        for (int w = 1; w < KS; w++) t += part[w][j][lane];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t tt = m0 + 4 * g + i;
+            if (tt < A.B) finalize_store(A, tt, col + j, t[i]);
+        }
+    }
+}
+
+// Decode-sized GPTQ linear (M <= GEMV_MAX_M tokens) on the vector ALU.  With
+// one or two tokens an MFMA tile would waste most of its rows, so each lane
+// owns one column and contracts packed words directly: a word's 8 codes become
+// four bf16 (128 + q) pairs (one and-or each) and v_dot2_f32_bf16 multiplies
+// each pair with the matching activation pair, so that
+//   sum_k x (q - z) = sum_k x (128 + q) - (128 + z) sum_k x
+// per group as in the MFMA kernels.  16 waves split the groups.
+//
+// Every load of a 32-row batch is issued up front and unconditionally, oldest
+// first in the order they are needed (the wave's activation slice, group
+// scales and zero codes, then the 32 packed words), so the wave waits for the
+// slice alone and then contracts each row as its word lands.  The slice is
+// permuted into pair order and parked in the wave's own LDS region (read back
+// as broadcasts); sum_k x per group is a reduction over the slice's lanes.
+constexpr uint32_t GEMV_MAX_M = 2;
+constexpr uint32_t GEMV_ROWS = 32;       // packed rows per wave batch (256 k)
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, a), __builtin_bit_cast(v2bf, b), c, false);
+}
+
+__device__ __forceinline__ float sum8_bf16(v4i v) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        s += bf16_to_f32((uint16_t)((uint32_t)v[q] & 0xFFFFu)) + bf16_to_f32((uint16_t)((uint32_t)v[q] >> 16));
+    return s;
+}
+
+template <int KS, int G, bool ZP>
+__global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
+    constexpr uint32_t GR = G / 8;                 // packed rows per group
+    constexpr uint32_t GPB = GEMV_ROWS / GR;       // groups per batch
+    static_assert(GR <= GEMV_ROWS && GEMV_ROWS % GR == 0, "group length must divide the batch");
+    __shared__ v4i xw[KS][GEMV_MAX_M][GEMV_ROWS];
+    __shared__ float part[KS][GEMV_MAX_M][64];
+    const uint32_t K = A.K, N = A.N, M = A.B, prow = K / 8;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, lr = lane & (GEMV_ROWS - 1);
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const uint32_t n0 = tile * 64;
+    if (n0 >= N) return;
+    const uint32_t col = n0 + lane;
+    const uint32_t ngroups = K / G;
+    const uint32_t nbatch = (ngroups + GPB - 1) / GPB;
+    const uint32_t per = (nbatch + KS - 1) / KS;
+    const uint32_t b0 = min(nbatch, wave * per), b1 = min(nbatch, b0 + per);
+    const uint32_t* wq = A.qw + col;
+    float acc[GEMV_MAX_M] = {0.f, 0.f};
+    for (uint32_t b = b0; b < b1; b++) {
+        const uint32_t grp0 = b * GPB, row0 = grp0 * GR;
+        // Loads, oldest first.
+        v4i xl[GEMV_MAX_M];
+#pragma unroll
+        for (uint32_t t = 0; t < GEMV_MAX_M; t++)
+            xl[t] = *reinterpret_cast<const v4i*>(A.x + (uint64_t)min(t, M - 1) * K + 8 * min(row0 + lr, prow - 1));
+        uint32_t zb[GPB];
+        uint16_t sb[GPB];
+#pragma unroll
+        for (uint32_t gb = 0; gb < GPB; gb++) {
+            const uint32_t gi = min(grp0 + gb, ngroups - 1);
+            sb[gb] = A.scales[(uint64_t)gi * N + col];
+            zb[gb] = ZP ? A.qzeros[(uint64_t)gi * (N / 8) + col / 8] : 0x88888888u;
+        }
+        // Scheduling fences keep the issue order (the compiler would otherwise
+        // hoist the packed-word loads ahead and then drain them all for the
+        // slice).
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t w[GEMV_ROWS];
+#pragma unroll
+        for (uint32_t r = 0; r < GEMV_ROWS; r++) w[r] = wq[(uint64_t)min(row0 + r, prow - 1) * N];
+        __builtin_amdgcn_sched_barrier(0);
+        // Activation slice: pair order into LDS, and per-group sums (lane lr
+        // holds row row0 + lr; lanes 32..63 mirror lanes 0..31).
+        float gsum[GEMV_MAX_M][GPB];
+#pragma unroll
+        for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
+            if (lane < GEMV_ROWS) xw[wave][t][lr] = permute_act(xl[t]);
+            float v = sum8_bf16(xl[t]);
+#pragma unroll
+            for (uint32_t d = 1; d < GR; d <<= 1) v += __shfl_xor(v, d);
+#pragma unroll
+            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = __shfl(v, gb * GR);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (uint32_t gb = 0; gb < GPB; gb++) {
+            const uint32_t gi = grp0 + gb;
+            if (gi >= ngroups) continue;
+            const float sc = decode_scale(sb[gb], A.scale_bf16);
+            const float off = 128.0f + (float)((zb[gb] >> (4 * (col % 8))) & 15u);
+            float ag[GEMV_MAX_M] = {0.f, 0.f};
+            // Activation rows are read from LDS four at a time ahead of use.
+            constexpr uint32_t XR = GR < 4 ? GR : 4;
+#pragma unroll
+            for (uint32_t r0 = 0; r0 < GR; r0 += XR) {
+                v4i xv[GEMV_MAX_M][XR];
+#pragma unroll
+                for (uint32_t t = 0; t < GEMV_MAX_M; t++)
+#pragma unroll
+                    for (uint32_t u = 0; u < XR; u++) xv[t][u] = xw[wave][t][gb * GR + r0 + u];
+#pragma unroll
+                for (uint32_t u = 0; u < XR; u++) {
+                    const v4i d = dequant_word(w[gb * GR + r0 + u]);
+#pragma unroll
+                    for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
+                        if (t < M) {
+                            ag[t] = dot2_bf16((uint32_t)xv[t][u].x, (uint32_t)d.x, ag[t]);
+                            ag[t] = dot2_bf16((uint32_t)xv[t][u].y, (uint32_t)d.y, ag[t]);
+                            ag[t] = dot2_bf16((uint32_t)xv[t][u].z, (uint32_t)d.z, ag[t]);
+                            ag[t] = dot2_bf16((uint32_t)xv[t][u].w, (uint32_t)d.w, ag[t]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (uint32_t t = 0; t < GEMV_MAX_M; t++) acc[t] = fmaf(sc, ag[t] - off * gsum[t][gb], acc[t]);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < GEMV_MAX_M; t++) part[wave][t][lane] = acc[t];
+    __syncthreads();
+    if (wave != 0) return;
+    for (uint32_t t = 0; t < M; t++) {
+        float v = part[0][t][lane];
+#pragma unroll
+        for (int w2 = 1; w2 < KS; w2++) v += part[w2][t][lane];
+        finalize_store(A, t, col, v);
     }
 }
 
@@ -144,24 +418,41 @@ __global__ __launch_bounds__(64 * KS) void int4_ct_kernel(Int4Args A) {
     const uint16_t* xrow = A.x + (uint64_t)(tv ? tok : 0) * A.K;
     const uint32_t* wrow = A.qw + (uint64_t)n * (A.K / 8);
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t grp = g0; grp < g1; grp++) {
-        v4f ag = v4f{0.f, 0.f, 0.f, 0.f}, as = v4f{0.f, 0.f, 0.f, 0.f};
-        for (uint32_t s = 0; s < steps; s++) {
-            const uint32_t kb = grp * A.G + 128 * s;
-            v4i wv = *reinterpret_cast<const v4i*>(wrow + kb / 8 + 4 * g);
+    v4f ag = v4f{0.f, 0.f, 0.f, 0.f}, as = v4f{0.f, 0.f, 0.f, 0.f};
+    // 128-k steps run in batches of CT_BATCH with every load of a batch issued
+    // before its first MFMA; a group is scaled and folded into acc after its
+    // last step.
+    constexpr uint32_t CT_BATCH = 4;
+    const uint32_t first = g0 * steps, last = g1 * steps;
+    for (uint32_t base = first; base < last; base += CT_BATCH) {
+        v4i wbuf[CT_BATCH], abuf[CT_BATCH][4];
+#pragma unroll
+        for (uint32_t u = 0; u < CT_BATCH; u++) {
+            const uint32_t kb = min(base + u, last - 1) * 128;
+            wbuf[u] = *reinterpret_cast<const v4i*>(wrow + kb / 8 + 4 * g);
             const uint16_t* xa = xrow + kb + 32 * g;
 #pragma unroll
+            for (int j = 0; j < 4; j++) abuf[u][j] = tv ? *reinterpret_cast<const v4i*>(xa + 8 * j) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < CT_BATCH; u++) {
+            const uint32_t i = base + u;
+            if (i >= last) break;
+#pragma unroll
             for (int j = 0; j < 4; j++) {
-                v4i av = tv ? *reinterpret_cast<const v4i*>(xa + 8 * j) : v4i{0, 0, 0, 0};
-                v4i ap = permute_act(av);
-                uint32_t wj = (uint32_t)(j == 0 ? wv.x : j == 1 ? wv.y : j == 2 ? wv.z : wv.w);
+                v4i ap = permute_act(abuf[u][j]);
+                uint32_t wj = (uint32_t)(j == 0 ? wbuf[u].x : j == 1 ? wbuf[u].y : j == 2 ? wbuf[u].z : wbuf[u].w);
                 ag = mfma_bf16(ap, dequant_word(wj), ag);
                 as = mfma_bf16(ap, v4i{(int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16, (int)ONES_BF16}, as);
             }
-        }
-        float sc = load_scale(A.scales + (uint64_t)n * ngroups + grp, A.scale_bf16);
+            if ((i + 1) % steps == 0) {
+                float sc = load_scale(A.scales + (uint64_t)n * ngroups + i / steps, A.scale_bf16);
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] = fmaf(sc, ag[i] - 136.0f * as[i], acc[i]);
+                for (int q = 0; q < 4; q++) acc[q] = fmaf(sc, ag[q] - 136.0f * as[q], acc[q]);
+                ag = v4f{0.f, 0.f, 0.f, 0.f};
+                as = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+        }
     }
     part[wave][lane] = acc;
     __syncthreads();
@@ -208,10 +499,40 @@ extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char
     A.finalize = s.op;
     hipStream_t strm = (hipStream_t)stream;
     if (s.layout == 0) {
-        if (A.N % 64) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 64 == 0");
+        if (A.N % 16) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 16 == 0");
         if (zeros && A.N % 8) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "qzeros need N % 8 == 0");
-        dim3 grid(A.N / 64, (batch_width + 15) / 16);
-        int4_gptq_kernel<8><<<grid, 512, 0, strm>>>(A);
+        // 64-column tiles (8 KiB of weights in flight per wave per batch);
+        // N % 64 != 0 uses 16-column tiles with deeper batches.
+        const uint32_t row_tiles = (batch_width + 15) / 16;
+        const bool wide = A.N % 64 == 0;
+        const uint32_t tiles = wide ? A.N / 64 : A.N / 16;
+        dim3 grid((tiles + 7) / 8 * 8, row_tiles);
+        const uint32_t steps = A.G / 32;
+        // Decode-sized batches go to the vector-ALU kernel.
+        if (wide && batch_width <= GEMV_MAX_M && (A.G == 32 || A.G == 64 || A.G == 128 || A.G == 256)) {
+            dim3 g1((tiles + 7) / 8 * 8);
+            const bool zp = zeros != nullptr;
+#define NERVE_INT4_GEMV(GG)                                                                  \
+    (zp ? int4_gptq_gemv_kernel<16, GG, true><<<g1, 1024, 0, strm>>>(A)                     \
+        : int4_gptq_gemv_kernel<16, GG, false><<<g1, 1024, 0, strm>>>(A))
+            if (A.G == 128) NERVE_INT4_GEMV(128);
+            else if (A.G == 64) NERVE_INT4_GEMV(64);
+            else if (A.G == 32) NERVE_INT4_GEMV(32);
+            else NERVE_INT4_GEMV(256);
+#undef NERVE_INT4_GEMV
+            return nh::check_launch("int4_linear_gptq_gemv");
+        }
+        // Few column tiles (decode-sized N): 16 waves split K so that each
+        // wave's share is one load batch.
+        const bool deep = tiles * row_tiles < 2u * (uint32_t)ctx->cu_count;
+        if (wide && steps == 4 && deep) int4_gptq_fixed_kernel<16, 4, 4><<<grid, 1024, 0, strm>>>(A);
+        else if (wide && steps == 4) int4_gptq_fixed_kernel<8, 4, 4><<<grid, 512, 0, strm>>>(A);
+        else if (wide && steps == 1) int4_gptq_fixed_kernel<8, 4, 1><<<grid, 512, 0, strm>>>(A);
+        else if (wide && steps == 2) int4_gptq_fixed_kernel<8, 4, 2><<<grid, 512, 0, strm>>>(A);
+        else if (wide && steps == 8) int4_gptq_fixed_kernel<8, 4, 8><<<grid, 512, 0, strm>>>(A);
+        else if (!wide && steps == 4) int4_gptq_fixed_kernel<8, 1, 4><<<grid, 512, 0, strm>>>(A);
+        else if (wide) int4_gptq_kernel<8, 4, 8><<<grid, 512, 0, strm>>>(A);
+        else int4_gptq_kernel<8, 1, 16><<<grid, 512, 0, strm>>>(A);
         return nh::check_launch("int4_linear_gptq");
     }
     if (zeros) return nh::fail(NERVE_HIP_UNSUPPORTED, "asymmetric zeros are supported for the GPTQ layout only");

@@ -35,17 +35,38 @@ def _run_int4(ctx, dev, spec, x, qw, scales, zeros, aux, B, N):
     return to_np(y, np.uint16)
 
 
+# (K, N) pairs cover both column-tile widths (16 columns when N % 64 != 0),
+# groups that straddle load batches and grids of many XCD-remapped tiles.
+@pytest.mark.parametrize("K,N", [(1024, 512), (512, 48), (256, 16384), (256, 32768)])
 @pytest.mark.parametrize("M", [1, 4, 16, 20])
 @pytest.mark.parametrize("symmetric", [True, False])
-def test_int4_gptq_parity(ctx, dev, M, symmetric):
-    K, N, G = 1024, 512, 128
-    rng = np.random.default_rng(M + 10 * symmetric)
+def test_int4_gptq_parity(ctx, dev, M, symmetric, K, N):
+    G = 128
+    rng = np.random.default_rng(M + 10 * symmetric + N)
     d = wl.int4_gptq(rng, K, N, G, symmetric)
     x = wl.bf16_normal(rng, (M, K))
     spec = f"linear_batch16_int4_gptq_sf16_g{G}_{K}x{N}.comp"
     y = _run_int4(ctx, dev, spec, x, d["qweight"], d["scales"], None if symmetric else d["qzeros"], None, M, N)
     ref = oracle.int4_linear("gptq", x, d["qweight"], d["scales"].view(np.uint16), G,
                              zeros=None if symmetric else d["qzeros"])
+    ok, worst, exact = bf16_close(y, ref)
+    assert ok and exact > 0.9, (worst, exact)
+
+
+# Group lengths with a compile-time kernel (32, 64, 128, 256) and one served
+# by the generic kernel (96), at both column-tile widths.
+# M = 2 takes the vector-ALU decode kernel where N % 64 == 0, M = 5 the MFMA one.
+@pytest.mark.parametrize("G", [32, 64, 96, 256])
+@pytest.mark.parametrize("N", [512, 48])
+@pytest.mark.parametrize("M", [2, 5])
+def test_int4_gptq_group_lengths(ctx, dev, G, N, M):
+    K = 768
+    rng = np.random.default_rng(G * 7 + N + M)
+    d = wl.int4_gptq(rng, K, N, G, False)
+    x = wl.bf16_normal(rng, (M, K))
+    spec = f"linear_batch16_int4_gptq_sf16_g{G}_{K}x{N}.comp"
+    y = _run_int4(ctx, dev, spec, x, d["qweight"], d["scales"], d["qzeros"], None, M, N)
+    ref = oracle.int4_linear("gptq", x, d["qweight"], d["scales"].view(np.uint16), G, zeros=d["qzeros"])
     ok, worst, exact = bf16_close(y, ref)
     assert ok and exact > 0.9, (worst, exact)
 

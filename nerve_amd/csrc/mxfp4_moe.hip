@@ -17,6 +17,8 @@
 //   fp4 operand: 16 bytes hold k = 32g..32g+31 (low nibble first) of row r;
 //   scale operand: lane (g, r) supplies the e8m0 scale of row r, k-block g;
 //   result: lane (g, r) holds D[4g+i][r], i = 0..3.
+#include <utility>
+
 #include "common.h"
 
 namespace {
@@ -568,15 +570,22 @@ constexpr uint32_t GS_MAX_K = 4096;
 
 __device__ __attribute__((aligned(16))) const uint8_t kZero16[16] = {0};
 
-__device__ __forceinline__ void wait_vm(uint32_t outstanding) {
-    // s_waitcnt vmcnt(n) with expcnt / lgkmcnt left at their maxima.
-    switch (outstanding) {
-        case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-        case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-        case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    }
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm_imm() {
+    // gfx9 s_waitcnt: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | 0x0F70u);
 }
+
+template <uint32_t... I>
+__device__ __forceinline__ void wait_vm_dispatch(uint32_t n, std::integer_sequence<uint32_t, I...>) {
+    (void)((n == I ? (wait_vm_imm<I>(), true) : false) || ...);
+}
+
+// vmcnt(n) for a wave-uniform run-time n (clamped to the 6-bit counter).
+__device__ __forceinline__ void wait_vm(uint32_t n) {
+    wait_vm_dispatch(n > 63 ? 63 : n, std::make_integer_sequence<uint32_t, 64>{});
+}
+
 
 
 // LDS reads of pipeline stages are issued as inline ds_read_b128 so the
@@ -983,6 +992,421 @@ nerve_hip_status launch_span(SpanArgs A, uint32_t tiles, hipStream_t st) {
     return nh::check_launch("mx_span_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Persistent span-streaming expert GEMV (decode-shaped batches).
+//
+// The span kernel above waits for its block's whole span before contracting
+// it, so a CU holding ~3 such blocks spends much of its time with nothing in
+// flight (record and activation round trips, MFMA, reduction, epilogue).  Here
+// one block per CU walks a contiguous range of work items (tile, 16-row block)
+// in tile-major order and keeps NBUF - 1 row spans in flight in a ring of LDS
+// slots while it contracts the current one:
+//   * activations of the current tile stay in registers (reloaded only when
+//     the tile changes, at most a few times per block);
+//   * every wave issues the same, fixed number of copies per item (short
+//     waves re-copy one of their own pieces), so "item i has landed" is
+//     vmcnt <= copies_per_item * (items issued after i).  Loads retire in
+//     issue order; the epilogue's global stores may retire in any order but
+//     can only hold the count up, so the wait never ends early;
+//   * tile records are read with scalar loads and all LDS traffic of the loop
+//     is inline ds_read/ds_write, so the compiler inserts no vmcnt drains.
+// ---------------------------------------------------------------------------
+struct StreamArgs {
+    const uint8_t* aq;
+    const float* as;
+    uint32_t a_row_div;
+    uint32_t K, N, k;
+    const uint32_t* routes;
+    const uint32_t* seg_list;
+    const TileRec* recs;
+    const uint32_t* n_tiles;
+    uint16_t* out16;
+    uint64_t frame_elems;
+    float limit;
+    uint32_t w_region, s_region, slot_bytes;   // LDS layout of one ring slot
+    uint32_t lw, ls;                            // copies per wave per matrix (weights, scales)
+    uint32_t copies_per_item;                   // per wave: NMAT * (lw + ls)
+};
+
+__device__ __forceinline__ uint32_t lds_read_u8(const uint8_t* p) {
+    uint32_t r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_read_b32(const uint8_t* p) {
+    uint32_t r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+__device__ __forceinline__ void lds_write16(uint8_t* p, v4f v) {
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+typedef uint32_t u4s __attribute__((ext_vector_type(4)));
+typedef uint32_t u8s __attribute__((ext_vector_type(8)));
+
+// A tile record through the scalar cache (begin, count, matrix and scale
+// pointers), so that reading it adds nothing to vmcnt.
+__device__ __forceinline__ void sload_rec(const TileRec* rec, uint32_t& begin, uint32_t& count,
+                                          const uint8_t* (&w)[2], const uint8_t* (&s)[2]) {
+    u4s h;
+    u8s p;
+    asm volatile("s_load_dwordx4 %0, %2, 0x0\n\ts_load_dwordx8 %1, %2, 0x10\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(h), "=s"(p)
+                 : "s"(rec));
+    begin = h.y;
+    count = h.z;
+    w[0] = reinterpret_cast<const uint8_t*>(((uint64_t)p[1] << 32) | p[0]);
+    w[1] = reinterpret_cast<const uint8_t*>(((uint64_t)p[3] << 32) | p[2]);
+    s[0] = reinterpret_cast<const uint8_t*>(((uint64_t)p[5] << 32) | p[4]);
+    s[1] = reinterpret_cast<const uint8_t*>(((uint64_t)p[7] << 32) | p[6]);
+}
+
+// x * sigmoid(x) with e^-x from the hardware base-2 exponential
+// (v_exp_f32, ~1 ulp): e^-x = 2^(-x log2 e).
+__device__ __forceinline__ float silu_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+    return x / (1.0f + e);
+}
+
+typedef uint32_t u16s __attribute__((ext_vector_type(16)));
+
+// 16 consecutive words through the scalar cache (the buffer must extend 64
+// bytes past p).
+__device__ __forceinline__ u16s sload_x16(const uint32_t* p) {
+    u16s v;
+    asm volatile("s_load_dwordx16 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t sload_u32(const uint32_t* p) {
+    uint32_t v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p));
+    return v;
+}
+
+// One contiguous range of work items [i0, i1) of a single tile, run by NW
+// waves that split each item's K chunks.
+template <int MODE, int NMAT, int NBUF, int NW>
+__device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, uint32_t i1, uint32_t nrb) {
+    constexpr uint32_t CH = 32 / NW;          // max K chunks per wave (K <= 4096)
+    constexpr uint32_t LWMAX = 32 / NW;       // max weight copies per wave per matrix
+    constexpr uint32_t LSMAX = (8 + NW - 1) / NW;
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
+    const uint32_t lw = A.lw, ls = A.ls;
+
+    // Ranges run back to back in one block: every wave has finished the
+    // previous one (ring slots and the reduction area are reused).
+    __builtin_amdgcn_s_barrier();
+    uint8_t* red = ring + NBUF * A.slot_bytes;   // [wave][NMAT][lane] v4f partial sums
+    const uint32_t npw = (16 * RB + 1023) / 1024, nps = (16 * SB + 255) / 256;
+
+    // ---- copy plan, fixed for the range: piece t of this wave starts at
+    // byte wpos(t) of the 16-row span (short waves repeat their first piece
+    // so every wave issues lw + ls copies per matrix).  The last piece is
+    // aligned to the span's end, overlapping its neighbour with identical
+    // bytes, so LDS regions need no padding.
+    uint32_t wpos[LWMAX], spos[LSMAX], woff[LWMAX], soff[LSMAX];
+#pragma unroll
+    for (uint32_t t = 0; t < LWMAX; t++) {
+        uint32_t pc = wave + NW * t;
+        if (pc >= npw) pc = wave < npw ? wave : 0;
+        wpos[t] = min(pc * 1024, 16 * RB - 1024);
+        woff[t] = wpos[t] + lane * 16;
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < LSMAX; t++) {
+        uint32_t pc = wave + NW * t;
+        if (pc >= nps) pc = wave < nps ? wave : 0;
+        spos[t] = min(pc * 256, 16 * SB - 256);
+        soff[t] = spos[t] + lane * 4;
+    }
+
+    // ---- issue side: copies of item `item` into ring slot `slot`
+    uint32_t itile = 0xffffffffu;
+    const uint8_t* iw[2] = {nullptr, nullptr};
+    const uint8_t* is[2] = {nullptr, nullptr};
+    auto issue = [&](uint32_t item, uint32_t slot) {
+        const uint32_t tile = item / nrb, n0 = (item - tile * nrb) * 16;
+        if (tile != itile) {
+            uint32_t b_, c_;
+            sload_rec(A.recs + tile, b_, c_, iw, is);
+            itile = tile;
+        }
+        const uint32_t rows = min(16u, N - n0);
+        const uint32_t wbytes = rows * RB, sbytes = rows * SB;
+        uint8_t* dst = ring + slot * A.slot_bytes;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            const uint8_t* ws = iw[m] + (uint64_t)n0 * RB;
+#pragma unroll
+            for (uint32_t t = 0; t < LWMAX; t++)
+                if (t < lw)
+                    __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? woff[t] : 0),
+                                                     dst + m * A.w_region + wpos[t], 16, 0, 0);
+            const uint8_t* ss = is[m] + (uint64_t)n0 * SB;
+#pragma unroll
+            for (uint32_t t = 0; t < LSMAX; t++)
+                if (t < ls)
+                    __builtin_amdgcn_global_load_lds(ss + (soff[t] < sbytes ? soff[t] : 0),
+                                                     dst + NMAT * A.w_region + m * A.s_region + spos[t], 4, 0, 0);
+        }
+    };
+
+    // ---- compute side: this wave's K chunks, their LDS offsets, the tile
+    const uint32_t per = (nch + NW - 1) / NW;
+    const uint32_t c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
+    uint32_t rw[CH], rs[CH];
+    bool kvalid[CH];
+#pragma unroll
+    for (uint32_t q = 0; q < CH; q++) {
+        const uint32_t c = c0 + q, kb = c * 128 + g * 32;
+        kvalid[q] = c < c1 && kb < K;
+        const uint32_t kk = kvalid[q] ? kb : 0;
+        rw[q] = rr * RB + kk / 2;
+        rs[q] = NMAT * A.w_region + rr * SB + kk / 32;
+    }
+    uint32_t ctile = 0xffffffffu;
+    v8i av[CH];
+    uint32_t sa[CH];
+    uint64_t obase = 0;        // output element offset of this lane's token (component `wave`)
+    float wr = 0.0f;
+    bool ovalid = false;
+
+    // Tile set-up in two halves.  tile_request() reads the tile record and its
+    // 16 route entries through the scalar cache, then issues this lane's
+    // activation and route loads without waiting; tile_finish() converts them
+    // after the caller's vmcnt wait.
+    v4i lo[CH], hi[CH];
+    float sraw[CH];
+    uint32_t wraw = 0;
+    bool arow_ok = false;
+    auto tile_request = [&](uint32_t tile) {
+        uint32_t begin, cnt;
+        const uint8_t* w_[2];
+        const uint8_t* s_[2];
+        sload_rec(A.recs + tile, begin, cnt, w_, s_);
+        u16s seg = sload_x16(A.seg_list + begin);
+        const uint32_t tl = 4 * g + wave;
+        uint32_t my_row = 0, my_out = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 16; q++) {
+            if (rr == q) my_row = seg[q];
+            if (tl == q) my_out = seg[q];
+        }
+        arow_ok = rr < cnt;
+        const uint8_t* arow = A.aq + (uint64_t)(arow_ok ? my_row / A.a_row_div : 0) * K;
+        const float* ascale = A.as + (uint64_t)(arow_ok ? my_row / A.a_row_div : 0) * nch;
+#pragma unroll
+        for (uint32_t q = 0; q < CH; q++) {
+            const uint32_t c = c0 + q, k0 = c * 128 + g * 16;
+            lo[q] = hi[q] = v4i{0, 0, 0, 0};
+            sraw[q] = 1.0f;
+            if (arow_ok && c < c1) {
+                if (k0 < K) lo[q] = *reinterpret_cast<const v4i*>(arow + k0);
+                if (k0 + 64 < K) hi[q] = *reinterpret_cast<const v4i*>(arow + k0 + 64);
+                sraw[q] = ascale[c];
+            }
+        }
+        ovalid = wave < 4 && tl < cnt;
+        if (ovalid) {
+            if (MODE == SPAN_GATE_UP) {
+                obase = (uint64_t)(my_out / A.k) * A.frame_elems + (uint64_t)(my_out % A.k) * N;
+            } else {
+                obase = (uint64_t)my_out * N;
+                wraw = A.routes[my_out];
+            }
+        }
+        ctile = tile;
+    };
+    auto tile_finish = [&]() {
+        // The empty asm pins every use of the loaded values after the
+        // caller's wait (the compiler would otherwise fold the conversions
+        // into the loads' branches and wait for each load there).
+#pragma unroll
+        for (uint32_t q = 0; q < CH; q++) asm volatile("" : "+v"(lo[q]), "+v"(hi[q]), "+v"(sraw[q]));
+        asm volatile("" : "+v"(wraw));
+#pragma unroll
+        for (uint32_t q = 0; q < CH; q++) {
+            av[q] = v8i{lo[q].x, lo[q].y, lo[q].z, lo[q].w, hi[q].x, hi[q].y, hi[q].z, hi[q].w};
+            sa[q] = arow_ok ? pow2_to_e8m0(sraw[q]) : 127u;
+        }
+        wr = bf16_to_f32(wraw >> 16);
+    };
+
+    // Prologue: the first items' copies, then the first tile's operands; one
+    // wait covers both round trips.
+#pragma unroll
+    for (uint32_t j = 0; j < NBUF - 1; j++)
+        if (i0 + j < i1) issue(i0 + j, j);
+    tile_request(i0 / nrb);
+    wait_vm(0);
+    tile_finish();
+
+    for (uint32_t i = i0; i < i1; i++) {
+        const uint32_t slot = (i - i0) % NBUF;
+        if (i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
+        const uint32_t tile = i / nrb, n0 = (i - tile * nrb) * 16;
+        if (tile != ctile) {
+            wait_vm(0);
+            tile_request(tile);
+            wait_vm(0);
+            tile_finish();
+        }
+        wait_vm(A.copies_per_item * min((uint32_t)(NBUF - 1), i1 - 1 - i));
+        __builtin_amdgcn_s_barrier();
+
+        // ---- contract this wave's chunks of the slot
+        const uint8_t* buf = ring + slot * A.slot_bytes;
+        v4f acc[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t q0 = 0; q0 < CH; q0 += 4) {
+            if (c0 + q0 >= c1) continue;
+            v4i w[4][NMAT];
+            uint32_t sw[4][NMAT];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) {
+                    w[u][m] = lds_read16(buf + m * A.w_region + rw[q0 + u]);
+                    sw[u][m] = lds_read_u8(buf + m * A.s_region + rs[q0 + u]);
+                }
+            }
+            lds_drain();
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                if (c0 + q0 + u >= c1) continue;
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) {
+                    // Operands of a drained read are opaque to the compiler;
+                    // launder them through an empty asm so their use stays
+                    // after the wait.
+                    v4i wv = w[u][m];
+                    uint32_t s8 = sw[u][m];
+                    asm volatile("" : "+v"(wv), "+v"(s8));
+                    if (!kvalid[q0 + u]) {
+                        wv = v4i{0, 0, 0, 0};
+                        s8 = 127;
+                    }
+                    acc[m] = mfma_fp8_fp4(av[q0 + u], wv, sa[q0 + u], s8, acc[m]);
+                }
+            }
+        }
+        // ---- cross-wave reduction; waves 0..3 finalize component `wave`.
+        // An MFMA result read by another instruction needs software wait
+        // states, which the compiler does not add in front of inline asm: the
+        // nops take the accumulators as operands so they sit between the last
+        // MFMA and the LDS write.
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc[m]));
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) lds_write16(red + ((wave * NMAT + m) * 64 + lane) * 16, acc[m]);
+        lds_drain();
+        __builtin_amdgcn_s_barrier();
+        if (wave >= 4) continue;
+        float t[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            uint32_t v[NW];
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) v[w2] = lds_read_b32(red + ((w2 * NMAT + m) * 64 + lane) * 16 + 4 * wave);
+            lds_drain();
+            float sum = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) {
+                asm volatile("" : "+v"(v[w2]));
+                sum += __uint_as_float(v[w2]);
+            }
+            t[m] = sum;
+        }
+        const uint32_t n = n0 + rr;
+        if (ovalid && n < N) {
+            if (MODE == SPAN_GATE_UP) {
+                float gv = round_bf16(t[0]);
+                float uv = round_bf16(t[NMAT - 1]);
+                if (A.limit > 0.0f) {
+                    gv = fminf(gv, A.limit);
+                    uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                }
+                const float h = silu_fast(gv) * uv;
+                A.out16[obase + n] = (uint16_t)f32_to_bf16(h);
+            } else {
+                A.out16[obase + n] = (uint16_t)f32_to_bf16(t[0] * wr);
+            }
+        }
+    }
+}
+
+template <int MODE, int NMAT, int NBUF, int NW>
+__global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
+    const uint32_t N = A.N;
+    const uint32_t nrb = (N + 15) / 16;
+    const uint32_t n_tiles = sload_u32(A.n_tiles);
+    // Work split that never crosses a tile inside a block when there are at
+    // least as many blocks as tiles: tile t gets q or q + 1 blocks, which
+    // split its row blocks evenly.  With fewer blocks than tiles a block
+    // takes whole tiles (b, b + G, ...), each a separate range.
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    if (n_tiles == 0) return;
+    if (G >= n_tiles) {
+        const uint32_t q = G / n_tiles, r = G % n_tiles;
+        // Blocks [0, r (q + 1)) serve tiles 0..r-1 with q + 1 blocks each.
+        uint32_t tile, part, parts;
+        if (b < r * (q + 1)) {
+            tile = b / (q + 1);
+            part = b % (q + 1);
+            parts = q + 1;
+        } else {
+            tile = r + (b - r * (q + 1)) / q;
+            part = (b - r * (q + 1)) % q;
+            parts = q;
+        }
+        const uint32_t lo_rb = nrb * part / parts, hi_rb = nrb * (part + 1) / parts;
+        if (lo_rb < hi_rb) stream_range<MODE, NMAT, NBUF, NW>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb);
+    } else {
+        for (uint32_t t = b; t < n_tiles; t += G) stream_range<MODE, NMAT, NBUF, NW>(A, t * nrb, (t + 1) * nrb, nrb);
+    }
+}
+
+// Launches the streaming kernel, or returns UNSUPPORTED when the shape does
+// not fit its LDS ring or copy-count limits (the caller then uses the span
+// kernel).
+template <int MODE, int NMAT, int NBUF, int NW = 8>
+nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream_t st) {
+    // 16-row spans of at least one 1 KB weight piece and one 256 B scale piece.
+    if (A.K > 4096 || A.K < 512 || A.K % 32) return NERVE_HIP_UNSUPPORTED;
+    A.w_region = 16 * (A.K / 2);
+    A.s_region = 16 * (A.K / 32);
+    A.slot_bytes = NMAT * (A.w_region + A.s_region);
+    const uint32_t npw = (16 * (A.K / 2) + 1023) / 1024, nps = (16 * (A.K / 32) + 255) / 256;
+    A.lw = (npw + NW - 1) / NW;
+    A.ls = (nps + NW - 1) / NW;
+    A.copies_per_item = NMAT * (A.lw + A.ls);
+    const size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * 64 * 16;
+    if (lds > 160 * 1024 || A.copies_per_item * (NBUF - 1) > 63) return NERVE_HIP_UNSUPPORTED;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)mx_stream_kernel<MODE, NMAT, NBUF, NW>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for mx_stream_kernel");
+        attr_set = true;
+    }
+    mx_stream_kernel<MODE, NMAT, NBUF, NW><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
+    return nh::check_launch("mx_stream_kernel");
+}
+
 nerve_hip_status launch_quant(const QuantArgs& Q, bool pow2, hipStream_t st) {
     if (Q.rows == 0) return nh::ok();
     const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
@@ -1084,7 +1508,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     nh::Carver cv;
     size_t o_aq = cv.take<uint8_t>((size_t)arows * K);
     size_t o_as = cv.take<float>((size_t)arows * nblk);
-    size_t o_seg = cv.take<uint32_t>(cap);
+    size_t o_seg = cv.take<uint32_t>(cap + 16);   // +16: the streaming kernel reads 16 entries at once
     size_t o_rec = cv.take<TileRec>(max_tiles);
     size_t o_nt = cv.take<uint32_t>(1);
     void* ws = nullptr;
@@ -1194,11 +1618,28 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         sa.n_tiles = ea.n_tiles;
         sa.frame_elems = ea.frame_elems;
         sa.limit = ea.limit;
+        StreamArgs qa{};
+        qa.aq = aq;
+        qa.as = as;
+        qa.a_row_div = ea.a_row_div;
+        qa.K = K;
+        qa.N = N;
+        qa.k = k;
+        qa.routes = ea.routes;
+        qa.seg_list = ea.seg_list;
+        qa.recs = ea.recs;
+        qa.n_tiles = ea.n_tiles;
+        qa.frame_elems = ea.frame_elems;
+        qa.limit = ea.limit;
         if (gate_up) {
-            sa.out16 = static_cast<uint16_t*>(intermediates);
+            sa.out16 = qa.out16 = static_cast<uint16_t*>(intermediates);
+            st = launch_stream<SPAN_GATE_UP, 2, 3>(qa, ctx, stream);
+            if (st != NERVE_HIP_UNSUPPORTED) return st;
             return launch_span<SPAN_GATE_UP, 2, 1>(sa, max_tiles, stream);
         }
-        sa.out16 = static_cast<uint16_t*>(expert_outputs);
+        sa.out16 = qa.out16 = static_cast<uint16_t*>(expert_outputs);
+        st = launch_stream<SPAN_DOWN, 1, 5>(qa, ctx, stream);
+        if (st != NERVE_HIP_UNSUPPORTED) return st;
         return launch_span<SPAN_DOWN, 1, 2>(sa, max_tiles, stream);
     }
     return nh::fail(NERVE_HIP_UNSUPPORTED, "no MXFP4 expert kernel for this shape");

@@ -1093,12 +1093,14 @@ __device__ __forceinline__ uint32_t sload_u32(const uint32_t* p) {
 }
 
 // One contiguous range of work items [i0, i1) of a single tile, run by NW
-// waves that split each item's K chunks.
-template <int MODE, int NMAT, int NBUF, int NW>
+// waves that split each item's K chunks.  An item is RI = 16 NSUB rows of
+// each of the NMAT matrices.
+template <int MODE, int NMAT, int NBUF, int NW, int NSUB>
 __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, uint32_t i1, uint32_t nrb) {
-    constexpr uint32_t CH = 32 / NW;          // max K chunks per wave (K <= 4096)
-    constexpr uint32_t LWMAX = 32 / NW;       // max weight copies per wave per matrix
-    constexpr uint32_t LSMAX = (8 + NW - 1) / NW;
+    constexpr uint32_t RI = 16 * NSUB;
+    constexpr uint32_t CH = 32 / NW;                            // max K chunks per wave (K <= 4096)
+    constexpr uint32_t LWMAX = (32 * NSUB + NW - 1) / NW;       // max weight copies per wave per matrix
+    constexpr uint32_t LSMAX = (8 * NSUB + NW - 1) / NW;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63, g = lane >> 4, rr = lane & 15;
@@ -1108,11 +1110,11 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     // Ranges run back to back in one block: every wave has finished the
     // previous one (ring slots and the reduction area are reused).
     __builtin_amdgcn_s_barrier();
-    uint8_t* red = ring + NBUF * A.slot_bytes;   // [wave][NMAT][lane] v4f partial sums
-    const uint32_t npw = (16 * RB + 1023) / 1024, nps = (16 * SB + 255) / 256;
+    uint8_t* red = ring + NBUF * A.slot_bytes;   // [wave][NMAT * NSUB][lane] v4f partial sums
+    const uint32_t npw = (RI * RB + 1023) / 1024, nps = (RI * SB + 255) / 256;
 
     // ---- copy plan, fixed for the range: piece t of this wave starts at
-    // byte wpos(t) of the 16-row span (short waves repeat their first piece
+    // byte wpos(t) of the RI-row span (short waves repeat their first piece
     // so every wave issues lw + ls copies per matrix).  The last piece is
     // aligned to the span's end, overlapping its neighbour with identical
     // bytes, so LDS regions need no padding.
@@ -1121,14 +1123,14 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     for (uint32_t t = 0; t < LWMAX; t++) {
         uint32_t pc = wave + NW * t;
         if (pc >= npw) pc = wave < npw ? wave : 0;
-        wpos[t] = min(pc * 1024, 16 * RB - 1024);
+        wpos[t] = min(pc * 1024, RI * RB - 1024);
         woff[t] = wpos[t] + lane * 16;
     }
 #pragma unroll
     for (uint32_t t = 0; t < LSMAX; t++) {
         uint32_t pc = wave + NW * t;
         if (pc >= nps) pc = wave < nps ? wave : 0;
-        spos[t] = min(pc * 256, 16 * SB - 256);
+        spos[t] = min(pc * 256, RI * SB - 256);
         soff[t] = spos[t] + lane * 4;
     }
 
@@ -1137,13 +1139,13 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     const uint8_t* iw[2] = {nullptr, nullptr};
     const uint8_t* is[2] = {nullptr, nullptr};
     auto issue = [&](uint32_t item, uint32_t slot) {
-        const uint32_t tile = item / nrb, n0 = (item - tile * nrb) * 16;
+        const uint32_t tile = item / nrb, n0 = (item - tile * nrb) * RI;
         if (tile != itile) {
             uint32_t b_, c_;
             sload_rec(A.recs + tile, b_, c_, iw, is);
             itile = tile;
         }
-        const uint32_t rows = min(16u, N - n0);
+        const uint32_t rows = min(RI, N - n0);
         const uint32_t wbytes = rows * RB, sbytes = rows * SB;
         uint8_t* dst = ring + slot * A.slot_bytes;
 #pragma unroll
@@ -1256,7 +1258,7 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     for (uint32_t i = i0; i < i1; i++) {
         const uint32_t slot = (i - i0) % NBUF;
         if (i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
-        const uint32_t tile = i / nrb, n0 = (i - tile * nrb) * 16;
+        const uint32_t tile = i / nrb, n0 = (i - tile * nrb) * RI;
         if (tile != ctile) {
             wait_vm(0);
             tile_request(tile);
@@ -1268,20 +1270,25 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
 
         // ---- contract this wave's chunks of the slot
         const uint8_t* buf = ring + slot * A.slot_bytes;
-        v4f acc[NMAT];
+        v4f acc[NMAT][NSUB];
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int j = 0; j < NSUB; j++) acc[m][j] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t q0 = 0; q0 < CH; q0 += 4) {
             if (c0 + q0 >= c1) continue;
-            v4i w[4][NMAT];
-            uint32_t sw[4][NMAT];
+            v4i w[4][NMAT][NSUB];
+            uint32_t sw[4][NMAT][NSUB];
 #pragma unroll
             for (uint32_t u = 0; u < 4; u++) {
 #pragma unroll
                 for (int m = 0; m < NMAT; m++) {
-                    w[u][m] = lds_read16(buf + m * A.w_region + rw[q0 + u]);
-                    sw[u][m] = lds_read_u8(buf + m * A.s_region + rs[q0 + u]);
+#pragma unroll
+                    for (int j = 0; j < NSUB; j++) {
+                        w[u][m][j] = lds_read16(buf + m * A.w_region + j * 16 * RB + rw[q0 + u]);
+                        sw[u][m][j] = lds_read_u8(buf + m * A.s_region + j * 16 * SB + rs[q0 + u]);
+                    }
                 }
             }
             lds_drain();
@@ -1290,17 +1297,20 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
                 if (c0 + q0 + u >= c1) continue;
 #pragma unroll
                 for (int m = 0; m < NMAT; m++) {
-                    // Operands of a drained read are opaque to the compiler;
-                    // launder them through an empty asm so their use stays
-                    // after the wait.
-                    v4i wv = w[u][m];
-                    uint32_t s8 = sw[u][m];
-                    asm volatile("" : "+v"(wv), "+v"(s8));
-                    if (!kvalid[q0 + u]) {
-                        wv = v4i{0, 0, 0, 0};
-                        s8 = 127;
+#pragma unroll
+                    for (int j = 0; j < NSUB; j++) {
+                        // Operands of a drained read are opaque to the
+                        // compiler; launder them through an empty asm so
+                        // their use stays after the wait.
+                        v4i wv = w[u][m][j];
+                        uint32_t s8 = sw[u][m][j];
+                        asm volatile("" : "+v"(wv), "+v"(s8));
+                        if (!kvalid[q0 + u]) {
+                            wv = v4i{0, 0, 0, 0};
+                            s8 = 127;
+                        }
+                        acc[m][j] = mfma_fp8_fp4(av[q0 + u], wv, sa[q0 + u], s8, acc[m][j]);
                     }
-                    acc[m] = mfma_fp8_fp4(av[q0 + u], wv, sa[q0 + u], s8, acc[m]);
                 }
             }
         }
@@ -1310,49 +1320,58 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         // nops take the accumulators as operands so they sit between the last
         // MFMA and the LDS write.
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc[m]));
+        for (int m = 0; m < NMAT; m++)
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) lds_write16(red + ((wave * NMAT + m) * 64 + lane) * 16, acc[m]);
+            for (int j = 0; j < NSUB; j++) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc[m][j]));
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int j = 0; j < NSUB; j++)
+                lds_write16(red + ((wave * NMAT * NSUB + m * NSUB + j) * 64 + lane) * 16, acc[m][j]);
         lds_drain();
         __builtin_amdgcn_s_barrier();
         if (wave >= 4) continue;
-        float t[NMAT];
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-            uint32_t v[NW];
+        for (int j = 0; j < NSUB; j++) {
+            float t[NMAT];
 #pragma unroll
-            for (int w2 = 0; w2 < NW; w2++) v[w2] = lds_read_b32(red + ((w2 * NMAT + m) * 64 + lane) * 16 + 4 * wave);
-            lds_drain();
-            float sum = 0.0f;
+            for (int m = 0; m < NMAT; m++) {
+                uint32_t v[NW];
 #pragma unroll
-            for (int w2 = 0; w2 < NW; w2++) {
-                asm volatile("" : "+v"(v[w2]));
-                sum += __uint_as_float(v[w2]);
-            }
-            t[m] = sum;
-        }
-        const uint32_t n = n0 + rr;
-        if (ovalid && n < N) {
-            if (MODE == SPAN_GATE_UP) {
-                float gv = round_bf16(t[0]);
-                float uv = round_bf16(t[NMAT - 1]);
-                if (A.limit > 0.0f) {
-                    gv = fminf(gv, A.limit);
-                    uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                for (int w2 = 0; w2 < NW; w2++)
+                    v[w2] = lds_read_b32(red + ((w2 * NMAT * NSUB + m * NSUB + j) * 64 + lane) * 16 + 4 * wave);
+                lds_drain();
+                float sum = 0.0f;
+#pragma unroll
+                for (int w2 = 0; w2 < NW; w2++) {
+                    asm volatile("" : "+v"(v[w2]));
+                    sum += __uint_as_float(v[w2]);
                 }
-                const float h = silu_fast(gv) * uv;
-                A.out16[obase + n] = (uint16_t)f32_to_bf16(h);
-            } else {
-                A.out16[obase + n] = (uint16_t)f32_to_bf16(t[0] * wr);
+                t[m] = sum;
+            }
+            const uint32_t n = n0 + j * 16 + rr;
+            if (ovalid && n < N) {
+                if (MODE == SPAN_GATE_UP) {
+                    float gv = round_bf16(t[0]);
+                    float uv = round_bf16(t[NMAT - 1]);
+                    if (A.limit > 0.0f) {
+                        gv = fminf(gv, A.limit);
+                        uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                    }
+                    const float h = silu_fast(gv) * uv;
+                    A.out16[obase + n] = (uint16_t)f32_to_bf16(h);
+                } else {
+                    A.out16[obase + n] = (uint16_t)f32_to_bf16(t[0] * wr);
+                }
             }
         }
     }
 }
 
-template <int MODE, int NMAT, int NBUF, int NW>
+template <int MODE, int NMAT, int NBUF, int NW, int NSUB>
 __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     const uint32_t N = A.N;
-    const uint32_t nrb = (N + 15) / 16;
+    const uint32_t nrb = (N + 16 * NSUB - 1) / (16 * NSUB);
     const uint32_t n_tiles = sload_u32(A.n_tiles);
     // Work split that never crosses a tile inside a block when there are at
     // least as many blocks as tiles: tile t gets q or q + 1 blocks, which
@@ -1374,36 +1393,37 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
             parts = q;
         }
         const uint32_t lo_rb = nrb * part / parts, hi_rb = nrb * (part + 1) / parts;
-        if (lo_rb < hi_rb) stream_range<MODE, NMAT, NBUF, NW>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb);
+        if (lo_rb < hi_rb) stream_range<MODE, NMAT, NBUF, NW, NSUB>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb);
     } else {
-        for (uint32_t t = b; t < n_tiles; t += G) stream_range<MODE, NMAT, NBUF, NW>(A, t * nrb, (t + 1) * nrb, nrb);
+        for (uint32_t t = b; t < n_tiles; t += G) stream_range<MODE, NMAT, NBUF, NW, NSUB>(A, t * nrb, (t + 1) * nrb, nrb);
     }
 }
 
 // Launches the streaming kernel, or returns UNSUPPORTED when the shape does
 // not fit its LDS ring or copy-count limits (the caller then uses the span
 // kernel).
-template <int MODE, int NMAT, int NBUF, int NW = 8>
+template <int MODE, int NMAT, int NBUF, int NW, int NSUB>
 nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream_t st) {
-    // 16-row spans of at least one 1 KB weight piece and one 256 B scale piece.
-    if (A.K > 4096 || A.K < 512 || A.K % 32) return NERVE_HIP_UNSUPPORTED;
-    A.w_region = 16 * (A.K / 2);
-    A.s_region = 16 * (A.K / 32);
+    constexpr uint32_t RI = 16 * NSUB;
+    // Spans of at least one 1 KB weight piece and one 256 B scale piece.
+    if (A.K > 4096 || A.K % 32 || RI * (A.K / 32) < 256) return NERVE_HIP_UNSUPPORTED;
+    A.w_region = RI * (A.K / 2);
+    A.s_region = RI * (A.K / 32);
     A.slot_bytes = NMAT * (A.w_region + A.s_region);
-    const uint32_t npw = (16 * (A.K / 2) + 1023) / 1024, nps = (16 * (A.K / 32) + 255) / 256;
+    const uint32_t npw = (A.w_region + 1023) / 1024, nps = (A.s_region + 255) / 256;
     A.lw = (npw + NW - 1) / NW;
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = NMAT * (A.lw + A.ls);
-    const size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * 64 * 16;
+    const size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
     if (lds > 160 * 1024 || A.copies_per_item * (NBUF - 1) > 63) return NERVE_HIP_UNSUPPORTED;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)mx_stream_kernel<MODE, NMAT, NBUF, NW>,
+        if (hipFuncSetAttribute((const void*)mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for mx_stream_kernel");
         attr_set = true;
     }
-    mx_stream_kernel<MODE, NMAT, NBUF, NW><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
+    mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
     return nh::check_launch("mx_stream_kernel");
 }
 
@@ -1633,12 +1653,12 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         qa.limit = ea.limit;
         if (gate_up) {
             sa.out16 = qa.out16 = static_cast<uint16_t*>(intermediates);
-            st = launch_stream<SPAN_GATE_UP, 2, 3>(qa, ctx, stream);
+            st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1>(qa, ctx, stream);
             if (st != NERVE_HIP_UNSUPPORTED) return st;
             return launch_span<SPAN_GATE_UP, 2, 1>(sa, max_tiles, stream);
         }
         sa.out16 = qa.out16 = static_cast<uint16_t*>(expert_outputs);
-        st = launch_stream<SPAN_DOWN, 1, 5>(qa, ctx, stream);
+        st = launch_stream<SPAN_DOWN, 1, 3, 8, 2>(qa, ctx, stream);
         if (st != NERVE_HIP_UNSUPPORTED) return st;
         return launch_span<SPAN_DOWN, 1, 2>(sa, max_tiles, stream);
     }

@@ -164,6 +164,8 @@ def _moe_case(E, k, B, H, I, seed):
 
 @pytest.mark.parametrize("E,k,B,H,I", [(8, 2, 4, 256, 256), (4, 4, 3, 160, 96), (32, 4, 16, 2880, 2880),
                                        (16, 1, 40, 512, 384),
+                                       # streaming kernel at a second shape (K >= 512 on both stages)
+                                       (8, 2, 6, 1024, 512), (12, 3, 9, 4096, 1024),
                                        # >= 512 routes: the LDS-staged grouped GEMM path
                                        (16, 4, 160, 512, 384), (8, 2, 300, 2880, 160), (64, 8, 70, 224, 288)])
 def test_moe_chain_parity(ctx, dev, E, k, B, H, I):

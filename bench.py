@@ -139,7 +139,7 @@ def moe_decode(args, ctx, dev):
     out["tokens_per_s"] = B / (ms * 1e-3)
     out["step_hbm_gbs"] = step_bytes / (ms * 1e-3) / 1e9
     out["step_hbm_frac"] = out["step_hbm_gbs"] / HBM_PEAK_GBS
-    out["roofline"] = {"bound": "hbm", "kernel": "mxfp4_moe_gate_up (moe_prep_kernel + mx_span_kernel<1,2,1>)",
+    out["roofline"] = {"bound": "hbm", "kernel": "mx_stream_kernel<GATE_UP> (nerve_hip_mxfp4_moe_gate_up, one launch)",
                        "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                        "traffic": None, "algorithmic_bytes_per_launch": float(np.mean(gate_up_bytes)),
                        "launch_ms": gu_ms}

@@ -273,33 +273,110 @@ struct TileArgs {
     uint32_t* n_tiles;
 };
 
+// Validity of one parameter from its (already loaded) slot word and address
+// record; the same rules as param_valid().
+__device__ __forceinline__ bool record_valid(uint32_t slot, uint32_t n_records, const uint32_t (&rec)[8],
+                                             uint64_t required, uint32_t align) {
+    if (slot == UNBOUND_SLOT || slot >= n_records) return false;
+    const uint64_t address = (uint64_t)rec[0] | ((uint64_t)rec[1] << 32);
+    const uint64_t bytes = (uint64_t)rec[2] | ((uint64_t)rec[3] << 32);
+    return address != 0 && (address & (uint64_t)(align - 1)) == 0 && bytes >= required && (rec[4] | rec[5]) != 0 &&
+           rec[6] == 1u;
+}
+
+constexpr uint32_t PREP_ROUTE_CACHE = 16384;   // compacted slots whose expert is kept in LDS
+constexpr uint16_t NO_EXPERT = 0xffffu;
+
+// Latency matters here (decode runs this once per projection), so the block
+// needs only two rounds of dependent global loads: (1) slot words of every
+// expert's parameters, the compacted route map entries and the control
+// words; (2) the address records and the route words.  Everything after that
+// is LDS work; a thread keeps its first expert's resolved pointers in
+// registers for the tile records.
 __device__ void build_tiles(const TileArgs& A) {
     __shared__ uint32_t cnt[MAX_EXPERTS];
     __shared__ uint32_t cur[MAX_EXPERTS];
     __shared__ uint32_t tst[MAX_EXPERTS];
     __shared__ uint8_t valid[MAX_EXPERTS];
+    __shared__ uint16_t rexp[PREP_ROUTE_CACHE];
     __shared__ uint32_t wave_tot[16];
     __shared__ uint32_t total;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    for (uint32_t e = tid; e < A.E; e += nt) {
+    const uint32_t cap = A.batch_width * A.k;
+    const uint32_t P = A.P;   // 4 (gate, gate scales, up, up scales) or 2 (down, down scales)
+
+    // ---- round 1: slot words of expert tid, route map entry tid, control
+    uint32_t slot[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
+    if (tid < A.E) {
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const uint32_t idx = tid * P + p;
+            if (p < P && idx < A.n_slot_words) slot[p] = A.slots[idx];
+        }
+    }
+    uint32_t rword = 0xffffffffu;
+    if (tid < cap) rword = A.frames[(uint64_t)(tid / A.k) * A.frame_words + A.data_words + tid % A.k];
+    const uint32_t c2 = A.control[2], c3 = A.control[3];
+    // ---- round 2: address records, route word
+    uint32_t rec[4][8];
+#pragma unroll
+    for (uint32_t p = 0; p < 4; p++) {
+        const bool has = slot[p] != UNBOUND_SLOT && slot[p] < A.n_records;
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? A.addr[(uint64_t)slot[p] * 8 + j] : 0u;
+    }
+    uint32_t route = 0;
+    if (rword < cap) route = A.routes[rword];
+
+    uint32_t n = c2 != 0u ? c3 : cap;
+    if (n > cap) n = cap;
+    const uint8_t* my_w[2] = {nullptr, nullptr};
+    const uint8_t* my_s[2] = {nullptr, nullptr};
+    if (tid < A.E) {
         bool ok = true;
-        for (uint32_t p = 0; p < A.P; p++) {
-            bool is_weight = (p % 2) == 0;
-            ok = ok && param_valid(A.addr, A.n_records, A.slots, A.n_slot_words, e * A.P + p,
-                                   is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u);
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            if (p >= P) continue;
+            const bool is_weight = (p % 2) == 0;
+            ok = record_valid(slot[p], A.n_records, rec[p], is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u) && ok;
+        }
+        valid[tid] = ok ? 1 : 0;
+        cnt[tid] = 0;
+#pragma unroll
+        for (uint32_t m = 0; m < 2; m++) {
+            if (2 * m >= P) continue;
+            my_w[m] = reinterpret_cast<const uint8_t*>((uint64_t)rec[2 * m][0] | ((uint64_t)rec[2 * m][1] << 32));
+            my_s[m] = reinterpret_cast<const uint8_t*>((uint64_t)rec[2 * m + 1][0] | ((uint64_t)rec[2 * m + 1][1] << 32));
+        }
+    }
+    // Experts beyond the block size (E > 1024) take the plain path.
+    for (uint32_t e = tid + nt; e < A.E; e += nt) {
+        bool ok = true;
+        for (uint32_t p = 0; p < P; p++) {
+            const bool is_weight = (p % 2) == 0;
+            ok = param_valid(A.addr, A.n_records, A.slots, A.n_slot_words, e * P + p, is_weight ? A.req_w : A.req_s,
+                             is_weight ? 16u : 4u) && ok;
         }
         valid[e] = ok ? 1 : 0;
         cnt[e] = 0;
     }
     __syncthreads();
-    const uint32_t cap = A.batch_width * A.k;
-    uint32_t n = A.control[2] != 0u ? A.control[3] : cap;
-    if (n > cap) n = cap;
-    for (uint32_t c = tid; c < n; c += nt) {
-        uint32_t r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-        if (r >= cap) continue;
-        uint32_t e = A.routes[r] & 0xffffu;
-        if (e < A.E && valid[e]) atomicAdd(&cnt[e], 1u);
+    // Expert of every compacted slot c < n (NO_EXPERT when invalid).
+    auto slot_expert = [&](uint32_t c, uint32_t rw, uint32_t rt) -> uint32_t {
+        if (c >= n || rw >= cap) return NO_EXPERT;
+        const uint32_t e = rt & 0xffffu;
+        return (e < A.E && valid[e]) ? e : NO_EXPERT;
+    };
+    if (tid < cap) {
+        const uint32_t e = slot_expert(tid, rword, route);
+        if (tid < PREP_ROUTE_CACHE) rexp[tid] = (uint16_t)e;
+        if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
+    }
+    for (uint32_t c = tid + nt; c < cap; c += nt) {
+        const uint32_t rw = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+        const uint32_t e = slot_expert(c, rw, rw < cap ? A.routes[rw] : 0u);
+        if (c < PREP_ROUTE_CACHE) rexp[c] = (uint16_t)e;
+        if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
     }
     __syncthreads();
     // Exclusive scans of route counts and tile counts over experts.
@@ -321,31 +398,41 @@ __device__ void build_tiles(const TileArgs& A) {
     }
     __syncthreads();
     for (uint32_t e = tid; e < A.E; e += nt) {
-        uint32_t nte = (cnt[e] + A.TM - 1) / A.TM;
+        const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM;
         for (uint32_t t = 0; t < nte; t++) {
-            uint32_t idx = tst[e] + t;
+            const uint32_t idx = tst[e] + t;
             if (idx < A.max_tiles) {
-                TileRec rec;
-                rec.expert = e;
-                rec.begin = cur[e] + t * A.TM;
-                rec.count = min(A.TM, cnt[e] - t * A.TM);
-                rec.pad = 0;
+                TileRec rec_out;
+                rec_out.expert = e;
+                rec_out.begin = cur[e] + t * A.TM;
+                rec_out.count = min(A.TM, cnt[e] - t * A.TM);
+                rec_out.pad = 0;
                 for (uint32_t m = 0; m < 2; m++) {
-                    const bool has = 2 * m < A.P;
-                    rec.w[m] = has ? param_ptr(A.addr, A.slots, e * A.P + 2 * m) : nullptr;
-                    rec.s[m] = has ? param_ptr(A.addr, A.slots, e * A.P + 2 * m + 1) : nullptr;
+                    const bool has = 2 * m < P;
+                    if (e == tid) {
+                        rec_out.w[m] = my_w[m];
+                        rec_out.s[m] = my_s[m];
+                    } else {
+                        rec_out.w[m] = has ? param_ptr(A.addr, A.slots, e * P + 2 * m) : nullptr;
+                        rec_out.s[m] = has ? param_ptr(A.addr, A.slots, e * P + 2 * m + 1) : nullptr;
+                    }
                 }
-                A.recs[idx] = rec;
+                A.recs[idx] = rec_out;
             }
         }
     }
     __syncthreads();
     for (uint32_t c = tid; c < n; c += nt) {
-        uint32_t r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-        if (r >= cap) continue;
-        uint32_t e = A.routes[r] & 0xffffu;
-        if (e < A.E && valid[e]) {
-            uint32_t pos = atomicAdd(&cur[e], 1u);
+        uint32_t e, r;
+        if (c < PREP_ROUTE_CACHE && c == tid) {
+            e = rexp[c];
+            r = rword;
+        } else {
+            r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+            e = c < PREP_ROUTE_CACHE ? rexp[c] : slot_expert(c, r, r < cap ? A.routes[r] : 0u);
+        }
+        if (e != NO_EXPERT) {
+            const uint32_t pos = atomicAdd(&cur[e], 1u);
             A.seg_list[pos] = r;
         }
     }
@@ -1026,6 +1113,22 @@ struct StreamArgs {
     uint32_t w_region, s_region, slot_bytes;   // LDS layout of one ring slot
     uint32_t lw, ls;                            // copies per wave per matrix (weights, scales)
     uint32_t copies_per_item;                   // per wave: NMAT * (lw + ls)
+    // Fused set-up (no preparation launch): the route map and parameter
+    // tables the block reads itself, and bf16 activation rows quantized in
+    // registers.  Activation row of route r: x16 + (r / k) * x_frame + (r % k) * x_seg.
+    TileArgs T;
+    const uint16_t* x16;
+    uint64_t x_frame, x_seg;
+};
+
+// One tile as the streaming loop sees it: its parameter pointers, its route
+// count, and per lane the route whose activations it loads (row rr) and the
+// route whose output it writes (token 4 g + wave), with that route's word.
+struct TileSrc {
+    const uint8_t* w[2];
+    const uint8_t* s[2];
+    uint32_t count;
+    uint32_t in_route, out_route, out_word;
 };
 
 __device__ __forceinline__ uint32_t lds_read_u8(const uint8_t* p) {
@@ -1092,11 +1195,12 @@ __device__ __forceinline__ uint32_t sload_u32(const uint32_t* p) {
     return v;
 }
 
-// One contiguous range of work items [i0, i1) of a single tile, run by NW
-// waves that split each item's K chunks.  An item is RI = 16 NSUB rows of
-// each of the NMAT matrices.
-template <int MODE, int NMAT, int NBUF, int NW, int NSUB>
-__device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, uint32_t i1, uint32_t nrb) {
+// One contiguous range of work items [i0, i1) of one tile, run by NW waves
+// that split each item's K chunks.  An item is RI = 16 NSUB rows of each of
+// the NMAT matrices.
+template <int MODE, int NMAT, int NBUF, int NW, int NSUB, bool FUSED>
+__device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, uint32_t i1, uint32_t nrb,
+                                             const TileSrc& ts) {
     constexpr uint32_t RI = 16 * NSUB;
     constexpr uint32_t CH = 32 / NW;                            // max K chunks per wave (K <= 4096)
     constexpr uint32_t LWMAX = (32 * NSUB + NW - 1) / NW;       // max weight copies per wave per matrix
@@ -1135,28 +1239,21 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     }
 
     // ---- issue side: copies of item `item` into ring slot `slot`
-    uint32_t itile = 0xffffffffu;
-    const uint8_t* iw[2] = {nullptr, nullptr};
-    const uint8_t* is[2] = {nullptr, nullptr};
+    const uint32_t tile_base = (i0 / nrb) * nrb;
     auto issue = [&](uint32_t item, uint32_t slot) {
-        const uint32_t tile = item / nrb, n0 = (item - tile * nrb) * RI;
-        if (tile != itile) {
-            uint32_t b_, c_;
-            sload_rec(A.recs + tile, b_, c_, iw, is);
-            itile = tile;
-        }
+        const uint32_t n0 = (item - tile_base) * RI;
         const uint32_t rows = min(RI, N - n0);
         const uint32_t wbytes = rows * RB, sbytes = rows * SB;
         uint8_t* dst = ring + slot * A.slot_bytes;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            const uint8_t* ws = iw[m] + (uint64_t)n0 * RB;
+            const uint8_t* ws = ts.w[m] + (uint64_t)n0 * RB;
 #pragma unroll
             for (uint32_t t = 0; t < LWMAX; t++)
                 if (t < lw)
                     __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? woff[t] : 0),
                                                      dst + m * A.w_region + wpos[t], 16, 0, 0);
-            const uint8_t* ss = is[m] + (uint64_t)n0 * SB;
+            const uint8_t* ss = ts.s[m] + (uint64_t)n0 * SB;
 #pragma unroll
             for (uint32_t t = 0; t < LSMAX; t++)
                 if (t < ls)
@@ -1165,7 +1262,7 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         }
     };
 
-    // ---- compute side: this wave's K chunks, their LDS offsets, the tile
+    // ---- compute side: this wave's K chunks and their LDS offsets
     const uint32_t per = (nch + NW - 1) / NW;
     const uint32_t c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
     uint32_t rw[CH], rs[CH];
@@ -1178,96 +1275,139 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         rw[q] = rr * RB + kk / 2;
         rs[q] = NMAT * A.w_region + rr * SB + kk / 32;
     }
-    uint32_t ctile = 0xffffffffu;
+
+    // ---- activations of the tile.  Loads are issued after the prologue
+    // copies and converted after one wait (the empty asm in the conversion
+    // keeps the compiler from folding it into the loads' branches, which
+    // would wait for each load there).
+    const bool arow_ok = rr < ts.count;
+    const bool ovalid = wave < 4 && 4 * g + wave < ts.count;
     v8i av[CH];
     uint32_t sa[CH];
-    uint64_t obase = 0;        // output element offset of this lane's token (component `wave`)
-    float wr = 0.0f;
-    bool ovalid = false;
-
-    // Tile set-up in two halves.  tile_request() reads the tile record and its
-    // 16 route entries through the scalar cache, then issues this lane's
-    // activation and route loads without waiting; tile_finish() converts them
-    // after the caller's vmcnt wait.
-    v4i lo[CH], hi[CH];
+    v4i lo[CH], hi[CH];          // e4m3 operand halves (pre-quantized input)
     float sraw[CH];
-    uint32_t wraw = 0;
-    bool arow_ok = false;
-    auto tile_request = [&](uint32_t tile) {
-        uint32_t begin, cnt;
-        const uint8_t* w_[2];
-        const uint8_t* s_[2];
-        sload_rec(A.recs + tile, begin, cnt, w_, s_);
-        u16s seg = sload_x16(A.seg_list + begin);
-        const uint32_t tl = 4 * g + wave;
-        uint32_t my_row = 0, my_out = 0;
+    v4i xb[CH][4];               // bf16 operand halves (fused quantization)
+    auto act_request = [&]() {
+        if (FUSED) {
+            const uint16_t* xr = A.x16 + (uint64_t)(ts.in_route / A.k) * A.x_frame + (uint64_t)(ts.in_route % A.k) * A.x_seg;
 #pragma unroll
-        for (uint32_t q = 0; q < 16; q++) {
-            if (rr == q) my_row = seg[q];
-            if (tl == q) my_out = seg[q];
-        }
-        arow_ok = rr < cnt;
-        const uint8_t* arow = A.aq + (uint64_t)(arow_ok ? my_row / A.a_row_div : 0) * K;
-        const float* ascale = A.as + (uint64_t)(arow_ok ? my_row / A.a_row_div : 0) * nch;
+            for (uint32_t q = 0; q < CH; q++) {
+                const uint32_t c = c0 + q, k0 = c * 128 + g * 16;
 #pragma unroll
-        for (uint32_t q = 0; q < CH; q++) {
-            const uint32_t c = c0 + q, k0 = c * 128 + g * 16;
-            lo[q] = hi[q] = v4i{0, 0, 0, 0};
-            sraw[q] = 1.0f;
-            if (arow_ok && c < c1) {
-                if (k0 < K) lo[q] = *reinterpret_cast<const v4i*>(arow + k0);
-                if (k0 + 64 < K) hi[q] = *reinterpret_cast<const v4i*>(arow + k0 + 64);
-                sraw[q] = ascale[c];
+                for (int h = 0; h < 4; h++) xb[q][h] = v4i{0, 0, 0, 0};
+                if (arow_ok && c < c1) {
+                    if (k0 < K) {
+                        xb[q][0] = *reinterpret_cast<const v4i*>(xr + k0);
+                        xb[q][1] = *reinterpret_cast<const v4i*>(xr + k0 + 8);
+                    }
+                    if (k0 + 64 < K) {
+                        xb[q][2] = *reinterpret_cast<const v4i*>(xr + k0 + 64);
+                        xb[q][3] = *reinterpret_cast<const v4i*>(xr + k0 + 72);
+                    }
+                }
+            }
+        } else {
+            const uint32_t row = ts.in_route / A.a_row_div;
+            const uint8_t* arow = A.aq + (uint64_t)(arow_ok ? row : 0) * K;
+            const float* ascale = A.as + (uint64_t)(arow_ok ? row : 0) * nch;
+#pragma unroll
+            for (uint32_t q = 0; q < CH; q++) {
+                const uint32_t c = c0 + q, k0 = c * 128 + g * 16;
+                lo[q] = hi[q] = v4i{0, 0, 0, 0};
+                sraw[q] = 1.0f;
+                if (arow_ok && c < c1) {
+                    if (k0 < K) lo[q] = *reinterpret_cast<const v4i*>(arow + k0);
+                    if (k0 + 64 < K) hi[q] = *reinterpret_cast<const v4i*>(arow + k0 + 64);
+                    sraw[q] = ascale[c];
+                }
             }
         }
-        ovalid = wave < 4 && tl < cnt;
-        if (ovalid) {
-            if (MODE == SPAN_GATE_UP) {
-                obase = (uint64_t)(my_out / A.k) * A.frame_elems + (uint64_t)(my_out % A.k) * N;
-            } else {
-                obase = (uint64_t)my_out * N;
-                wraw = A.routes[my_out];
+    };
+    auto act_finish = [&]() {
+        if (FUSED) {
+            // Blockwise e4m3 quantization of this lane's 32 values of each
+            // 128-column block (the same arithmetic as quant_unit: pow2
+            // scale of the block amax, x / scale rounded to e4m3).  The four
+            // lanes of a row (g = 0..3) hold the block's 128 columns.
+#pragma unroll
+            for (uint32_t q = 0; q < CH; q++) {
+#pragma unroll
+                for (int h = 0; h < 4; h++) asm volatile("" : "+v"(xb[q][h]));
+                float v[32];
+#pragma unroll
+                for (int h = 0; h < 4; h++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t w = (uint32_t)xb[q][h][j];
+                        v[h * 8 + 2 * j] = bf16_to_f32((uint16_t)(w & 0xFFFFu));
+                        v[h * 8 + 2 * j + 1] = bf16_to_f32((uint16_t)(w >> 16));
+                    }
+                float m = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(v[j]));
+                m = fmaxf(m, __shfl_xor(m, 16));
+                m = fmaxf(m, __shfl_xor(m, 32));
+                const float sc = pow2_fp8_scale(m);
+                uint32_t pk[8];
+                // sc is a power of two, so v * (1 / sc) equals v / sc.  For a
+                // finite block max every quotient lies in [-448, 448], where
+                // v_cvt_pk_fp8_f32 rounds exactly like f32_to_e4m3; a NaN
+                // input (its code 0x7f / 0xff) or an infinite max takes the
+                // software conversion instead.
+                bool soft = !(m <= 3.4028235e38f);
+                if (!soft) {
+                    const float inv = __uint_as_float((254u << 23) - __float_as_uint(sc));
+                    uint32_t nan_bytes = 0;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j] * inv, v[4 * j + 1] * inv, 0, false);
+                        w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j + 2] * inv, v[4 * j + 3] * inv, w, true);
+                        pk[j] = (uint32_t)w;
+                        nan_bytes |= ((pk[j] & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+                    }
+                    soft = nan_bytes != 0;
+                }
+                if (soft) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        pk[j] = f32_to_e4m3(v[4 * j] / sc) | (f32_to_e4m3(v[4 * j + 1] / sc) << 8) |
+                                (f32_to_e4m3(v[4 * j + 2] / sc) << 16) | (f32_to_e4m3(v[4 * j + 3] / sc) << 24);
+                }
+                av[q] = v8i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3], (int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]};
+                sa[q] = arow_ok ? pow2_to_e8m0(sc) : 127u;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t q = 0; q < CH; q++) asm volatile("" : "+v"(lo[q]), "+v"(hi[q]), "+v"(sraw[q]));
+#pragma unroll
+            for (uint32_t q = 0; q < CH; q++) {
+                av[q] = v8i{lo[q].x, lo[q].y, lo[q].z, lo[q].w, hi[q].x, hi[q].y, hi[q].z, hi[q].w};
+                sa[q] = arow_ok ? pow2_to_e8m0(sraw[q]) : 127u;
             }
         }
-        ctile = tile;
     };
-    auto tile_finish = [&]() {
-        // The empty asm pins every use of the loaded values after the
-        // caller's wait (the compiler would otherwise fold the conversions
-        // into the loads' branches and wait for each load there).
-#pragma unroll
-        for (uint32_t q = 0; q < CH; q++) asm volatile("" : "+v"(lo[q]), "+v"(hi[q]), "+v"(sraw[q]));
-        asm volatile("" : "+v"(wraw));
-#pragma unroll
-        for (uint32_t q = 0; q < CH; q++) {
-            av[q] = v8i{lo[q].x, lo[q].y, lo[q].z, lo[q].w, hi[q].x, hi[q].y, hi[q].z, hi[q].w};
-            sa[q] = arow_ok ? pow2_to_e8m0(sraw[q]) : 127u;
-        }
-        wr = bf16_to_f32(wraw >> 16);
-    };
+    uint64_t obase = 0;        // output element offset of this lane's token (component `wave`)
+    if (MODE == SPAN_GATE_UP)
+        obase = (uint64_t)(ts.out_route / A.k) * A.frame_elems + (uint64_t)(ts.out_route % A.k) * N;
+    else
+        obase = (uint64_t)ts.out_route * N;
+    const float wr = bf16_to_f32(ts.out_word >> 16);
 
-    // Prologue: the first items' copies, then the first tile's operands; one
+    // Prologue: the first items' copies, then the tile's activations; one
     // wait covers both round trips.
 #pragma unroll
     for (uint32_t j = 0; j < NBUF - 1; j++)
         if (i0 + j < i1) issue(i0 + j, j);
-    tile_request(i0 / nrb);
+    act_request();
     wait_vm(0);
-    tile_finish();
+    act_finish();
 
     for (uint32_t i = i0; i < i1; i++) {
         const uint32_t slot = (i - i0) % NBUF;
         if (i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
-        const uint32_t tile = i / nrb, n0 = (i - tile * nrb) * RI;
-        if (tile != ctile) {
-            wait_vm(0);
-            tile_request(tile);
-            wait_vm(0);
-            tile_finish();
-        }
+        const uint32_t n0 = (i - tile_base) * RI;
         wait_vm(A.copies_per_item * min((uint32_t)(NBUF - 1), i1 - 1 - i));
         __builtin_amdgcn_s_barrier();
-
         // ---- contract this wave's chunks of the slot
         const uint8_t* buf = ring + slot * A.slot_bytes;
         v4f acc[NMAT][NSUB];
@@ -1368,11 +1508,185 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     }
 }
 
-template <int MODE, int NMAT, int NBUF, int NW, int NSUB>
+// Fused set-up tables (in the LDS ring, before any copy is issued).
+constexpr uint32_t FUSED_MAX_EXPERTS = 1024;
+constexpr uint32_t FUSED_MAX_SLOTS = 1024;
+
+struct FusedTables {
+    uint32_t cnt[FUSED_MAX_EXPERTS];      // valid routes per expert
+    uint32_t tst[FUSED_MAX_EXPERTS];      // first tile of each expert
+    uint32_t rw[FUSED_MAX_SLOTS];         // route index of compacted slot c
+    uint32_t rword[FUSED_MAX_SLOTS];      // its route word
+    uint16_t eslot[FUSED_MAX_SLOTS];      // its expert (NO_EXPERT: skipped)
+    uint8_t valid[FUSED_MAX_EXPERTS];
+    uint32_t list[16];                    // slots of the tile being set up
+    uint64_t ptr[4];
+    uint32_t wave_tot[16];
+    uint32_t total, n_tiles, tile_e, tile_k;
+};
+
+// Route -> tile tables of one projection, built by every streaming block for
+// itself (the same rules as build_tiles: invalid parameters or expert ids
+// skip a route; 16 routes per tile in slot order).  Two rounds of dependent
+// global loads, then LDS work.  Thread e keeps expert e's resolved pointers.
+template <int NW>
+__device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, const uint8_t* (&my_ptr)[4]) {
+    const uint32_t tid = threadIdx.x, nt = 64 * NW;
+    const uint32_t cap = A.batch_width * A.k, P = A.P;
+    // Round 1: slot words of expert tid, route map entry tid, control words.
+    uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
+#pragma unroll
+    for (uint32_t p = 0; p < 4; p++) {
+        const uint32_t idx = tid * P + p;
+        if (tid < A.E && p < P && idx < A.n_slot_words) sl[p] = A.slots[idx];
+    }
+    const uint32_t r0 = tid < cap ? A.frames[(uint64_t)(tid / A.k) * A.frame_words + A.data_words + tid % A.k] : 0u;
+    const uint32_t c2 = A.control[2], c3 = A.control[3];
+    // Round 2: address records, route word.
+    uint32_t rec[4][8];
+#pragma unroll
+    for (uint32_t p = 0; p < 4; p++) {
+        const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? A.addr[(uint64_t)sl[p] * 8 + j] : 0u;
+    }
+    const uint32_t w0 = (tid < cap && r0 < cap) ? A.routes[r0] : 0u;
+    if (tid < A.E) {
+        bool ok = true;
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            if (p >= P) continue;
+            const bool is_weight = (p % 2) == 0;
+            ok = record_valid(sl[p], A.n_records, rec[p], is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u) && ok;
+        }
+        F.valid[tid] = ok ? 1 : 0;
+        F.cnt[tid] = 0;
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++)
+            my_ptr[p] = reinterpret_cast<const uint8_t*>((uint64_t)rec[p][0] | ((uint64_t)rec[p][1] << 32));
+    }
+    if (tid < cap) {
+        F.rw[tid] = r0;
+        F.rword[tid] = w0;
+    }
+    // Experts and slots beyond one per thread take the plain path.
+    for (uint32_t e = tid + nt; e < A.E; e += nt) {
+        bool ok = true;
+        for (uint32_t p = 0; p < P; p++) {
+            const bool is_weight = (p % 2) == 0;
+            ok = param_valid(A.addr, A.n_records, A.slots, A.n_slot_words, e * P + p, is_weight ? A.req_w : A.req_s,
+                             is_weight ? 16u : 4u) && ok;
+        }
+        F.valid[e] = ok ? 1 : 0;
+        F.cnt[e] = 0;
+    }
+    uint32_t n = c2 != 0u ? c3 : cap;
+    if (n > cap) n = cap;
+    for (uint32_t c = tid + nt; c < cap; c += nt) {
+        const uint32_t r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+        F.rw[c] = r;
+        F.rword[c] = r < cap ? A.routes[r] : 0u;
+    }
+    __syncthreads();
+    for (uint32_t c = tid; c < cap; c += nt) {
+        const uint32_t r = F.rw[c], e = F.rword[c] & 0xffffu;
+        const bool ok = c < n && r < cap && e < A.E && F.valid[e];
+        F.eslot[c] = ok ? (uint16_t)e : NO_EXPERT;
+        if (ok) atomicAdd(&F.cnt[e], 1u);
+    }
+    __syncthreads();
+    const uint32_t per = (A.E + nt - 1) / nt;
+    const uint32_t e0 = min(A.E, tid * per), e1 = min(A.E, e0 + per);
+    uint32_t lt = 0;
+    for (uint32_t e = e0; e < e1; e++) lt += (F.cnt[e] + 15) / 16;
+    uint32_t ot = block_exclusive_scan(lt, F.wave_tot, &F.total);
+    for (uint32_t e = e0; e < e1; e++) {
+        F.tst[e] = ot;
+        ot += (F.cnt[e] + 15) / 16;
+    }
+    if (tid == 0) F.n_tiles = F.total;
+    __syncthreads();
+}
+
+// Tile `t` of the fused tables: its expert's pointers, its routes and this
+// lane's route ids.
+template <int NW>
+__device__ __forceinline__ TileSrc fused_tile(const StreamArgs& A, FusedTables& F, const uint8_t* const (&my_ptr)[4], uint32_t t) {
+    const TileArgs& T = A.T;
+    const uint32_t tid = threadIdx.x, nt = 64 * NW;
+    const uint32_t cap = T.batch_width * T.k;
+    for (uint32_t e = tid; e < T.E; e += nt) {
+        const uint32_t nte = (F.cnt[e] + 15) / 16;
+        if (t >= F.tst[e] && t < F.tst[e] + nte) {
+            F.tile_e = e;
+            F.tile_k = t - F.tst[e];
+#pragma unroll
+            for (uint32_t p = 0; p < 4; p++)
+                F.ptr[p] = e == tid ? (uint64_t)my_ptr[p]
+                                    : (p < T.P ? (uint64_t)param_ptr(T.addr, T.slots, e * T.P + p) : 0ull);
+        }
+    }
+    __syncthreads();
+    const uint32_t e = F.tile_e, kk = F.tile_k;
+    // Rank of each slot among the expert's slots (slot order), block-wide;
+    // the host launches the fused form only when every slot has a thread.
+    {
+        const uint32_t c = tid;
+        const uint32_t f = (c < cap && F.eslot[c] == e) ? 1u : 0u;
+        const uint32_t rank = block_exclusive_scan(f, F.wave_tot, &F.total);
+        if (f && rank >= 16 * kk && rank < 16 * kk + 16) F.list[rank - 16 * kk] = c;
+    }
+    __syncthreads();
+    TileSrc ts;
+    ts.w[0] = reinterpret_cast<const uint8_t*>(F.ptr[0]);
+    ts.s[0] = reinterpret_cast<const uint8_t*>(F.ptr[1]);
+    ts.w[1] = reinterpret_cast<const uint8_t*>(F.ptr[2]);
+    ts.s[1] = reinterpret_cast<const uint8_t*>(F.ptr[3]);
+    ts.count = min(16u, F.cnt[e] - 16 * kk);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t rr = lane & 15, tl = 4 * (lane >> 4) + wave;
+    ts.in_route = rr < ts.count ? F.rw[F.list[rr]] : 0u;
+    const bool ov = wave < 4 && tl < ts.count;
+    ts.out_route = ov ? F.rw[F.list[tl]] : 0u;
+    ts.out_word = ov ? F.rword[F.list[tl]] : 0u;
+    __syncthreads();
+    return ts;
+}
+
+template <int MODE, int NMAT, int NBUF, int NW, int NSUB, bool FUSED>
 __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     const uint32_t N = A.N;
     const uint32_t nrb = (N + 16 * NSUB - 1) / (16 * NSUB);
-    const uint32_t n_tiles = sload_u32(A.n_tiles);
+    FusedTables& F = *reinterpret_cast<FusedTables*>(ring);
+    const uint8_t* my_ptr[4] = {nullptr, nullptr, nullptr, nullptr};
+    uint32_t n_tiles;
+    if (FUSED) {
+        fused_tables<NW>(A.T, F, my_ptr);
+        n_tiles = F.n_tiles;
+    } else {
+        n_tiles = sload_u32(A.n_tiles);
+    }
+    auto tile_src = [&](uint32_t t) -> TileSrc {
+        if (FUSED) return fused_tile<NW>(A, F, my_ptr, t);
+        TileSrc ts;
+        uint32_t begin, cnt;
+        sload_rec(A.recs + t, begin, cnt, ts.w, ts.s);
+        const u16s seg = sload_x16(A.seg_list + begin);
+        const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const uint32_t rr = lane & 15, tl = 4 * (lane >> 4) + wave;
+        uint32_t in_r = 0, out_r = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 16; q++) {
+            if (rr == q) in_r = seg[q];
+            if (tl == q) out_r = seg[q];
+        }
+        ts.count = cnt;
+        ts.in_route = in_r;
+        ts.out_route = out_r;
+        ts.out_word = (MODE == SPAN_DOWN && wave < 4 && tl < cnt) ? A.routes[out_r] : 0u;
+        return ts;
+    };
     // Work split that never crosses a tile inside a block when there are at
     // least as many blocks as tiles: tile t gets q or q + 1 blocks, which
     // split its row blocks evenly.  With fewer blocks than tiles a block
@@ -1393,16 +1707,23 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
             parts = q;
         }
         const uint32_t lo_rb = nrb * part / parts, hi_rb = nrb * (part + 1) / parts;
-        if (lo_rb < hi_rb) stream_range<MODE, NMAT, NBUF, NW, NSUB>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb);
+        if (lo_rb >= hi_rb) return;
+        const TileSrc ts = tile_src(tile);
+        stream_range<MODE, NMAT, NBUF, NW, NSUB, FUSED>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb, ts);
     } else {
-        for (uint32_t t = b; t < n_tiles; t += G) stream_range<MODE, NMAT, NBUF, NW, NSUB>(A, t * nrb, (t + 1) * nrb, nrb);
+        for (uint32_t t = b; t < n_tiles; t += G) {
+            // The tables share LDS with the ring: rebuild them after a range.
+            if (FUSED && t != b) fused_tables<NW>(A.T, F, my_ptr);
+            const TileSrc ts = tile_src(t);
+            stream_range<MODE, NMAT, NBUF, NW, NSUB, FUSED>(A, t * nrb, (t + 1) * nrb, nrb, ts);
+        }
     }
 }
 
 // Launches the streaming kernel, or returns UNSUPPORTED when the shape does
 // not fit its LDS ring or copy-count limits (the caller then uses the span
 // kernel).
-template <int MODE, int NMAT, int NBUF, int NW, int NSUB>
+template <int MODE, int NMAT, int NBUF, int NW, int NSUB, bool FUSED>
 nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream_t st) {
     constexpr uint32_t RI = 16 * NSUB;
     // Spans of at least one 1 KB weight piece and one 256 B scale piece.
@@ -1414,16 +1735,25 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.lw = (npw + NW - 1) / NW;
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = NMAT * (A.lw + A.ls);
-    const size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
+    size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
+    if (FUSED && lds < sizeof(FusedTables)) lds = sizeof(FusedTables);
     if (lds > 160 * 1024 || A.copies_per_item * (NBUF - 1) > 63) return NERVE_HIP_UNSUPPORTED;
+    if (FUSED) {
+        // Every compacted slot needs a thread in the tables, and activation
+        // rows are read in 16-byte pieces.
+        const uint32_t cap = A.T.batch_width * A.T.k;
+        if (cap > 64 * NW || cap > FUSED_MAX_SLOTS || A.T.E > FUSED_MAX_EXPERTS || A.T.P > 4 ||
+            ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || A.x_seg % 8)
+            return NERVE_HIP_UNSUPPORTED;
+    }
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB>,
+        if (hipFuncSetAttribute((const void*)mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB, FUSED>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for mx_stream_kernel");
         attr_set = true;
     }
-    mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
+    mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB, FUSED><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
     return nh::check_launch("mx_stream_kernel");
 }
 
@@ -1583,6 +1913,33 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.seg_list = reinterpret_cast<uint32_t*>(base + o_seg);
     ta.recs = reinterpret_cast<TileRec*>(base + o_rec);
     ta.n_tiles = reinterpret_cast<uint32_t*>(base + o_nt);
+    // Decode-shaped batches: one streaming launch that builds its own tiles
+    // and quantizes its own activation chunks (no preparation launch).
+    if (!grouped && !(gate_up && ms.prequant)) {
+        StreamArgs fa{};
+        fa.K = K;
+        fa.N = N;
+        fa.k = k;
+        fa.a_row_div = gate_up ? k : 1;
+        fa.routes = ta.routes;
+        fa.frame_elems = frame_words * 2;
+        fa.limit = ms.limit;
+        fa.T = ta;
+        if (gate_up) {
+            fa.x16 = static_cast<const uint16_t*>(act_bf16);
+            fa.x_frame = H;
+            fa.x_seg = 0;
+            fa.out16 = static_cast<uint16_t*>(intermediates);
+            st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1, true>(fa, ctx, stream);
+        } else {
+            fa.x16 = frames16;
+            fa.x_frame = frame_words * 2;
+            fa.x_seg = I;
+            fa.out16 = static_cast<uint16_t*>(expert_outputs);
+            st = launch_stream<SPAN_DOWN, 1, 3, 8, 2, true>(fa, ctx, stream);
+        }
+        if (st != NERVE_HIP_UNSUPPORTED) return st;
+    }
     const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
     moe_prep_kernel<<<1 + (uint32_t)((units + 31) / 32), 1024, 0, stream>>>(ta, Q);
     if ((st = nh::check_launch("moe_prep"))) return st;
@@ -1653,12 +2010,12 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         qa.limit = ea.limit;
         if (gate_up) {
             sa.out16 = qa.out16 = static_cast<uint16_t*>(intermediates);
-            st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1>(qa, ctx, stream);
+            st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1, false>(qa, ctx, stream);
             if (st != NERVE_HIP_UNSUPPORTED) return st;
             return launch_span<SPAN_GATE_UP, 2, 1>(sa, max_tiles, stream);
         }
         sa.out16 = qa.out16 = static_cast<uint16_t*>(expert_outputs);
-        st = launch_stream<SPAN_DOWN, 1, 3, 8, 2>(qa, ctx, stream);
+        st = launch_stream<SPAN_DOWN, 1, 3, 8, 2, false>(qa, ctx, stream);
         if (st != NERVE_HIP_UNSUPPORTED) return st;
         return launch_span<SPAN_DOWN, 1, 2>(sa, max_tiles, stream);
     }

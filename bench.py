@@ -40,7 +40,9 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="moe_decode",
-                   choices=["moe_decode", "moe_prefill", "mxfp4_gemv", "int4_gemv", "fp8_head"])
+                   choices=["moe_decode", "moe_prefill", "mxfp4_gemv", "int4_gemv", "fp8_head", "hbm_copy"])
+    p.add_argument("--summarize-traffic", nargs=4, metavar="DIR",
+                   help="FETCH_SIZE and WRITE_SIZE rocprofv3 CSV dirs of a run, then of the hbm_copy run")
     p.add_argument("--m", type=int, default=1, help="batch rows for int4_gemv / fp8_head")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
@@ -69,6 +71,36 @@ def event_ms(fn, n, stream):
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     return float(np.median([a.elapsed_time(b) for a, b in ev]))
+
+
+def batch_event_ms(fn, n, stream, warmup=5):
+    """Average duration (ms) of fn() over n back-to-back calls between one
+    pair of HIP events on `stream` (launch latency overlaps the previous
+    call, as it does inside a model step)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(n):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return float(a.elapsed_time(b)) / n
+
+
+def traffic_for(kernel_key):
+    """HBM bytes per launch of `kernel_key` from profiles/traffic.json (two
+    rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, each scaled by what the
+    counter reads for a copy of known size; see --summarize-traffic), or None."""
+    path = os.path.join(HERE, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return float(t["kernels"][kernel_key]["hbm_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def wall_ms(fn, steps, warmup):
@@ -131,7 +163,7 @@ def moe_decode(args, ctx, dev):
                               L.bank.gate_slots, b["control"], B, stream)
 
     # routes / maps of both layers are in their own buffers already
-    gu_ms = event_ms(gate_up, max(100, args.steps), stream)
+    gu_ms = batch_event_ms(gate_up, max(100, args.steps), stream)
     achieved = float(np.mean(gate_up_bytes)) / (gu_ms * 1e-3) / 1e9
     out = base_line(args, B * k / (ms * 1e-3), "expert-tokens/s", ms, "e4m3xe2m1->f32",
                     {"workload": "moe_decode_e32_k4_h2880_i2880_b16", "experts": E, "top_k": k, "hidden": H,
@@ -141,8 +173,8 @@ def moe_decode(args, ctx, dev):
     out["step_hbm_frac"] = out["step_hbm_gbs"] / HBM_PEAK_GBS
     out["roofline"] = {"bound": "hbm", "kernel": "mx_stream_kernel<GATE_UP> (nerve_hip_mxfp4_moe_gate_up, one launch)",
                        "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                       "traffic": None, "algorithmic_bytes_per_launch": float(np.mean(gate_up_bytes)),
-                       "launch_ms": gu_ms}
+                       "traffic": traffic_for("mx_stream_kernel<1, 2, 3, 8, 1, true>"),
+                       "algorithmic_bytes_per_launch": float(np.mean(gate_up_bytes)), "launch_ms": gu_ms}
     return out, data[0]
 
 
@@ -233,7 +265,7 @@ def mxfp4_gemv(args, ctx, dev):
     stream = torch.cuda.current_stream()
     fn = lambda i: ctx.mxfp4_gemv(q, s, 1, K, W[i % copies], S[i % copies], N, y, stream)
     ms = wall_ms(fn, args.steps, args.warmup)
-    kms = event_ms(fn, max(200, args.steps), stream)
+    kms = batch_event_ms(fn, max(200, args.steps), stream)
     alg = nbytes + K + 4 * 23 + N * 4
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "e4m3xe2m1->f32",
@@ -263,12 +295,13 @@ def int4_gemv(args, ctx, dev):
     stream = torch.cuda.current_stream()
     fn = lambda i: ctx.int4_linear(spec, x, qw[i % copies], sc[i % copies], qz[i % copies], None, y, M, stream)
     ms = wall_ms(fn, args.steps, args.warmup)
-    kms = event_ms(fn, max(200, args.steps), stream)
+    kms = batch_event_ms(fn, max(200, args.steps), stream)
     alg = nbytes + M * K * 2 + M * N * 2
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "bf16xint4->f32",
                     {"workload": f"int4_gptq_g128_asym_m{M}_k4096_n14336", "weight_copies_rotated": copies})
-    out["roofline"] = {"bound": "hbm", "kernel": "int4_gptq_kernel<8>", "achieved": gbs, "peak": HBM_PEAK_GBS,
+    kname = "int4_gptq_gemv_kernel<16, 128, true>" if M <= 2 else "int4_gptq_fixed_kernel<8, 4, 4>"
+    out["roofline"] = {"bound": "hbm", "kernel": kname, "achieved": gbs, "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                        "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
     return out
@@ -297,7 +330,7 @@ def fp8_head(args, ctx, dev):
     stream = torch.cuda.current_stream()
     fn = lambda i: ctx.fp8_output_projection(spec, x, W, grid, None, lb, am, M, stream)
     ms = wall_ms(fn, args.steps, args.warmup)
-    kms = event_ms(fn, max(50, args.steps), stream)
+    kms = batch_event_ms(fn, max(50, args.steps), stream)
     alg = N * K + N * nblk * 2 + M * K * 2 + M * N * 2 + M * 4
     flop = 2.0 * M * N * K
     gbs = alg / (kms * 1e-3) / 1e9
@@ -311,6 +344,67 @@ def fp8_head(args, ctx, dev):
                        "frac": (tf / FP8_PEAK_TFLOPS) if mfma_bound else (gbs / HBM_PEAK_GBS), "traffic": None,
                        "hbm_gbs": gbs, "tflops": tf, "launch_ms": kms}
     return out
+
+
+def hbm_copy(args, ctx, dev):
+    """Calibration workload for the HBM traffic counters: a device-to-device
+    copy of 512 MiB (read 512 MiB, write 512 MiB per launch)."""
+    import torch
+
+    n = 512 * 2 ** 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(7)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    fn = lambda i: dst.copy_(src)
+    ms = wall_ms(fn, args.steps, args.warmup)
+    kms = batch_event_ms(fn, max(20, args.steps), stream)
+    gbs = 2 * n / (kms * 1e-3) / 1e9
+    out = base_line(args, gbs, "GB/s", ms, "u8", {"workload": "hbm_copy_512MiB", "bytes_read": n, "bytes_written": n})
+    out["roofline"] = {"bound": "hbm", "kernel": "device copy", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": gbs / HBM_PEAK_GBS, "traffic": 2 * n, "launch_ms": kms}
+    return out
+
+
+def _pmc_per_dispatch(csv_dir, counter):
+    """{kernel name: mean counter value per dispatch} from rocprofv3 CSVs."""
+    import csv
+    import glob
+
+    vals = {}
+    for f in glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0].strip()
+                if name.startswith("void "):
+                    name = name[5:]
+                vals.setdefault(name, []).append(float(row["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def summarize_traffic(dirs):
+    """--summarize-traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR:
+    per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of every kernel, scaled by the
+    copy calibration (512 MiB read and written per dispatch), written to
+    profiles/traffic.json and printed as a markdown table."""
+    fetch, write, cf, cw = (_pmc_per_dispatch(d, c) for d, c in
+                            zip(dirs, ("FETCH_SIZE", "WRITE_SIZE", "FETCH_SIZE", "WRITE_SIZE")))
+    copy_name = max(cf, key=lambda k: cf[k])
+    n_kib = 512 * 1024
+    ff, wf = n_kib / cf[copy_name], n_kib / cw[copy_name]
+    out = {"copy_kernel": copy_name, "copy_fetch_kib": cf[copy_name], "copy_write_kib": cw[copy_name],
+           "fetch_factor": ff, "write_factor": wf, "kernels": {}}
+    for k in fetch:
+        fk, wk = fetch[k], write.get(k, 0.0)
+        out["kernels"][k] = {"fetch_kib": fk, "write_kib": wk, "hbm_bytes": (fk * ff + wk * wf) * 1024}
+    with open(os.path.join(HERE, "profiles", "traffic.json"), "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+    print(f"copy calibration ({copy_name}): FETCH_SIZE {cf[copy_name]:.0f} KiB, WRITE_SIZE {cw[copy_name]:.0f} KiB "
+          f"for 524288 KiB each -> factors {ff:.4f} / {wf:.4f}\n")
+    print("| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) |\n|---|---|---|---|")
+    for k, v in sorted(out["kernels"].items(), key=lambda kv: -kv[1]["hbm_bytes"]):
+        print(f"| {k} | {v['fetch_kib']:.0f} | {v['write_kib']:.0f} | {v['hbm_bytes']:.4g} |")
 
 
 def cpu_baseline(d, budget_s):
@@ -341,6 +435,9 @@ def cpu_baseline(d, budget_s):
 
 def main():
     args = parse()
+    if args.summarize_traffic:
+        summarize_traffic(args.summarize_traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -372,6 +469,8 @@ def main():
         out = mxfp4_gemv(args, ctx, dev)
     elif args.workload == "int4_gemv":
         out = int4_gemv(args, ctx, dev)
+    elif args.workload == "hbm_copy":
+        out = hbm_copy(args, ctx, dev)
     else:
         out = fp8_head(args, ctx, dev)
     print(json.dumps(out))

@@ -17,6 +17,7 @@
 //   fp4 operand: 16 bytes hold k = 32g..32g+31 (low nibble first) of row r;
 //   scale operand: lane (g, r) supplies the e8m0 scale of row r, k-block g;
 //   result: lane (g, r) holds D[4g+i][r], i = 0..3.
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -255,6 +256,26 @@ struct TileRec {
     const uint8_t* s[2];
 };
 
+// One work item of the persistent grouped GEMM: row block `rb` of tile
+// `tile` (count routes) with its expert's pointers.
+struct ItemRec {
+    uint32_t rb, count, tile, pad;
+    const uint8_t* w[2];
+    const uint8_t* s[2];
+};
+
+// Route list of one 128-route tile of the persistent grouped GEMM, in the
+// order the tile's rows are laid out (entries past the count repeat the
+// first route): route id, activation row and route weight.  2 KB, so a tile
+// is copied into LDS by two 1 KB wave copies.
+constexpr uint32_t PG_TILE = 128;
+struct PgList {
+    uint32_t route[PG_TILE];
+    uint32_t arow[PG_TILE];
+    float wr[PG_TILE];
+    uint32_t pad[PG_TILE];
+};
+
 struct TileArgs {
     const uint32_t* frames;     // intermediate frames (u32 words)
     uint64_t frame_words;       // k*I/2 + k
@@ -271,6 +292,10 @@ struct TileArgs {
     uint32_t* seg_list;
     TileRec* recs;
     uint32_t* n_tiles;
+    ItemRec* items;             // persistent grouped GEMM work items, or null
+    PgList* lists;              // its per-tile route lists
+    uint32_t item_nrb;          // row blocks per tile for the work items
+    uint32_t a_row_div;         // activation row of route r = r / a_row_div
 };
 
 // Validity of one parameter from its (already loaded) slot word and address
@@ -406,7 +431,7 @@ __device__ void build_tiles(const TileArgs& A) {
                 rec_out.expert = e;
                 rec_out.begin = cur[e] + t * A.TM;
                 rec_out.count = min(A.TM, cnt[e] - t * A.TM);
-                rec_out.pad = 0;
+                rec_out.pad = (t << 16) | nte;   // tile index within the expert, expert's tile count
                 for (uint32_t m = 0; m < 2; m++) {
                     const bool has = 2 * m < P;
                     if (e == tid) {
@@ -437,6 +462,38 @@ __device__ void build_tiles(const TileArgs& A) {
         }
     }
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
+    if (A.items) {
+        // Work items (expert, row block, tile) with tiles fastest, and the
+        // route list of every tile.  The tile records and route slots written
+        // above by this block are visible after the barrier.
+        __syncthreads();
+        const uint32_t nrb = A.item_nrb, n_t = min(tiles_total, A.max_tiles), n_items = n_t * nrb;
+        for (uint32_t i = tid; i < n_items; i += nt) {
+            const uint32_t tp = i / nrb, pad = A.recs[tp].pad;
+            const uint32_t first = tp - (pad >> 16), nte = pad & 0xffffu;
+            const uint32_t local = i - first * nrb, t = first + local % nte;
+            const TileRec& R = A.recs[t];
+            ItemRec o;
+            o.rb = local / nte;
+            o.count = R.count;
+            o.tile = t;
+            o.pad = 0;
+            o.w[0] = R.w[0];
+            o.w[1] = R.w[1];
+            o.s[0] = R.s[0];
+            o.s[1] = R.s[1];
+            A.items[i] = o;
+        }
+        for (uint32_t i = tid; i < n_t * PG_TILE; i += nt) {
+            const uint32_t t = i / PG_TILE, j = i % PG_TILE;
+            const uint32_t begin = A.recs[t].begin, count = A.recs[t].count;
+            const uint32_t r = A.seg_list[begin + (j < count ? j : 0)];
+            PgList& L = A.lists[t];
+            L.route[j] = r;
+            L.arow[j] = r / A.a_row_div;
+            L.wr[j] = bf16_to_f32(A.routes[r] >> 16);
+        }
+    }
 }
 
 // Preparation launch of one MoE projection: block 0 turns the route map into
@@ -1757,6 +1814,419 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     return nh::check_launch("mx_stream_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Persistent grouped GEMM for prefill-shaped batches.
+//
+// Work item = (tile of <= 128 routes of one expert, block of 256 weight rows).
+// For gate_up the 256 rows are 128 gate and 128 up rows of the same channels,
+// so SwiGLU runs on the accumulators.  The preparation launch lists the items
+// as (expert, row block, tile) with tiles fastest; block b of the grid takes
+// items b, b + G, b + 2G, ..., so the tiles of one expert at one row block
+// run side by side and read the same weight rows while they are in L2 / the
+// Infinity Cache.  One 512-thread block per CU streams every 128-k chunk of
+// its items (activations 128 x 128 B e4m3, weights 256 x 64 B e2m1, their
+// scales) global -> LDS with global_load_lds into a 4-stage ring that runs
+// across item boundaries: the copies of the next item are in flight while
+// the last chunks of the current one are contracted.
+//
+// The loop is built for few instructions per chunk: every wave issues the
+// same 6 copies per stage (an SGPR base advanced per chunk plus a fixed
+// 32-bit lane offset), so the vmcnt waits are compile-time constants; one
+// barrier per chunk; the step body is unrolled over the 4 stages so every
+// LDS operand read is a fixed register plus an immediate offset.  The next
+// item's descriptor (item record, then its tile's route list) also arrives
+// by LDS copies issued by wave 0 inside the same pipeline.
+//
+// Wave (wm, wn) contracts routes [64 wm, 64 wm + 64) against 64 weight rows
+// (gate_up: 32 gate + the same 32 up channels).
+// ---------------------------------------------------------------------------
+constexpr uint32_t PG_TM = PG_TILE;
+constexpr uint32_t PG_ROWS = 256;
+constexpr uint32_t PG_NST = 4;
+// LDS map (bytes).  Regions are grouped by kind so a stage is an immediate.
+constexpr uint32_t PG_A_OFF = 0;          // [4][128 routes][128 B], 16-byte pieces XOR-swizzled
+constexpr uint32_t PG_B_OFF = 65536;      // [4][256 rows][64 B], swizzled
+constexpr uint32_t PG_SB_OFF = 131072;    // [4][256 rows][8 B]: the aligned dword pair holding 4 e8m0 bytes
+constexpr uint32_t PG_SA_OFF = 139264;    // [4][128 routes] f32 block scales
+constexpr uint32_t PG_SINK_OFF = 141312;  // 256 B written by padding copies
+constexpr uint32_t PG_REC_OFF = 141568;   // [2][256 B] item records (48 B used)
+constexpr uint32_t PG_LIST_OFF = 142080;  // [2][2 KB] tile route lists
+constexpr uint32_t PG_LDS = 146176;
+constexpr uint32_t PG_COPIES = 6;         // per wave per stage
+constexpr uint32_t PG_MIN_CHUNKS = 10;    // descriptor copies ride on chunks 3 and 6; the list is read at nch - 4
+
+__device__ __attribute__((aligned(16))) const uint8_t kZeroPage[1024] = {0};
+
+struct PgArgs {
+    const uint8_t* aq;          // e4m3 activations, row stride K
+    const float* as;            // pow2 scales, row stride nch
+    uint32_t K, N, k;
+    const ItemRec* items;
+    const PgList* lists;
+    const uint32_t* n_tiles;
+    uint16_t* out;              // gate_up: frames as u16; down: expert_outputs
+    uint64_t frame_elems;
+    float limit;
+};
+
+__device__ __forceinline__ uint32_t pg_swz_a(uint32_t t) { return (t & 7u) ^ ((t >> 3) & 1u); }
+__device__ __forceinline__ uint32_t pg_swz_b(uint32_t r) { return (r ^ (r >> 2)) & 3u; }
+
+template <uint32_t OFF>
+__device__ __forceinline__ v4i lds_rd128(uint32_t a) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+template <uint32_t OFF>
+__device__ __forceinline__ uint32_t lds_rd32(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+template <uint32_t OFF>
+__device__ __forceinline__ uint32_t lds_rd8(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+// Row of weight tile j inside a wave's 64 rows (gate_up: gate 0, 16, up 128, 144).
+template <int NMAT>
+__host__ __device__ constexpr uint32_t pg_jrow(uint32_t j) { return NMAT == 2 ? (j >> 1) * 128 + (j & 1) * 16 : j * 16; }
+
+template <typename F, uint32_t... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<uint32_t, I...>) {
+    (f(std::integral_constant<uint32_t, I>{}), ...);
+}
+// f(integral_constant<0>), ..., f(integral_constant<N-1>).
+template <uint32_t N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<uint32_t, N>{});
+}
+
+// LDS dword read that waits for itself inside the same asm statement, so
+// no use of the result can be scheduled ahead of the wait.
+template <uint32_t OFF>
+__device__ __forceinline__ uint32_t lds_rd32_sync(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)(lds_u8*)p; }
+
+// Issue-side state of the item whose chunks are being copied.
+struct PgIssue {
+    const uint8_t* a_base;      // uniform: activations (chunk 0)
+    const uint8_t* b_base[2];   // uniform: weight matrices of copy slots 2, 3
+    const uint8_t* sb_base;     // uniform: scale matrix of slot 4
+    const uint8_t* sa_base;     // uniform: activation scales (or the zero page)
+    uint32_t off[PG_COPIES];    // per lane
+    uint32_t tail_ok;           // per lane: bit i = slot i's piece lies inside K in the last chunk
+};
+
+template <int NMAT>
+__global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t pg_ring[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
+    constexpr uint32_t RPM = PG_ROWS / NMAT;           // rows per matrix in an item
+    const uint32_t nrb = (N + RPM - 1) / RPM;
+    const uint32_t n_items = __builtin_amdgcn_readfirstlane(*A.n_tiles) * nrb;
+    const uint32_t G = gridDim.x;
+    const uint32_t ring = lds_addr(pg_ring);
+
+    // ---- descriptor copies (wave 0): item record, then the tile's list ----
+    auto copy_rec = [&](uint32_t item, uint32_t par) __attribute__((always_inline)) {
+        const uint32_t idx = item < n_items ? item : 0u;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(A.items + idx) + (lane < 12 ? lane : 0);
+        __builtin_amdgcn_global_load_lds(src, pg_ring + PG_REC_OFF + par * 256, 4, 0, 0);
+    };
+    auto copy_list = [&](uint32_t par) __attribute__((always_inline)) {
+        const uint32_t tile = lds_rd32_sync<0>(ring + PG_REC_OFF + par * 256 + 8);
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(A.lists + __builtin_amdgcn_readfirstlane(tile)) + lane * 16;
+        __builtin_amdgcn_global_load_lds(src, pg_ring + PG_LIST_OFF + par * 2048, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(src + 1024, pg_ring + PG_LIST_OFF + par * 2048 + 1024, 16, 0, 0);
+    };
+    auto rec_word = [&](uint32_t par, uint32_t w) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t v = lds_rd32_sync<0>(ring + PG_REC_OFF + par * 256 + 4 * w);
+        return __builtin_amdgcn_readfirstlane(v);
+    };
+    auto rec_ptr = [&](uint32_t par, uint32_t w) __attribute__((always_inline)) -> const uint8_t* {
+        const uint64_t lo = rec_word(par, w), hi = rec_word(par, w + 1);
+        return reinterpret_cast<const uint8_t*>(lo | (hi << 32));
+    };
+
+    // ---- issue side: set-up of an item's copies (after its descriptor landed) ----
+    // Slots: 0, 1 = activations of routes 8w.., 64+8w..; 2, 3 = weight rows
+    // 16w.., 128+16w..; 4 = scale dword pairs of rows 32w..; 5 = activation
+    // scales of routes 64w.. (waves 0, 1; a padding copy elsewhere).
+    auto setup_issue = [&](uint32_t par, PgIssue& S) __attribute__((always_inline)) {
+        const uint32_t rb = rec_word(par, 0), count = rec_word(par, 1);
+        const uint8_t* wp[2] = {rec_ptr(par, 4), rec_ptr(par, 6)};
+        const uint8_t* sp[2] = {rec_ptr(par, 8), rec_ptr(par, 10)};
+        const uint32_t list = ring + PG_LIST_OFF + par * 2048;
+        const uint32_t last = nch - 1;
+        uint32_t tail = 0;
+        // activations
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t t = 64 * h + 8 * wave + (lane >> 3);
+            const uint32_t p = (lane & 7) ^ pg_swz_a(t);
+            const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
+            S.off[h] = row * K + p * 16;
+            tail |= (last * 128 + p * 16 < K ? 1u : 0u) << h;
+        }
+        S.a_base = A.aq;
+        // weight rows
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t r = 128 * h + 16 * wave + (lane >> 2);
+            const uint32_t p = (lane & 3) ^ pg_swz_b(r);
+            const uint32_t mat = r / RPM, n = rb * RPM + r % RPM;
+            S.off[2 + h] = (n < N ? n : 0) * RB + p * 16;
+            S.b_base[h] = wp[(128 * h) / RPM];
+            (void)mat;
+            tail |= (last * 128 + p * 32 < K ? 1u : 0u) << (2 + h);
+        }
+        // weight scale dword pairs
+        {
+            const uint32_t r = 32 * wave + (lane >> 1), hh = lane & 1;
+            const uint32_t n = rb * RPM + r % RPM;
+            const uint32_t rowoff = (n < N ? n : 0) * SB;
+            S.off[4] = (rowoff & ~3u) + 4 * hh;
+            S.sb_base = sp[(32 * wave) / RPM];
+            const uint32_t a_last = (rowoff & ~3u) + 4 * last;
+            tail |= (hh == 0 || a_last + 4 < rowoff + SB ? 1u : 0u) << 4;
+        }
+        // activation scales
+        if (wave < 2) {
+            const uint32_t t = 64 * wave + lane;
+            const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
+            S.off[5] = row * nch * 4;
+            S.sa_base = reinterpret_cast<const uint8_t*>(A.as);
+        } else {
+            S.off[5] = 0;
+            S.sa_base = kZeroPage;
+        }
+        tail |= 1u << 5;
+        S.tail_ok = tail;
+    };
+
+    // Copies of chunk c of the issue item into stage ST.
+    auto issue_chunk = [&](const PgIssue& S, uint32_t c, auto st_tag) __attribute__((always_inline)) {
+        constexpr uint32_t ST = decltype(st_tag)::value;
+        uint8_t* const dA = pg_ring + PG_A_OFF + ST * 16384 + wave * 1024;
+        uint8_t* const dB = pg_ring + PG_B_OFF + ST * 16384 + wave * 1024;
+        uint8_t* const dS = pg_ring + PG_SB_OFF + ST * 2048 + wave * 256;
+        uint8_t* const dT = wave < 2 ? pg_ring + PG_SA_OFF + ST * 512 + wave * 256 : pg_ring + PG_SINK_OFF;
+        const uint32_t sa_step = wave < 2 ? 4u : 0u;
+        if (c + 1 < nch) {
+            const uint8_t* a = S.a_base + c * 128;
+            __builtin_amdgcn_global_load_lds(a + S.off[0], dA, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a + S.off[1], dA + 8192, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(S.b_base[0] + c * 64 + S.off[2], dB, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(S.b_base[1] + c * 64 + S.off[3], dB + 8192, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(S.sb_base + c * 4 + S.off[4], dS, 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(S.sa_base + c * sa_step + S.off[5], dT, 4, 0, 0);
+        } else {
+            // Last chunk: pieces past K (and the scale dword past a row's
+            // end) come from the zero page.
+            const uint32_t ok = S.tail_ok;
+            const uint8_t* a = S.a_base + c * 128;
+            __builtin_amdgcn_global_load_lds((ok & 1) ? a + S.off[0] : kZeroPage, dA, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((ok & 2) ? a + S.off[1] : kZeroPage, dA + 8192, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((ok & 4) ? S.b_base[0] + c * 64 + S.off[2] : kZeroPage, dB, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((ok & 8) ? S.b_base[1] + c * 64 + S.off[3] : kZeroPage, dB + 8192, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((ok & 16) ? S.sb_base + c * 4 + S.off[4] : kZeroPage, dS, 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(S.sa_base + c * sa_step + S.off[5], dT, 4, 0, 0);
+        }
+    };
+
+    // ---- first item: descriptor copied synchronously ----
+    uint32_t item = blockIdx.x;
+    if (item >= n_items) return;
+    if (wave == 0) copy_rec(item, 0);
+    wait_vm_imm<0>();
+    __syncthreads();
+    if (wave == 0) copy_list(0);
+    wait_vm_imm<0>();
+    __syncthreads();
+
+    PgIssue S;
+    setup_issue(0, S);
+    uint32_t ic = 0, ipar = 0, iitem = item;   // issue item: next chunk, descriptor slot, index
+    bool issuing = true;
+    // Issues the next chunk group (one per stage) and moves to the next item
+    // after the last chunk of the current one.
+    auto issue_next = [&](auto st_tag) __attribute__((always_inline)) {
+        if (issuing) {
+            issue_chunk(S, ic, st_tag);
+            if (++ic == nch) {
+                ic = 0;
+                ipar ^= 1u;
+                iitem += G;
+                issuing = iitem < n_items;
+                if (issuing) setup_issue(ipar, S);
+            }
+        }
+    };
+    issue_next(std::integral_constant<uint32_t, 0>{});
+    issue_next(std::integral_constant<uint32_t, 1>{});
+    issue_next(std::integral_constant<uint32_t, 2>{});
+
+    // ---- compute side ----
+    const uint32_t wm = wave >> 2, wn = wave & 3;
+    const uint32_t brow0 = NMAT == 2 ? wn * 32 : wn * 64;
+    auto jrow = [](int j) __attribute__((always_inline)) -> uint32_t { return pg_jrow<NMAT>((uint32_t)j); };
+    const uint32_t ta = 64 * wm + rr, fa = pg_swz_a(rr);
+    const uint32_t LA_lo = ring + PG_A_OFF + ta * 128 + (g ^ fa) * 16;
+    const uint32_t LA_hi = ring + PG_A_OFF + ta * 128 + ((g ^ fa) ^ 4u) * 16;
+    const uint32_t LSA = ring + PG_SA_OFF + ta * 4;
+    const uint32_t LB = ring + PG_B_OFF + (brow0 + rr) * 64 + (g ^ pg_swz_b(rr)) * 16;
+
+    uint32_t cpar = 0, c = 0;              // compute item descriptor slot, chunk
+    uint32_t count = 0, rb = 0, alim = 0;
+    uint32_t LSB[4];
+    v4f acc[4][4];
+    auto start_item = [&]() __attribute__((always_inline)) {
+        rb = rec_word(cpar, 0);
+        count = rec_word(cpar, 1);
+        alim = count > 64 * wm ? min(4u, (count - 64 * wm + 15) / 16) : 0u;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t r = brow0 + jrow(j) + rr, n = rb * RPM + r % RPM;
+            LSB[j] = ring + PG_SB_OFF + r * 8 + (((n < N ? n : 0) * SB) & 3u) + g;
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    start_item();
+    bool cnext = item + G < n_items;        // is there an item after the compute item
+
+    auto epilogue = [&]() __attribute__((always_inline)) {
+        const uint32_t list = ring + PG_LIST_OFF + cpar * 2048;
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            if ((uint32_t)a >= alim) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t t = 64 * wm + 16 * a + 4 * g + i;
+                const uint32_t r = lds_rd32_sync<0>(list + 4 * t);
+                const uint32_t wrb = lds_rd32_sync<1024>(list + 4 * t);
+                if (t >= count) continue;
+                if (NMAT == 2) {
+                    const uint64_t ob = (uint64_t)(r / A.k) * A.frame_elems + (uint64_t)(r % A.k) * N;
+#pragma unroll
+                    for (int j2 = 0; j2 < 2; j2++) {
+                        const uint32_t ch = rb * RPM + brow0 + j2 * 16 + rr;
+                        if (ch >= N) continue;
+                        float gv = round_bf16(acc[a][j2][i]);
+                        float uv = round_bf16(acc[a][2 + j2][i]);
+                        if (A.limit > 0.0f) {
+                            gv = fminf(gv, A.limit);
+                            uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                        }
+                        const float h = (gv / (1.0f + expf(-gv))) * uv;
+                        A.out[ob + ch] = (uint16_t)f32_to_bf16(h);
+                    }
+                } else {
+                    const float wr = __uint_as_float(wrb);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t row = rb * RPM + brow0 + jrow(j) + rr;
+                        if (row < N) A.out[(uint64_t)r * N + row] = (uint16_t)f32_to_bf16(acc[a][j][i] * wr);
+                    }
+                }
+            }
+        }
+    };
+
+    // One pipeline step on stage ST: wait for this chunk, barrier, issue the
+    // chunk three ahead (and the descriptor copies riding on chunks 3 and 6),
+    // contract, and on the item's last chunk write it out and switch items.
+    // Returns false when the block has no more work.
+    auto step = [&](auto st_tag) __attribute__((always_inline)) -> bool {
+        constexpr uint32_t ST = decltype(st_tag)::value;
+        // Copy groups issued after this chunk's: the next two chunks (when
+        // they exist), plus wave 0's descriptor copies riding on them.
+        const uint32_t l1 = c + 1 < nch ? c + 1 : c + 1 - nch, l2 = c + 2 < nch ? c + 2 : c + 2 - nch;
+        const bool g1 = c + 1 < nch || cnext, g2 = c + 2 < nch || cnext;
+        uint32_t x = (g1 ? PG_COPIES : 0u) + (g2 ? PG_COPIES : 0u);
+        if (wave == 0) x += (l1 == 3 ? 1u : 0u) + (l1 == 6 ? 2u : 0u) + (l2 == 3 ? 1u : 0u) + (l2 == 6 ? 2u : 0u);
+        wait_vm(x);
+        __builtin_amdgcn_s_barrier();
+        // Chunk c + 3 (of this item or the next) goes into stage ST + 3.
+        issue_next(std::integral_constant<uint32_t, (ST + 3) % PG_NST>{});
+        if (wave == 0) {
+            if (c == 0) copy_rec(item + G, cpar ^ 1u);
+            else if (c == 3) copy_list(cpar ^ 1u);
+        }
+        // ---- contract chunk c from stage ST ----
+        v4i lo[4], hi[4], w[4];
+        uint32_t sav[4], sbv[4];
+        static_for<4>([&](auto ai) __attribute__((always_inline)) {
+            constexpr uint32_t a = decltype(ai)::value;
+            lo[a] = lds_rd128<ST * 16384 + a * 2048>(LA_lo);
+            hi[a] = lds_rd128<ST * 16384 + a * 2048>(LA_hi);
+            sav[a] = lds_rd32<ST * 512 + a * 64>(LSA);
+        });
+        static_for<4>([&](auto ji) __attribute__((always_inline)) {
+            constexpr uint32_t j = decltype(ji)::value;
+            w[j] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 64>(LB);
+        });
+#pragma unroll
+        for (int j = 0; j < 4; j++) sbv[j] = lds_rd8<ST * 2048>(LSB[j]);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]), "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]),
+                       "+v"(hi[3]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(sav[0]), "+v"(sav[1]),
+                       "+v"(sav[2]), "+v"(sav[3]), "+v"(sbv[0]), "+v"(sbv[1]), "+v"(sbv[2]), "+v"(sbv[3]));
+        // Scale blocks past K (last chunk) read bytes beyond the row.
+        const bool bvalid = c * 4 + g < SB;
+#pragma unroll
+        for (int j = 0; j < 4; j++) sbv[j] = bvalid ? sbv[j] : 127u;
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            if ((uint32_t)a >= alim) continue;
+            const v8i av = v8i{lo[a].x, lo[a].y, lo[a].z, lo[a].w, hi[a].x, hi[a].y, hi[a].z, hi[a].w};
+            const uint32_t se = (sav[a] >> 23) & 0xffu;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[a][j] = mfma_fp8_fp4(av, w[j], se, sbv[j], acc[a][j]);
+        }
+        if (++c < nch) return true;
+        // ---- end of the item ----
+        epilogue();
+        if (!cnext) return false;
+        c = 0;
+        cpar ^= 1u;
+        item += G;
+        cnext = item + G < n_items;
+        start_item();
+        return true;
+    };
+    while (true) {
+        if (!step(std::integral_constant<uint32_t, 0>{})) break;
+        if (!step(std::integral_constant<uint32_t, 1>{})) break;
+        if (!step(std::integral_constant<uint32_t, 2>{})) break;
+        if (!step(std::integral_constant<uint32_t, 3>{})) break;
+    }
+}
+
+template <int NMAT>
+nerve_hip_status launch_pgemm(const PgArgs& A, const nerve_hip_ctx* ctx, hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)moe_pgemm_kernel<NMAT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                PG_LDS) != hipSuccess)
+            return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for moe_pgemm_kernel");
+        attr_set = true;
+    }
+    moe_pgemm_kernel<NMAT><<<ctx->cu_count, 512, PG_LDS, st>>>(A);
+    return nh::check_launch("moe_pgemm_kernel");
+}
+
 nerve_hip_status launch_quant(const QuantArgs& Q, bool pow2, hipStream_t st) {
     if (Q.rows == 0) return nh::ok();
     const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
@@ -1853,7 +2323,10 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     // routes; prefill-shaped batches use the LDS-staged grouped GEMM with
     // 64-route tiles.
     const bool grouped = cap >= 512 || K > 4096;
-    const uint32_t TM = grouped ? 64 : 16;
+    // Persistent grouped GEMM: enough chunks per item for the descriptor
+    // prefetch rounds.
+    const bool persistent = grouped && (K + 127) / 128 >= PG_MIN_CHUNKS;
+    const uint32_t TM = persistent ? PG_TM : grouped ? 64 : 16;
     const uint32_t max_tiles = (cap + TM - 1) / TM + (E < cap ? E : cap);
     nh::Carver cv;
     size_t o_aq = cv.take<uint8_t>((size_t)arows * K);
@@ -1861,6 +2334,9 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     size_t o_seg = cv.take<uint32_t>(cap + 16);   // +16: the streaming kernel reads 16 entries at once
     size_t o_rec = cv.take<TileRec>(max_tiles);
     size_t o_nt = cv.take<uint32_t>(1);
+    const uint32_t item_nrb = (N + (gate_up ? PG_ROWS / 2 : PG_ROWS) - 1) / (gate_up ? PG_ROWS / 2 : PG_ROWS);
+    size_t o_items = cv.take<ItemRec>(persistent ? (size_t)max_tiles * item_nrb : 0);
+    size_t o_lists = cv.take<PgList>(persistent ? max_tiles : 0);
     void* ws = nullptr;
     nerve_hip_status st = nh::workspace(ctx, cv.offset, &ws);
     if (st) return st;
@@ -1913,6 +2389,10 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.seg_list = reinterpret_cast<uint32_t*>(base + o_seg);
     ta.recs = reinterpret_cast<TileRec*>(base + o_rec);
     ta.n_tiles = reinterpret_cast<uint32_t*>(base + o_nt);
+    ta.items = persistent ? reinterpret_cast<ItemRec*>(base + o_items) : nullptr;
+    ta.item_nrb = item_nrb;
+    ta.lists = persistent ? reinterpret_cast<PgList*>(base + o_lists) : nullptr;
+    ta.a_row_div = gate_up ? k : 1;
     // Decode-shaped batches: one streaming launch that builds its own tiles
     // and quantizes its own activation chunks (no preparation launch).
     if (!grouped && !(gate_up && ms.prequant)) {
@@ -1960,6 +2440,25 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ea.n_tiles = ta.n_tiles;
     ea.frame_elems = frame_words * 2;
     ea.limit = ms.limit;
+    if (persistent) {
+        PgArgs pa;
+        pa.aq = aq;
+        pa.as = as;
+        pa.K = K;
+        pa.N = N;
+        pa.k = k;
+        pa.items = ta.items;
+        pa.lists = ta.lists;
+        pa.n_tiles = ta.n_tiles;
+        pa.frame_elems = frame_words * 2;
+        pa.limit = ms.limit;
+        if (gate_up) {
+            pa.out = static_cast<uint16_t*>(intermediates);
+            return launch_pgemm<2>(pa, ctx, stream);
+        }
+        pa.out = static_cast<uint16_t*>(expert_outputs);
+        return launch_pgemm<1>(pa, ctx, stream);
+    }
     if (grouped) {
         const uint32_t rows_per_block = gate_up ? 64 : 128;
         dim3 ggrid(max_tiles, (N + rows_per_block - 1) / rows_per_block);

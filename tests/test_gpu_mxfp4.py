@@ -167,7 +167,10 @@ def _moe_case(E, k, B, H, I, seed):
                                        # streaming kernel at a second shape (K >= 512 on both stages)
                                        (8, 2, 6, 1024, 512), (12, 3, 9, 4096, 1024),
                                        # >= 512 routes: the LDS-staged grouped GEMM path
-                                       (16, 4, 160, 512, 384), (8, 2, 300, 2880, 160), (64, 8, 70, 224, 288)])
+                                       (16, 4, 160, 512, 384), (8, 2, 300, 2880, 160), (64, 8, 70, 224, 288),
+                                       # persistent grouped GEMM on both stages: K tail of 64,
+                                       # partial row blocks, experts with several 128-route tiles
+                                       (16, 4, 140, 1344, 1408), (4, 2, 300, 1344, 1408)])
 def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
     d, routes, hidden = _moe_case(E, k, B, H, I, seed=E * 100 + B)
     rig = MoeRig(dev, d, routes)

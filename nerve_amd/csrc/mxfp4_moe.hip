@@ -17,6 +17,7 @@
 //   fp4 operand: 16 bytes hold k = 32g..32g+31 (low nibble first) of row r;
 //   scale operand: lane (g, r) supplies the e8m0 scale of row r, k-block g;
 //   result: lane (g, r) holds D[4g+i][r], i = 0..3.
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -309,7 +310,7 @@ __device__ __forceinline__ bool record_valid(uint32_t slot, uint32_t n_records, 
            rec[6] == 1u;
 }
 
-constexpr uint32_t PREP_ROUTE_CACHE = 16384;   // compacted slots whose expert is kept in LDS
+constexpr uint32_t PREP_R = 8;                 // slots per thread whose route ids stay in registers
 constexpr uint16_t NO_EXPERT = 0xffffu;
 
 // Latency matters here (decode runs this once per projection), so the block
@@ -318,12 +319,13 @@ constexpr uint16_t NO_EXPERT = 0xffffu;
 // words; (2) the address records and the route words.  Everything after that
 // is LDS work; a thread keeps its first expert's resolved pointers in
 // registers for the tile records.
+template <uint32_t MAXE>
 __device__ void build_tiles(const TileArgs& A) {
-    __shared__ uint32_t cnt[MAX_EXPERTS];
-    __shared__ uint32_t cur[MAX_EXPERTS];
-    __shared__ uint32_t tst[MAX_EXPERTS];
-    __shared__ uint8_t valid[MAX_EXPERTS];
-    __shared__ uint16_t rexp[PREP_ROUTE_CACHE];
+    __shared__ uint32_t cnt[MAXE];
+    __shared__ uint32_t cur[MAXE];
+    __shared__ uint32_t tst[MAXE];
+    __shared__ uint32_t est[MAXE];
+    __shared__ uint8_t valid[MAXE];
     __shared__ uint32_t wave_tot[16];
     __shared__ uint32_t total;
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
@@ -394,13 +396,34 @@ __device__ void build_tiles(const TileArgs& A) {
     };
     if (tid < cap) {
         const uint32_t e = slot_expert(tid, rword, route);
-        if (tid < PREP_ROUTE_CACHE) rexp[tid] = (uint16_t)e;
         if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
     }
-    for (uint32_t c = tid + nt; c < cap; c += nt) {
+    // Slots c = tid + i nt for i < PREP_R keep their route index and route
+    // word in registers: two batched rounds of loads instead of a dependent
+    // pair per slot.  (Slots beyond PREP_R nt take the plain loop.)
+    uint32_t rw_r[PREP_R], rt_r[PREP_R];
+    rw_r[0] = rword;
+    rt_r[0] = route;
+#pragma unroll
+    for (uint32_t i = 1; i < PREP_R; i++) {
+        const uint32_t c = tid + i * nt;
+        rw_r[i] = c < cap ? A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k] : 0xffffffffu;
+    }
+#pragma unroll
+    for (uint32_t i = 1; i < PREP_R; i++) {
+        const uint32_t c = tid + i * nt;
+        rt_r[i] = (c < cap && rw_r[i] < cap) ? A.routes[rw_r[i]] : 0u;
+    }
+#pragma unroll
+    for (uint32_t i = 1; i < PREP_R; i++) {
+        const uint32_t c = tid + i * nt;
+        if (c >= cap) continue;
+        const uint32_t e = slot_expert(c, rw_r[i], rt_r[i]);
+        if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
+    }
+    for (uint32_t c = tid + PREP_R * nt; c < cap; c += nt) {
         const uint32_t rw = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
         const uint32_t e = slot_expert(c, rw, rw < cap ? A.routes[rw] : 0u);
-        if (c < PREP_ROUTE_CACHE) rexp[c] = (uint16_t)e;
         if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
     }
     __syncthreads();
@@ -417,6 +440,7 @@ __device__ void build_tiles(const TileArgs& A) {
     const uint32_t tiles_total = total;
     for (uint32_t e = e0; e < e1; e++) {
         cur[e] = oc;
+        est[e] = oc;
         tst[e] = ot;
         oc += cnt[e];
         ot += (cnt[e] + A.TM - 1) / A.TM;
@@ -447,51 +471,64 @@ __device__ void build_tiles(const TileArgs& A) {
         }
     }
     __syncthreads();
-    for (uint32_t c = tid; c < n; c += nt) {
-        uint32_t e, r;
-        if (c < PREP_ROUTE_CACHE && c == tid) {
-            e = rexp[c];
-            r = rword;
-        } else {
-            r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-            e = c < PREP_ROUTE_CACHE ? rexp[c] : slot_expert(c, r, r < cap ? A.routes[r] : 0u);
+    // Route slots in expert order.  For the persistent grouped GEMM the slot
+    // also goes into its tile's route list (position rank % TM of tile
+    // tst[e] + rank / TM), with its activation row and route weight.
+    auto place = [&](uint32_t e, uint32_t r, uint32_t rt) {
+        const uint32_t pos = atomicAdd(&cur[e], 1u);
+        A.seg_list[pos] = r;
+        if (A.lists) {
+            const uint32_t rank = pos - est[e], t = tst[e] + rank / A.TM, j = rank % A.TM;
+            if (t < A.max_tiles) {
+                PgList& L = A.lists[t];
+                L.route[j] = r;
+                L.arow[j] = r / A.a_row_div;
+                L.wr[j] = bf16_to_f32(rt >> 16);
+            }
         }
-        if (e != NO_EXPERT) {
-            const uint32_t pos = atomicAdd(&cur[e], 1u);
-            A.seg_list[pos] = r;
-        }
+    };
+#pragma unroll
+    for (uint32_t i = 0; i < PREP_R; i++) {
+        const uint32_t c = tid + i * nt;
+        if (c >= n) continue;
+        const uint32_t e = slot_expert(c, rw_r[i], rt_r[i]);
+        if (e != NO_EXPERT) place(e, rw_r[i], rt_r[i]);
+    }
+    for (uint32_t c = tid + PREP_R * nt; c < n; c += nt) {
+        const uint32_t r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+        const uint32_t rt = r < cap ? A.routes[r] : 0u;
+        const uint32_t e = slot_expert(c, r, rt);
+        if (e != NO_EXPERT) place(e, r, rt);
     }
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
     if (A.items) {
-        // Work items (expert, row block, tile) with tiles fastest, and the
-        // route list of every tile.  The tile records and route slots written
-        // above by this block are visible after the barrier.
+        // Work items (expert, row block, tile) with tiles fastest, decoded
+        // from the LDS tables; the tile records written above by this block
+        // are visible after the barrier.
         __syncthreads();
         const uint32_t nrb = A.item_nrb, n_t = min(tiles_total, A.max_tiles), n_items = n_t * nrb;
         for (uint32_t i = tid; i < n_items; i += nt) {
-            const uint32_t tp = i / nrb, pad = A.recs[tp].pad;
-            const uint32_t first = tp - (pad >> 16), nte = pad & 0xffffu;
-            const uint32_t local = i - first * nrb, t = first + local % nte;
-            const TileRec& R = A.recs[t];
+            const uint32_t tp = i / nrb;
+            // Expert of tile tp: the last e with tst[e] <= tp (experts without
+            // tiles share their successor's start, so it has tiles).
+            uint32_t lo = 0, hi = A.E;
+            while (hi - lo > 1) {
+                const uint32_t mid = (lo + hi) / 2;
+                if (tst[mid] <= tp) lo = mid;
+                else hi = mid;
+            }
+            const uint32_t e = lo, first = tst[e], nte = (cnt[e] + A.TM - 1) / A.TM;
+            const uint32_t local = i - first * nrb, kk = local % nte, t = first + kk;
             ItemRec o;
             o.rb = local / nte;
-            o.count = R.count;
+            o.count = min(A.TM, cnt[e] - kk * A.TM);
             o.tile = t;
             o.pad = 0;
-            o.w[0] = R.w[0];
-            o.w[1] = R.w[1];
-            o.s[0] = R.s[0];
-            o.s[1] = R.s[1];
+            o.w[0] = A.recs[t].w[0];
+            o.w[1] = A.recs[t].w[1];
+            o.s[0] = A.recs[t].s[0];
+            o.s[1] = A.recs[t].s[1];
             A.items[i] = o;
-        }
-        for (uint32_t i = tid; i < n_t * PG_TILE; i += nt) {
-            const uint32_t t = i / PG_TILE, j = i % PG_TILE;
-            const uint32_t begin = A.recs[t].begin, count = A.recs[t].count;
-            const uint32_t r = A.seg_list[begin + (j < count ? j : 0)];
-            PgList& L = A.lists[t];
-            L.route[j] = r;
-            L.arow[j] = r / A.a_row_div;
-            L.wr[j] = bf16_to_f32(A.routes[r] >> 16);
         }
     }
 }
@@ -499,12 +536,16 @@ __device__ void build_tiles(const TileArgs& A) {
 // Preparation launch of one MoE projection: block 0 turns the route map into
 // tile records while the other blocks quantize the activation rows (32
 // (row, 128-column) units per block).
+template <uint32_t MAXE>
 __global__ __launch_bounds__(1024) void moe_prep_kernel(TileArgs T, QuantArgs Q) {
     if (blockIdx.x == 0) {
-        build_tiles(T);
+        build_tiles<MAXE>(T);
         return;
     }
-    quant_unit<true>(Q, (blockIdx.x - 1) * 32 + (threadIdx.x >> 5), threadIdx.x & 31);
+    // Quantization blocks stride over the (row, 128-column) units, 32 per pass.
+    const uint64_t nblk = (Q.cols + 127) / 128, units = (uint64_t)Q.rows * nblk;
+    for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 32; u < units; u += (uint64_t)(gridDim.x - 1) * 32)
+        quant_unit<true>(Q, (uint32_t)u + (threadIdx.x >> 5), threadIdx.x & 31);
 }
 
 // ---------------------------------------------------------------------------
@@ -1820,10 +1861,10 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
 // Work item = (tile of <= 128 routes of one expert, block of 256 weight rows).
 // For gate_up the 256 rows are 128 gate and 128 up rows of the same channels,
 // so SwiGLU runs on the accumulators.  The preparation launch lists the items
-// as (expert, row block, tile) with tiles fastest; block b of the grid takes
-// items b, b + G, b + 2G, ..., so the tiles of one expert at one row block
-// run side by side and read the same weight rows while they are in L2 / the
-// Infinity Cache.  One 512-thread block per CU streams every 128-k chunk of
+// as (expert, row block, tile) with tiles fastest; every block takes every
+// G-th item, with consecutive items on blocks of one XCD, so the tiles of one
+// expert at one row block run side by side and read the same weight rows
+// while they are in that XCD's L2.  One 512-thread block per CU streams every 128-k chunk of
 // its items (activations 128 x 128 B e4m3, weights 256 x 64 B e2m1, their
 // scales) global -> LDS with global_load_lds into a 4-stage ring that runs
 // across item boundaries: the copies of the next item are in flight while
@@ -1848,11 +1889,10 @@ constexpr uint32_t PG_A_OFF = 0;          // [4][128 routes][128 B], 16-byte pie
 constexpr uint32_t PG_B_OFF = 65536;      // [4][256 rows][64 B], swizzled
 constexpr uint32_t PG_SB_OFF = 131072;    // [4][256 rows][8 B]: the aligned dword pair holding 4 e8m0 bytes
 constexpr uint32_t PG_SA_OFF = 139264;    // [4][128 routes] f32 block scales
-constexpr uint32_t PG_SINK_OFF = 141312;  // 256 B written by padding copies
-constexpr uint32_t PG_REC_OFF = 141568;   // [2][256 B] item records (48 B used)
+constexpr uint32_t PG_REC_OFF = 141568;   // [2][256 B] item records (48 B used); 141312.. unused
 constexpr uint32_t PG_LIST_OFF = 142080;  // [2][2 KB] tile route lists
 constexpr uint32_t PG_LDS = 146176;
-constexpr uint32_t PG_COPIES = 6;         // per wave per stage
+constexpr uint32_t PG_COPIES = 6;         // copy slots per wave per stage
 constexpr uint32_t PG_MIN_CHUNKS = 10;    // descriptor copies ride on chunks 3 and 6; the list is read at nch - 4
 
 __device__ __attribute__((aligned(16))) const uint8_t kZeroPage[1024] = {0};
@@ -1923,6 +1963,8 @@ struct PgIssue {
     const uint8_t* sa_base;     // uniform: activation scales (or the zero page)
     uint32_t off[PG_COPIES];    // per lane
     uint32_t tail_ok;           // per lane: bit i = slot i's piece lies inside K in the last chunk
+    uint32_t on;                // uniform: bit i = slot i is copied (routes / rows that exist)
+    uint32_t n;                 // uniform: copies per chunk
 };
 
 template <int NMAT>
@@ -1999,9 +2041,10 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
             const uint32_t a_last = (rowoff & ~3u) + 4 * last;
             tail |= (hh == 0 || a_last + 4 < rowoff + SB ? 1u : 0u) << 4;
         }
-        // activation scales
+        // activation scales, stored so that LDS word 4 rr + a of half p holds
+        // route 64 p + 16 a + rr: a lane reads its 4 subtiles' scales at once
         if (wave < 2) {
-            const uint32_t t = 64 * wave + lane;
+            const uint32_t t = 64 * wave + 16 * (lane & 3) + (lane >> 2);
             const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
             S.off[5] = row * nch * 4;
             S.sa_base = reinterpret_cast<const uint8_t*>(A.as);
@@ -2011,6 +2054,17 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
         }
         tail |= 1u << 5;
         S.tail_ok = tail;
+        // Slots with nothing to copy: route groups past the count, weight
+        // rows past N, the activation scales outside waves 0-1.
+        uint32_t on = 0;
+        on |= (8 * wave < count ? 1u : 0u) << 0;
+        on |= (64 + 8 * wave < count ? 1u : 0u) << 1;
+        on |= (rb * RPM + (16 * wave) % RPM < N ? 1u : 0u) << 2;
+        on |= (rb * RPM + (128 + 16 * wave) % RPM < N ? 1u : 0u) << 3;
+        on |= (rb * RPM + (32 * wave) % RPM < N ? 1u : 0u) << 4;
+        on |= (wave < 2 && 64 * wave < count ? 1u : 0u) << 5;
+        S.on = on;
+        S.n = __builtin_popcount(on);
     };
 
     // Copies of chunk c of the issue item into stage ST.
@@ -2019,32 +2073,39 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
         uint8_t* const dA = pg_ring + PG_A_OFF + ST * 16384 + wave * 1024;
         uint8_t* const dB = pg_ring + PG_B_OFF + ST * 16384 + wave * 1024;
         uint8_t* const dS = pg_ring + PG_SB_OFF + ST * 2048 + wave * 256;
-        uint8_t* const dT = wave < 2 ? pg_ring + PG_SA_OFF + ST * 512 + wave * 256 : pg_ring + PG_SINK_OFF;
-        const uint32_t sa_step = wave < 2 ? 4u : 0u;
+        uint8_t* const dT = pg_ring + PG_SA_OFF + ST * 512 + (wave & 1) * 256;
+        const uint32_t on = S.on;
         if (c + 1 < nch) {
             const uint8_t* a = S.a_base + c * 128;
-            __builtin_amdgcn_global_load_lds(a + S.off[0], dA, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(a + S.off[1], dA + 8192, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(S.b_base[0] + c * 64 + S.off[2], dB, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(S.b_base[1] + c * 64 + S.off[3], dB + 8192, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(S.sb_base + c * 4 + S.off[4], dS, 4, 0, 0);
-            __builtin_amdgcn_global_load_lds(S.sa_base + c * sa_step + S.off[5], dT, 4, 0, 0);
+            if (on & 1) __builtin_amdgcn_global_load_lds(a + S.off[0], dA, 16, 0, 0);
+            if (on & 2) __builtin_amdgcn_global_load_lds(a + S.off[1], dA + 8192, 16, 0, 0);
+            if (on & 4) __builtin_amdgcn_global_load_lds(S.b_base[0] + c * 64 + S.off[2], dB, 16, 0, 0);
+            if (on & 8) __builtin_amdgcn_global_load_lds(S.b_base[1] + c * 64 + S.off[3], dB + 8192, 16, 0, 0);
+            if (on & 16) __builtin_amdgcn_global_load_lds(S.sb_base + c * 4 + S.off[4], dS, 4, 0, 0);
+            if (on & 32) __builtin_amdgcn_global_load_lds(S.sa_base + c * 4 + S.off[5], dT, 4, 0, 0);
         } else {
             // Last chunk: pieces past K (and the scale dword past a row's
             // end) come from the zero page.
             const uint32_t ok = S.tail_ok;
             const uint8_t* a = S.a_base + c * 128;
-            __builtin_amdgcn_global_load_lds((ok & 1) ? a + S.off[0] : kZeroPage, dA, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((ok & 2) ? a + S.off[1] : kZeroPage, dA + 8192, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((ok & 4) ? S.b_base[0] + c * 64 + S.off[2] : kZeroPage, dB, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((ok & 8) ? S.b_base[1] + c * 64 + S.off[3] : kZeroPage, dB + 8192, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((ok & 16) ? S.sb_base + c * 4 + S.off[4] : kZeroPage, dS, 4, 0, 0);
-            __builtin_amdgcn_global_load_lds(S.sa_base + c * sa_step + S.off[5], dT, 4, 0, 0);
+            if (on & 1) __builtin_amdgcn_global_load_lds((ok & 1) ? a + S.off[0] : kZeroPage, dA, 16, 0, 0);
+            if (on & 2) __builtin_amdgcn_global_load_lds((ok & 2) ? a + S.off[1] : kZeroPage, dA + 8192, 16, 0, 0);
+            if (on & 4)
+                __builtin_amdgcn_global_load_lds((ok & 4) ? S.b_base[0] + c * 64 + S.off[2] : kZeroPage, dB, 16, 0, 0);
+            if (on & 8)
+                __builtin_amdgcn_global_load_lds((ok & 8) ? S.b_base[1] + c * 64 + S.off[3] : kZeroPage, dB + 8192, 16,
+                                                 0, 0);
+            if (on & 16) __builtin_amdgcn_global_load_lds((ok & 16) ? S.sb_base + c * 4 + S.off[4] : kZeroPage, dS, 4, 0, 0);
+            if (on & 32) __builtin_amdgcn_global_load_lds(S.sa_base + c * 4 + S.off[5], dT, 4, 0, 0);
         }
     };
 
     // ---- first item: descriptor copied synchronously ----
-    uint32_t item = blockIdx.x;
+    // Item s*G + q goes to the block in slot q, and the hardware deals
+    // consecutive blocks to the 8 XCDs in turn: slot q = (b % 8) * (G / 8) +
+    // b / 8 puts consecutive items (the tiles of one expert row block) on
+    // one XCD, where they share its L2 copy of the weight rows.
+    uint32_t item = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
     if (item >= n_items) return;
     if (wave == 0) copy_rec(item, 0);
     wait_vm_imm<0>();
@@ -2059,7 +2120,14 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     bool issuing = true;
     // Issues the next chunk group (one per stage) and moves to the next item
     // after the last chunk of the current one.
+    uint32_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;   // copies this wave issued into each stage
     auto issue_next = [&](auto st_tag) __attribute__((always_inline)) {
+        constexpr uint32_t ST = decltype(st_tag)::value;
+        const uint32_t nq = issuing ? S.n : 0u;
+        if (ST == 0) q0 = nq;
+        if (ST == 1) q1 = nq;
+        if (ST == 2) q2 = nq;
+        if (ST == 3) q3 = nq;
         if (issuing) {
             issue_chunk(S, ic, st_tag);
             if (++ic == nch) {
@@ -2082,7 +2150,7 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     const uint32_t ta = 64 * wm + rr, fa = pg_swz_a(rr);
     const uint32_t LA_lo = ring + PG_A_OFF + ta * 128 + (g ^ fa) * 16;
     const uint32_t LA_hi = ring + PG_A_OFF + ta * 128 + ((g ^ fa) ^ 4u) * 16;
-    const uint32_t LSA = ring + PG_SA_OFF + ta * 4;
+    const uint32_t LSA = ring + PG_SA_OFF + wm * 256 + rr * 16;
     const uint32_t LB = ring + PG_B_OFF + (brow0 + rr) * 64 + (g ^ pg_swz_b(rr)) * 16;
 
     uint32_t cpar = 0, c = 0;              // compute item descriptor slot, chunk
@@ -2150,11 +2218,12 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     // Returns false when the block has no more work.
     auto step = [&](auto st_tag) __attribute__((always_inline)) -> bool {
         constexpr uint32_t ST = decltype(st_tag)::value;
-        // Copy groups issued after this chunk's: the next two chunks (when
-        // they exist), plus wave 0's descriptor copies riding on them.
+        // Copies issued after this chunk's: those of the next two chunks
+        // (counted per stage when issued), plus wave 0's descriptor copies
+        // riding on them.
         const uint32_t l1 = c + 1 < nch ? c + 1 : c + 1 - nch, l2 = c + 2 < nch ? c + 2 : c + 2 - nch;
-        const bool g1 = c + 1 < nch || cnext, g2 = c + 2 < nch || cnext;
-        uint32_t x = (g1 ? PG_COPIES : 0u) + (g2 ? PG_COPIES : 0u);
+        constexpr uint32_t S1 = (ST + 1) % PG_NST, S2 = (ST + 2) % PG_NST;
+        uint32_t x = (S1 == 0 ? q0 : S1 == 1 ? q1 : S1 == 2 ? q2 : q3) + (S2 == 0 ? q0 : S2 == 1 ? q1 : S2 == 2 ? q2 : q3);
         if (wave == 0) x += (l1 == 3 ? 1u : 0u) + (l1 == 6 ? 2u : 0u) + (l2 == 3 ? 1u : 0u) + (l2 == 6 ? 2u : 0u);
         wait_vm(x);
         __builtin_amdgcn_s_barrier();
@@ -2164,36 +2233,42 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
             if (c == 0) copy_rec(item + G, cpar ^ 1u);
             else if (c == 3) copy_list(cpar ^ 1u);
         }
-        // ---- contract chunk c from stage ST ----
-        v4i lo[4], hi[4], w[4];
-        uint32_t sav[4], sbv[4];
-        static_for<4>([&](auto ai) __attribute__((always_inline)) {
-            constexpr uint32_t a = decltype(ai)::value;
-            lo[a] = lds_rd128<ST * 16384 + a * 2048>(LA_lo);
-            hi[a] = lds_rd128<ST * 16384 + a * 2048>(LA_hi);
-            sav[a] = lds_rd32<ST * 512 + a * 64>(LSA);
-        });
-        static_for<4>([&](auto ji) __attribute__((always_inline)) {
-            constexpr uint32_t j = decltype(ji)::value;
-            w[j] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 64>(LB);
-        });
+        // ---- contract chunk c from stage ST (waves without routes skip it) ----
+        if (alim != 0) {
+            v4i lo[4], hi[4], w[4];
+            v4i sa4;
+            uint32_t sbv[4];
+            static_for<4>([&](auto ji) __attribute__((always_inline)) {
+                constexpr uint32_t j = decltype(ji)::value;
+                w[j] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 64>(LB);
+            });
 #pragma unroll
-        for (int j = 0; j < 4; j++) sbv[j] = lds_rd8<ST * 2048>(LSB[j]);
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]), "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]),
-                       "+v"(hi[3]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(sav[0]), "+v"(sav[1]),
-                       "+v"(sav[2]), "+v"(sav[3]), "+v"(sbv[0]), "+v"(sbv[1]), "+v"(sbv[2]), "+v"(sbv[3]));
-        // Scale blocks past K (last chunk) read bytes beyond the row.
-        const bool bvalid = c * 4 + g < SB;
+            for (int j = 0; j < 4; j++) sbv[j] = lds_rd8<ST * 2048>(LSB[j]);
+            sa4 = lds_rd128<ST * 512>(LSA);
+            static_for<4>([&](auto ai) __attribute__((always_inline)) {
+                constexpr uint32_t a = decltype(ai)::value;
+                if (a < alim) {
+                    lo[a] = lds_rd128<ST * 16384 + a * 2048>(LA_lo);
+                    hi[a] = lds_rd128<ST * 16384 + a * 2048>(LA_hi);
+                }
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]), "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]),
+                           "+v"(hi[3]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(sa4), "+v"(sbv[0]),
+                           "+v"(sbv[1]), "+v"(sbv[2]), "+v"(sbv[3]));
+            // Scale blocks past K (last chunk) read bytes beyond the row.
+            const bool bvalid = c * 4 + g < SB;
 #pragma unroll
-        for (int j = 0; j < 4; j++) sbv[j] = bvalid ? sbv[j] : 127u;
+            for (int j = 0; j < 4; j++) sbv[j] = bvalid ? sbv[j] : 127u;
+            const uint32_t sav[4] = {(uint32_t)sa4.x, (uint32_t)sa4.y, (uint32_t)sa4.z, (uint32_t)sa4.w};
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-            if ((uint32_t)a >= alim) continue;
-            const v8i av = v8i{lo[a].x, lo[a].y, lo[a].z, lo[a].w, hi[a].x, hi[a].y, hi[a].z, hi[a].w};
-            const uint32_t se = (sav[a] >> 23) & 0xffu;
+            for (int a = 0; a < 4; a++) {
+                if ((uint32_t)a >= alim) continue;
+                const v8i av = v8i{lo[a].x, lo[a].y, lo[a].z, lo[a].w, hi[a].x, hi[a].y, hi[a].z, hi[a].w};
+                const uint32_t se = (sav[a] >> 23) & 0xffu;
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[a][j] = mfma_fp8_fp4(av, w[j], se, sbv[j], acc[a][j]);
+                for (int j = 0; j < 4; j++) acc[a][j] = mfma_fp8_fp4(av, w[j], se, sbv[j], acc[a][j]);
+            }
         }
         if (++c < nch) return true;
         // ---- end of the item ----
@@ -2421,7 +2496,13 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         if (st != NERVE_HIP_UNSUPPORTED) return st;
     }
     const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
-    moe_prep_kernel<<<1 + (uint32_t)((units + 31) / 32), 1024, 0, stream>>>(ta, Q);
+    {
+        // Block 0 builds the tiles; the others stride over the quantization
+        // units (a few per CU keep the loads in flight).
+        const uint32_t qblocks = (uint32_t)std::min<uint64_t>((units + 31) / 32, (uint64_t)4 * ctx->cu_count);
+        if (E <= 1024) moe_prep_kernel<1024><<<1 + qblocks, 1024, 0, stream>>>(ta, Q);
+        else moe_prep_kernel<MAX_EXPERTS><<<1 + qblocks, 1024, 0, stream>>>(ta, Q);
+    }
     if ((st = nh::check_launch("moe_prep"))) return st;
 
     ExpertArgs ea;

@@ -1217,6 +1217,7 @@ struct StreamArgs {
     TileArgs T;
     const uint16_t* x16;
     uint64_t x_frame, x_seg;
+    uint32_t addr_lds_records;                   // address tables up to this many records are copied to LDS
 };
 
 // One tile as the streaming loop sees it: its parameter pointers, its route
@@ -1615,7 +1616,9 @@ struct FusedTables {
     uint32_t tst[FUSED_MAX_EXPERTS];      // first tile of each expert
     uint32_t rw[FUSED_MAX_SLOTS];         // route index of compacted slot c
     uint32_t rword[FUSED_MAX_SLOTS];      // its route word
+    uint32_t rtab[FUSED_MAX_SLOTS];       // route word of route index r
     uint16_t eslot[FUSED_MAX_SLOTS];      // its expert (NO_EXPERT: skipped)
+    uint16_t rank[FUSED_MAX_SLOTS];       // its position among its expert's slots
     uint8_t valid[FUSED_MAX_EXPERTS];
     uint32_t list[16];                    // slots of the tile being set up
     uint64_t ptr[4];
@@ -1625,13 +1628,16 @@ struct FusedTables {
 
 // Route -> tile tables of one projection, built by every streaming block for
 // itself (the same rules as build_tiles: invalid parameters or expert ids
-// skip a route; 16 routes per tile in slot order).  Two rounds of dependent
-// global loads, then LDS work.  Thread e keeps expert e's resolved pointers.
+// skip a route; 16 routes per tile).  One round of independent global loads
+// (slot words, route map, route words, control words and, when it fits after
+// the tables, the whole address table into LDS), then LDS work.  Each slot's
+// rank among its expert's slots comes from the counting atomic.  Thread e
+// keeps expert e's resolved pointers.
 template <int NW>
-__device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, const uint8_t* (&my_ptr)[4]) {
+__device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, uint32_t* addr_lds, bool addr_in_lds,
+                                             const uint8_t* (&my_ptr)[4]) {
     const uint32_t tid = threadIdx.x, nt = 64 * NW;
     const uint32_t cap = A.batch_width * A.k, P = A.P;
-    // Round 1: slot words of expert tid, route map entry tid, control words.
     uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
 #pragma unroll
     for (uint32_t p = 0; p < 4; p++) {
@@ -1639,16 +1645,30 @@ __device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, 
         if (tid < A.E && p < P && idx < A.n_slot_words) sl[p] = A.slots[idx];
     }
     const uint32_t r0 = tid < cap ? A.frames[(uint64_t)(tid / A.k) * A.frame_words + A.data_words + tid % A.k] : 0u;
+    const uint32_t rt0 = tid < cap ? A.routes[tid] : 0u;
     const uint32_t c2 = A.control[2], c3 = A.control[3];
-    // Round 2: address records, route word.
+    if (addr_in_lds) {
+        const v4i* src = reinterpret_cast<const v4i*>(A.addr);
+        v4i* dst = reinterpret_cast<v4i*>(addr_lds);
+        for (uint32_t i = tid; i < 2 * A.n_records; i += nt) dst[i] = src[i];
+    }
+    if (tid < cap) {
+        F.rw[tid] = r0;
+        F.rtab[tid] = rt0;
+    }
+    for (uint32_t c = tid + nt; c < cap; c += nt) {
+        F.rw[c] = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+        F.rtab[c] = A.routes[c];
+    }
+    __syncthreads();
     uint32_t rec[4][8];
 #pragma unroll
     for (uint32_t p = 0; p < 4; p++) {
         const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
 #pragma unroll
-        for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? A.addr[(uint64_t)sl[p] * 8 + j] : 0u;
+        for (uint32_t j = 0; j < 8; j++)
+            rec[p][j] = !has ? 0u : addr_in_lds ? addr_lds[sl[p] * 8 + j] : A.addr[(uint64_t)sl[p] * 8 + j];
     }
-    const uint32_t w0 = (tid < cap && r0 < cap) ? A.routes[r0] : 0u;
     if (tid < A.E) {
         bool ok = true;
 #pragma unroll
@@ -1663,11 +1683,7 @@ __device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, 
         for (uint32_t p = 0; p < 4; p++)
             my_ptr[p] = reinterpret_cast<const uint8_t*>((uint64_t)rec[p][0] | ((uint64_t)rec[p][1] << 32));
     }
-    if (tid < cap) {
-        F.rw[tid] = r0;
-        F.rword[tid] = w0;
-    }
-    // Experts and slots beyond one per thread take the plain path.
+    // Experts beyond one per thread take the plain path.
     for (uint32_t e = tid + nt; e < A.E; e += nt) {
         bool ok = true;
         for (uint32_t p = 0; p < P; p++) {
@@ -1680,17 +1696,13 @@ __device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, 
     }
     uint32_t n = c2 != 0u ? c3 : cap;
     if (n > cap) n = cap;
-    for (uint32_t c = tid + nt; c < cap; c += nt) {
-        const uint32_t r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-        F.rw[c] = r;
-        F.rword[c] = r < cap ? A.routes[r] : 0u;
-    }
     __syncthreads();
     for (uint32_t c = tid; c < cap; c += nt) {
-        const uint32_t r = F.rw[c], e = F.rword[c] & 0xffffu;
+        const uint32_t r = F.rw[c], w = r < cap ? F.rtab[r] : 0u, e = w & 0xffffu;
+        F.rword[c] = w;
         const bool ok = c < n && r < cap && e < A.E && F.valid[e];
         F.eslot[c] = ok ? (uint16_t)e : NO_EXPERT;
-        if (ok) atomicAdd(&F.cnt[e], 1u);
+        if (ok) F.rank[c] = (uint16_t)atomicAdd(&F.cnt[e], 1u);
     }
     __syncthreads();
     const uint32_t per = (A.E + nt - 1) / nt;
@@ -1726,13 +1738,11 @@ __device__ __forceinline__ TileSrc fused_tile(const StreamArgs& A, FusedTables& 
     }
     __syncthreads();
     const uint32_t e = F.tile_e, kk = F.tile_k;
-    // Rank of each slot among the expert's slots (slot order), block-wide;
-    // the host launches the fused form only when every slot has a thread.
+    // The tile's slots: ranks 16 kk .. 16 kk + 15 of the expert (the host
+    // launches the fused form only when every slot has a thread).
     {
         const uint32_t c = tid;
-        const uint32_t f = (c < cap && F.eslot[c] == e) ? 1u : 0u;
-        const uint32_t rank = block_exclusive_scan(f, F.wave_tot, &F.total);
-        if (f && rank >= 16 * kk && rank < 16 * kk + 16) F.list[rank - 16 * kk] = c;
+        if (c < cap && F.eslot[c] == e && F.rank[c] >= 16 * kk && F.rank[c] < 16 * kk + 16) F.list[F.rank[c] - 16 * kk] = c;
     }
     __syncthreads();
     TileSrc ts;
@@ -1759,8 +1769,10 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     FusedTables& F = *reinterpret_cast<FusedTables*>(ring);
     const uint8_t* my_ptr[4] = {nullptr, nullptr, nullptr, nullptr};
     uint32_t n_tiles;
+    uint32_t* addr_lds = reinterpret_cast<uint32_t*>(ring + (sizeof(FusedTables) + 15) / 16 * 16);
+    const bool addr_in_lds = FUSED && A.T.n_records <= A.addr_lds_records && ((uintptr_t)A.T.addr & 15) == 0;
     if (FUSED) {
-        fused_tables<NW>(A.T, F, my_ptr);
+        fused_tables<NW>(A.T, F, addr_lds, addr_in_lds, my_ptr);
         n_tiles = F.n_tiles;
     } else {
         n_tiles = sload_u32(A.n_tiles);
@@ -1811,7 +1823,7 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     } else {
         for (uint32_t t = b; t < n_tiles; t += G) {
             // The tables share LDS with the ring: rebuild them after a range.
-            if (FUSED && t != b) fused_tables<NW>(A.T, F, my_ptr);
+            if (FUSED && t != b) fused_tables<NW>(A.T, F, addr_lds, addr_in_lds, my_ptr);
             const TileSrc ts = tile_src(t);
             stream_range<MODE, NMAT, NBUF, NW, NSUB, FUSED>(A, t * nrb, (t + 1) * nrb, nrb, ts);
         }
@@ -1835,6 +1847,7 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.copies_per_item = NMAT * (A.lw + A.ls);
     size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
     if (FUSED && lds < sizeof(FusedTables)) lds = sizeof(FusedTables);
+    A.addr_lds_records = FUSED ? (uint32_t)((lds - (sizeof(FusedTables) + 15) / 16 * 16) / 32) : 0u;
     if (lds > 160 * 1024 || A.copies_per_item * (NBUF - 1) > 63) return NERVE_HIP_UNSUPPORTED;
     if (FUSED) {
         // Every compacted slot needs a thread in the tables, and activation

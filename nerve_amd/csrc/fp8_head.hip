@@ -12,13 +12,14 @@
 //
 // Argmax follows greedy_sampler_f32.comp.template:25-109: larger f32 logit
 // wins, ties go to the lower token id.
+#include <algorithm>
 #include <cfloat>
 
 #include "common.h"
 
 namespace nh {
 nerve_hip_status quantize_rows(const uint16_t* x, uint32_t cols, uint32_t rows, bool pow2, uint8_t* q, float* s,
-                               hipStream_t st);
+                               hipStream_t st, uint32_t* zero_word = nullptr);
 }
 
 namespace {
@@ -138,6 +139,141 @@ __global__ __launch_bounds__(64 * HEAD_WAVES) void fp8_head_kernel(HeadArgs A) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Skinny form (M <= 16, the decode LM head): a pure weight stream.  A block of
+// 4 waves owns one group of 16 vocabulary rows at a time and the waves split
+// its K chunks; each wave holds its whole K slice of the group's weights in
+// registers (two sets: the next group's loads are in flight while this one
+// is contracted), the block's activations and block scales sit in LDS, and
+// the 4 partial sums meet in LDS.  The grid is persistent (groups strided
+// over the blocks).
+// ---------------------------------------------------------------------------
+constexpr int SK_WAVES = 4;
+
+template <int CHW>
+struct SkSet {
+    v4i w[CHW][2];
+    uint32_t s[CHW];
+};
+
+template <int CHW>
+__global__ __launch_bounds__(64 * SK_WAVES) void fp8_head_skinny_kernel(HeadArgs A, uint32_t groups) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sk_lds[];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, M = A.M, N = A.N, nblk = (K + 127) / 128;
+    uint8_t* xa = sk_lds;
+    float* xs = reinterpret_cast<float*>(sk_lds + (M * K + 15) / 16 * 16);
+    float* red = xs + (M * nblk + 3) / 4 * 4;          // [3][64][4]
+    for (uint32_t i = tid * 16; i < M * K; i += 64 * SK_WAVES * 16)
+        *reinterpret_cast<v4i*>(xa + i) = *reinterpret_cast<const v4i*>(A.xq + i);
+    for (uint32_t i = tid; i < M * nblk; i += 64 * SK_WAVES) xs[i] = A.xs[i];
+    __syncthreads();
+    float best_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    uint32_t best_i[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+
+    const uint32_t per = (nblk + SK_WAVES - 1) / SK_WAVES;
+    const uint32_t c0 = min(nblk, wave * per), nc = min(per, nblk - c0);
+    // Loads of one group's K slice (unconditional, clamped: out-of-range
+    // pieces are zeroed after the fact, so every load is always issued).
+    auto load = [&](SkSet<CHW>& S, uint32_t grp) __attribute__((always_inline)) {
+        const uint32_t gg = grp < groups ? grp : groups - 1;
+        const uint32_t n = min(gg * 16 + rr, N - 1);
+        const uint8_t* wrow = A.W + (uint64_t)n * K;
+        const uint16_t* srow = A.scale_inv + (uint64_t)(n / A.BR) * nblk;
+#pragma unroll
+        for (int q = 0; q < CHW; q++) {
+            const uint32_t c = c0 + min((uint32_t)q, nc ? nc - 1 : 0u);
+            const uint32_t k = min(c * 128 + 32 * g, K - 32);
+            S.w[q][0] = *reinterpret_cast<const v4i*>(wrow + k);
+            S.w[q][1] = *reinterpret_cast<const v4i*>(wrow + k + 16);
+            S.s[q] = srow[c < nblk ? c : 0];
+        }
+    };
+    auto compute = [&](const SkSet<CHW>& S, uint32_t grp) __attribute__((always_inline)) {
+        const uint32_t n = grp * 16 + rr;
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < CHW; q++) {
+            if ((uint32_t)q >= nc) break;
+            const uint32_t c = c0 + q, k = c * 128 + 32 * g;
+            const bool kv = k < K;
+            v4i a0 = v4i{0, 0, 0, 0}, a1 = v4i{0, 0, 0, 0};
+            if (rr < M && kv) {
+                a0 = *reinterpret_cast<const v4i*>(xa + rr * K + k);
+                a1 = *reinterpret_cast<const v4i*>(xa + rr * K + k + 16);
+            }
+            const v4i b0 = kv ? S.w[q][0] : v4i{0, 0, 0, 0}, b1 = kv ? S.w[q][1] : v4i{0, 0, 0, 0};
+            const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                v8i{a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w}, v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w},
+                v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+            const float sw = bf16_to_f32(S.s[q]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t t = 4 * g + i;
+                const float sx = t < M ? xs[t * nblk + c] : 0.0f;
+                acc[i] = fmaf(p[i], sx * sw, acc[i]);
+            }
+        }
+        if (wave > 0) *reinterpret_cast<v4f*>(red + ((wave - 1) * 64 + lane) * 4) = acc;
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int w = 0; w < SK_WAVES - 1; w++) {
+                const v4f o = *reinterpret_cast<const v4f*>(red + (w * 64 + lane) * 4);
+                acc += o;
+            }
+            const bool cv = n < N;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t t = 4 * g + i;
+                const float v = acc[i] * A.out_scale;
+                if (t < M && cv) {
+                    if (A.logits_f32) A.logits_f32[(uint64_t)t * N + n] = v;
+                    if (A.logits_bf16) A.logits_bf16[(uint64_t)t * N + n] = (uint16_t)f32_to_bf16(v);
+                }
+                if (A.part_val) {
+                    float bv = cv ? v : -INFINITY;
+                    uint32_t bi = cv ? n : 0xffffffffu;
+#pragma unroll
+                    for (int d = 1; d < 16; d <<= 1) {
+                        const float ov = __shfl_xor(bv, d);
+                        const uint32_t oi = __shfl_xor(bi, d);
+                        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                    }
+                    if (better(bv, bi, best_v[i], best_i[i])) {
+                        best_v[i] = bv;
+                        best_i[i] = bi;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    };
+    const uint32_t G = gridDim.x;
+    SkSet<CHW> s0, s1;
+    load(s0, blockIdx.x);
+    for (uint32_t grp = blockIdx.x; grp < groups; grp += 2 * G) {
+        load(s1, grp + G);
+        compute(s0, grp);
+        load(s0, grp + 2 * G);
+        if (grp + G < groups) compute(s1, grp + G);
+    }
+    if (!A.part_val) return;
+    // One argmax partial per block and token (wave 0's lanes hold token
+    // 4 g + i's best); argmax_partials_kernel reduces them.
+    if (wave == 0 && rr == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t t = 4 * g + i;
+            if (t < M) {
+                A.part_val[(uint64_t)t * G + blockIdx.x] = best_v[i];
+                A.part_idx[(uint64_t)t * G + blockIdx.x] = best_i[i];
+            }
+        }
+    }
+}
+
 // Second pass: one block per row over the partials (argmax_candidate_reduce.
 // comp.template:10-37).
 __global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
@@ -212,11 +348,17 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
     if ((uintptr_t)weight_e4m3 & 15) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "weight must be 16-byte aligned");
     const uint32_t M = batch_width, K = s.in, N = s.vocab, nblk = (K + 127) / 128;
     const uint32_t nblocks = (N + 16 * HEAD_WAVES - 1) / (16 * HEAD_WAVES);
+    // Skinny form: <= 16 tokens, K <= 4096 in 32-byte pieces.
+    const bool skinny = M <= 16 && K <= 4096 && K % 32 == 0 && K >= 32;
+    const uint32_t groups = (N + 15) / 16;
+    // Skinny grid: groups strided over 4 blocks per CU.
+    const uint32_t sk_grid = std::min<uint32_t>(groups, 4u * (uint32_t)ctx->cu_count);
+    const uint32_t nparts = skinny ? sk_grid : nblocks;
     nh::Carver cv;
     size_t o_q = cv.take<uint8_t>((size_t)M * K);
     size_t o_s = cv.take<float>((size_t)M * nblk);
-    size_t o_pv = cv.take<float>(argmax_u32 ? (size_t)M * nblocks : 0);
-    size_t o_pi = cv.take<uint32_t>(argmax_u32 ? (size_t)M * nblocks : 0);
+    size_t o_pv = cv.take<float>(argmax_u32 ? (size_t)M * nparts : 0);
+    size_t o_pi = cv.take<uint32_t>(argmax_u32 ? (size_t)M * nparts : 0);
     void* ws = nullptr;
     if ((st = nh::workspace(ctx, cv.offset, &ws))) return st;
     uint8_t* base = static_cast<uint8_t*>(ws);
@@ -239,11 +381,22 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
     A.part_val = argmax_u32 ? reinterpret_cast<float*>(base + o_pv) : nullptr;
     A.part_idx = argmax_u32 ? reinterpret_cast<uint32_t*>(base + o_pi) : nullptr;
     A.nblocks = nblocks;
-    dim3 grid(nblocks, (M + 16 * HEAD_MT - 1) / (16 * HEAD_MT));
-    fp8_head_kernel<<<grid, 64 * HEAD_WAVES, 0, strm>>>(A);
+    if (skinny) {
+        A.nblocks = sk_grid;
+        const uint32_t per = (nblk + SK_WAVES - 1) / SK_WAVES;
+        const size_t lds = ((size_t)M * K + 15) / 16 * 16 + ((size_t)M * nblk + 3) / 4 * 4 * 4 + 3 * 64 * 4 * 4;
+        const uint32_t grid = sk_grid;
+        if (per <= 2) fp8_head_skinny_kernel<2><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
+        else if (per <= 4) fp8_head_skinny_kernel<4><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
+        else if (per <= 6) fp8_head_skinny_kernel<6><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
+        else fp8_head_skinny_kernel<8><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
+    } else {
+        dim3 grid(nblocks, (M + 16 * HEAD_MT - 1) / (16 * HEAD_MT));
+        fp8_head_kernel<<<grid, 64 * HEAD_WAVES, 0, strm>>>(A);
+    }
     if ((st = nh::check_launch("fp8_output_projection"))) return st;
     if (argmax_u32) {
-        argmax_partials_kernel<<<M, 256, 0, strm>>>(A.part_val, A.part_idx, nblocks, static_cast<uint32_t*>(argmax_u32));
+        argmax_partials_kernel<<<M, 256, 0, strm>>>(A.part_val, A.part_idx, A.nblocks, static_cast<uint32_t*>(argmax_u32));
         return nh::check_launch("fp8_output_projection_argmax");
     }
     return nh::ok();

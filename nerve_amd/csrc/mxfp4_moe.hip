@@ -42,6 +42,7 @@ struct QuantArgs {
     uint32_t cols, rows;
     uint8_t* q;              // e4m3 [rows, cols]
     float* s;                // f32 [rows, ceil(cols/128)]
+    uint32_t* zero_word;     // set to 0 by the standalone quantizer (a counter of the next kernel), or null
 };
 
 // One 32-lane cluster quantizes one (row, 128-column block) unit.  All 32
@@ -76,6 +77,7 @@ __device__ __forceinline__ void quant_unit(const QuantArgs& Q, uint32_t unit, ui
 // template:41-59).  8 clusters of 32 lanes per 256-thread block.
 template <bool POW2>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs Q) {
+    if (Q.zero_word && blockIdx.x == 0 && threadIdx.x == 0) *Q.zero_word = 0u;
     quant_unit<POW2>(Q, blockIdx.x * 8 + (threadIdx.x >> 5), threadIdx.x & 31);
 }
 
@@ -2336,6 +2338,7 @@ QuantArgs plain_rows(const uint16_t* x, uint32_t cols, uint32_t rows, uint8_t* q
     Q.rows = rows;
     Q.q = q;
     Q.s = s;
+    Q.zero_word = nullptr;
     return Q;
 }
 
@@ -2343,8 +2346,10 @@ QuantArgs plain_rows(const uint16_t* x, uint32_t cols, uint32_t rows, uint8_t* q
 
 namespace nh {
 nerve_hip_status quantize_rows(const uint16_t* x, uint32_t cols, uint32_t rows, bool pow2, uint8_t* q, float* s,
-                               hipStream_t st) {
-    return launch_quant(plain_rows(x, cols, rows, q, s), pow2, st);
+                               hipStream_t st, uint32_t* zero_word) {
+    QuantArgs Q = plain_rows(x, cols, rows, q, s);
+    Q.zero_word = zero_word;
+    return launch_quant(Q, pow2, st);
 }
 }  // namespace nh
 
@@ -2439,6 +2444,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     // 366-382), every route slice of the intermediate frames for down
     // (quantize_intermediate, …down_batch1_mxfp4.comp.template:332-353).
     QuantArgs Q;
+    Q.zero_word = nullptr;
     if (gate_up) {
         Q = plain_rows(static_cast<const uint16_t*>(act_bf16), H, batch_width, aq, as);
         if (ms.prequant) {

@@ -18,18 +18,19 @@ namespace {
 // ---------------------------------------------------------------------------
 constexpr int RL_WAVES = 8;
 
-__global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint16_t* __restrict__ x,
-                                                                       const uint16_t* __restrict__ W, uint32_t B,
-                                                                       uint32_t H, uint32_t E,
-                                                                       uint16_t* __restrict__ logits) {
-    __shared__ v4f part[RL_WAVES][64];
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// One 16-token x 16-expert tile computed by 8 waves (wave8 = 0..7) that split
+// K; `part` is the tile's [8][64] LDS reduction area.  Every thread of the
+// block must call it (it synchronizes the block); out (global or LDS) gets
+// the bf16 logits at [token * out_stride + expert].
+__device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ W, uint32_t B,
+                                            uint32_t H, uint32_t E, uint32_t b0, uint32_t e0, uint32_t wave8, bool active,
+                                            v4f (*part)[64], uint16_t* out, uint32_t out_stride) {
+    const uint32_t lane = threadIdx.x & 63;
     const uint32_t g = lane >> 4, rr = lane & 15;
-    const uint32_t b0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
     const uint32_t tok = b0 + rr, ex = e0 + rr;
     const uint32_t nsteps = (H + 31) / 32;
     const uint32_t per = (nsteps + RL_WAVES - 1) / RL_WAVES;
-    const uint32_t s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
+    const uint32_t s0 = min(nsteps, wave8 * per), s1 = active ? min(nsteps, s0 + per) : s0;
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
     const bool H8 = (H % 8) == 0;
     auto operands = [&](uint32_t s, v4i& av, v4i& bv) {
@@ -64,9 +65,9 @@ __global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av[u]),
                                                           __builtin_bit_cast(v8bf, bv[u]), acc, 0, 0, 0);
     }
-    part[wave][lane] = acc;
+    part[wave8][lane] = acc;
     __syncthreads();
-    if (wave == 0) {
+    if (wave8 == 0 && active) {
         v4f t = part[0][lane];
 #pragma unroll
         for (int w = 1; w < RL_WAVES; w++) t += part[w][lane];
@@ -74,9 +75,17 @@ __global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             uint32_t bt = b0 + 4 * g + i;
-            if (bt < B && ex < E) logits[(uint64_t)bt * E + ex] = (uint16_t)f32_to_bf16(t[i]);
+            if (bt < B && ex < E) out[(uint64_t)bt * out_stride + ex] = (uint16_t)f32_to_bf16(t[i]);
         }
     }
+}
+
+__global__ __launch_bounds__(64 * RL_WAVES) void router_linear_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ W, uint32_t B,
+                                                                       uint32_t H, uint32_t E,
+                                                                       uint16_t* __restrict__ logits) {
+    __shared__ v4f part[RL_WAVES][64];
+    router_tile(x, W, B, H, E, blockIdx.x * 16, blockIdx.y * 16, threadIdx.x >> 6, true, part, logits, E);
 }
 
 // ---------------------------------------------------------------------------
@@ -96,12 +105,17 @@ __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + expf
 
 // Route words and telemetry (…topk_routed_batch1_bf16.comp.template:168-179),
 // spread over the wave: lane r writes route r, lanes take one counter each.
+// With tel_lds the counts go to that LDS copy of the telemetry array instead.
 __device__ __forceinline__ void topk_publish(uint32_t b, uint32_t lane, const uint32_t* top, const float* wts,
                                              uint32_t total_sel, uint32_t total_res, uint32_t* routes,
-                                             uint32_t* telemetry) {
+                                             uint32_t* telemetry, uint32_t* tel_lds) {
+    auto count = [&](uint32_t i) {
+        if (tel_lds) atomicAdd(&tel_lds[i], 1u);
+        else __hip_atomic_fetch_add(&telemetry[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     if (lane < total_sel) {
         routes[(uint64_t)b * total_sel + lane] = (f32_to_bf16(wts[lane]) << 16) | top[lane];
-        if (telemetry) __hip_atomic_fetch_add(&telemetry[top[lane]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (telemetry) count(top[lane]);
     }
     if (!telemetry) return;
     const uint32_t pairs = total_sel * (total_sel - 1) / 2;
@@ -116,28 +130,36 @@ __device__ __forceinline__ void topk_publish(uint32_t b, uint32_t lane, const ui
         const uint32_t left = top[l], right = top[r];
         if (left < right) {
             const uint32_t preceding = left * (2u * total_res - left - 1u) / 2u;
-            __hip_atomic_fetch_add(&telemetry[total_res + preceding + right - left - 1u], 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            count(total_res + preceding + right - left - 1u);
         }
     }
 }
 
-__global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ logits, const void* __restrict__ bias,
-                                                  uint32_t* __restrict__ routes, uint32_t* __restrict__ telemetry,
-                                                  uint32_t B, TopkParams P) {
-    extern __shared__ float sh[];
-    float* raw = sh;                 // [E] router values (after softcap / activation)
-    uint32_t* sel = reinterpret_cast<uint32_t*>(sh + P.E);  // [E]
-    __shared__ uint32_t top[128];
-    __shared__ float wts[128];
-    __shared__ float smax_sh, sden_sh;
-    __shared__ uint32_t sel_total, res_total;
-    const uint32_t b = blockIdx.x;
-    if (b >= B) return;
-    const uint32_t lane = threadIdx.x;
+// LDS work area of one token's top-k (one wave).
+struct TopkScratch {
+    float* raw;          // [E] router values (after softcap / activation)
+    uint32_t* sel;       // [E]
+    uint32_t* top;       // [128]
+    float* wts;          // [128]
+    float* smax;
+    float* sden;
+    uint32_t* sel_total;
+    uint32_t* res_total;
+};
+
+// Top-k of token b from its E bf16 logits `lg` (global or LDS) by one wave.
+// It synchronizes the block: every wave of the block calls it the same
+// number of times (`valid` false writes nothing).
+__device__ void topk_token(const uint16_t* lg, const void* bias, uint32_t* routes, uint32_t* telemetry, uint32_t b,
+                           bool valid, const TopkParams& P, const TopkScratch& S, uint32_t* tel_lds = nullptr) {
+    const uint32_t lane = threadIdx.x & 63;
     const uint32_t E = P.E;
+    float* raw = S.raw;
+    uint32_t* sel = S.sel;
+    uint32_t* top = S.top;
+    float* wts = S.wts;
     for (uint32_t e = lane; e < E; e += 64) {
-        float v = bf16_to_f32(logits[(uint64_t)b * E + e]);
+        float v = bf16_to_f32(lg[e]);
         if (P.mode == 0 && P.softcap > 0.0f) v = tanhf(v / P.softcap) * P.softcap;
         raw[e] = v;
         sel[e] = 0;
@@ -153,13 +175,13 @@ __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ l
             float s = 0.0f;
             for (uint32_t e = lane; e < E; e += 64) s += expf(raw[e] - m);
             for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d);
-            if (lane == 0) { smax_sh = m; sden_sh = s; }
+            if (lane == 0) { *S.smax = m; *S.sden = s; }
         }
         __syncthreads();
         for (uint32_t e = lane; e < E; e += 64) {
             float v = raw[e];
             if (P.activation == 0) v = sigmoidf_(v);
-            else if (P.activation == 1) v = expf(v - smax_sh) / sden_sh;
+            else if (P.activation == 1) v = expf(v - *S.smax) / *S.sden;
             else v = sqrtf(fmaxf(v, 0.0f) + logf(1.0f + expf(-fabsf(v))));
             raw[e] = v;
         }
@@ -246,13 +268,120 @@ __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ l
                 wts[ins] = w;
             }
         }
-        sel_total = total_sel;
-        res_total = total_res;
+        *S.sel_total = total_sel;
+        *S.res_total = total_res;
     }
     __syncthreads();
-    topk_publish(b, lane, top, wts, sel_total, res_total, routes, telemetry);
+    if (valid) topk_publish(b, lane, top, wts, *S.sel_total, *S.res_total, routes, telemetry, tel_lds);
 }
 
+// Lane-parallel top-k for moe_topk with E <= 64 (lane e holds expert e):
+// the result of topk_token's k arg-max rounds, bit for bit.  Each lane's rank
+// is the number of experts that beat it under the same strict order (value
+// descending, index ascending; a NaN never beats and is never selected), so
+// round r selects the expert of rank r.  Weights use the same formulas and
+// summation orders (selection order, or expert order for the full softmax),
+// carried out identically in every lane.  The block is not synchronized.
+__device__ void topk_token_fast(const uint16_t* lg, const void* bias, uint32_t* routes, uint32_t* telemetry, uint32_t b,
+                                bool valid, const TopkParams& P, uint32_t* tel_lds) {
+    const uint32_t lane = threadIdx.x & 63, E = P.E, k = P.k;
+    const bool have = lane < E;
+    float raw = 0.0f, s = -INFINITY;
+    if (have) {
+        raw = bf16_to_f32(lg[lane]);
+        if (P.softcap > 0.0f) raw = tanhf(raw / P.softcap) * P.softcap;
+        s = P.activation ? sigmoidf_(raw) : raw;
+        if (P.bias == 1) s = s + static_cast<const float*>(bias)[lane];
+        else if (P.bias == 2) s = s + bf16_to_f32(static_cast<const uint16_t*>(bias)[lane]);
+    }
+    const bool nan = have && !(s == s);
+    auto lane_f = [](float v, uint32_t j) __attribute__((always_inline)) {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+    };
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < E; j++) rank += better(lane_f(s, j), j, s, lane) ? 1u : 0u;
+    const bool chosen = have && !nan && rank < k;
+    const uint64_t chosen_mask = __ballot(chosen);
+    // Expert selected in round r (rounds past the selectable experts pick 0,
+    // as topk_token does).
+    auto top_of = [&](uint32_t r) -> uint32_t {
+        const uint64_t m = __ballot(chosen && rank == r);
+        return m ? (uint32_t)__builtin_ctzll(m) : 0u;
+    };
+    const bool sig = P.activation != 0;
+    float maximum = lane_f(raw, top_of(0));
+    float den = 0.0f;
+    if (P.normalize) {
+        // Per-lane terms, then added in selection order.
+        const float term = sig ? sigmoidf_(raw) : expf(raw - maximum);
+        for (uint32_t r = 0; r < k; r++) den += lane_f(term, top_of(r));
+    } else if (!sig) {
+        maximum = -INFINITY;
+        for (uint32_t e = 0; e < E; e++) maximum = fmaxf(maximum, lane_f(raw, e));
+        const float term = expf(raw - maximum);
+        for (uint32_t e = 0; e < E; e++) den += lane_f(term, e);
+    }
+    // Rounds that found nothing select expert 0 with expert 0's logit.
+    const uint32_t nsel = __popcll(chosen_mask);
+    if (!valid) return;
+    if (chosen || (lane == 0 && nsel < k)) {
+        // Position in ascending expert order (the reference's insertion
+        // sort); missing selections are expert 0 and sort first.
+        const uint32_t pos0 = chosen ? (uint32_t)__popcll(chosen_mask & ((1ull << lane) - 1ull)) + (k - nsel) : 0u;
+        const uint32_t copies = chosen ? 1u : k - nsel;
+        float w = sig ? sigmoidf_(raw) : expf(raw - maximum);
+        if (P.normalize || !sig) w /= den;
+        const uint32_t word = (f32_to_bf16(w) << 16) | lane;
+        for (uint32_t c = 0; c < copies; c++) routes[(uint64_t)b * k + pos0 + c] = word;
+    }
+    if (!telemetry) return;
+    auto count = [&](uint32_t i) {
+        if (tel_lds) atomicAdd(&tel_lds[i], 1u);
+        else __hip_atomic_fetch_add(&telemetry[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    // counts[expert] per selection, and every pair of selections (left < right
+    // in the sorted list; equal experts are not counted as a pair).
+    if (chosen) count(lane);
+    if (lane == 0 && nsel < k)
+        for (uint32_t c = 0; c < k - nsel; c++) count(0);
+    if (chosen) {
+        uint64_t higher = chosen_mask & ~((2ull << lane) - 1ull);
+        while (higher) {
+            const uint32_t right = (uint32_t)__builtin_ctzll(higher);
+            higher &= higher - 1ull;
+            count(E + lane * (2u * E - lane - 1u) / 2u + right - lane - 1u);
+        }
+    }
+    if (lane == 0 && nsel < k && nsel > 0) {
+        // Pairs (0, right) between the padding zeros and real selections.
+        for (uint32_t c = 0; c < k - nsel; c++) {
+            uint64_t m = chosen_mask & ~1ull;
+            while (m) {
+                const uint32_t right = (uint32_t)__builtin_ctzll(m);
+                m &= m - 1ull;
+                count(E + right - 1u);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ logits, const void* __restrict__ bias,
+                                                  uint32_t* __restrict__ routes, uint32_t* __restrict__ telemetry,
+                                                  uint32_t B, TopkParams P) {
+    extern __shared__ float sh[];
+    __shared__ uint32_t top[128];
+    __shared__ float wts[128];
+    __shared__ float smax_sh, sden_sh;
+    __shared__ uint32_t sel_total, res_total;
+    const uint32_t b = blockIdx.x;
+    if (b >= B) return;
+    if (P.mode == 0 && P.E <= 64) {
+        topk_token_fast(logits + (uint64_t)b * P.E, bias, routes, telemetry, b, true, P, nullptr);
+        return;
+    }
+    TopkScratch S{sh, reinterpret_cast<uint32_t*>(sh + P.E), top, wts, &smax_sh, &sden_sh, &sel_total, &res_total};
+    topk_token(logits + (uint64_t)b * P.E, bias, routes, telemetry, b, true, P, S);
+}
 
 // ---------------------------------------------------------------------------
 // a7: route compaction (moe_route_compact_batch1.comp.template:26-106,
@@ -400,12 +529,12 @@ __device__ uint32_t compact_owned(const CompactArgs& A, uint32_t* wave_tot, uint
     return *base_sh;
 }
 
-__global__ __launch_bounds__(1024) void compact_kernel(CompactArgs A) {
-    __shared__ uint32_t scratch[16 * COUNT_MAX_EXPERTS];
-    __shared__ uint32_t wave_tot[16];
-    __shared__ uint32_t misc[2];
+// The whole compaction by one block of up to 1024 threads (scratch: 16 *
+// COUNT_MAX_EXPERTS words, wave_tot: 16, misc: 2).
+__device__ void compact_body(const CompactArgs& A, uint32_t* scratch, uint32_t* wave_tot, uint32_t* misc,
+                             const uint32_t* ctl2 = nullptr) {
     uint32_t* control = A.control;
-    if (control[2] != 0u) {
+    if ((ctl2 ? *ctl2 : control[2]) != 0u) {
         const uint32_t owned = compact_owned(A, wave_tot, &misc[0]);
         if (threadIdx.x == 0) {
             control[3] = owned;
@@ -429,6 +558,161 @@ __global__ __launch_bounds__(1024) void compact_kernel(CompactArgs A) {
     compact_rank_loop(A, reinterpret_cast<uint16_t*>(scratch));
 }
 
+__global__ __launch_bounds__(1024) void compact_kernel(CompactArgs A) {
+    __shared__ uint32_t scratch[16 * COUNT_MAX_EXPERTS];
+    __shared__ uint32_t wave_tot[16];
+    __shared__ uint32_t misc[2];
+    compact_body(A, scratch, wave_tot, misc);
+}
+
+// The control words alone (no intermediates to map), by one wave: what
+// compact_body writes when A.frames is null, with the control words read in
+// one round of loads and the owned routes counted by ballots.
+__global__ __launch_bounds__(64) void route_count_kernel(CompactArgs A) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t c0 = A.control[0], c1 = A.control[1], c2 = A.control[2];
+    uint32_t owned = 0;
+    if (c2 != 0u) {
+        for (uint32_t i0 = 0; i0 < A.n; i0 += 64) {
+            const uint32_t i = i0 + lane;
+            const uint32_t e = i < A.n ? (A.routes[i] & 0xffffu) : 0xffffffffu;
+            owned += (uint32_t)__popcll(__ballot(e >= c1 && e < c1 + c2));
+        }
+    }
+    if (lane == 0) {
+        const bool part = c2 != 0u;
+        A.control[3] = part ? owned : A.n;
+        A.control[4] = part ? owned * A.tiles_per_route : A.k * A.tiles_per_route;
+        A.control[5] = part ? 1u : c0;
+        A.control[6] = 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Router projection + top-k + compaction for decode-sized batches in two
+// launches.  router_partial_kernel spreads the projection over many blocks:
+// block (expert tile, K slice) writes f32 partial sums of its 16 experts over
+// its K slice for every token.  route_fused_kernel (one block) adds the
+// slices in slice order, rounds to bf16 (the logits), then runs the top-k
+// (one token per wave) and the compaction with the same code as topk_kernel
+// and compact_kernel.
+// ---------------------------------------------------------------------------
+constexpr uint32_t FR_MAX_TOKENS = 64;
+constexpr uint32_t FR_MAX_EXPERTS = 256;
+constexpr uint32_t FR_SLICES = 16;
+
+__global__ __launch_bounds__(256) void router_partial_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ W, uint32_t B, uint32_t H,
+                                                             uint32_t E, float* __restrict__ part) {
+    __shared__ v4f red[4][64];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t e0 = blockIdx.x * 16, slice = blockIdx.y;
+    const uint32_t nsteps = (H + 31) / 32, per = (nsteps + FR_SLICES - 1) / FR_SLICES;
+    const uint32_t s0 = min(nsteps, slice * per), s1 = min(nsteps, s0 + per);
+    const uint32_t ex = e0 + rr;
+    const bool H8 = (H % 8) == 0;
+    for (uint32_t b0 = 0; b0 < B; b0 += 16) {
+        const uint32_t tok = b0 + rr;
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t s = s0 + wave; s < s1; s += 4) {
+            const uint32_t k0 = s * 32 + g * 8;
+            v4i av = v4i{0, 0, 0, 0}, bv = v4i{0, 0, 0, 0};
+            if (H8) {
+                if (tok < B && k0 < H) av = *reinterpret_cast<const v4i*>(x + (uint64_t)tok * H + k0);
+                if (ex < E && k0 < H) bv = *reinterpret_cast<const v4i*>(W + (uint64_t)ex * H + k0);
+            } else {
+                uint16_t at[8], bt[8];
+                for (int j = 0; j < 8; j++) {
+                    at[j] = (tok < B && k0 + j < H) ? x[(uint64_t)tok * H + k0 + j] : 0;
+                    bt[j] = (ex < E && k0 + j < H) ? W[(uint64_t)ex * H + k0 + j] : 0;
+                }
+                av = *reinterpret_cast<v4i*>(at);
+                bv = *reinterpret_cast<v4i*>(bt);
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bv),
+                                                          acc, 0, 0, 0);
+        }
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            const v4f t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t bt = b0 + 4 * g + i;
+                if (bt < B && ex < E) part[((uint64_t)slice * B + bt) * E + ex] = t[i];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+struct FusedRouteArgs {
+    const float* part;     // [FR_SLICES][B][E] router partial sums
+    uint32_t B;
+    uint16_t* logits;      // optional global copy of the logits
+    const void* bias;
+    uint32_t* routes;
+    uint32_t* telemetry;
+    TopkParams P;
+    CompactArgs C;
+};
+
+constexpr uint32_t FR_LDS_TELEMETRY = 4096;   // telemetry arrays up to this size are counted in LDS
+
+__global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
+    __shared__ uint16_t lg[FR_MAX_TOKENS * FR_MAX_EXPERTS];
+    __shared__ float t_raw[16][FR_MAX_EXPERTS];
+    __shared__ uint32_t t_sel[16][FR_MAX_EXPERTS];
+    __shared__ uint32_t t_top[16][128];
+    __shared__ float t_wts[16][128];
+    __shared__ float t_f[16][2];
+    __shared__ uint32_t t_u[16][2];
+    __shared__ uint32_t rl[1024];                  // route words, [B][total_sel]
+    __shared__ uint32_t tel[FR_LDS_TELEMETRY];
+    __shared__ uint32_t wave_tot[16];
+    __shared__ uint32_t misc[2];
+    __shared__ uint32_t ctl2;
+    const uint32_t wave = threadIdx.x >> 6, E = F.P.E, B = F.B;
+    const uint32_t total_sel = F.P.k + F.P.always_count, total_res = E + F.P.always_count;
+    const uint32_t T = total_res + total_res * (total_res - 1) / 2;
+    const bool tel_in_lds = F.telemetry && T <= FR_LDS_TELEMETRY;
+    if (threadIdx.x == 0) ctl2 = F.C.control[2];
+    if (tel_in_lds)
+        for (uint32_t i = threadIdx.x; i < T; i += blockDim.x) tel[i] = 0;
+    // Logits: the slices added in slice order, rounded to bf16.
+    for (uint32_t i = threadIdx.x; i < B * E; i += blockDim.x) {
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t sl = 0; sl < FR_SLICES; sl++) s += F.part[(uint64_t)sl * B * E + i];
+        lg[i] = (uint16_t)f32_to_bf16(s);
+    }
+    __syncthreads();
+    // Top-k, one token per wave; routes and counts stay in LDS so that no
+    // barrier below waits for global stores or atomics.
+    TopkScratch S{t_raw[wave], t_sel[wave], t_top[wave], t_wts[wave], &t_f[wave][0], &t_f[wave][1], &t_u[wave][0],
+                  &t_u[wave][1]};
+    const bool fast = F.P.mode == 0 && E <= 64;
+    for (uint32_t b0 = 0; b0 < B; b0 += 16) {
+        const uint32_t b = b0 + wave;
+        uint32_t* telp = F.telemetry ? (tel_in_lds ? tel : F.telemetry) : nullptr;
+        if (fast) topk_token_fast(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, tel_in_lds ? tel : nullptr);
+        else topk_token(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, S, tel_in_lds ? tel : nullptr);
+    }
+    __syncthreads();
+    CompactArgs C = F.C;
+    C.routes = rl;
+    compact_body(C, reinterpret_cast<uint32_t*>(&t_raw[0][0]), wave_tot, misc, &ctl2);
+    __syncthreads();
+    // Global outputs last: logits, route words, telemetry counts.
+    if (F.logits)
+        for (uint32_t i = threadIdx.x; i < B * E; i += blockDim.x) F.logits[i] = lg[i];
+    for (uint32_t i = threadIdx.x; i < B * total_sel; i += blockDim.x) F.routes[i] = rl[i];
+    if (tel_in_lds)
+        for (uint32_t i = threadIdx.x; i < T; i += blockDim.x)
+            if (tel[i]) __hip_atomic_fetch_add(&F.telemetry[i], tel[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------
 // a8: weighted combine (moe_reduce_batch1_bf16.comp.template:29-54).
 // ---------------------------------------------------------------------------
@@ -441,6 +725,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* __restrict_
     for (uint32_t r = 0; r < k; r++) acc = round_bf16(acc + bf16_to_f32(eo[((uint64_t)b * k + r) * H + j]));
     out[idx] = (uint16_t)f32_to_bf16(acc * routed_scale);
 }
+
 
 }  // namespace
 
@@ -515,8 +800,71 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
     A.data_words = data_words;
     A.control = static_cast<uint32_t*>(control_u32);
     A.tiles_per_route = tiles;
-    compact_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(A);
+    if (intermediates) compact_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(A);
+    else route_count_kernel<<<1, 64, 0, (hipStream_t)stream>>>(A);
     return nh::check_launch("moe_route_compact");
+}
+
+nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_spec, const char* moe_spec,
+                                           const void* x_bf16, const void* router_weight_bf16, void* logits_bf16,
+                                           const void* bias, void* routes_u32, void* telemetry_u32,
+                                           void* intermediates, void* control_u32, uint32_t batch_width,
+                                           void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::TopkSpec ts;
+    nh::MoeSpec ms;
+    if ((st = nh::parse_topk_spec(topk_spec, &ts))) return st;
+    if ((st = nh::parse_moe_spec(moe_spec, &ms))) return st;
+    if (!x_bf16 || !router_weight_bf16 || !routes_u32 || !control_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (ts.bias != 0 && !bias) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "specialization requires a selection bias");
+    if (ts.experts != ms.experts || ts.k + ts.always_count != ms.k)
+        return nh::fail(NERVE_HIP_INVALID_SPEC, "top-k and projection specializations disagree on experts or k");
+    if (batch_width == 0) return nh::ok();
+    const uint32_t H = ms.hidden;
+    if (batch_width > FR_MAX_TOKENS || ts.experts > FR_MAX_EXPERTS || batch_width * ms.k > 1024 || ts.k > 128 ||
+        ms.k > 128)
+        return nh::fail(NERVE_HIP_UNSUPPORTED, "fused routing takes <= 64 tokens, <= 256 experts, <= 1024 routes");
+    if (H % 8 == 0 && (((uintptr_t)x_bf16 | (uintptr_t)router_weight_bf16) & 15))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "router buffers must be 16-byte aligned");
+    nh::Carver cv;
+    const size_t o_part = cv.take<float>((size_t)FR_SLICES * batch_width * ts.experts);
+    void* ws = nullptr;
+    if ((st = nh::workspace(ctx, cv.offset, &ws))) return st;
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + o_part);
+    router_partial_kernel<<<dim3((ts.experts + 15) / 16, FR_SLICES), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(x_bf16), static_cast<const uint16_t*>(router_weight_bf16), batch_width, H,
+        ts.experts, part);
+    if ((st = nh::check_launch("moe_route_fused (router)"))) return st;
+    FusedRouteArgs F;
+    F.part = part;
+    F.B = batch_width;
+    F.logits = static_cast<uint16_t*>(logits_bf16);
+    F.bias = bias;
+    F.routes = static_cast<uint32_t*>(routes_u32);
+    F.telemetry = static_cast<uint32_t*>(telemetry_u32);
+    F.P.E = ts.experts;
+    F.P.k = ts.k;
+    F.P.always_count = ts.always_count;
+    F.P.mode = ts.mode;
+    F.P.activation = ts.activation;
+    F.P.normalize = ts.normalize;
+    F.P.bias = ts.bias;
+    F.P.softcap = ts.softcap;
+    F.P.routed_scale = ts.routed_scale;
+    F.P.always_weight = ts.always_weight;
+    CompactArgs& A = F.C;
+    A.routes = F.routes;
+    A.n = batch_width * ms.k;
+    A.k = ms.k;
+    A.E = ms.experts;
+    A.frames = static_cast<uint32_t*>(intermediates);
+    A.frame_words = (uint64_t)ms.k * ms.inter / 2 + ms.k;
+    A.data_words = ms.k * ms.inter / 2;
+    A.control = static_cast<uint32_t*>(control_u32);
+    A.tiles_per_route = ms.gate_up ? (ms.inter + 31) / 32 : (ms.hidden + 63) / 64;
+    route_fused_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(F);
+    return nh::check_launch("moe_route_fused");
 }
 
 nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_outputs, void* out_bf16,

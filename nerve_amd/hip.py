@@ -25,6 +25,7 @@ EXPORTS = (
     "nerve_hip_router_linear_bf16",
     "nerve_hip_moe_router_topk",
     "nerve_hip_moe_route_compact",
+    "nerve_hip_moe_route_fused",
     "nerve_hip_mxfp4_moe_gate_up",
     "nerve_hip_mxfp4_moe_down",
     "nerve_hip_moe_reduce",
@@ -41,6 +42,9 @@ STATUS = {
     4: "DEVICE_ERROR",
     5: "OUT_OF_MEMORY",
 }
+
+
+UNSUPPORTED = 3
 
 
 class NerveHipUnavailable(RuntimeError):
@@ -74,6 +78,7 @@ def _declare(lib) -> None:
         "nerve_hip_router_linear_bf16": (ctypes.c_int, [P, P, P, P, U32, U32, U32, P]),
         "nerve_hip_moe_router_topk": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
         "nerve_hip_moe_route_compact": (ctypes.c_int, [P, S, P, P, P, U32, P]),
+        "nerve_hip_moe_route_fused": (ctypes.c_int, [P, S, S, P, P, P, P, P, P, P, P, U32, P]),
         "nerve_hip_mxfp4_moe_gate_up": (ctypes.c_int, [P, S, P, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_mxfp4_moe_down": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_moe_reduce": (ctypes.c_int, [P, P, P, U32, U32, U32, ctypes.c_float, P]),
@@ -182,6 +187,20 @@ class Context:
     def moe_route_compact(self, spec, routes, intermediates, control, batch_width, stream=None):
         _check(self.lib.nerve_hip_moe_route_compact(self.handle, _spec(spec), ptr(routes), ptr(intermediates),
                                                     ptr(control), batch_width, _stream(stream)))
+
+    # ---- a5 + a6 + a7
+    def moe_route_fused(self, topk_spec, moe_spec, x, router_weight, logits, bias, routes, telemetry, intermediates,
+                        control, batch_width, stream=None) -> bool:
+        """One launch for router linear + top-k + compaction.  Returns False
+        (nothing launched) when the batch is too large for the fused form."""
+        st = self.lib.nerve_hip_moe_route_fused(self.handle, _spec(topk_spec), _spec(moe_spec), ptr(x),
+                                                ptr(router_weight), ptr(logits), ptr(bias), ptr(routes),
+                                                ptr(telemetry), ptr(intermediates), ptr(control), batch_width,
+                                                _stream(stream))
+        if st == UNSUPPORTED:
+            return False
+        _check(st)
+        return True
 
     # ---- a3
     def mxfp4_moe_gate_up(self, spec, hidden, hidden_scales, routes, intermediates, addresses, param_slots, control,

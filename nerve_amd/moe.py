@@ -117,6 +117,7 @@ class MoEBlock:
         self.gate_up = gate_up_spec(self.H, self.I, self.E, k, limit)
         self.down = down_spec(self.H, self.I, self.E, k)
         self.topk = topk_spec(self.E, k, sigmoid=sigmoid, normalize=normalize)
+        self.fuse_routing = True
         self._bufs = {}
 
     def buffers(self, B: int) -> dict:
@@ -143,9 +144,13 @@ class MoEBlock:
         c = self.ctx
         b = self.buffers(B)
         bank = self.bank
-        c.router_linear_bf16(hidden, self.router_w, b["logits"], B, self.H, self.E, stream)
-        c.moe_router_topk(self.topk, b["logits"], None, b["routes"], b["telemetry"], B, stream)
-        c.moe_route_compact(self.gate_up, b["routes"], b["inter"], b["control"], B, stream)
+        # Decode-sized batches: router linear + top-k + compaction in one launch.
+        if not (self.fuse_routing and c.moe_route_fused(self.topk, self.gate_up, hidden, self.router_w, b["logits"],
+                                                        None, b["routes"], b["telemetry"], b["inter"], b["control"],
+                                                        B, stream)):
+            c.router_linear_bf16(hidden, self.router_w, b["logits"], B, self.H, self.E, stream)
+            c.moe_router_topk(self.topk, b["logits"], None, b["routes"], b["telemetry"], B, stream)
+            c.moe_route_compact(self.gate_up, b["routes"], b["inter"], b["control"], B, stream)
         c.mxfp4_moe_gate_up(self.gate_up, hidden, None, b["routes"], b["inter"], bank.addresses, bank.gate_slots,
                             b["control"], B, stream)
         c.moe_route_compact(self.down, b["routes"], None, b["control"], B, stream)

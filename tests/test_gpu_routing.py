@@ -6,7 +6,7 @@ import pytest
 
 import oracle
 from nerve_amd import workloads as wl
-from nerve_amd.moe import gate_up_spec, topk_spec
+from nerve_amd.moe import down_spec, gate_up_spec, topk_spec
 
 from helpers import to_dev, to_np
 
@@ -124,6 +124,23 @@ def test_route_compact(ctx, dev, B, k, E, partition):
         assert np.array_equal(fr, np.argsort(routes.reshape(-1) & 0xFFFF, kind="stable"))
 
 
+@pytest.mark.parametrize("B,k,E", [(16, 4, 32), (2048, 4, 128), (1, 1, 8), (300, 6, 64)])
+@pytest.mark.parametrize("partition", [None, (8, 20), (0, 1)])
+def test_route_count_control_words(ctx, dev, B, k, E, partition):
+    """The count stage before down (no intermediates): control words only,
+    with the down projection's 64-row tiles per route."""
+    rng = np.random.default_rng(B + 3 * k + E)
+    routes, _ = oracle.topk(wl.bf16_normal(rng, (B, E)), k, telemetry=False)
+    I, H = 256, 320
+    start, count = partition or (0, 0)
+    control = to_dev(np.array([B, start, count, 9, 9, 9, 9, 9], np.uint32), dev)
+    ctx.moe_route_compact(down_spec(H, I, E, k), to_dev(routes, dev), None, control, B)
+    _, ctl = oracle.route_compact(routes, k, (H + 63) // 64, B, start, count)
+    got = to_np(control, np.uint32)
+    assert np.array_equal(got[:7], ctl)
+    assert got[7] == 9
+
+
 def test_route_compact_expert_ids_beyond_spec(ctx, dev):
     """Garbage expert ids (>= E) still sort by the full 16-bit key, as the
     reference's rank loop does."""
@@ -141,3 +158,73 @@ def test_route_compact_expert_ids_beyond_spec(ctx, dev):
     ctx.moe_route_compact(spec, to_dev(routes, dev), inter, control, B)
     fr = to_np(inter, np.uint32).reshape(B, frame_words)[:, k * I // 2:].reshape(-1)
     assert np.array_equal(fr, np.argsort(ex.reshape(-1), kind="stable"))
+
+
+@pytest.mark.parametrize("B,H,E,k,kind", [
+    (16, 2880, 32, 4, "softmax"),          # the MoE decode block (config 2)
+    (1, 2880, 32, 4, "softmax"),
+    (64, 512, 128, 8, "sigmoid_biasbf16"),
+    (5, 160, 48, 3, "score_softmax"),      # E not a multiple of 32, always-selected experts
+])
+def test_route_fused_matches_separate(ctx, dev, B, H, E, k, kind):
+    """nerve_hip_moe_route_fused: logits within one bf16 ulp of the router linear's
+    (and of the oracle's); routes, telemetry, route map and control words
+    bit-identical to top-k + compaction run on its own logits."""
+    torch = _torch()
+    rng = np.random.default_rng(B * E + k)
+    x = wl.bf16_normal(rng, (B, H))
+    w = wl.bf16_normal(rng, (E, H), 0.05)
+    bias, A = None, 0
+    if kind == "softmax":
+        tspec = topk_spec(E, k)
+    elif kind == "sigmoid_biasbf16":
+        bias = to_dev(wl.bf16_normal(rng, (E,), 0.1), dev)
+        tspec = topk_spec(E, k, sigmoid=True, bias="biasbf16")
+    else:
+        A = 2
+        bias = to_dev(rng.standard_normal(E).astype(np.float32) * np.float32(0.01), dev)
+        tspec = f"moe_router_batch1_score_topk_softmax_bf16_r{E}_k{k}_a{A}w0.5_norm1_scale2.5_biasf32.comp"
+    kt = k + A
+    I = 256
+    mspec = gate_up_spec(H, I, E, kt, 7.0)
+    T = (E + A) + (E + A) * (E + A - 1) // 2
+    frame_words = kt * I // 2 + kt
+
+    def bufs():
+        return dict(logits=torch.zeros(B, E, dtype=torch.int16, device=dev),
+                    routes=torch.zeros(B, kt, dtype=torch.int32, device=dev),
+                    tel=torch.zeros(T, dtype=torch.int32, device=dev),
+                    inter=torch.zeros(B * frame_words, dtype=torch.int32, device=dev),
+                    control=to_dev(np.array([B, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev))
+
+    xd, wd = to_dev(x, dev), to_dev(w, dev)
+    f = bufs()
+    assert ctx.moe_route_fused(tspec, mspec, xd, wd, f["logits"], bias, f["routes"], f["tel"], f["inter"],
+                               f["control"], B)
+    lin = torch.zeros(B, E, dtype=torch.int16, device=dev)
+    ctx.router_linear_bf16(xd, wd, lin, B, H, E)
+    got = wl.bf16_bits_to_f32(to_np(f["logits"], np.uint16)).astype(np.float64)
+    ref = wl.bf16_bits_to_f32(oracle.router_linear(x, w)).astype(np.float64)
+    ulp = np.maximum(np.abs(ref), 1e-30) * 2.0 ** -7
+    assert np.all(np.abs(got - ref) <= ulp + 1e-6)
+    assert np.all(np.abs(got - wl.bf16_bits_to_f32(to_np(lin, np.uint16))) <= ulp + 1e-6)
+    # the separate top-k and compaction on the fused logits
+    s = bufs()
+    ctx.moe_router_topk(tspec, f["logits"], bias, s["routes"], s["tel"], B)
+    ctx.moe_route_compact(mspec, s["routes"], s["inter"], s["control"], B)
+    for name, dt in (("routes", np.uint32), ("tel", np.uint32), ("inter", np.uint32), ("control", np.uint32)):
+        assert np.array_equal(to_np(f[name], dt), to_np(s[name], dt)), name
+    if kind == "softmax":
+        ref, _ = oracle.topk(to_np(f["logits"], np.uint16), k)
+        assert np.array_equal(to_np(f["routes"], np.uint32) & 0xFFFF, ref & 0xFFFF)
+
+
+def test_route_fused_declines_large_batches(ctx, dev):
+    torch = _torch()
+    B, H, E, k = 65, 64, 8, 2
+    routes = torch.zeros(B, k, dtype=torch.int32, device=dev)
+    control = to_dev(np.array([B, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev)
+    x = torch.zeros(B, H, dtype=torch.int16, device=dev)
+    w = torch.zeros(E, H, dtype=torch.int16, device=dev)
+    assert not ctx.moe_route_fused(topk_spec(E, k), gate_up_spec(H, 64, E, k, 7.0), x, w, None, None, routes, None,
+                                   None, control, B)

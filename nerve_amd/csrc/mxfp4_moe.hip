@@ -1251,6 +1251,30 @@ __device__ __forceinline__ void lds_write16(uint8_t* p, v4f v) {
     asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
 }
 
+// max(v, v of lane ^ 16) and max(v, v of lane ^ 32) with the gfx950 row swaps
+// (VALU only: an LDS-routed shuffle would queue behind the LDS copies in
+// flight).  With both operands v, the swap returns rows (0, 0, 2, 2) and
+// (1, 1, 3, 3), resp. halves (lo, lo) and (hi, hi).  For the non-negative,
+// NaN-free block maxima reduced here the order of the max is immaterial.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// 16-byte global load the compiler's wait insertion does not see: the caller
+// waits for it with wait_vm and passes the result through an empty asm before
+// any use.
+__device__ __forceinline__ v4i gload16_untracked(const void* p) {
+    v4i v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+    return v;
+}
+
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef uint32_t u4s __attribute__((ext_vector_type(4)));
@@ -1388,23 +1412,27 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     v4i lo[CH], hi[CH];          // e4m3 operand halves (pre-quantized input)
     float sraw[CH];
     v4i xb[CH][4];               // bf16 operand halves (fused quantization)
-    auto act_request = [&]() {
+    // Which of this lane's activation pieces exist (k0 < K covers a whole
+    // 16-column half since K % 32 == 0).
+    auto piece_ok = [&](uint32_t q, int h) __attribute__((always_inline)) {
+        const uint32_t c = c0 + q, k0 = c * 128 + g * 16 + (h >= 2 ? 64u : 0u);
+        return arow_ok && c < c1 && k0 < K;
+    };
+    auto act_request = [&]() __attribute__((always_inline)) {
         if (FUSED) {
+            // Inline-asm loads: the compiler does not count them, so it adds
+            // no wait for them in front of the weight copies issued next.
+            // Every piece is loaded (absent ones from the row start, which
+            // exists) and zeroed after the wait, so no load sits in a branch.
             const uint16_t* xr = A.x16 + (uint64_t)(ts.in_route / A.k) * A.x_frame + (uint64_t)(ts.in_route % A.k) * A.x_seg;
 #pragma unroll
             for (uint32_t q = 0; q < CH; q++) {
-                const uint32_t c = c0 + q, k0 = c * 128 + g * 16;
+                if (c0 + q >= c1) continue;   // wave-uniform: chunks this wave never contracts
+                const uint32_t k0 = (c0 + q) * 128 + g * 16;
 #pragma unroll
-                for (int h = 0; h < 4; h++) xb[q][h] = v4i{0, 0, 0, 0};
-                if (arow_ok && c < c1) {
-                    if (k0 < K) {
-                        xb[q][0] = *reinterpret_cast<const v4i*>(xr + k0);
-                        xb[q][1] = *reinterpret_cast<const v4i*>(xr + k0 + 8);
-                    }
-                    if (k0 + 64 < K) {
-                        xb[q][2] = *reinterpret_cast<const v4i*>(xr + k0 + 64);
-                        xb[q][3] = *reinterpret_cast<const v4i*>(xr + k0 + 72);
-                    }
+                for (int h = 0; h < 4; h++) {
+                    const uint32_t off = k0 + (h >= 2 ? 64u : 0u) + (h & 1 ? 8u : 0u);
+                    xb[q][h] = gload16_untracked(xr + (piece_ok(q, h) ? off : 0u));
                 }
             }
         } else {
@@ -1432,8 +1460,17 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
             // lanes of a row (g = 0..3) hold the block's 128 columns.
 #pragma unroll
             for (uint32_t q = 0; q < CH; q++) {
+                // Chunks past this wave's share are neither loaded nor contracted.
+                if (c0 + q >= c1) {
+                    av[q] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    sa[q] = 127u;
+                    continue;
+                }
 #pragma unroll
-                for (int h = 0; h < 4; h++) asm volatile("" : "+v"(xb[q][h]));
+                for (int h = 0; h < 4; h++) {
+                    asm volatile("" : "+v"(xb[q][h]));
+                    if (!piece_ok(q, h)) xb[q][h] = v4i{0, 0, 0, 0};
+                }
                 float v[32];
 #pragma unroll
                 for (int h = 0; h < 4; h++)
@@ -1446,8 +1483,8 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
                 float m = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(v[j]));
-                m = fmaxf(m, __shfl_xor(m, 16));
-                m = fmaxf(m, __shfl_xor(m, 32));
+                m = max_xor16(m);
+                m = max_xor32(m);
                 const float sc = pow2_fp8_scale(m);
                 uint32_t pk[8];
                 // sc is a power of two, so v * (1 / sc) equals v / sc.  For a
@@ -1494,18 +1531,28 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         obase = (uint64_t)ts.out_route * N;
     const float wr = bf16_to_f32(ts.out_word >> 16);
 
-    // Prologue: the first items' copies, then the tile's activations; one
-    // wait covers both round trips.
-#pragma unroll
-    for (uint32_t j = 0; j < NBUF - 1; j++)
-        if (i0 + j < i1) issue(i0 + j, j);
+    // Prologue: the tile's activations, then the first item's copies.  Loads
+    // retire in issue order, so waiting until only that item's copies are in
+    // flight lands the activations, which are quantized while the item
+    // streams; the other ring slots are filled after that (issuing them
+    // first would stall this wave until the CU's miss queue drains).  The
+    // loop's first iteration would issue into the last slot; that copy is
+    // already in flight.
     act_request();
-    wait_vm(0);
+    // Every wave's activation loads enter the CU's memory pipeline before
+    // any copy: behind the copies they would wait for HBM-bound traffic.
+    __builtin_amdgcn_s_barrier();
+    const uint32_t pro = min((uint32_t)NBUF, i1 - i0);
+    issue(i0, 0);
+    wait_vm(A.copies_per_item);
     act_finish();
+#pragma unroll
+    for (uint32_t j = 1; j < NBUF; j++)
+        if (j < pro) issue(i0 + j, j);
 
     for (uint32_t i = i0; i < i1; i++) {
         const uint32_t slot = (i - i0) % NBUF;
-        if (i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
+        if (i > i0 && i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
         const uint32_t n0 = (i - tile_base) * RI;
         wait_vm(A.copies_per_item * min((uint32_t)(NBUF - 1), i1 - 1 - i));
         __builtin_amdgcn_s_barrier();
@@ -1610,34 +1657,32 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
 }
 
 // Fused set-up tables (in the LDS ring, before any copy is issued).
-constexpr uint32_t FUSED_MAX_EXPERTS = 1024;
+constexpr uint32_t FUSED_MAX_EXPERTS = 512;
 constexpr uint32_t FUSED_MAX_SLOTS = 1024;
+constexpr uint32_t FUSED_MAX_WAVES = 8;
 
 struct FusedTables {
+    uint64_t eptr[FUSED_MAX_EXPERTS][4];  // resolved parameter pointers of each expert
     uint32_t cnt[FUSED_MAX_EXPERTS];      // valid routes per expert
-    uint32_t tst[FUSED_MAX_EXPERTS];      // first tile of each expert
     uint32_t rw[FUSED_MAX_SLOTS];         // route index of compacted slot c
     uint32_t rword[FUSED_MAX_SLOTS];      // its route word
     uint32_t rtab[FUSED_MAX_SLOTS];       // route word of route index r
     uint16_t eslot[FUSED_MAX_SLOTS];      // its expert (NO_EXPERT: skipped)
     uint16_t rank[FUSED_MAX_SLOTS];       // its position among its expert's slots
     uint8_t valid[FUSED_MAX_EXPERTS];
-    uint32_t list[16];                    // slots of the tile being set up
-    uint64_t ptr[4];
-    uint32_t wave_tot[16];
-    uint32_t total, n_tiles, tile_e, tile_k;
+    uint32_t wlist[FUSED_MAX_WAVES][16];  // per wave: slots of the tile being set up
 };
 
 // Route -> tile tables of one projection, built by every streaming block for
 // itself (the same rules as build_tiles: invalid parameters or expert ids
 // skip a route; 16 routes per tile).  One round of independent global loads
-// (slot words, route map, route words, control words and, when it fits after
-// the tables, the whole address table into LDS), then LDS work.  Each slot's
-// rank among its expert's slots comes from the counting atomic.  Thread e
-// keeps expert e's resolved pointers.
+// (slot words, route map, route words, control words and the whole address
+// table, copied into LDS after the tables), then LDS work.  Each slot's rank
+// among its expert's slots comes from the counting atomic.  The launch has a
+// thread per expert and per compacted slot.
 template <int NW>
-__device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, uint32_t* addr_lds, bool addr_in_lds,
-                                             const uint8_t* (&my_ptr)[4]) {
+__device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, uint32_t* addr_lds) {
+    static_assert(NW <= (int)FUSED_MAX_WAVES, "per-wave lists");
     const uint32_t tid = threadIdx.x, nt = 64 * NW;
     const uint32_t cap = A.batch_width * A.k, P = A.P;
     uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
@@ -1649,7 +1694,7 @@ __device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, 
     const uint32_t r0 = tid < cap ? A.frames[(uint64_t)(tid / A.k) * A.frame_words + A.data_words + tid % A.k] : 0u;
     const uint32_t rt0 = tid < cap ? A.routes[tid] : 0u;
     const uint32_t c2 = A.control[2], c3 = A.control[3];
-    if (addr_in_lds) {
+    {
         const v4i* src = reinterpret_cast<const v4i*>(A.addr);
         v4i* dst = reinterpret_cast<v4i*>(addr_lds);
         for (uint32_t i = tid; i < 2 * A.n_records; i += nt) dst[i] = src[i];
@@ -1658,43 +1703,28 @@ __device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, 
         F.rw[tid] = r0;
         F.rtab[tid] = rt0;
     }
-    for (uint32_t c = tid + nt; c < cap; c += nt) {
-        F.rw[c] = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-        F.rtab[c] = A.routes[c];
-    }
     __syncthreads();
-    uint32_t rec[4][8];
-#pragma unroll
-    for (uint32_t p = 0; p < 4; p++) {
-        const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
-#pragma unroll
-        for (uint32_t j = 0; j < 8; j++)
-            rec[p][j] = !has ? 0u : addr_in_lds ? addr_lds[sl[p] * 8 + j] : A.addr[(uint64_t)sl[p] * 8 + j];
-    }
     if (tid < A.E) {
         bool ok = true;
 #pragma unroll
         for (uint32_t p = 0; p < 4; p++) {
-            if (p >= P) continue;
-            const bool is_weight = (p % 2) == 0;
-            ok = record_valid(sl[p], A.n_records, rec[p], is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u) && ok;
+            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
+            const v4i* r = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
+            const v4i lo = r[0], hi = r[1];
+            uint32_t rec[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                rec[j] = has ? (uint32_t)lo[j] : 0u;
+                rec[4 + j] = has ? (uint32_t)hi[j] : 0u;
+            }
+            if (p < P) {
+                const bool is_weight = (p % 2) == 0;
+                ok = record_valid(sl[p], A.n_records, rec, is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u) && ok;
+            }
+            F.eptr[tid][p] = (uint64_t)rec[0] | ((uint64_t)rec[1] << 32);
         }
         F.valid[tid] = ok ? 1 : 0;
         F.cnt[tid] = 0;
-#pragma unroll
-        for (uint32_t p = 0; p < 4; p++)
-            my_ptr[p] = reinterpret_cast<const uint8_t*>((uint64_t)rec[p][0] | ((uint64_t)rec[p][1] << 32));
-    }
-    // Experts beyond one per thread take the plain path.
-    for (uint32_t e = tid + nt; e < A.E; e += nt) {
-        bool ok = true;
-        for (uint32_t p = 0; p < P; p++) {
-            const bool is_weight = (p % 2) == 0;
-            ok = param_valid(A.addr, A.n_records, A.slots, A.n_slot_words, e * P + p, is_weight ? A.req_w : A.req_s,
-                             is_weight ? 16u : 4u) && ok;
-        }
-        F.valid[e] = ok ? 1 : 0;
-        F.cnt[e] = 0;
     }
     uint32_t n = c2 != 0u ? c3 : cap;
     if (n > cap) n = cap;
@@ -1707,58 +1737,69 @@ __device__ __forceinline__ void fused_tables(const TileArgs& A, FusedTables& F, 
         if (ok) F.rank[c] = (uint16_t)atomicAdd(&F.cnt[e], 1u);
     }
     __syncthreads();
-    const uint32_t per = (A.E + nt - 1) / nt;
-    const uint32_t e0 = min(A.E, tid * per), e1 = min(A.E, e0 + per);
-    uint32_t lt = 0;
-    for (uint32_t e = e0; e < e1; e++) lt += (F.cnt[e] + 15) / 16;
-    uint32_t ot = block_exclusive_scan(lt, F.wave_tot, &F.total);
-    for (uint32_t e = e0; e < e1; e++) {
-        F.tst[e] = ot;
-        ot += (F.cnt[e] + 15) / 16;
+}
+
+// Tiles of the fused tables, computed by each wave on its own (no barrier):
+// expert e owns tiles [first(e), first(e) + ceil(cnt[e] / 16)), first() being
+// the exclusive prefix sum in expert order.  Returns the tile count; for
+// t < count also the tile's expert and its index among the expert's tiles.
+__device__ __forceinline__ uint32_t fused_tile_scan(const FusedTables& F, uint32_t E, uint32_t t, uint32_t& te,
+                                                    uint32_t& tk) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint32_t base = 0;
+    te = 0;
+    tk = 0;
+    for (uint32_t e0 = 0; e0 < E; e0 += 64) {
+        const uint32_t e = e0 + lane;
+        const uint32_t nte = e < E ? (F.cnt[e] + 15u) / 16u : 0u;   // <= 64 (slots <= 1024)
+        uint32_t excl = 0, tot = 0;
+#pragma unroll
+        for (uint32_t bit = 0; bit < 7; bit++) {
+            const uint64_t m = __ballot((nte >> bit) & 1u);
+            excl += (uint32_t)__popcll(m & below) << bit;
+            tot += (uint32_t)__popcll(m) << bit;
+        }
+        const uint32_t first = base + excl;
+        const uint64_t hit = __ballot(nte != 0u && t >= first && t < first + nte);
+        if (hit) {
+            const uint32_t l = (uint32_t)__builtin_ctzll(hit);
+            te = e0 + l;
+            tk = t - (uint32_t)__builtin_amdgcn_readlane((int)first, (int)l);
+        }
+        base += tot;
     }
-    if (tid == 0) F.n_tiles = F.total;
-    __syncthreads();
+    return base;
 }
 
 // Tile `t` of the fused tables: its expert's pointers, its routes and this
-// lane's route ids.
+// lane's route ids.  Ends with a block barrier, after which the ring may be
+// overwritten.
 template <int NW>
-__device__ __forceinline__ TileSrc fused_tile(const StreamArgs& A, FusedTables& F, const uint8_t* const (&my_ptr)[4], uint32_t t) {
+__device__ __forceinline__ TileSrc fused_tile(const StreamArgs& A, FusedTables& F, uint32_t t) {
     const TileArgs& T = A.T;
-    const uint32_t tid = threadIdx.x, nt = 64 * NW;
     const uint32_t cap = T.batch_width * T.k;
-    for (uint32_t e = tid; e < T.E; e += nt) {
-        const uint32_t nte = (F.cnt[e] + 15) / 16;
-        if (t >= F.tst[e] && t < F.tst[e] + nte) {
-            F.tile_e = e;
-            F.tile_k = t - F.tst[e];
-#pragma unroll
-            for (uint32_t p = 0; p < 4; p++)
-                F.ptr[p] = e == tid ? (uint64_t)my_ptr[p]
-                                    : (p < T.P ? (uint64_t)param_ptr(T.addr, T.slots, e * T.P + p) : 0ull);
-        }
-    }
-    __syncthreads();
-    const uint32_t e = F.tile_e, kk = F.tile_k;
-    // The tile's slots: ranks 16 kk .. 16 kk + 15 of the expert (the host
-    // launches the fused form only when every slot has a thread).
-    {
-        const uint32_t c = tid;
-        if (c < cap && F.eslot[c] == e && F.rank[c] >= 16 * kk && F.rank[c] < 16 * kk + 16) F.list[F.rank[c] - 16 * kk] = c;
-    }
-    __syncthreads();
-    TileSrc ts;
-    ts.w[0] = reinterpret_cast<const uint8_t*>(F.ptr[0]);
-    ts.s[0] = reinterpret_cast<const uint8_t*>(F.ptr[1]);
-    ts.w[1] = reinterpret_cast<const uint8_t*>(F.ptr[2]);
-    ts.s[1] = reinterpret_cast<const uint8_t*>(F.ptr[3]);
-    ts.count = min(16u, F.cnt[e] - 16 * kk);
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t e, kk;
+    fused_tile_scan(F, T.E, t, e, kk);
+    // The tile's slots: ranks 16 kk .. 16 kk + 15 of the expert, listed by
+    // this wave for itself (a wave's LDS accesses complete in order).
+    uint32_t* wl = F.wlist[wave];
+    for (uint32_t c = lane; c < cap; c += 64) {
+        const uint32_t rk = F.rank[c];
+        if (F.eslot[c] == e && rk >= 16 * kk && rk < 16 * kk + 16) wl[rk - 16 * kk] = c;
+    }
+    TileSrc ts;
+    ts.w[0] = reinterpret_cast<const uint8_t*>(F.eptr[e][0]);
+    ts.s[0] = reinterpret_cast<const uint8_t*>(F.eptr[e][1]);
+    ts.w[1] = reinterpret_cast<const uint8_t*>(F.eptr[e][2]);
+    ts.s[1] = reinterpret_cast<const uint8_t*>(F.eptr[e][3]);
+    ts.count = min(16u, F.cnt[e] - 16 * kk);
     const uint32_t rr = lane & 15, tl = 4 * (lane >> 4) + wave;
-    ts.in_route = rr < ts.count ? F.rw[F.list[rr]] : 0u;
+    ts.in_route = rr < ts.count ? F.rw[wl[rr]] : 0u;
     const bool ov = wave < 4 && tl < ts.count;
-    ts.out_route = ov ? F.rw[F.list[tl]] : 0u;
-    ts.out_word = ov ? F.rword[F.list[tl]] : 0u;
+    ts.out_route = ov ? F.rw[wl[tl]] : 0u;
+    ts.out_word = ov ? F.rword[wl[tl]] : 0u;
     __syncthreads();
     return ts;
 }
@@ -1769,18 +1810,17 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     const uint32_t N = A.N;
     const uint32_t nrb = (N + 16 * NSUB - 1) / (16 * NSUB);
     FusedTables& F = *reinterpret_cast<FusedTables*>(ring);
-    const uint8_t* my_ptr[4] = {nullptr, nullptr, nullptr, nullptr};
     uint32_t n_tiles;
     uint32_t* addr_lds = reinterpret_cast<uint32_t*>(ring + (sizeof(FusedTables) + 15) / 16 * 16);
-    const bool addr_in_lds = FUSED && A.T.n_records <= A.addr_lds_records && ((uintptr_t)A.T.addr & 15) == 0;
     if (FUSED) {
-        fused_tables<NW>(A.T, F, addr_lds, addr_in_lds, my_ptr);
-        n_tiles = F.n_tiles;
+        fused_tables<NW>(A.T, F, addr_lds);
+        uint32_t te, tk;
+        n_tiles = fused_tile_scan(F, A.T.E, ~0u, te, tk);
     } else {
         n_tiles = sload_u32(A.n_tiles);
     }
     auto tile_src = [&](uint32_t t) -> TileSrc {
-        if (FUSED) return fused_tile<NW>(A, F, my_ptr, t);
+        if (FUSED) return fused_tile<NW>(A, F, t);
         TileSrc ts;
         uint32_t begin, cnt;
         sload_rec(A.recs + t, begin, cnt, ts.w, ts.s);
@@ -1825,7 +1865,7 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     } else {
         for (uint32_t t = b; t < n_tiles; t += G) {
             // The tables share LDS with the ring: rebuild them after a range.
-            if (FUSED && t != b) fused_tables<NW>(A.T, F, addr_lds, addr_in_lds, my_ptr);
+            if (FUSED && t != b) fused_tables<NW>(A.T, F, addr_lds);
             const TileSrc ts = tile_src(t);
             stream_range<MODE, NMAT, NBUF, NW, NSUB, FUSED>(A, t * nrb, (t + 1) * nrb, nrb, ts);
         }
@@ -1850,13 +1890,14 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
     if (FUSED && lds < sizeof(FusedTables)) lds = sizeof(FusedTables);
     A.addr_lds_records = FUSED ? (uint32_t)((lds - (sizeof(FusedTables) + 15) / 16 * 16) / 32) : 0u;
-    if (lds > 160 * 1024 || A.copies_per_item * (NBUF - 1) > 63) return NERVE_HIP_UNSUPPORTED;
+    if (lds > 160 * 1024 || A.copies_per_item * NBUF > 63) return NERVE_HIP_UNSUPPORTED;
     if (FUSED) {
         // Every compacted slot needs a thread in the tables, and activation
         // rows are read in 16-byte pieces.
         const uint32_t cap = A.T.batch_width * A.T.k;
-        if (cap > 64 * NW || cap > FUSED_MAX_SLOTS || A.T.E > FUSED_MAX_EXPERTS || A.T.P > 4 ||
-            ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || A.x_seg % 8)
+        if (cap > 64 * NW || cap > FUSED_MAX_SLOTS || A.T.E > FUSED_MAX_EXPERTS || A.T.E > 64 * NW || A.T.P > 4 ||
+            ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || A.x_seg % 8 || A.T.n_records > A.addr_lds_records ||
+            ((uintptr_t)A.T.addr & 15))
             return NERVE_HIP_UNSUPPORTED;
     }
     static bool attr_set = false;

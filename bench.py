@@ -90,6 +90,35 @@ def batch_event_ms(fn, n, stream, warmup=5):
     return float(a.elapsed_time(b)) / n
 
 
+def graph_event_ms(fn, n, reps=10):
+    """Average duration (ms) of one fn(i, stream) call, for kernels shorter
+    than the host's per-call cost: n calls (i = 0..n-1) are captured once
+    into a HIP graph, and `reps` replays run back to back between one pair of
+    HIP events on the replaying stream.  fn must launch on the stream it is
+    given and must not allocate (one eager call per i runs first, so the
+    library's workspace has its final size before the capture)."""
+    import torch
+
+    for i in range(n):
+        fn(i, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream()
+        for i in range(n):
+            fn(i, s)
+    st = torch.cuda.current_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(reps):
+        g.replay()
+    b.record(st)
+    torch.cuda.synchronize()
+    return float(a.elapsed_time(b)) / (n * reps)
+
+
 def traffic_for(kernel_key):
     """HBM bytes per launch of `kernel_key` from profiles/traffic.json (two
     rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, each scaled by what the
@@ -262,10 +291,10 @@ def mxfp4_gemv(args, ctx, dev):
     s = torch.zeros(1, (K + 127) // 128, dtype=torch.float32, device=dev)
     y = torch.zeros(1, N, dtype=torch.float32, device=dev)
     ctx.quantize_fp8_e4m3(f"quantize_fp8_e4m3_spow2_b128_h{K}.comp", x, 1, q, s)
-    stream = torch.cuda.current_stream()
-    fn = lambda i: ctx.mxfp4_gemv(q, s, 1, K, W[i % copies], S[i % copies], N, y, stream)
-    ms = wall_ms(fn, args.steps, args.warmup)
-    kms = batch_event_ms(fn, max(200, args.steps), stream)
+    call = lambda i, st: ctx.mxfp4_gemv(q, s, 1, K, W[i % copies], S[i % copies], N, y, st)
+    ms = wall_ms(lambda i: call(i, torch.cuda.current_stream()), args.steps, args.warmup)
+    # one launch per call, shorter than the host's per-call cost: graph replay
+    kms = graph_event_ms(call, copies)
     alg = nbytes + K + 4 * 23 + N * 4
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "e4m3xe2m1->f32",
@@ -292,15 +321,15 @@ def int4_gemv(args, ctx, dev):
     x = to_dev(d["x"], dev)
     y = torch.zeros(M, N, dtype=torch.int16, device=dev)
     spec = f"linear_batch16_int4_gptq_sf16_g{G}_{K}x{N}.comp"
-    stream = torch.cuda.current_stream()
-    fn = lambda i: ctx.int4_linear(spec, x, qw[i % copies], sc[i % copies], qz[i % copies], None, y, M, stream)
-    ms = wall_ms(fn, args.steps, args.warmup)
-    kms = batch_event_ms(fn, max(200, args.steps), stream)
+    call = lambda i, st: ctx.int4_linear(spec, x, qw[i % copies], sc[i % copies], qz[i % copies], None, y, M, st)
+    ms = wall_ms(lambda i: call(i, torch.cuda.current_stream()), args.steps, args.warmup)
+    # one launch per call, shorter than the host's per-call cost: graph replay
+    kms = graph_event_ms(call, copies)
     alg = nbytes + M * K * 2 + M * N * 2
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "bf16xint4->f32",
                     {"workload": f"int4_gptq_g128_asym_m{M}_k4096_n14336", "weight_copies_rotated": copies})
-    kname = "int4_gptq_gemv_kernel<16, 128, true>" if M <= 2 else "int4_gptq_fixed_kernel<8, 4, 4>"
+    kname = "int4_gptq_gemv_kernel<16, 128, true>" if M <= 2 else "int4_gptq_fixed_kernel<16, 4, 4>"
     out["roofline"] = {"bound": "hbm", "kernel": kname, "achieved": gbs, "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                        "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
@@ -338,7 +367,9 @@ def fp8_head(args, ctx, dev):
     out = base_line(args, M / (kms * 1e-3), "tokens/s", ms, "e4m3xe4m3->f32",
                     {"workload": f"fp8_lm_head_m{M}_k2880_n201088_argmax"})
     mfma_bound = M >= 512
-    out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": "fp8_head_kernel",
+    kname = ("fp8_head_skinny_kernel (+ row quantization, argmax of the partials)" if M <= 16
+             else "fp8_head_kernel (+ row quantization, argmax of the partials)")
+    out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": kname,
                        "achieved": tf if mfma_bound else gbs, "peak": FP8_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
                        "unit": "TFLOP/s" if mfma_bound else "GB/s",
                        "frac": (tf / FP8_PEAK_TFLOPS) if mfma_bound else (gbs / HBM_PEAK_GBS), "traffic": None,

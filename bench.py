@@ -200,9 +200,9 @@ def moe_decode(args, ctx, dev):
     out["tokens_per_s"] = B / (ms * 1e-3)
     out["step_hbm_gbs"] = step_bytes / (ms * 1e-3) / 1e9
     out["step_hbm_frac"] = out["step_hbm_gbs"] / HBM_PEAK_GBS
-    out["roofline"] = {"bound": "hbm", "kernel": "mx_stream_kernel<GATE_UP> (nerve_hip_mxfp4_moe_gate_up, one launch)",
+    out["roofline"] = {"bound": "hbm", "kernel": "mx_tokens_kernel<3, 8> (nerve_hip_mxfp4_moe_gate_up, one launch)",
                        "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                       "traffic": traffic_for("mx_stream_kernel<1, 2, 3, 8, 1, true>"),
+                       "traffic": traffic_for("mx_tokens_kernel<3, 8>"),
                        "algorithmic_bytes_per_launch": float(np.mean(gate_up_bytes)), "launch_ms": gu_ms}
     return out, data[0]
 

@@ -1220,6 +1220,7 @@ struct StreamArgs {
     const uint16_t* x16;
     uint64_t x_frame, x_seg;
     uint32_t addr_lds_records;                   // address tables up to this many records are copied to LDS
+    uint32_t small_plan;                         // fused set-up by one wave (E <= 64, B k <= 64, >= 64 blocks)
 };
 
 // One tile as the streaming loop sees it: its parameter pointers, its route
@@ -1273,6 +1274,55 @@ __device__ __forceinline__ v4i gload16_untracked(const void* p) {
     v4i v;
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
     return v;
+}
+
+// Blockwise e4m3 quantization of one lane's 32 bf16 values of a 128-column
+// block (the same arithmetic as quant_unit: pow2 scale of the block amax,
+// x / scale rounded to e4m3).  The four lanes of a row (g = 0..3, lanes
+// l, l + 16, l + 32, l + 48) hold the block's 128 columns, so all 64 lanes
+// must call it.  Outputs the MFMA operand and the scale's e8m0 byte.
+__device__ __forceinline__ void quant_chunk_e4m3(const v4i (&x)[4], v8i& out, uint32_t& e8m0) {
+    float v[32];
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t w = (uint32_t)x[h][j];
+            v[h * 8 + 2 * j] = bf16_to_f32((uint16_t)(w & 0xFFFFu));
+            v[h * 8 + 2 * j + 1] = bf16_to_f32((uint16_t)(w >> 16));
+        }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(v[j]));
+    m = max_xor16(m);
+    m = max_xor32(m);
+    const float sc = pow2_fp8_scale(m);
+    uint32_t pk[8];
+    // sc is a power of two, so v * (1 / sc) equals v / sc.  For a finite
+    // block max every quotient lies in [-448, 448], where v_cvt_pk_fp8_f32
+    // rounds exactly like f32_to_e4m3; a NaN input (its code 0x7f / 0xff) or
+    // an infinite max takes the software conversion instead.
+    bool soft = !(m <= 3.4028235e38f);
+    if (!soft) {
+        const float inv = __uint_as_float((254u << 23) - __float_as_uint(sc));
+        uint32_t nan_bytes = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j] * inv, v[4 * j + 1] * inv, 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j + 2] * inv, v[4 * j + 3] * inv, w, true);
+            pk[j] = (uint32_t)w;
+            nan_bytes |= ((pk[j] & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+        }
+        soft = nan_bytes != 0;
+    }
+    if (soft) {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            pk[j] = f32_to_e4m3(v[4 * j] / sc) | (f32_to_e4m3(v[4 * j + 1] / sc) << 8) |
+                    (f32_to_e4m3(v[4 * j + 2] / sc) << 16) | (f32_to_e4m3(v[4 * j + 3] / sc) << 24);
+    }
+    out = v8i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3], (int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]};
+    e8m0 = pow2_to_e8m0(sc);
 }
 
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -1471,48 +1521,9 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
                     asm volatile("" : "+v"(xb[q][h]));
                     if (!piece_ok(q, h)) xb[q][h] = v4i{0, 0, 0, 0};
                 }
-                float v[32];
-#pragma unroll
-                for (int h = 0; h < 4; h++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint32_t w = (uint32_t)xb[q][h][j];
-                        v[h * 8 + 2 * j] = bf16_to_f32((uint16_t)(w & 0xFFFFu));
-                        v[h * 8 + 2 * j + 1] = bf16_to_f32((uint16_t)(w >> 16));
-                    }
-                float m = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 32; j++) m = fmaxf(m, fabsf(v[j]));
-                m = max_xor16(m);
-                m = max_xor32(m);
-                const float sc = pow2_fp8_scale(m);
-                uint32_t pk[8];
-                // sc is a power of two, so v * (1 / sc) equals v / sc.  For a
-                // finite block max every quotient lies in [-448, 448], where
-                // v_cvt_pk_fp8_f32 rounds exactly like f32_to_e4m3; a NaN
-                // input (its code 0x7f / 0xff) or an infinite max takes the
-                // software conversion instead.
-                bool soft = !(m <= 3.4028235e38f);
-                if (!soft) {
-                    const float inv = __uint_as_float((254u << 23) - __float_as_uint(sc));
-                    uint32_t nan_bytes = 0;
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j] * inv, v[4 * j + 1] * inv, 0, false);
-                        w = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * j + 2] * inv, v[4 * j + 3] * inv, w, true);
-                        pk[j] = (uint32_t)w;
-                        nan_bytes |= ((pk[j] & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
-                    }
-                    soft = nan_bytes != 0;
-                }
-                if (soft) {
-#pragma unroll
-                    for (int j = 0; j < 8; j++)
-                        pk[j] = f32_to_e4m3(v[4 * j] / sc) | (f32_to_e4m3(v[4 * j + 1] / sc) << 8) |
-                                (f32_to_e4m3(v[4 * j + 2] / sc) << 16) | (f32_to_e4m3(v[4 * j + 3] / sc) << 24);
-                }
-                av[q] = v8i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3], (int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]};
-                sa[q] = arow_ok ? pow2_to_e8m0(sc) : 127u;
+                uint32_t e8;
+                quant_chunk_e4m3(xb[q], av[q], e8);
+                sa[q] = arow_ok ? e8 : 127u;
             }
         } else {
 #pragma unroll
@@ -1661,7 +1672,19 @@ constexpr uint32_t FUSED_MAX_EXPERTS = 512;
 constexpr uint32_t FUSED_MAX_SLOTS = 1024;
 constexpr uint32_t FUSED_MAX_WAVES = 8;
 
+// A block's whole work as the one-wave set-up publishes it: the tile's
+// parameter pointers, its route ids and words, and the block's row-block
+// range (lo_rb == hi_rb: no work).
+struct SmallPlan {
+    uint64_t ptr[4];
+    uint32_t count, tile, lo_rb, hi_rb;
+    uint32_t route[16];
+    uint32_t word[16];
+    uint32_t cnt[64];                     // valid routes per expert (scratch)
+};
+
 struct FusedTables {
+    SmallPlan plan;                       // the one-wave set-up's result
     uint64_t eptr[FUSED_MAX_EXPERTS][4];  // resolved parameter pointers of each expert
     uint32_t cnt[FUSED_MAX_EXPERTS];      // valid routes per expert
     uint32_t rw[FUSED_MAX_SLOTS];         // route index of compacted slot c
@@ -1672,6 +1695,7 @@ struct FusedTables {
     uint8_t valid[FUSED_MAX_EXPERTS];
     uint32_t wlist[FUSED_MAX_WAVES][16];  // per wave: slots of the tile being set up
 };
+
 
 // Route -> tile tables of one projection, built by every streaming block for
 // itself (the same rules as build_tiles: invalid parameters or expert ids
@@ -1804,6 +1828,144 @@ __device__ __forceinline__ TileSrc fused_tile(const StreamArgs& A, FusedTables& 
     return ts;
 }
 
+// Row-block range of block b when there are at least as many blocks as
+// tiles: tile t gets q or q + 1 blocks, which split its row blocks evenly.
+__device__ __forceinline__ void block_share(uint32_t G, uint32_t b, uint32_t n_tiles, uint32_t nrb, uint32_t& tile,
+                                            uint32_t& lo_rb, uint32_t& hi_rb) {
+    const uint32_t q = G / n_tiles, r = G % n_tiles;
+    // Blocks [0, r (q + 1)) serve tiles 0..r-1 with q + 1 blocks each.
+    uint32_t part, parts;
+    if (b < r * (q + 1)) {
+        tile = b / (q + 1);
+        part = b % (q + 1);
+        parts = q + 1;
+    } else {
+        tile = r + (b - r * (q + 1)) / q;
+        part = (b - r * (q + 1)) % q;
+        parts = q;
+    }
+    lo_rb = nrb * part / parts;
+    hi_rb = nrb * (part + 1) / parts;
+}
+
+// The fused set-up for small decode batches (E <= 64 experts, B k <= 64
+// routes, at least 64 blocks): wave 0 alone computes the block's plan with
+// one lane per expert and one per compacted slot, the same rules as
+// fused_tables (a slot counts when it is below the owned count, its route
+// index and expert are in range and every parameter record of its expert is
+// valid; 16 routes per tile in expert order), while the other waves wait at
+// one barrier.  Routes of a tile are taken in slot order.  The address table
+// is staged in LDS by all waves first.
+__device__ __forceinline__ void fused_small_plan(const TileArgs& A, SmallPlan& S, uint32_t* addr_lds, uint32_t nrb) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t cap = A.batch_width * A.k, P = A.P, E = A.E;
+    uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
+    uint32_t r0 = 0, rt0 = 0, c2 = 0, c3 = 0;
+    if (wave == 0) {
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const uint32_t idx = lane * P + p;
+            if (lane < E && p < P && idx < A.n_slot_words) sl[p] = A.slots[idx];
+        }
+        r0 = lane < cap ? A.frames[(uint64_t)(lane / A.k) * A.frame_words + A.data_words + lane % A.k] : 0u;
+        rt0 = lane < cap ? A.routes[lane] : 0u;
+        c2 = A.control[2];
+        c3 = A.control[3];
+    }
+    {
+        const v4i* src = reinterpret_cast<const v4i*>(A.addr);
+        v4i* dst = reinterpret_cast<v4i*>(addr_lds);
+        for (uint32_t i = tid; i < 2 * A.n_records; i += nt) dst[i] = src[i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // Records of expert `lane`: all eight 16-byte reads first.
+        v4i lo[4], hi[4];
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
+            const v4i* r = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
+            lo[p] = r[0];
+            hi[p] = r[1];
+        }
+        bool valid = lane < E;
+        uint64_t ptr[4];
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
+            uint32_t rec[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                rec[j] = has ? (uint32_t)lo[p][j] : 0u;
+                rec[4 + j] = has ? (uint32_t)hi[p][j] : 0u;
+            }
+            if (p < P) {
+                const bool is_weight = (p % 2) == 0;
+                valid = record_valid(sl[p], A.n_records, rec, is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u) && valid;
+            }
+            ptr[p] = (uint64_t)rec[0] | ((uint64_t)rec[1] << 32);
+        }
+        const uint64_t vmask = __ballot(valid);
+        // Slot `lane`: its route, expert and validity.
+        uint32_t n = c2 != 0u ? c3 : cap;
+        if (n > cap) n = cap;
+        const uint32_t r = r0;
+        // Every lane takes part in the shuffle (a lane reading from an inactive
+        // lane gets 0), and the out-of-range routes are dropped afterwards.
+        const uint32_t wsh = (uint32_t)__shfl((int)rt0, (int)(r & 63u));
+        const uint32_t w = r < cap ? wsh : 0u;
+        const uint32_t e = w & 0xffffu;
+        const bool ok = lane < n && r < cap && e < E && ((vmask >> (e & 63u)) & 1ull);
+        // Slots of the same expert (E <= 64: six bits), rank in slot order.
+        uint64_t same = __ballot(ok);
+#pragma unroll
+        for (uint32_t bit = 0; bit < 6; bit++) {
+            const uint64_t m = __ballot(ok && ((e >> bit) & 1u));
+            same &= ((e >> bit) & 1u) ? m : ~m;
+        }
+        const uint64_t below = (1ull << lane) - 1ull;
+        const uint32_t rank = (uint32_t)__popcll(same & below);
+        // Per-expert counts through LDS (a wave's LDS accesses complete in order).
+        S.cnt[lane] = 0;
+        if (ok && rank == 0) S.cnt[e] = (uint32_t)__popcll(same);
+        const uint32_t cnt = lane < E ? S.cnt[lane] : 0u;
+        // Tiles in expert order: exclusive prefix of ceil(cnt / 16) by bits.
+        const uint32_t nte = (cnt + 15u) / 16u;
+        uint32_t first = 0, total = 0;
+#pragma unroll
+        for (uint32_t bit = 0; bit < 3; bit++) {       // nte <= 4 (cap <= 64)
+            const uint64_t m = __ballot((nte >> bit) & 1u);
+            first += (uint32_t)__popcll(m & below) << bit;
+            total += (uint32_t)__popcll(m) << bit;
+        }
+        uint32_t tile = 0, lo_rb = 0, hi_rb = 0, te = 0, kk = 0;
+        if (total) {
+            block_share(gridDim.x, blockIdx.x, total, nrb, tile, lo_rb, hi_rb);
+            const uint64_t hit = __ballot(nte != 0u && tile >= first && tile < first + nte);
+            te = hit ? (uint32_t)__builtin_ctzll(hit) : 0u;
+            kk = tile - (uint32_t)__builtin_amdgcn_readlane((int)first, (int)te);
+        }
+        const uint32_t tcnt = (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)te);
+        if (ok && e == te && rank >= 16 * kk && rank < 16 * kk + 16) {
+            S.route[rank - 16 * kk] = r;
+            S.word[rank - 16 * kk] = w;
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const uint32_t plo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ptr[p], (int)te);
+            const uint32_t phi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ptr[p] >> 32), (int)te);
+            if (lane == 0) S.ptr[p] = ((uint64_t)phi << 32) | plo;
+        }
+        if (lane == 0) {
+            S.count = total ? min(16u, tcnt - 16 * kk) : 0u;
+            S.tile = tile;
+            S.lo_rb = total ? lo_rb : 0u;
+            S.hi_rb = total ? hi_rb : 0u;
+        }
+    }
+    __syncthreads();
+}
+
 template <int MODE, int NMAT, int NBUF, int NW, int NSUB, bool FUSED>
 __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
@@ -1812,6 +1974,27 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     FusedTables& F = *reinterpret_cast<FusedTables*>(ring);
     uint32_t n_tiles;
     uint32_t* addr_lds = reinterpret_cast<uint32_t*>(ring + (sizeof(FusedTables) + 15) / 16 * 16);
+    if (FUSED && A.small_plan) {
+        SmallPlan& S = F.plan;
+        fused_small_plan(A.T, S, addr_lds, nrb);
+        const uint32_t lo_rb = S.lo_rb, hi_rb = S.hi_rb, tile = S.tile;
+        if (lo_rb >= hi_rb) return;
+        TileSrc ts;
+        ts.w[0] = reinterpret_cast<const uint8_t*>(S.ptr[0]);
+        ts.s[0] = reinterpret_cast<const uint8_t*>(S.ptr[1]);
+        ts.w[1] = reinterpret_cast<const uint8_t*>(S.ptr[2]);
+        ts.s[1] = reinterpret_cast<const uint8_t*>(S.ptr[3]);
+        ts.count = S.count;
+        const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const uint32_t rr = lane & 15, tl = 4 * (lane >> 4) + wave;
+        ts.in_route = rr < ts.count ? S.route[rr] : 0u;
+        const bool ov = wave < 4 && tl < ts.count;
+        ts.out_route = ov ? S.route[tl] : 0u;
+        ts.out_word = ov ? S.word[tl] : 0u;
+        lds_drain();   // the plan is read before any copy can overwrite it
+        stream_range<MODE, NMAT, NBUF, NW, NSUB, FUSED>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb, ts);
+        return;
+    }
     if (FUSED) {
         fused_tables<NW>(A.T, F, addr_lds);
         uint32_t te, tk;
@@ -1846,19 +2029,8 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     const uint32_t G = gridDim.x, b = blockIdx.x;
     if (n_tiles == 0) return;
     if (G >= n_tiles) {
-        const uint32_t q = G / n_tiles, r = G % n_tiles;
-        // Blocks [0, r (q + 1)) serve tiles 0..r-1 with q + 1 blocks each.
-        uint32_t tile, part, parts;
-        if (b < r * (q + 1)) {
-            tile = b / (q + 1);
-            part = b % (q + 1);
-            parts = q + 1;
-        } else {
-            tile = r + (b - r * (q + 1)) / q;
-            part = (b - r * (q + 1)) % q;
-            parts = q;
-        }
-        const uint32_t lo_rb = nrb * part / parts, hi_rb = nrb * (part + 1) / parts;
+        uint32_t tile, lo_rb, hi_rb;
+        block_share(G, b, n_tiles, nrb, tile, lo_rb, hi_rb);
         if (lo_rb >= hi_rb) return;
         const TileSrc ts = tile_src(tile);
         stream_range<MODE, NMAT, NBUF, NW, NSUB, FUSED>(A, tile * nrb + lo_rb, tile * nrb + hi_rb, nrb, ts);
@@ -1891,6 +2063,7 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     if (FUSED && lds < sizeof(FusedTables)) lds = sizeof(FusedTables);
     A.addr_lds_records = FUSED ? (uint32_t)((lds - (sizeof(FusedTables) + 15) / 16 * 16) / 32) : 0u;
     if (lds > 160 * 1024 || A.copies_per_item * NBUF > 63) return NERVE_HIP_UNSUPPORTED;
+    A.small_plan = FUSED && A.T.E <= 64 && A.T.batch_width * A.T.k <= 64 && ctx->cu_count >= 64 ? 1u : 0u;
     if (FUSED) {
         // Every compacted slot needs a thread in the tables, and activation
         // rows are read in 16-byte pieces.
@@ -1909,6 +2082,393 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     }
     mx_stream_kernel<MODE, NMAT, NBUF, NW, NSUB, FUSED><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
     return nh::check_launch("mx_stream_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Decode gate/up in token form (at most 16 tokens, 64 experts, 64 routes).
+//
+// A route's gate/up activations are its token's hidden row, so the MFMA's 16
+// activation rows are simply the batch's tokens: every active expert's weight
+// rows are contracted against all tokens, and the epilogue writes the rows of
+// the (token, slot) routes that select that expert.  The activations then do
+// not depend on the routing, which takes the route tables off the critical
+// path: wave 0 alone loads the routing inputs and builds the plan while waves
+// 1.. load and quantize their K chunks of all tokens.  A work item is 16 rows
+// of gate and up of one active expert; items are numbered expert-major and
+// every block takes an equal contiguous share (no tiles, so shares may cross
+// experts at no cost).  The streaming loop is the stream kernel's: a ring of
+// NBUF LDS slots fed by global_load_lds, a fixed number of copies per wave
+// and item, explicit vmcnt waits and an LDS cross-wave reduction.
+// ---------------------------------------------------------------------------
+constexpr uint32_t TOK_MAX_TOKENS = 16;
+constexpr uint32_t TOK_MAX_EXPERTS = 64;
+
+struct TokPlan {
+    uint64_t ptr[TOK_MAX_EXPERTS][4];             // parameter pointers of active expert u
+    uint32_t mask[TOK_MAX_EXPERTS][TOK_MAX_TOKENS];  // bit j: slot j of token t selects active expert u
+    uint32_t flag[TOK_MAX_EXPERTS];                  // scratch: expert e has a valid slot
+    uint32_t n_act;
+};
+constexpr uint32_t TOK_MAX_RECORDS = 512;            // address table staged by wave 0 in one round
+
+// The body is a device function: the host pass instantiates kernel template
+// bodies, and the gfx950-only builtins below would fail there.
+template <int NBUF, int NW>
+__device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
+    constexpr uint32_t RI = 16, NMAT = 2, NSUB = 1;
+    constexpr uint32_t CH = 32 / NW;                              // chunks per computing wave (K <= (NW-1) CH 128)
+    constexpr uint32_t LWMAX = (32 * NSUB + NW - 1) / NW;
+    constexpr uint32_t LSMAX = (8 * NSUB + NW - 1) / NW;
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    TokPlan& S = *reinterpret_cast<TokPlan*>(ring);
+    uint32_t* addr_lds = reinterpret_cast<uint32_t*>(ring + (sizeof(TokPlan) + 15) / 16 * 16);
+    const TileArgs& T = A.T;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, g = lane >> 4, rr = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
+    const uint32_t nrb = (N + RI - 1) / RI;
+    const uint32_t B = T.batch_width, kr = T.k, cap = B * kr, E = T.E, P = T.P;
+    // Waves 1.. split the K chunks; wave 0 builds the plan and contracts nothing.
+    const uint32_t per = (nch + NW - 2) / (NW - 1);
+    const uint32_t c0 = wave == 0 ? nch : min(nch, (wave - 1) * per), c1 = wave == 0 ? nch : min(nch, c0 + per);
+    const bool row_ok = rr < B;
+
+    // ---- activations: token rr's pieces of this wave's chunks (inline-asm
+    // loads, absent pieces from the row start and zeroed after the wait).
+    v4i xb[CH][4];
+    auto piece_ok = [&](uint32_t q, int h) __attribute__((always_inline)) {
+        const uint32_t c = c0 + q, k0 = c * 128 + g * 16 + (h >= 2 ? 64u : 0u);
+        return row_ok && c < c1 && k0 < K;
+    };
+    // ---- wave 0's routing inputs and address table go to memory first, so
+    // they are not queued behind the activation loads of the other waves.
+    const uint32_t n16 = 2 * T.n_records;
+    uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
+    uint32_t r = 0, rt = 0, c2 = 0, c3 = 0;
+    v4i tab[TOK_MAX_RECORDS * 2 / 64];
+    if (wave == 0) {
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const uint32_t idx = lane * P + p;
+            if (lane < E && p < P && idx < T.n_slot_words) sl[p] = T.slots[idx];
+        }
+        r = lane < cap ? T.frames[(uint64_t)(lane / kr) * T.frame_words + T.data_words + lane % kr] : 0u;
+        rt = lane < cap ? T.routes[lane] : 0u;
+        c2 = T.control[2];
+        c3 = T.control[3];
+        const v4i* src = reinterpret_cast<const v4i*>(T.addr);
+#pragma unroll
+        for (uint32_t j = 0; j < TOK_MAX_RECORDS * 2 / 64; j++) {
+            const uint32_t i = j * 64 + lane;
+            tab[j] = i < n16 ? src[i] : v4i{0, 0, 0, 0};
+        }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (wave != 0) {
+        const uint16_t* xr = A.x16 + (uint64_t)(row_ok ? rr : 0u) * A.x_frame;
+#pragma unroll
+        for (uint32_t q = 0; q < CH; q++) {
+            if (c0 + q >= c1) continue;
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const uint32_t off = (c0 + q) * 128 + g * 16 + (h >= 2 ? 64u : 0u) + (h & 1 ? 8u : 0u);
+                xb[q][h] = gload16_untracked(xr + (piece_ok(q, h) ? off : 0u));
+            }
+        }
+    }
+    v8i av[CH];
+    uint32_t sa[CH];
+    if (wave == 0) {
+        // ---- the plan: the same validity rules as fused_tables.
+        {
+            v4i* dst = reinterpret_cast<v4i*>(addr_lds);
+#pragma unroll
+            for (uint32_t j = 0; j < TOK_MAX_RECORDS * 2 / 64; j++) {
+                const uint32_t i = j * 64 + lane;
+                if (i < n16) dst[i] = tab[j];
+            }
+            v4i* mz = reinterpret_cast<v4i*>(&S.mask[0][0]);
+#pragma unroll
+            for (uint32_t j = 0; j < TOK_MAX_EXPERTS * TOK_MAX_TOKENS / 4 / 64; j++) mz[j * 64 + lane] = v4i{0, 0, 0, 0};
+            S.flag[lane] = 0;
+        }
+        // Records of expert `lane` (a wave's LDS accesses complete in order).
+        v4i lo[4], hi[4];
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < T.n_records;
+            const v4i* rp = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
+            lo[p] = rp[0];
+            hi[p] = rp[1];
+        }
+        bool valid = lane < E;
+        uint64_t ptr[4];
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < T.n_records;
+            uint32_t rec[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                rec[j] = has ? (uint32_t)lo[p][j] : 0u;
+                rec[4 + j] = has ? (uint32_t)hi[p][j] : 0u;
+            }
+            if (p < P) {
+                const bool is_weight = (p % 2) == 0;
+                valid = record_valid(sl[p], T.n_records, rec, is_weight ? T.req_w : T.req_s, is_weight ? 16u : 4u) && valid;
+            }
+            ptr[p] = (uint64_t)rec[0] | ((uint64_t)rec[1] << 32);
+        }
+        const uint64_t vmask = __ballot(valid);
+        // Slot `lane`: route r, its word, expert and validity.
+        uint32_t n = c2 != 0u ? c3 : cap;
+        if (n > cap) n = cap;
+        // Every lane takes part in the shuffle (a lane reading from an inactive
+        // lane gets 0), and the out-of-range routes are dropped afterwards.
+        const uint32_t wsh = (uint32_t)__shfl((int)rt, (int)(r & 63u));
+        const uint32_t w = r < cap ? wsh : 0u;
+        const uint32_t e = w & 0xffffu;
+        const bool ok = lane < n && r < cap && e < E && ((vmask >> (e & 63u)) & 1ull);
+        // Active experts (at least one valid slot), numbered in expert order
+        // (a wave's LDS accesses complete in order).
+        if (ok) S.flag[e] = 1u;
+        const uint64_t act = __ballot(lane < E && S.flag[lane] != 0u);
+        const uint64_t below = (1ull << lane) - 1ull;
+        const uint32_t u_of_lane = (uint32_t)__popcll(act & below);          // lane as an expert id
+        const uint32_t u = (uint32_t)__shfl((int)u_of_lane, (int)(e & 63u)); // active index of this slot's expert
+        if (ok) atomicOr(&S.mask[u][r / kr], 1u << (r % kr));
+        if ((act >> lane) & 1ull) {
+#pragma unroll
+            for (uint32_t p = 0; p < 4; p++) S.ptr[u_of_lane][p] = ptr[p];
+        }
+        if (lane == 0) S.n_act = (uint32_t)__popcll(act);
+    }
+    __syncthreads();
+    // ---- this block's share of the items, and the (at most two) experts it spans
+    const uint32_t n_act = S.n_act;
+    const uint64_t total = (uint64_t)n_act * nrb;
+    const uint32_t i0 = (uint32_t)(total * blockIdx.x / gridDim.x), i1 = (uint32_t)(total * (blockIdx.x + 1) / gridDim.x);
+    if (i0 >= i1) return;
+    const uint32_t u0 = i0 / nrb;
+    const uint32_t u1 = min(u0 + 1, n_act - 1);
+    const uint8_t* wp[2][2];
+    const uint8_t* sp[2][2];
+    wp[0][0] = reinterpret_cast<const uint8_t*>(S.ptr[u0][0]);
+    sp[0][0] = reinterpret_cast<const uint8_t*>(S.ptr[u0][1]);
+    wp[0][1] = reinterpret_cast<const uint8_t*>(S.ptr[u0][2]);
+    sp[0][1] = reinterpret_cast<const uint8_t*>(S.ptr[u0][3]);
+    wp[1][0] = reinterpret_cast<const uint8_t*>(S.ptr[u1][0]);
+    sp[1][0] = reinterpret_cast<const uint8_t*>(S.ptr[u1][1]);
+    wp[1][1] = reinterpret_cast<const uint8_t*>(S.ptr[u1][2]);
+    sp[1][1] = reinterpret_cast<const uint8_t*>(S.ptr[u1][3]);
+    // Output token of this lane (waves 0..3 finalize component `wave`).
+    const uint32_t tok = 4 * g + (wave & 3u);
+    const uint32_t om0 = wave < 4 ? S.mask[u0][tok] : 0u, om1 = wave < 4 ? S.mask[u1][tok] : 0u;
+    lds_drain();   // the plan is read before any copy can overwrite it
+    __builtin_amdgcn_s_barrier();
+
+    uint8_t* red = ring + NBUF * A.slot_bytes;   // [wave][NMAT][lane] v4f partial sums
+    const uint32_t npw = (RI * RB + 1023) / 1024, nps = (RI * SB + 255) / 256;
+    const uint32_t lw = A.lw, ls = A.ls;
+    uint32_t wpos[LWMAX], spos[LSMAX], woff[LWMAX], soff[LSMAX];
+#pragma unroll
+    for (uint32_t q = 0; q < LWMAX; q++) {
+        uint32_t pc = wave + NW * q;
+        if (pc >= npw) pc = wave < npw ? wave : 0;
+        wpos[q] = min(pc * 1024, RI * RB - 1024);
+        woff[q] = wpos[q] + lane * 16;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < LSMAX; q++) {
+        uint32_t pc = wave + NW * q;
+        if (pc >= nps) pc = wave < nps ? wave : 0;
+        spos[q] = min(pc * 256, RI * SB - 256);
+        soff[q] = spos[q] + lane * 4;
+    }
+    // Item i: expert index i / nrb (u0 or u0 + 1), rows (i % nrb) * 16.
+    auto issue = [&](uint32_t item, uint32_t slot) __attribute__((always_inline)) {
+        const uint32_t second = item / nrb != u0 ? 1u : 0u;
+        const uint32_t n0 = (item - (u0 + second) * nrb) * RI;
+        const uint32_t rows = min(RI, N - n0);
+        const uint32_t wbytes = rows * RB, sbytes = rows * SB;
+        uint8_t* dst = ring + slot * A.slot_bytes;
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) {
+            const uint8_t* ws = (second ? wp[1][m] : wp[0][m]) + (uint64_t)n0 * RB;
+#pragma unroll
+            for (uint32_t q = 0; q < LWMAX; q++)
+                if (q < lw)
+                    __builtin_amdgcn_global_load_lds(ws + (woff[q] < wbytes ? woff[q] : 0),
+                                                     dst + m * A.w_region + wpos[q], 16, 0, 0);
+            const uint8_t* ss = (second ? sp[1][m] : sp[0][m]) + (uint64_t)n0 * SB;
+#pragma unroll
+            for (uint32_t q = 0; q < LSMAX; q++)
+                if (q < ls)
+                    __builtin_amdgcn_global_load_lds(ss + (soff[q] < sbytes ? soff[q] : 0),
+                                                     dst + NMAT * A.w_region + m * A.s_region + spos[q], 4, 0, 0);
+        }
+    };
+    uint32_t rw[CH], rs[CH];
+    bool kvalid[CH];
+#pragma unroll
+    for (uint32_t q = 0; q < CH; q++) {
+        const uint32_t c = c0 + q, kb = c * 128 + g * 32;
+        kvalid[q] = c < c1 && kb < K;
+        const uint32_t kk = kvalid[q] ? kb : 0;
+        rw[q] = rr * RB + kk / 2;
+        rs[q] = NMAT * A.w_region + rr * SB + kk / 32;
+    }
+
+    // Prologue: the first item's copies, then the quantization while it
+    // streams, then the other ring slots (issuing every slot up front stalls
+    // the wave at issue until the CU's miss queue drains).
+    const uint32_t pro = min((uint32_t)NBUF, i1 - i0);
+    issue(i0, 0);
+    if (wave != 0) {
+        // ---- quantize this wave's chunks of all tokens: loads retire in
+        // issue order, so once only the first item's copies are in flight
+        // the activations have landed.
+        wait_vm(A.copies_per_item);
+#pragma unroll
+        for (uint32_t q = 0; q < CH; q++) {
+            if (c0 + q >= c1) {
+                av[q] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                sa[q] = 127u;
+                continue;
+            }
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                asm volatile("" : "+v"(xb[q][h]));
+                if (!piece_ok(q, h)) xb[q][h] = v4i{0, 0, 0, 0};
+            }
+            uint32_t e8;
+            quant_chunk_e4m3(xb[q], av[q], e8);
+            sa[q] = row_ok ? e8 : 127u;
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 1; j < NBUF; j++)
+        if (j < pro) issue(i0 + j, j);
+
+    for (uint32_t i = i0; i < i1; i++) {
+        const uint32_t slot = (i - i0) % NBUF;
+        if (i > i0 && i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
+        const uint32_t second = i / nrb != u0 ? 1u : 0u;
+        const uint32_t n0 = (i - (u0 + second) * nrb) * RI;
+        wait_vm(A.copies_per_item * min((uint32_t)(NBUF - 1), i1 - 1 - i));
+        __builtin_amdgcn_s_barrier();
+        const uint8_t* buf = ring + slot * A.slot_bytes;
+        v4f acc[NMAT];
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
+        if (c0 < c1) {
+#pragma unroll
+            for (uint32_t q0 = 0; q0 < CH; q0 += 4) {
+                if (c0 + q0 >= c1) continue;
+                v4i w[4][NMAT];
+                uint32_t sw[4][NMAT];
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++)
+#pragma unroll
+                    for (uint32_t m = 0; m < NMAT; m++) {
+                        w[q][m] = lds_read16(buf + m * A.w_region + rw[q0 + q]);
+                        sw[q][m] = lds_read_u8(buf + m * A.s_region + rs[q0 + q]);
+                    }
+                lds_drain();
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++) {
+                    if (c0 + q0 + q >= c1) continue;
+#pragma unroll
+                    for (uint32_t m = 0; m < NMAT; m++) {
+                        v4i wv = w[q][m];
+                        uint32_t s8 = sw[q][m];
+                        asm volatile("" : "+v"(wv), "+v"(s8));
+                        if (!kvalid[q0 + q]) {
+                            wv = v4i{0, 0, 0, 0};
+                            s8 = 127;
+                        }
+                        acc[m] = mfma_fp8_fp4(av[q0 + q], wv, sa[q0 + q], s8, acc[m]);
+                    }
+                }
+            }
+        }
+        // Software wait states between the last MFMA and the inline-asm LDS
+        // write of its result (see stream_range).
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc[m]));
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) lds_write16(red + ((wave * NMAT + m) * 64 + lane) * 16, acc[m]);
+        lds_drain();
+        __builtin_amdgcn_s_barrier();
+        if (wave >= 4) continue;
+        const uint32_t om = second ? om1 : om0;
+        float tsum[NMAT];
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) {
+            uint32_t v[NW];
+#pragma unroll
+            for (uint32_t w2 = 0; w2 < NW; w2++) v[w2] = lds_read_b32(red + ((w2 * NMAT + m) * 64 + lane) * 16 + 4 * wave);
+            lds_drain();
+            float sum = 0.0f;
+#pragma unroll
+            for (uint32_t w2 = 0; w2 < NW; w2++) {
+                asm volatile("" : "+v"(v[w2]));
+                sum += __uint_as_float(v[w2]);
+            }
+            tsum[m] = sum;
+        }
+        const uint32_t nrow = n0 + rr;
+        if (om != 0u && nrow < N) {
+            float gv = round_bf16(tsum[0]);
+            float uv = round_bf16(tsum[1]);
+            if (A.limit > 0.0f) {
+                gv = fminf(gv, A.limit);
+                uv = fminf(fmaxf(uv, -A.limit), A.limit);
+            }
+            const uint16_t h = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
+            for (uint32_t bits = om; bits; bits &= bits - 1u) {
+                const uint32_t j = (uint32_t)__builtin_ctz(bits);
+                A.out16[(uint64_t)tok * A.frame_elems + (uint64_t)j * N + nrow] = h;
+            }
+        }
+    }
+}
+
+template <int NBUF, int NW>
+__global__ __launch_bounds__(64 * NW) void mx_tokens_kernel(StreamArgs A) {
+    mx_tokens_body<NBUF, NW>(A);
+}
+
+// Launches the token-form gate/up kernel, or returns UNSUPPORTED when the
+// batch or the shape does not fit it.
+template <int NBUF, int NW>
+nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream_t st) {
+    constexpr uint32_t RI = 16, CH = 32 / NW;
+    const uint32_t nch = (A.K + 127) / 128;
+    if (A.T.batch_width > TOK_MAX_TOKENS || A.T.E > TOK_MAX_EXPERTS || A.T.batch_width * A.T.k > 64 || A.T.P != 4 ||
+        A.T.n_records > TOK_MAX_RECORDS || A.K % 32 || A.K > 4096 || (nch + NW - 2) / (NW - 1) > CH || RI * (A.K / 32) < 256 || A.x_seg != 0 ||
+        ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || ((uintptr_t)A.T.addr & 15) || A.T.k > 32 ||
+        (uint32_t)ctx->cu_count < A.T.E)   // >= E blocks: a block's share spans at most two experts
+        return NERVE_HIP_UNSUPPORTED;
+    A.w_region = RI * (A.K / 2);
+    A.s_region = RI * (A.K / 32);
+    A.slot_bytes = 2 * (A.w_region + A.s_region);
+    const uint32_t npw = (A.w_region + 1023) / 1024, nps = (A.s_region + 255) / 256;
+    A.lw = (npw + NW - 1) / NW;
+    A.ls = (nps + NW - 1) / NW;
+    A.copies_per_item = 2 * (A.lw + A.ls);
+    const size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * 2 * 64 * 16;
+    const size_t plan = (sizeof(TokPlan) + 15) / 16 * 16 + (size_t)A.T.n_records * 32;
+    if (lds > 160 * 1024 || plan > lds || A.copies_per_item * NBUF > 63) return NERVE_HIP_UNSUPPORTED;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)mx_tokens_kernel<NBUF, NW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024) != hipSuccess)
+            return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for mx_tokens_kernel");
+        attr_set = true;
+    }
+    mx_tokens_kernel<NBUF, NW><<<ctx->cu_count, 64 * NW, lds, st>>>(A);
+    return nh::check_launch("mx_tokens_kernel");
 }
 
 // ---------------------------------------------------------------------------
@@ -2545,7 +3105,8 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
             fa.x_frame = H;
             fa.x_seg = 0;
             fa.out16 = static_cast<uint16_t*>(intermediates);
-            st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1, true>(fa, ctx, stream);
+            st = launch_tokens<3, 8>(fa, ctx, stream);
+            if (st == NERVE_HIP_UNSUPPORTED) st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1, true>(fa, ctx, stream);
         } else {
             fa.x16 = frames16;
             fa.x_frame = frame_words * 2;

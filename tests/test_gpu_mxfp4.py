@@ -199,11 +199,14 @@ def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
     assert rel_err_normwise(wl.bf16_bits_to_f32(to_np(rig.out, np.uint16)), out_chain) <= 2e-2
 
 
-def test_fail_closed_invalid_metadata(ctx, dev):
+# H = 128: the span kernels; H = 512: the token-form gate_up kernel and the
+# streaming down kernel.
+@pytest.mark.parametrize("H,I", [(128, 128), (512, 256)])
+def test_fail_closed_invalid_metadata(ctx, dev, H, I):
     """mxfp4_tests.rs:218-315: invalid expert ids, unbound slots, non-resident
     records, zero generation and short byte counts write nothing."""
     torch = _torch()
-    E, k, B, H, I = 4, 2, 2, 128, 128
+    E, k, B = 4, 2, 2
     d, _, hidden = _moe_case(E, k, B, H, I, seed=7)
     # token 0: expert 0 (valid) and expert 9 (>= E); token 1: expert 1 (to be
     # invalidated) and expert 2 (valid)
@@ -229,6 +232,55 @@ def test_fail_closed_invalid_metadata(ctx, dev):
         assert np.all(h[1, 0] == sentinel), name           # invalidated expert record
         assert not np.any(h[0, 0] == sentinel), name       # valid routes still computed
         assert not np.any(h[1, 1] == sentinel), name
+
+
+# E <= 64: the token-form gate_up kernel; E = 80: the streaming kernel's tiles.
+@pytest.mark.parametrize("E", [8, 80])
+def test_gate_up_repeated_expert_in_a_token(ctx, dev, E):
+    """A token may list one expert in several slots (top-k padding of an
+    all-NaN row repeats expert 0): every such route gets its own frame."""
+    k, B, H, I = 3, 5, 512, 256
+    d, _, hidden = _moe_case(E, k, B, H, I, seed=31 + E)
+    ex = np.array([[0, 0, 3], [1, 2, 0], [5, 5, 5], [7, 1, 0], [2, 3, 4]])
+    routes = _route_words(ex, np.full((B, k), 0.25, np.float32))
+    rig = MoeRig(dev, d, routes)
+    rig.run(ctx, hidden)
+    cmap, _ = oracle.route_compact(routes, k, (I + 31) // 32, B)
+    h_ref = oracle.moe_gate_up(hidden, routes, cmap, B * k, k, d["gate_w"], d["gate_s"], d["up_w"], d["up_s"], 7.0)
+    ok, worst, exact = bf16_close(rig.h_np(), h_ref)
+    assert ok and exact > 0.9, (worst, exact)
+    h = rig.h_np()
+    assert np.array_equal(h[0, 0], h[0, 1]) and np.array_equal(h[2, 0], h[2, 2])
+
+
+@pytest.mark.parametrize("E,start,count", [(32, 8, 12), (80, 30, 40)])
+def test_owned_expert_range_gate_up_down(ctx, dev, E, start, count):
+    """Expert-parallel ownership (BatchControl expert_start/expert_count,
+    moe_route_compact_batch1.comp.template:27-59): only routes of owned
+    experts are computed; every other frame and output row is left as it was."""
+    k, B, H, I = 4, 16, 512, 256
+    d, routes, hidden = _moe_case(E, k, B, H, I, seed=E + start)
+    rig = MoeRig(dev, d, routes)
+    rig.control = to_dev(np.array([B, start, count, 0, 0, 0, 0, 0], np.uint32), dev)
+    rig.inter.fill_(0x7F7F7F7F)
+    rig.expert_out.fill_(0x7F7F)
+    rig.run(ctx, hidden)
+    cmap, ctl = oracle.route_compact(routes, k, (I + 31) // 32, B, start, count)
+    n = int(ctl[3])
+    assert 0 < n < B * k
+    sentinel_h = np.full((B, k, I), 0x7F7F, np.uint16)
+    h_ref = oracle.moe_gate_up(hidden, routes, cmap, n, k, d["gate_w"], d["gate_s"], d["up_w"], d["up_s"], 7.0,
+                               inter=sentinel_h)
+    owned = ((routes & 0xFFFF) >= start) & ((routes & 0xFFFF) < start + count)
+    h = rig.h_np()
+    assert np.all(h[~owned] == 0x7F7F)
+    ok, worst, exact = bf16_close(h[owned], h_ref[owned])     # compared on owned routes only
+    assert ok and exact > 0.9, (worst, exact)
+    eo_ref = oracle.moe_down(h, routes, cmap, n, d["down_w"], d["down_s"], out=np.full((B, k, H), 0x7F7F, np.uint16))
+    eo = to_np(rig.expert_out, np.uint16)
+    assert np.all(eo[~owned] == 0x7F7F)
+    ok, worst, exact = bf16_close(eo[owned], eo_ref[owned])
+    assert ok and exact > 0.9, (worst, exact)
 
 
 def test_moe_prefill_config3_subset(ctx, dev):

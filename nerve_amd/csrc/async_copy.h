@@ -1,0 +1,63 @@
+// Device helpers of the asynchronous global -> LDS pipelines (gfx950):
+// explicit vmcnt waits for copies issued with global_load_lds, and inline-asm
+// LDS accesses the compiler's wait insertion does not pair with those copies.
+#pragma once
+
+#include <utility>
+
+#include "common.h"
+
+namespace {
+
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm_imm() {
+    // gfx9 s_waitcnt: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | 0x0F70u);
+}
+
+template <uint32_t... I>
+__device__ __forceinline__ void wait_vm_dispatch(uint32_t n, std::integer_sequence<uint32_t, I...>) {
+    (void)((n == I ? (wait_vm_imm<I>(), true) : false) || ...);
+}
+
+// vmcnt(n) for a wave-uniform run-time n (clamped to the 6-bit counter).
+__device__ __forceinline__ void wait_vm(uint32_t n) {
+    wait_vm_dispatch(n > 63 ? 63 : n, std::make_integer_sequence<uint32_t, 64>{});
+}
+
+// LDS reads of pipeline stages are issued as inline asm so the compiler does
+// not pair them with the asynchronous copies (its waitcnt insertion would
+// otherwise drain every copy in flight before each read).  Their results are
+// used only after lds_drain() (or a waitcnt asm that takes them as operands)
+// and an empty asm that launders them.
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+
+__device__ __forceinline__ v4i lds_read16(const uint8_t* p) {
+    v4i r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_read_u8(const uint8_t* p) {
+    uint32_t r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_read_b32(const uint8_t* p) {
+    uint32_t r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+__device__ __forceinline__ void lds_write16(uint8_t* p, v4f v) {
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+}  // namespace

@@ -22,6 +22,7 @@
 #include <utility>
 
 #include "common.h"
+#include "async_copy.h"
 
 namespace {
 
@@ -757,36 +758,6 @@ constexpr uint32_t GS_MAX_K = 4096;
 
 __device__ __attribute__((aligned(16))) const uint8_t kZero16[16] = {0};
 
-template <uint32_t N>
-__device__ __forceinline__ void wait_vm_imm() {
-    // gfx9 s_waitcnt: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
-    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | 0x0F70u);
-}
-
-template <uint32_t... I>
-__device__ __forceinline__ void wait_vm_dispatch(uint32_t n, std::integer_sequence<uint32_t, I...>) {
-    (void)((n == I ? (wait_vm_imm<I>(), true) : false) || ...);
-}
-
-// vmcnt(n) for a wave-uniform run-time n (clamped to the 6-bit counter).
-__device__ __forceinline__ void wait_vm(uint32_t n) {
-    wait_vm_dispatch(n > 63 ? 63 : n, std::make_integer_sequence<uint32_t, 64>{});
-}
-
-
-
-// LDS reads of pipeline stages are issued as inline ds_read_b128 so the
-// compiler does not pair them with the asynchronous copies (its waitcnt
-// insertion would otherwise drain every copy in flight before each read);
-// lds_wait() then orders the reads' results before their use.
-typedef __attribute__((address_space(3))) const uint8_t lds_u8;
-
-__device__ __forceinline__ v4i lds_read16(const uint8_t* p) {
-    v4i r;
-    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
-    return r;
-}
 
 __device__ __forceinline__ void lds_wait(v4i& a0, v4i& a1, v4i& a2, v4i& a3, v4i& b0, v4i& b1, v4i& b2, v4i& b3) {
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -1233,25 +1204,6 @@ struct TileSrc {
     uint32_t in_route, out_route, out_word;
 };
 
-__device__ __forceinline__ uint32_t lds_read_u8(const uint8_t* p) {
-    uint32_t r;
-    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
-    asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
-    return r;
-}
-
-__device__ __forceinline__ uint32_t lds_read_b32(const uint8_t* p) {
-    uint32_t r;
-    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
-    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
-    return r;
-}
-
-__device__ __forceinline__ void lds_write16(uint8_t* p, v4f v) {
-    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
-    asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
-}
-
 // max(v, v of lane ^ 16) and max(v, v of lane ^ 32) with the gfx950 row swaps
 // (VALU only: an LDS-routed shuffle would queue behind the LDS copies in
 // flight).  With both operands v, the swap returns rows (0, 0, 2, 2) and
@@ -1325,7 +1277,6 @@ __device__ __forceinline__ void quant_chunk_e4m3(const v4i (&x)[4], v8i& out, ui
     e8m0 = pow2_to_e8m0(sc);
 }
 
-__device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef uint32_t u4s __attribute__((ext_vector_type(4)));
 typedef uint32_t u8s __attribute__((ext_vector_type(8)));

@@ -1,6 +1,7 @@
 // Device helpers of the asynchronous global -> LDS pipelines (gfx950):
-// explicit vmcnt waits for copies issued with global_load_lds, and inline-asm
-// LDS accesses the compiler's wait insertion does not pair with those copies.
+// explicit vmcnt waits for copies issued with global_load_lds, inline-asm
+// LDS and global accesses the compiler's wait insertion does not pair with
+// those copies, and cross-lane maxima that stay off the LDS.
 #pragma once
 
 #include <utility>
@@ -58,6 +59,43 @@ __device__ __forceinline__ void lds_write16(uint8_t* p, v4f v) {
     asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
 }
 
+__device__ __forceinline__ uint32_t lds_read_u16(const uint8_t* p) {
+    uint32_t r;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_u8*)p;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+// Global loads the compiler's wait insertion does not see: the caller waits
+// for them with wait_vm and passes the result through an empty asm before
+// any use.
+__device__ __forceinline__ v4i gload16_untracked(const void* p) {
+    v4i v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t gload4_untracked(const void* p) {
+    uint32_t v;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p));
+    return v;
+}
+
 __device__ __forceinline__ void lds_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// max(v, v of lane ^ 16) and max(v, v of lane ^ 32) with the gfx950 row swaps
+// (VALU only: an LDS-routed shuffle would queue behind the LDS copies in
+// flight).  With both operands v, the swap returns rows (0, 0, 2, 2) and
+// (1, 1, 3, 3), resp. halves (lo, lo) and (hi, hi).  For the non-negative,
+// NaN-free block maxima reduced here the order of the max is immaterial.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 }  // namespace

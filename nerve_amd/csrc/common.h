@@ -33,20 +33,18 @@ __device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to
 // f32 -> OCP e4m3 with round-to-nearest-even and saturation at +-448: the
 // GLSL fe4m3vec4(x) conversion of the activation quantizers
 // (…gate_up_batch1_mxfp4.comp.template:380).
+// Written without branches (both paths computed, then selected), which keeps
+// per-lane quantization loops free of divergent control flow.
 __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
-    uint32_t b = __float_as_uint(x);
-    uint32_t sign = (b >> 24) & 0x80u;
-    uint32_t a = b & 0x7fffffffu;
-    if (a > 0x7f800000u) return sign | 0x7fu;
-    if (a < 0x3c800000u) {  // below 2^-6: subnormal grid of 2^-9
-        float y = __uint_as_float(a) * 512.0f;
-        return sign | (uint32_t)__builtin_rintf(y);
-    }
-    uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
-    int e4 = (int)(r >> 23) - 120;
-    uint32_t m = (r >> 20) & 7u;
-    if (e4 > 15 || (e4 == 15 && m == 7u)) return sign | 0x7eu;
-    return sign | ((uint32_t)e4 << 3) | m;
+    const uint32_t b = __float_as_uint(x), sign = (b >> 24) & 0x80u, a = b & 0x7fffffffu;
+    // below 2^-6: the subnormal grid of 2^-9 (clamped so the conversion is
+    // always in range; the value is only selected below 2^-6)
+    const uint32_t sub = (uint32_t)__builtin_rintf(fminf(__uint_as_float(a) * 512.0f, 8.0f));
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    const uint32_t e4 = (r >> 23) - 120u, m = (r >> 20) & 7u;
+    const uint32_t nrm = (e4 > 15u && e4 < 0x80000000u) || (e4 == 15u && m == 7u) ? 0x7eu : ((e4 << 3) | m) & 0x7fu;
+    const uint32_t v = a > 0x7f800000u ? 0x7fu : a < 0x3c800000u ? sub : nrm;
+    return sign | v;
 }
 
 // rounded_fp8_scale (…gate_up_batch1_mxfp4.comp.template:357-363).

@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <cfloat>
 
+#include "async_copy.h"
 #include "common.h"
 
 namespace nh {
@@ -274,6 +275,221 @@ __global__ __launch_bounds__(64 * SK_WAVES) void fp8_head_skinny_kernel(HeadArgs
     }
 }
 
+// ---------------------------------------------------------------------------
+// Stream form (M <= 16, per-row weight scales): one 8-wave block per CU over
+// a contiguous range of 16-row vocabulary groups.  A group's weights are one
+// contiguous 16 K-byte span of W and its scales one contiguous 32 nblk-byte
+// span of scale_inv; both are copied into an NBUF-slot LDS ring by
+// global_load_lds (1 KiB and 256 B per wave instruction), so every wave keeps
+// NBUF - 1 groups of copies in flight while it contracts the current one.
+// The tokens are the MFMA A operand and stay in registers for the whole
+// range; each wave contracts its share of the K chunks of every group and the
+// 8 partial sums meet in LDS, where waves 0..3 finalize token 4 g + wave.
+// ---------------------------------------------------------------------------
+constexpr int HS_NW = 8;
+constexpr uint32_t HS_CH = 4;        // K chunks per wave (K <= 4096; the LDS wait below names 4)
+constexpr uint32_t HS_LWMAX = 8;     // weight copies per wave per group (16 K <= 64 KiB)
+
+struct HeadStream {
+    uint32_t groups;
+    uint32_t lw;                     // weight copies per wave per group
+    uint32_t cpi;                    // copies per wave per group (weights + one scale copy)
+    uint32_t slot_bytes, s_off;      // ring slot size; scale region offset in a slot
+};
+
+template <int NBUF>
+__device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const HeadStream& S) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, M = A.M, N = A.N, nblk = (K + 127) / 128;
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t i0 = (uint32_t)((uint64_t)S.groups * b / G), i1 = (uint32_t)((uint64_t)S.groups * (b + 1) / G);
+    uint8_t* red = ring + NBUF * S.slot_bytes;      // [wave][lane] v4f partial sums
+
+    // ---- copy plan: piece t of this wave starts at byte wpos[t] of the
+    // group's span (waves past the last piece repeat their first one, so
+    // every wave issues lw copies).  The last piece is aligned to the span's
+    // end and overlaps its neighbour with identical bytes.
+    const uint32_t span = 16 * K, sspan = 32 * nblk;
+    const uint32_t npw = (span + 1023) / 1024, nps = (sspan + 255) / 256;
+    uint32_t wpos[HS_LWMAX], woff[HS_LWMAX];
+#pragma unroll
+    for (uint32_t t = 0; t < HS_LWMAX; t++) {
+        uint32_t pc = wave + HS_NW * t;
+        if (pc >= npw) pc = wave < npw ? wave : 0;
+        wpos[t] = min(pc * 1024, span - 1024);
+        woff[t] = wpos[t] + lane * 16;
+    }
+    const uint32_t spc = wave < nps ? wave : 0;
+    const uint32_t spos = sspan >= 256 ? min(spc * 256, sspan - 256) : 0u;
+    const uint32_t soff = spos + lane * 4;
+
+    auto issue = [&](uint32_t item, uint32_t slot) __attribute__((always_inline)) {
+        const uint32_t n0 = item * 16, rows = min(16u, N - n0);
+        const uint32_t wbytes = rows * K, sbytes = (rows * nblk * 2 + 3) & ~3u;
+        const uint8_t* ws = A.W + (uint64_t)n0 * K;
+        uint8_t* dst = ring + slot * S.slot_bytes;
+#pragma unroll
+        for (uint32_t t = 0; t < HS_LWMAX; t++)
+            if (t < S.lw)
+                __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? woff[t] : 0u), dst + wpos[t], 16, 0, 0);
+        const uint8_t* ss = reinterpret_cast<const uint8_t*>(A.scale_inv) + (uint64_t)n0 * nblk * 2;
+        __builtin_amdgcn_global_load_lds(ss + (soff < sbytes ? soff : 0u), dst + S.s_off + spos, 4, 0, 0);
+    };
+
+    // ---- this wave's K chunks and their LDS offsets
+    const uint32_t per = (nblk + HS_NW - 1) / HS_NW;
+    const uint32_t c0 = min(nblk, wave * per), c1 = min(nblk, c0 + per);
+    uint32_t rw[HS_CH], rs[HS_CH];
+    bool kvalid[HS_CH];
+#pragma unroll
+    for (uint32_t q = 0; q < HS_CH; q++) {
+        const uint32_t c = c0 + q, kb = c * 128 + g * 32;
+        kvalid[q] = c < c1 && kb < K;
+        rw[q] = rr * K + (kvalid[q] ? kb : 0u);
+        rs[q] = S.s_off + (rr * nblk + (c < c1 ? c : 0u)) * 2;
+    }
+
+    // ---- tokens: e4m3 operand pieces and block scales, loaded with
+    // untracked loads before the first copies and waited for together with
+    // the first group's copies (loads retire in issue order).  Quantizing
+    // the tokens here instead would repeat the whole M x K quantization in
+    // every block, vector-ALU work that outlasts the ring's first groups.
+    const bool arow = rr < M;
+    v4i xlo[HS_CH], xhi[HS_CH];
+    uint32_t sxr[HS_CH][4];
+    {
+        const uint8_t* xr = A.xq + (uint64_t)(arow ? rr : 0u) * K;
+#pragma unroll
+        for (uint32_t q = 0; q < HS_CH; q++) {
+            if (c0 + q >= c1) continue;                 // wave-uniform
+            const uint32_t kb = kvalid[q] ? (c0 + q) * 128 + g * 32 : 0u;
+            xlo[q] = gload16_untracked(xr + kb);
+            xhi[q] = gload16_untracked(xr + kb + 16);
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) {
+                const uint32_t tk = 4 * g + i;
+                sxr[q][i] = gload4_untracked(A.xs + (tk < M ? tk * nblk + c0 + q : 0u));
+            }
+        }
+    }
+    if (i0 >= i1) {
+        wait_vm_imm<0>();
+    } else {
+        issue(i0, 0);
+        wait_vm(S.cpi);
+    }
+    v8i av[HS_CH];
+    float sx[HS_CH][4];
+#pragma unroll
+    for (uint32_t q = 0; q < HS_CH; q++) {
+        av[q] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) sx[q][i] = 0.0f;
+        if (c0 + q >= c1) continue;
+        asm volatile("" : "+v"(xlo[q]), "+v"(xhi[q]));
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) asm volatile("" : "+v"(sxr[q][i]));
+        if (arow && kvalid[q])
+            av[q] = v8i{xlo[q].x, xlo[q].y, xlo[q].z, xlo[q].w, xhi[q].x, xhi[q].y, xhi[q].z, xhi[q].w};
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) sx[q][i] = 4 * g + i < M ? __uint_as_float(sxr[q][i]) : 0.0f;
+    }
+    const uint32_t pro = min((uint32_t)NBUF, i1 - i0);
+#pragma unroll
+    for (uint32_t j = 1; j < NBUF; j++)
+        if (j < pro) issue(i0 + j, j);
+
+    const uint32_t tok = 4 * g + wave;                  // finalized token (waves 0..3)
+    float best_v = -INFINITY;
+    uint32_t best_i = 0xffffffffu;
+    for (uint32_t i = i0; i < i1; i++) {
+        const uint32_t slot = (i - i0) % NBUF;
+        if (i > i0 && i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
+        wait_vm(S.cpi * min((uint32_t)(NBUF - 1), i1 - 1 - i));
+        __builtin_amdgcn_s_barrier();
+        const uint8_t* buf = ring + slot * S.slot_bytes;
+        v4i w0[HS_CH], w1[HS_CH];
+        uint32_t sw[HS_CH];
+#pragma unroll
+        for (uint32_t q = 0; q < HS_CH; q++) {
+            if (c0 + q >= c1) continue;
+            w0[q] = lds_read16(buf + rw[q]);
+            w1[q] = lds_read16(buf + rw[q] + 16);
+            sw[q] = lds_read_u16(buf + rs[q]);
+        }
+        // The wait takes the read results as operands, so no copy of them
+        // is scheduled in front of it.
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(w0[0]), "+v"(w1[0]), "+v"(sw[0]), "+v"(w0[1]), "+v"(w1[1]), "+v"(sw[1]), "+v"(w0[2]),
+                       "+v"(w1[2]), "+v"(sw[2]), "+v"(w0[3]), "+v"(w1[3]), "+v"(sw[3])
+                     :
+                     : "memory");
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t q = 0; q < HS_CH; q++) {
+            if (c0 + q >= c1) continue;
+            v4i b0 = w0[q], b1 = w1[q];
+            uint32_t s16 = sw[q];
+            if (!kvalid[q]) b0 = b1 = v4i{0, 0, 0, 0};
+            const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                av[q], v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
+                0, 127);
+            const float s = bf16_to_f32(s16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(p[e], sx[q][e] * s, acc[e]);
+        }
+        // An MFMA result read by inline asm needs software wait states the
+        // compiler does not add: the nops take the sums as operands.
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc));
+        lds_write16(red + (wave * 64 + lane) * 16, acc);
+        lds_drain();
+        __builtin_amdgcn_s_barrier();
+        if (wave >= 4) continue;
+        uint32_t v[HS_NW];
+#pragma unroll
+        for (int w2 = 0; w2 < HS_NW; w2++) v[w2] = lds_read_b32(red + (w2 * 64 + lane) * 16 + 4 * wave);
+        lds_drain();
+        float sum = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < HS_NW; w2++) {
+            asm volatile("" : "+v"(v[w2]));
+            sum += __uint_as_float(v[w2]);
+        }
+        const float val = sum * A.out_scale;
+        const uint32_t n = i * 16 + rr;
+        const bool cv = n < N;
+        if (tok < M && cv) {
+            if (A.logits_f32) A.logits_f32[(uint64_t)tok * N + n] = val;
+            if (A.logits_bf16) A.logits_bf16[(uint64_t)tok * N + n] = (uint16_t)f32_to_bf16(val);
+        }
+        if (A.part_val) {
+            float bv = cv ? val : -INFINITY;
+            uint32_t bi = cv ? n : 0xffffffffu;
+#pragma unroll
+            for (int d = 1; d < 16; d <<= 1) {
+                const float ov = __shfl_xor(bv, d);
+                const uint32_t oi = __shfl_xor(bi, d);
+                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            if (better(bv, bi, best_v, best_i)) {
+                best_v = bv;
+                best_i = bi;
+            }
+        }
+    }
+    if (A.part_val && wave < 4 && rr == 0 && tok < M) {
+        A.part_val[(uint64_t)tok * G + b] = best_v;
+        A.part_idx[(uint64_t)tok * G + b] = best_i;
+    }
+}
+
+template <int NBUF>
+__global__ __launch_bounds__(64 * HS_NW) void fp8_head_stream_kernel(HeadArgs A, HeadStream S) {
+    fp8_head_stream_body<NBUF>(A, S);
+}
+
 // Second pass: one block per row over the partials (argmax_candidate_reduce.
 // comp.template:10-37).
 __global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
@@ -353,7 +569,22 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
     const uint32_t groups = (N + 15) / 16;
     // Skinny grid: groups strided over 4 blocks per CU.
     const uint32_t sk_grid = std::min<uint32_t>(groups, 4u * (uint32_t)ctx->cu_count);
-    const uint32_t nparts = skinny ? sk_grid : nblocks;
+    // Stream form: per-row scales (whole groups' scale spans are contiguous
+    // and 4-byte aligned), 64 <= K <= 4096, the ring fits in LDS.
+    HeadStream hs{};
+    hs.groups = groups;
+    hs.s_off = 16 * K;
+    const uint32_t sspan = 32 * nblk;
+    hs.slot_bytes = hs.s_off + ((sspan < 256 ? 256 : sspan) + 15) / 16 * 16;
+    hs.lw = (16 * K + 1023) / 1024 / HS_NW + ((16 * K + 1023) / 1024 % HS_NW ? 1 : 0);
+    hs.cpi = hs.lw + 1;
+    const size_t hs_red = HS_NW * 64 * 16;
+    const int hs_nbuf = (3 * (size_t)hs.slot_bytes + hs_red <= 160 * 1024) ? 3 : 2;
+    const bool stream_form = skinny && s.block_rows == 1 && K >= 64 && ((uint64_t)N * nblk) % 2 == 0 &&
+                             ((uintptr_t)scale_inv_bf16 & 3) == 0 && hs.lw <= HS_LWMAX &&
+                             hs_nbuf * (size_t)hs.slot_bytes + hs_red <= 160 * 1024 && hs.cpi * hs_nbuf <= 63;
+    const uint32_t hs_grid = (uint32_t)ctx->cu_count;
+    const uint32_t nparts = stream_form ? hs_grid : skinny ? sk_grid : nblocks;
     nh::Carver cv;
     size_t o_q = cv.take<uint8_t>((size_t)M * K);
     size_t o_s = cv.take<float>((size_t)M * nblk);
@@ -381,7 +612,21 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
     A.part_val = argmax_u32 ? reinterpret_cast<float*>(base + o_pv) : nullptr;
     A.part_idx = argmax_u32 ? reinterpret_cast<uint32_t*>(base + o_pi) : nullptr;
     A.nblocks = nblocks;
-    if (skinny) {
+    if (stream_form) {
+        A.nblocks = hs_grid;
+        const size_t lds = hs_nbuf * (size_t)hs.slot_bytes + hs_red;
+        static bool attr_set = false;
+        if (!attr_set) {
+            if (hipFuncSetAttribute((const void*)fp8_head_stream_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    160 * 1024) != hipSuccess ||
+                hipFuncSetAttribute((const void*)fp8_head_stream_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    160 * 1024) != hipSuccess)
+                return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for fp8_head_stream_kernel");
+            attr_set = true;
+        }
+        if (hs_nbuf == 3) fp8_head_stream_kernel<3><<<hs_grid, 64 * HS_NW, lds, strm>>>(A, hs);
+        else fp8_head_stream_kernel<2><<<hs_grid, 64 * HS_NW, lds, strm>>>(A, hs);
+    } else if (skinny) {
         A.nblocks = sk_grid;
         const uint32_t per = (nblk + SK_WAVES - 1) / SK_WAVES;
         const size_t lds = ((size_t)M * K + 15) / 16 * 16 + ((size_t)M * nblk + 3) / 4 * 4 * 4 + 3 * 64 * 4 * 4;

@@ -1204,30 +1204,6 @@ struct TileSrc {
     uint32_t in_route, out_route, out_word;
 };
 
-// max(v, v of lane ^ 16) and max(v, v of lane ^ 32) with the gfx950 row swaps
-// (VALU only: an LDS-routed shuffle would queue behind the LDS copies in
-// flight).  With both operands v, the swap returns rows (0, 0, 2, 2) and
-// (1, 1, 3, 3), resp. halves (lo, lo) and (hi, hi).  For the non-negative,
-// NaN-free block maxima reduced here the order of the max is immaterial.
-__device__ __forceinline__ float max_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-__device__ __forceinline__ float max_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-// 16-byte global load the compiler's wait insertion does not see: the caller
-// waits for it with wait_vm and passes the result through an empty asm before
-// any use.
-__device__ __forceinline__ v4i gload16_untracked(const void* p) {
-    v4i v;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
-    return v;
-}
-
 // Blockwise e4m3 quantization of one lane's 32 bf16 values of a 128-column
 // block (the same arithmetic as quant_unit: pow2 scale of the block amax,
 // x / scale rounded to e4m3).  The four lanes of a row (g = 0..3, lanes

@@ -136,7 +136,12 @@ def _argmax_ok(ids, ref_logits, tol):
     return True
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (7, 4096, 2880), (64, 2048, 512), (130, 600, 384)])
+# M <= 16 with per-row scales takes the LDS-ring stream kernel (two ring
+# slots at K = 4096, a partial last 16-row group at N % 16 != 0, fewer groups
+# than blocks at small N); an odd N * nblk falls back to the register form;
+# M > 16 takes the tiled kernel.
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (7, 4096, 2880), (64, 2048, 512), (130, 600, 384),
+                                   (16, 2000, 4096), (2, 777, 64), (5, 1001, 384), (3, 30010, 2880)])
 def test_fp8_head_parity(ctx, dev, M, N, K):
     rng = np.random.default_rng(M * N + K)
     d = wl.fp8_head(rng, N, K, M)

@@ -216,6 +216,24 @@ nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec,
                                           const void* control_u32, uint32_t batch_width,
                                           void* stream);
 
+/* Count stage + down in one launch: nerve_hip_moe_route_compact(spec,
+ * routes, NULL, control) followed by nerve_hip_mxfp4_moe_down (the reference
+ * runs moe_route_count_batch1 then the down shader,
+ * nerve/model_package_batching.py:265-284).  It requires that control[3],
+ * [5] and [6] already hold what the count stage writes, which is the case
+ * after a compaction (nerve_hip_moe_route_compact or
+ * nerve_hip_moe_route_fused) of the same routes and control[0..2]; it then
+ * writes control[4] = (expert_count ? control[3] : k) * ceil(H / 64), the one
+ * word the count stage changes, and the same expert_outputs as the down
+ * entry point. */
+nerve_hip_status nerve_hip_mxfp4_moe_down_counted(nerve_hip_ctx* ctx, const char* spec,
+                                                  const void* intermediates, const void* routes_u32,
+                                                  void* expert_outputs,
+                                                  const void* addresses_u32, uint32_t address_records,
+                                                  const void* param_slots_u32, uint32_t param_slot_words,
+                                                  void* control_u32, uint32_t batch_width,
+                                                  void* stream);
+
 /* ---- a8: weighted combine ----------------------------------------------- */
 
 /* Replaces moe_reduce[_batch1]_bf16 (moe_reduce_batch1_bf16.comp.template:

@@ -1192,6 +1192,12 @@ struct StreamArgs {
     uint64_t x_frame, x_seg;
     uint32_t addr_lds_records;                   // address tables up to this many records are copied to LDS
     uint32_t small_plan;                         // fused set-up by one wave (E <= 64, B k <= 64, >= 64 blocks)
+    // Count stage folded into the launch (down only): block 0 writes
+    // control[4] = (expert_count ? control[3] : k) * count_tiles, the one
+    // control word the count stage changes after a compaction of the same
+    // routes.  No block of this launch reads control[4].
+    uint32_t* count_control;
+    uint32_t count_tiles;
 };
 
 // One tile as the streaming loop sees it: its parameter pointers, its route
@@ -1896,6 +1902,10 @@ __device__ __forceinline__ void fused_small_plan(const TileArgs& A, SmallPlan& S
 template <int MODE, int NMAT, int NBUF, int NW, int NSUB, bool FUSED>
 __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    if (A.count_control && blockIdx.x == 0 && threadIdx.x == 0) {
+        const uint32_t c2 = A.count_control[2], c3 = A.count_control[3];
+        A.count_control[4] = (c2 != 0u ? c3 : A.k) * A.count_tiles;
+    }
     const uint32_t N = A.N;
     const uint32_t nrb = (N + 16 * NSUB - 1) / (16 * NSUB);
     FusedTables& F = *reinterpret_cast<FusedTables*>(ring);
@@ -2928,14 +2938,24 @@ nerve_hip_status nerve_hip_mxfp4_gemv(nerve_hip_ctx* ctx, const void* q_e4m3, co
     return nh::check_launch("mxfp4_gemv");
 }
 
+// control[4] as the count stage writes it after a compaction of the same
+// routes (control[3], [5] and [6] already hold its values).
+__global__ __launch_bounds__(64) void count_control_kernel(uint32_t* control, uint32_t k, uint32_t tiles) {
+    if (threadIdx.x == 0) control[4] = (control[2] != 0u ? control[3] : k) * tiles;
+}
+
 static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bool gate_up, const void* act_bf16,
                                    const void* pre_q, const void* pre_s, const void* routes, void* intermediates,
                                    void* expert_outputs, const void* addresses, uint32_t address_records,
                                    const void* slots, uint32_t slot_words, const void* control, uint32_t batch_width,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, uint32_t* count_control = nullptr) {
     const uint32_t H = ms.hidden, I = ms.inter, k = ms.k, E = ms.experts;
     const uint32_t cap = batch_width * k;
-    if (cap == 0) return nh::ok();
+    if (cap == 0) {
+        if (!count_control) return nh::ok();
+        count_control_kernel<<<1, 64, 0, stream>>>(count_control, k, (H + 63) / 64);
+        return nh::check_launch("moe_route_count");
+    }
     const uint32_t K = gate_up ? H : I;       // contraction
     const uint32_t N = gate_up ? I : H;       // output rows per matrix
     const uint32_t nblk = (K + 127) / 128;
@@ -3039,9 +3059,18 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
             fa.x_frame = frame_words * 2;
             fa.x_seg = I;
             fa.out16 = static_cast<uint16_t*>(expert_outputs);
+            fa.count_control = count_control;
+            fa.count_tiles = (H + 63) / 64;
             st = launch_stream<SPAN_DOWN, 1, 3, 8, 2, true>(fa, ctx, stream);
+            if (st == NERVE_HIP_OK) count_control = nullptr;
         }
         if (st != NERVE_HIP_UNSUPPORTED) return st;
+    }
+    if (count_control) {
+        // Count stage as its own launch (its one changed word, computed the
+        // same way) for the other down paths.
+        count_control_kernel<<<1, 64, 0, stream>>>(count_control, k, (H + 63) / 64);
+        if ((st = nh::check_launch("moe_route_count"))) return st;
     }
     const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
     {
@@ -3184,6 +3213,23 @@ nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec, 
     return moe_common(ctx, ms, false, nullptr, nullptr, nullptr, routes_u32, const_cast<void*>(intermediates),
                       expert_outputs, addresses_u32, address_records, param_slots_u32, param_slot_words, control_u32,
                       batch_width, (hipStream_t)stream);
+}
+
+nerve_hip_status nerve_hip_mxfp4_moe_down_counted(nerve_hip_ctx* ctx, const char* spec, const void* intermediates,
+                                                  const void* routes_u32, void* expert_outputs,
+                                                  const void* addresses_u32, uint32_t address_records,
+                                                  const void* param_slots_u32, uint32_t param_slot_words,
+                                                  void* control_u32, uint32_t batch_width, void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::MoeSpec ms;
+    if ((st = nh::parse_moe_spec(spec, &ms))) return st;
+    if (ms.gate_up) return nh::fail(NERVE_HIP_INVALID_SPEC, "down entry given a gate_up specialization");
+    if (!intermediates || !routes_u32 || !expert_outputs || !addresses_u32 || !param_slots_u32 || !control_u32)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    return moe_common(ctx, ms, false, nullptr, nullptr, nullptr, routes_u32, const_cast<void*>(intermediates),
+                      expert_outputs, addresses_u32, address_records, param_slots_u32, param_slot_words, control_u32,
+                      batch_width, (hipStream_t)stream, static_cast<uint32_t*>(control_u32));
 }
 
 }  // extern "C"

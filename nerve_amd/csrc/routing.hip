@@ -281,9 +281,11 @@ __device__ void topk_token(const uint16_t* lg, const void* bias, uint32_t* route
 // descending, index ascending; a NaN never beats and is never selected), so
 // round r selects the expert of rank r.  Weights use the same formulas and
 // summation orders (selection order, or expert order for the full softmax),
-// carried out identically in every lane.  The block is not synchronized.
+// carried out identically in every lane.  The block is not synchronized;
+// s_sh is the wave's own 16-byte aligned LDS scratch of at least E rounded
+// up to 4 floats.
 __device__ void topk_token_fast(const uint16_t* lg, const void* bias, uint32_t* routes, uint32_t* telemetry, uint32_t b,
-                                bool valid, const TopkParams& P, uint32_t* tel_lds) {
+                                bool valid, const TopkParams& P, uint32_t* tel_lds, float* s_sh) {
     const uint32_t lane = threadIdx.x & 63, E = P.E, k = P.k;
     const bool have = lane < E;
     float raw = 0.0f, s = -INFINITY;
@@ -298,8 +300,23 @@ __device__ void topk_token_fast(const uint16_t* lg, const void* bias, uint32_t* 
     auto lane_f = [](float v, uint32_t j) __attribute__((always_inline)) {
         return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
     };
+    // Every lane compares against all E scores, read back from the wave's
+    // LDS row as broadcasts (a readlane per comparison would serialize on
+    // its hazard waits).
+    if (lane < (E + 3) / 4 * 4) s_sh[lane] = s;     // -inf pads the row to whole float4s
+    __builtin_amdgcn_wave_barrier();
     uint32_t rank = 0;
-    for (uint32_t j = 0; j < E; j++) rank += better(lane_f(s, j), j, s, lane) ? 1u : 0u;
+    const uint32_t E4 = (E + 3) / 4;
+#pragma unroll 4
+    for (uint32_t j4 = 0; j4 < E4; j4++) {
+        const float4 v = *reinterpret_cast<const float4*>(s_sh + 4 * j4);
+        const uint32_t j = 4 * j4;
+        rank += better(v.x, j, s, lane) ? 1u : 0u;
+        rank += better(v.y, j + 1, s, lane) ? 1u : 0u;
+        rank += better(v.z, j + 2, s, lane) ? 1u : 0u;
+        rank += better(v.w, j + 3, s, lane) ? 1u : 0u;
+    }
+    __builtin_amdgcn_wave_barrier();
     const bool chosen = have && !nan && rank < k;
     const uint64_t chosen_mask = __ballot(chosen);
     // Expert selected in round r (rounds past the selectable experts pick 0,
@@ -368,7 +385,7 @@ __device__ void topk_token_fast(const uint16_t* lg, const void* bias, uint32_t* 
 __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ logits, const void* __restrict__ bias,
                                                   uint32_t* __restrict__ routes, uint32_t* __restrict__ telemetry,
                                                   uint32_t B, TopkParams P) {
-    extern __shared__ float sh[];
+    extern __shared__ __attribute__((aligned(16))) float sh[];
     __shared__ uint32_t top[128];
     __shared__ float wts[128];
     __shared__ float smax_sh, sden_sh;
@@ -376,7 +393,7 @@ __global__ __launch_bounds__(64) void topk_kernel(const uint16_t* __restrict__ l
     const uint32_t b = blockIdx.x;
     if (b >= B) return;
     if (P.mode == 0 && P.E <= 64) {
-        topk_token_fast(logits + (uint64_t)b * P.E, bias, routes, telemetry, b, true, P, nullptr);
+        topk_token_fast(logits + (uint64_t)b * P.E, bias, routes, telemetry, b, true, P, nullptr, sh);
         return;
     }
     TopkScratch S{sh, reinterpret_cast<uint32_t*>(sh + P.E), top, wts, &smax_sh, &sden_sh, &sel_total, &res_total};
@@ -532,7 +549,7 @@ __device__ uint32_t compact_owned(const CompactArgs& A, uint32_t* wave_tot, uint
 // The whole compaction by one block of up to 1024 threads (scratch: 16 *
 // COUNT_MAX_EXPERTS words, wave_tot: 16, misc: 2).
 __device__ void compact_body(const CompactArgs& A, uint32_t* scratch, uint32_t* wave_tot, uint32_t* misc,
-                             const uint32_t* ctl2 = nullptr) {
+                             const uint32_t* ctl2 = nullptr, const uint32_t* ctl0 = nullptr) {
     uint32_t* control = A.control;
     if ((ctl2 ? *ctl2 : control[2]) != 0u) {
         const uint32_t owned = compact_owned(A, wave_tot, &misc[0]);
@@ -547,10 +564,33 @@ __device__ void compact_body(const CompactArgs& A, uint32_t* scratch, uint32_t* 
     if (threadIdx.x == 0) {
         control[3] = A.n;
         control[4] = A.k * A.tiles_per_route;
-        control[5] = control[0];
+        control[5] = ctl0 ? *ctl0 : control[0];
         control[6] = 1;
     }
     if (!A.frames || A.n == 0) return;
+    if (A.n <= 64) {
+        // One wave: route i's rank by the same key, comparing against every
+        // route's expert read back from LDS as 16-byte broadcasts.
+        if (threadIdx.x < 64) {
+            const uint32_t lane = threadIdx.x;
+            const uint32_t e = lane < A.n ? (A.routes[lane] & 0xffffu) : 0xffffffffu;
+            scratch[lane] = e;
+            __builtin_amdgcn_wave_barrier();
+            uint32_t rank = 0;
+            const uint32_t n4 = (A.n + 3) / 4;
+#pragma unroll 4
+            for (uint32_t c4 = 0; c4 < n4; c4++) {
+                const uint4 ce = *reinterpret_cast<const uint4*>(scratch + 4 * c4);
+                const uint32_t c = 4 * c4;
+                rank += (ce.x < e || (ce.x == e && c < lane)) ? 1u : 0u;
+                rank += (ce.y < e || (ce.y == e && c + 1 < lane)) ? 1u : 0u;
+                rank += (ce.z < e || (ce.z == e && c + 2 < lane)) ? 1u : 0u;
+                rank += (ce.w < e || (ce.w == e && c + 3 < lane)) ? 1u : 0u;
+            }
+            if (lane < A.n) put_map(A, rank, lane);
+        }
+        return;
+    }
     if (A.n > blockDim.x && A.E <= COUNT_MAX_EXPERTS) {
         if (compact_counting(A, scratch, wave_tot, &misc[1])) return;
         __syncthreads();
@@ -559,7 +599,7 @@ __device__ void compact_body(const CompactArgs& A, uint32_t* scratch, uint32_t* 
 }
 
 __global__ __launch_bounds__(1024) void compact_kernel(CompactArgs A) {
-    __shared__ uint32_t scratch[16 * COUNT_MAX_EXPERTS];
+    __shared__ __attribute__((aligned(16))) uint32_t scratch[16 * COUNT_MAX_EXPERTS];
     __shared__ uint32_t wave_tot[16];
     __shared__ uint32_t misc[2];
     compact_body(A, scratch, wave_tot, misc);
@@ -662,7 +702,7 @@ constexpr uint32_t FR_LDS_TELEMETRY = 4096;   // telemetry arrays up to this siz
 
 __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     __shared__ uint16_t lg[FR_MAX_TOKENS * FR_MAX_EXPERTS];
-    __shared__ float t_raw[16][FR_MAX_EXPERTS];
+    __shared__ __attribute__((aligned(16))) float t_raw[16][FR_MAX_EXPERTS];
     __shared__ uint32_t t_sel[16][FR_MAX_EXPERTS];
     __shared__ uint32_t t_top[16][128];
     __shared__ float t_wts[16][128];
@@ -672,12 +712,15 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     __shared__ uint32_t tel[FR_LDS_TELEMETRY];
     __shared__ uint32_t wave_tot[16];
     __shared__ uint32_t misc[2];
-    __shared__ uint32_t ctl2;
+    __shared__ uint32_t ctl2, ctl0;
     const uint32_t wave = threadIdx.x >> 6, E = F.P.E, B = F.B;
     const uint32_t total_sel = F.P.k + F.P.always_count, total_res = E + F.P.always_count;
     const uint32_t T = total_res + total_res * (total_res - 1) / 2;
     const bool tel_in_lds = F.telemetry && T <= FR_LDS_TELEMETRY;
-    if (threadIdx.x == 0) ctl2 = F.C.control[2];
+    if (threadIdx.x == 0) {
+        ctl2 = F.C.control[2];
+        ctl0 = F.C.control[0];
+    }
     if (tel_in_lds)
         for (uint32_t i = threadIdx.x; i < T; i += blockDim.x) tel[i] = 0;
     // Logits: the slices added in slice order, rounded to bf16.
@@ -696,13 +739,15 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     for (uint32_t b0 = 0; b0 < B; b0 += 16) {
         const uint32_t b = b0 + wave;
         uint32_t* telp = F.telemetry ? (tel_in_lds ? tel : F.telemetry) : nullptr;
-        if (fast) topk_token_fast(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, tel_in_lds ? tel : nullptr);
+        if (fast)
+            topk_token_fast(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, tel_in_lds ? tel : nullptr,
+                            t_raw[wave]);
         else topk_token(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, S, tel_in_lds ? tel : nullptr);
     }
     __syncthreads();
     CompactArgs C = F.C;
     C.routes = rl;
-    compact_body(C, reinterpret_cast<uint32_t*>(&t_raw[0][0]), wave_tot, misc, &ctl2);
+    compact_body(C, reinterpret_cast<uint32_t*>(&t_raw[0][0]), wave_tot, misc, &ctl2, &ctl0);
     __syncthreads();
     // Global outputs last: logits, route words, telemetry counts.
     if (F.logits)
@@ -769,7 +814,7 @@ nerve_hip_status nerve_hip_moe_router_topk(nerve_hip_ctx* ctx, const char* spec,
     P.softcap = ts.softcap;
     P.routed_scale = ts.routed_scale;
     P.always_weight = ts.always_weight;
-    size_t lds = (size_t)ts.experts * 8;
+    size_t lds = (size_t)(ts.experts + 3) / 4 * 4 * 8;   // >= E floats rounded up to float4s, twice
     topk_kernel<<<batch_width, 64, lds, (hipStream_t)stream>>>(static_cast<const uint16_t*>(logits_bf16), bias,
                                                                static_cast<uint32_t*>(routes_u32),
                                                                static_cast<uint32_t*>(telemetry_u32), batch_width, P);

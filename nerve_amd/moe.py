@@ -153,8 +153,13 @@ class MoEBlock:
             c.moe_route_compact(self.gate_up, b["routes"], b["inter"], b["control"], B, stream)
         c.mxfp4_moe_gate_up(self.gate_up, hidden, None, b["routes"], b["inter"], bank.addresses, bank.gate_slots,
                             b["control"], B, stream)
-        c.moe_route_compact(self.down, b["routes"], None, b["control"], B, stream)
-        c.mxfp4_moe_down(self.down, b["inter"], b["routes"], b["expert_out"], bank.addresses, bank.down_slots,
-                         b["control"], B, stream)
+        if self.fuse_routing:
+            # Count stage folded into the down launch (same control words).
+            c.mxfp4_moe_down_counted(self.down, b["inter"], b["routes"], b["expert_out"], bank.addresses,
+                                     bank.down_slots, b["control"], B, stream)
+        else:
+            c.moe_route_compact(self.down, b["routes"], None, b["control"], B, stream)
+            c.mxfp4_moe_down(self.down, b["inter"], b["routes"], b["expert_out"], bank.addresses, bank.down_slots,
+                             b["control"], B, stream)
         c.moe_reduce(b["expert_out"], b["out"], B, self.H, self.k, self.routed_scale, stream)
         return b["out"]

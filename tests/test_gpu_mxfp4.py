@@ -283,6 +283,34 @@ def test_owned_expert_range_gate_up_down(ctx, dev, E, start, count):
     assert ok and exact > 0.9, (worst, exact)
 
 
+# Decode token/stream path, owned expert ranges and a prefill-sized batch
+# (the grouped path, where the count is its own launch).
+@pytest.mark.parametrize("E,k,B,H,I,start,count", [(32, 4, 16, 2880, 2880, 0, 0), (32, 4, 16, 512, 256, 8, 12),
+                                                   (8, 2, 4, 256, 256, 2, 3), (8, 4, 160, 256, 256, 0, 0)])
+def test_down_counted_matches_count_then_down(ctx, dev, E, k, B, H, I, start, count):
+    """nerve_hip_mxfp4_moe_down_counted == moe_route_compact (count form) then
+    mxfp4_moe_down: the same expert outputs and the same control words."""
+    d, routes, hidden = _moe_case(E, k, B, H, I, seed=B + E + start)
+    rig = MoeRig(dev, d, routes)
+    rig.control = to_dev(np.array([B, start, count, 0, 0, 0, 0, 0], np.uint32), dev)
+    rig.run(ctx, hidden)
+    ref_ctl = to_np(rig.control, np.uint32).copy()
+    ref_eo = to_np(rig.expert_out, np.uint16).copy()
+    rig.expert_out.fill_(0x7F7F)
+    rig.control = to_dev(np.array([B, start, count, 0, 0, 0, 0, 0], np.uint32), dev)
+    ctx.moe_route_compact(rig.gu, rig.routes, rig.inter, rig.control, B)
+    ctx.mxfp4_moe_gate_up(rig.gu, to_dev(hidden, dev), None, rig.routes, rig.inter, rig.bank.addresses,
+                          rig.bank.gate_slots, rig.control, B)
+    ctx.mxfp4_moe_down_counted(rig.dn, rig.inter, rig.routes, rig.expert_out, rig.bank.addresses,
+                               rig.bank.down_slots, rig.control, B)
+    assert np.array_equal(to_np(rig.control, np.uint32), ref_ctl)
+    if count:
+        owned = ((routes & 0xFFFF) >= start) & ((routes & 0xFFFF) < start + count)
+        assert np.array_equal(to_np(rig.expert_out, np.uint16)[owned], ref_eo[owned])
+    else:
+        assert np.array_equal(to_np(rig.expert_out, np.uint16), ref_eo)
+
+
 def test_moe_prefill_config3_subset(ctx, dev):
     """Config 3 (2048 tokens, 128 Zipf-loaded experts, H = I = 2880) on the GPU;
     24 tokens re-computed by the oracle (each token's result depends only on

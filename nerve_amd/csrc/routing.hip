@@ -548,10 +548,12 @@ __device__ uint32_t compact_owned(const CompactArgs& A, uint32_t* wave_tot, uint
 
 // The whole compaction by one block of up to 1024 threads (scratch: 16 *
 // COUNT_MAX_EXPERTS words, wave_tot: 16, misc: 2).
+// pre: control[0] and control[2] already read by the caller (values, so
+// that no generic load of an LDS copy is needed), when `have_ctl` is set.
 __device__ void compact_body(const CompactArgs& A, uint32_t* scratch, uint32_t* wave_tot, uint32_t* misc,
-                             const uint32_t* ctl2 = nullptr, const uint32_t* ctl0 = nullptr) {
+                             bool have_ctl = false, uint32_t ctl2 = 0, uint32_t ctl0 = 0) {
     uint32_t* control = A.control;
-    if ((ctl2 ? *ctl2 : control[2]) != 0u) {
+    if ((have_ctl ? ctl2 : control[2]) != 0u) {
         const uint32_t owned = compact_owned(A, wave_tot, &misc[0]);
         if (threadIdx.x == 0) {
             control[3] = owned;
@@ -564,29 +566,28 @@ __device__ void compact_body(const CompactArgs& A, uint32_t* scratch, uint32_t* 
     if (threadIdx.x == 0) {
         control[3] = A.n;
         control[4] = A.k * A.tiles_per_route;
-        control[5] = ctl0 ? *ctl0 : control[0];
+        control[5] = have_ctl ? ctl0 : control[0];
         control[6] = 1;
     }
     if (!A.frames || A.n == 0) return;
     if (A.n <= 64) {
-        // One wave: route i's rank by the same key, comparing against every
-        // route's expert read back from LDS as 16-byte broadcasts.
+        // One wave: route i's rank by the same key from ballots, most
+        // significant key bit first: the routes that agree with it on the
+        // higher bits and have a 0 where it has a 1 are smaller; those that
+        // agree on every bit and sit at a lower index come before it.
         if (threadIdx.x < 64) {
             const uint32_t lane = threadIdx.x;
-            const uint32_t e = lane < A.n ? (A.routes[lane] & 0xffffu) : 0xffffffffu;
-            scratch[lane] = e;
-            __builtin_amdgcn_wave_barrier();
+            const uint32_t e = lane < A.n ? (A.routes[lane] & 0xffffu) : 0u;
+            uint64_t eq = __ballot(lane < A.n);
             uint32_t rank = 0;
-            const uint32_t n4 = (A.n + 3) / 4;
-#pragma unroll 4
-            for (uint32_t c4 = 0; c4 < n4; c4++) {
-                const uint4 ce = *reinterpret_cast<const uint4*>(scratch + 4 * c4);
-                const uint32_t c = 4 * c4;
-                rank += (ce.x < e || (ce.x == e && c < lane)) ? 1u : 0u;
-                rank += (ce.y < e || (ce.y == e && c + 1 < lane)) ? 1u : 0u;
-                rank += (ce.z < e || (ce.z == e && c + 2 < lane)) ? 1u : 0u;
-                rank += (ce.w < e || (ce.w == e && c + 3 < lane)) ? 1u : 0u;
+#pragma unroll
+            for (int bit = 15; bit >= 0; bit--) {
+                const bool one = (e >> bit) & 1u;
+                const uint64_t m = __ballot(one);
+                if (one) rank += (uint32_t)__popcll(eq & ~m);
+                eq &= one ? m : ~m;
             }
+            rank += (uint32_t)__popcll(eq & ((1ull << lane) - 1ull));
             if (lane < A.n) put_map(A, rank, lane);
         }
         return;
@@ -747,7 +748,7 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     __syncthreads();
     CompactArgs C = F.C;
     C.routes = rl;
-    compact_body(C, reinterpret_cast<uint32_t*>(&t_raw[0][0]), wave_tot, misc, &ctl2, &ctl0);
+    compact_body(C, reinterpret_cast<uint32_t*>(&t_raw[0][0]), wave_tot, misc, true, ctl2, ctl0);
     __syncthreads();
     // Global outputs last: logits, route words, telemetry counts.
     if (F.logits)

@@ -106,7 +106,11 @@ static nerve_hip_status parse_moe_spec_uncached(const char* spec, MoeSpec* out) 
     if (s.tensor_parallel) return fail(NERVE_HIP_UNSUPPORTED, "tensor-parallel expert partials are a multi-GPU path; this backend is single-GPU");
     if (s.weight_repr != 0 || s.native_fp8_start >= 0)
         return fail(NERVE_HIP_UNSUPPORTED, "resident/adaptive FP8 and native-FP8 expert banks are not implemented yet");
-    if (s.input_block_major) return fail(NERVE_HIP_UNSUPPORTED, "input_block_major_b128 layout is not implemented yet");
+    // input_block_major_b128 is a down-weight layout
+    // (nerve/model_package_independent_experts.py:164-170) and needs whole
+    // 128-column blocks.
+    if (s.input_block_major && (s.gate_up || s.inter % 128))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("input_block_major_b128 needs a down kernel with I % 128 == 0: ") + spec);
     if (s.prequant && !s.gate_up) return fail(NERVE_HIP_INVALID_SPEC, "prequant applies to gate_up only");
     *out = s;
     return NERVE_HIP_OK;

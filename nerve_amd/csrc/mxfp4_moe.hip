@@ -1198,6 +1198,11 @@ struct StreamArgs {
     // routes.  No block of this launch reads control[4].
     uint32_t* count_control;
     uint32_t count_tiles;
+    // Down weights in the input-block-major layout (W [K/128, N, 64] bytes,
+    // S [K/128, N, 4]): byte (row r, packed column j) of row-major W sits at
+    // ((j / 64) N + r) 64 + j % 64, scale byte (r, group q) at
+    // ((q / 4) N + r) 4 + q % 4.
+    uint32_t block_major;
 };
 
 // One tile as the streaming loop sees it: its parameter pointers, its route
@@ -1346,6 +1351,19 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         soff[t] = spos[t] + lane * 4;
     }
 
+    // Source offsets of the same LDS pieces (relative to the item's first
+    // row): the row-major span, or gathered from the input-block-major
+    // layout (a 16-byte piece never straddles a 64-byte block row, a scale
+    // dword never straddles a 4-byte one, since K % 128 == 0 there).
+    uint32_t wsrc[LWMAX], ssrc[LSMAX];
+#pragma unroll
+    for (uint32_t t = 0; t < LWMAX; t++)
+        wsrc[t] = A.block_major ? ((woff[t] % RB) / 64) * N * 64 + (woff[t] / RB) * 64 + woff[t] % 64 : woff[t];
+#pragma unroll
+    for (uint32_t t = 0; t < LSMAX; t++)
+        ssrc[t] = A.block_major ? ((soff[t] % SB) / 4) * N * 4 + (soff[t] / SB) * 4 : soff[t];
+    const uint32_t wrow = A.block_major ? 64u : RB, srow = A.block_major ? 4u : SB;
+
     // ---- issue side: copies of item `item` into ring slot `slot`
     const uint32_t tile_base = (i0 / nrb) * nrb;
     auto issue = [&](uint32_t item, uint32_t slot) {
@@ -1355,17 +1373,17 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         uint8_t* dst = ring + slot * A.slot_bytes;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            const uint8_t* ws = ts.w[m] + (uint64_t)n0 * RB;
+            const uint8_t* ws = ts.w[m] + (uint64_t)n0 * wrow;
 #pragma unroll
             for (uint32_t t = 0; t < LWMAX; t++)
                 if (t < lw)
-                    __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? woff[t] : 0),
+                    __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? wsrc[t] : 0),
                                                      dst + m * A.w_region + wpos[t], 16, 0, 0);
-            const uint8_t* ss = ts.s[m] + (uint64_t)n0 * SB;
+            const uint8_t* ss = ts.s[m] + (uint64_t)n0 * srow;
 #pragma unroll
             for (uint32_t t = 0; t < LSMAX; t++)
                 if (t < ls)
-                    __builtin_amdgcn_global_load_lds(ss + (soff[t] < sbytes ? soff[t] : 0),
+                    __builtin_amdgcn_global_load_lds(ss + (soff[t] < sbytes ? ssrc[t] : 0),
                                                      dst + NMAT * A.w_region + m * A.s_region + spos[t], 4, 0, 0);
         }
     };
@@ -1997,7 +2015,10 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = NMAT * (A.lw + A.ls);
     size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
-    if (FUSED && lds < sizeof(FusedTables)) lds = sizeof(FusedTables);
+    // The set-up tables and the staged address table share the ring's LDS
+    // (short rings are extended to hold them).
+    const size_t tables = (sizeof(FusedTables) + 15) / 16 * 16 + (size_t)A.T.n_records * 32;
+    if (FUSED && lds < tables) lds = tables;
     A.addr_lds_records = FUSED ? (uint32_t)((lds - (sizeof(FusedTables) + 15) / 16 * 16) / 32) : 0u;
     if (lds > 160 * 1024 || A.copies_per_item * NBUF > 63) return NERVE_HIP_UNSUPPORTED;
     A.small_plan = FUSED && A.T.E <= 64 && A.T.batch_width * A.T.k <= 64 && ctx->cu_count >= 64 ? 1u : 0u;
@@ -3061,11 +3082,16 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
             fa.out16 = static_cast<uint16_t*>(expert_outputs);
             fa.count_control = count_control;
             fa.count_tiles = (H + 63) / 64;
+            fa.block_major = ms.input_block_major ? 1u : 0u;
             st = launch_stream<SPAN_DOWN, 1, 3, 8, 2, true>(fa, ctx, stream);
             if (st == NERVE_HIP_OK) count_control = nullptr;
         }
         if (st != NERVE_HIP_UNSUPPORTED) return st;
     }
+    if (ms.input_block_major)
+        return nh::fail(NERVE_HIP_UNSUPPORTED,
+                        "input_block_major_b128 down weights are supported on the decode streaming path only (B k < "
+                        "512, 256 <= I <= 4096, intermediate frames of whole 16-byte pieces)");
     if (count_control) {
         // Count stage as its own launch (its one changed word, computed the
         // same way) for the other down paths.

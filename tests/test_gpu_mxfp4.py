@@ -6,6 +6,7 @@ import pytest
 
 import oracle
 from nerve_amd import workloads as wl
+from nerve_amd.hip import NerveHipError, check_specialization
 from nerve_amd.moe import ExpertBank, address_record, down_spec, gate_up_spec, u32_tensor
 
 from helpers import bf16_close, rel_err_normwise, to_dev, to_np
@@ -309,6 +310,59 @@ def test_down_counted_matches_count_then_down(ctx, dev, E, k, B, H, I, start, co
         assert np.array_equal(to_np(rig.expert_out, np.uint16)[owned], ref_eo[owned])
     else:
         assert np.array_equal(to_np(rig.expert_out, np.uint16), ref_eo)
+
+
+def _block_major(w, s):
+    """Row-major down parameters -> input_block_major_b128 (W [E, I/128, H,
+    64], S [E, I/128, H, 4]): byte (row r, packed column j) goes to
+    ((j / 64) H + r) 64 + j % 64, scale byte (r, group q) to ((q / 4) H + r) 4
+    + q % 4 (independent_sparse_moe_down_batch1_mxfp4.comp.template:229-233,
+    :260-263)."""
+    E, H, RB = w.shape
+    wb = np.ascontiguousarray(w.reshape(E, H, RB // 64, 64).transpose(0, 2, 1, 3))
+    sb = np.ascontiguousarray(s.reshape(E, H, RB // 64, 4).transpose(0, 2, 1, 3))
+    return wb, sb
+
+
+@pytest.mark.parametrize("E,k,B,H,I,start,count", [(8, 4, 16, 512, 256, 0, 0), (32, 4, 16, 2880, 2816, 0, 0),
+                                                   (32, 4, 16, 384, 512, 4, 20), (8, 4, 3, 160, 256, 0, 0)])
+def test_down_input_block_major(ctx, dev, E, k, B, H, I, start, count):
+    """input_block_major_b128 down weights give the row-major result bit for
+    bit (the same products, only the addresses differ), and match the oracle
+    on the row-major copy; prefill-sized batches are refused."""
+    d, routes, hidden = _moe_case(E, k, B, H, I, seed=H + I + start)
+    rig = MoeRig(dev, d, routes)
+    rig.control = to_dev(np.array([B, start, count, 0, 0, 0, 0, 0], np.uint32), dev)
+    rig.run(ctx, hidden)
+    ref_eo = to_np(rig.expert_out, np.uint16).copy()
+    wb, sb = _block_major(d["down_w"], d["down_s"])
+    bank = ExpertBank(rig.bank.gate_w, rig.bank.gate_s, rig.bank.up_w, rig.bank.up_s, to_dev(wb, dev), to_dev(sb, dev))
+    spec = rig.dn.replace("_mxfp4_e2m1", "_input_block_major_b128_mxfp4_e2m1")
+    assert check_specialization(spec) == 0
+    rig.expert_out.fill_(0x7F7F)
+    ctx.mxfp4_moe_down(spec, rig.inter, rig.routes, rig.expert_out, bank.addresses, bank.down_slots, rig.control, B)
+    eo = to_np(rig.expert_out, np.uint16)
+    owned = np.ones(routes.shape, bool) if not count else \
+        ((routes & 0xFFFF) >= start) & ((routes & 0xFFFF) < start + count)
+    assert np.array_equal(eo[owned], ref_eo[owned])
+    cmap, ctl = oracle.route_compact(routes, k, (H + 63) // 64, B, start, count)
+    eo_ref = oracle.moe_down(rig.h_np(), routes, cmap, int(ctl[3]), d["down_w"], d["down_s"])
+    ok, worst, exact = bf16_close(eo[owned], eo_ref[owned])
+    assert ok and exact > 0.9, (worst, exact)
+
+
+def test_down_input_block_major_refused_for_prefill(ctx, dev):
+    E, k, B, H, I = 8, 4, 160, 256, 256
+    d, routes, hidden = _moe_case(E, k, B, H, I, seed=7)
+    rig = MoeRig(dev, d, routes)
+    rig.run(ctx, hidden)
+    wb, sb = _block_major(d["down_w"], d["down_s"])
+    bank = ExpertBank(rig.bank.gate_w, rig.bank.gate_s, rig.bank.up_w, rig.bank.up_s, to_dev(wb, dev), to_dev(sb, dev))
+    spec = rig.dn.replace("_mxfp4_e2m1", "_input_block_major_b128_mxfp4_e2m1")
+    with pytest.raises(NerveHipError) as ei:
+        ctx.mxfp4_moe_down(spec, rig.inter, rig.routes, rig.expert_out, bank.addresses, bank.down_slots,
+                           rig.control, B)
+    assert ei.value.status == 3
 
 
 def test_moe_prefill_config3_subset(ctx, dev):

@@ -192,7 +192,13 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
  * (gate_w, gate_s, up_w, up_s).  control: device BatchControl (batch_width
  * given on the host; expert_count and owned_route_count read on the device).
  * The grid is sized for batch_width * k routes; routes past the owned count
- * exit on the device, which replaces the reference's indirect dispatch. */
+ * exit on the device, which replaces the reference's indirect dispatch.
+ * e4m3 expert banks (…_mxfp4_e2m1_{resident,adaptive}_fp8_e4m3_g32 and
+ * …_g32_native_fp8_e4m3_se8m0_b128_nf{N}; gate_up template :173-229,
+ * :299-355) take e4m3 weights [I, H] with the per-32 scales (pre-expanded)
+ * or a [ceil(I/128), ceil(H/128)] e8m0 grid (experts >= N); adaptive banks
+ * pick compact or expanded per expert by address-record word 7.  Both
+ * projection entry points accept them for E <= 1024. */
 nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spec,
                                              const void* hidden, const void* hidden_scales,
                                              const void* routes_u32, void* intermediates,

@@ -104,8 +104,11 @@ static nerve_hip_status parse_moe_spec_uncached(const char* spec, MoeSpec* out) 
         s.gate_up != s.has_limit || s.experts > 65536)
         return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid demand-addressed MXFP4 expert kernel ") + spec);
     if (s.tensor_parallel) return fail(NERVE_HIP_UNSUPPORTED, "tensor-parallel expert partials are a multi-GPU path; this backend is single-GPU");
-    if (s.weight_repr != 0 || s.native_fp8_start >= 0)
-        return fail(NERVE_HIP_UNSUPPORTED, "resident/adaptive FP8 and native-FP8 expert banks are not implemented yet");
+    // Native FP8 banks: 0 < start < E, not with tensor-parallel partials or
+    // the block-major layout (nerve/model_package_shader_templates.py:4809-4817).
+    if (s.native_fp8_start >= 0 && (s.native_fp8_start == 0 || (uint32_t)s.native_fp8_start >= s.experts ||
+                                    s.input_block_major))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid native FP8 expert range in ") + spec);
     // input_block_major_b128 is a down-weight layout
     // (nerve/model_package_independent_experts.py:164-170) and needs whole
     // 128-column blocks.

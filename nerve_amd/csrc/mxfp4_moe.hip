@@ -292,6 +292,13 @@ struct TileArgs {
     const uint32_t* slots;
     uint32_t n_slot_words, P;
     uint64_t req_w, req_s;
+    // Weight representations (…gate_up_batch1_mxfp4.comp.template:173-229):
+    // wmode 0 compact MXFP4 only, 1 every MXFP4 expert pre-expanded to e4m3
+    // bytes, 2 per expert by address-record word 7 (0 compact, 1 expanded);
+    // experts >= native_start are native e4m3 with a 128 x 128 e8m0 grid.
+    // req_w8 / req_sn: expanded weight bytes, native scale bytes.
+    uint32_t wmode, native_start;
+    uint64_t req_w8, req_sn;
     uint32_t TM, max_tiles;
     uint32_t* seg_list;
     TileRec* recs;
@@ -362,13 +369,24 @@ __device__ void build_tiles(const TileArgs& A) {
     if (n > cap) n = cap;
     const uint8_t* my_w[2] = {nullptr, nullptr};
     const uint8_t* my_s[2] = {nullptr, nullptr};
+    uint32_t my_fmt = 0;
     if (tid < A.E) {
         bool ok = true;
+        // Format of this expert: 0 compact, 1 expanded, 2 native e4m3
+        // (dynamic_expert_is_valid, …gate_up_batch1_mxfp4.comp.template:190-229).
+        const bool native = tid >= A.native_start;
+        const uint32_t repr0 = rec[0][7], repr2 = P > 2 ? rec[2][7] : repr0;
+        const bool pre0 = !native && (A.wmode == 1 || (A.wmode == 2 && repr0 == 1u));
+        const bool pre2 = !native && (A.wmode == 1 || (A.wmode == 2 && repr2 == 1u));
+        if (native) ok = repr0 == 0u && repr2 == 0u;
+        else if (A.wmode == 2) ok = repr0 <= 1u && repr2 <= 1u && pre0 == pre2;
+        my_fmt = native ? 2u : pre0 ? 1u : 0u;
+        const uint64_t rw = my_fmt ? A.req_w8 : A.req_w, rs = native ? A.req_sn : A.req_s;
 #pragma unroll
         for (uint32_t p = 0; p < 4; p++) {
             if (p >= P) continue;
             const bool is_weight = (p % 2) == 0;
-            ok = record_valid(slot[p], A.n_records, rec[p], is_weight ? A.req_w : A.req_s, is_weight ? 16u : 4u) && ok;
+            ok = record_valid(slot[p], A.n_records, rec[p], is_weight ? rw : rs, is_weight ? 16u : native ? 1u : 4u) && ok;
         }
         valid[tid] = ok ? 1 : 0;
         cnt[tid] = 0;
@@ -379,7 +397,9 @@ __device__ void build_tiles(const TileArgs& A) {
             my_s[m] = reinterpret_cast<const uint8_t*>((uint64_t)rec[2 * m + 1][0] | ((uint64_t)rec[2 * m + 1][1] << 32));
         }
     }
-    // Experts beyond the block size (E > 1024) take the plain path.
+    // Experts beyond the block size (E > 1024) take the plain path (compact
+    // MXFP4 only: the host sends the other representations here only with
+    // E <= the block size).
     for (uint32_t e = tid + nt; e < A.E; e += nt) {
         bool ok = true;
         for (uint32_t p = 0; p < P; p++) {
@@ -455,7 +475,9 @@ __device__ void build_tiles(const TileArgs& A) {
             const uint32_t idx = tst[e] + t;
             if (idx < A.max_tiles) {
                 TileRec rec_out;
-                rec_out.expert = e;
+                // Bits 16-17: the expert's weight format (known to its own
+                // thread; experts past the block size are compact).
+                rec_out.expert = e | ((e == tid ? my_fmt : 0u) << 16);
                 rec_out.begin = cur[e] + t * A.TM;
                 rec_out.count = min(A.TM, cnt[e] - t * A.TM);
                 rec_out.pad = (t << 16) | nte;   // tile index within the expert, expert's tile count
@@ -1127,6 +1149,116 @@ __global__ __launch_bounds__(256) void mx_span_kernel(SpanArgs A) {
                 const float wr = bf16_to_f32(A.routes[r] >> 16);
                 A.out16[(uint64_t)r * N + n] = (uint16_t)f32_to_bf16(t[0][i] * wr);
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Expert banks with e4m3 weights (resident/adaptive pre-expanded MXFP4 and
+// native FP8 experts, …gate_up_batch1_mxfp4.comp.template:173-229, :299-355;
+// …down_batch1_mxfp4.comp.template:151-183, :355-418).  One block = 16
+// weight rows of one tile (<= 16 routes) of the preparation launch; its 4
+// waves split the 128-column chunks.  The tile's format (bits 16-17 of its
+// record's expert word) picks the operands per block:
+//  - 0 compact MXFP4: fp4 weights, the fp8 x fp4 operand layout of load_a;
+//  - 1 expanded: e4m3 weights in the activation operand's layout, with the
+//    row's per-32 e8m0 scales (lane group g carries block g's);
+//  - 2 native: e4m3 bytes with the e8m0 byte of the weight's 128 x 128 block
+//    (a zero byte is the scale 0.0, so the weights are zeroed).
+// The weights are read straight from global memory into registers.
+// ---------------------------------------------------------------------------
+template <int MODE, int NMAT>
+__global__ __launch_bounds__(256) void mx_wfmt_kernel(SpanArgs A) {
+    __shared__ v4f red[4][NMAT][64];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, N = A.N, nch = (K + 127) / 128, SB = K / 32;
+    const uint32_t n0 = blockIdx.x * 16;
+    const uint32_t tile = blockIdx.y;
+    if (n0 >= N || tile >= *A.n_tiles) return;
+    const TileRec rec = A.recs[tile];
+    const uint32_t fmt = (rec.expert >> 16) & 3u, begin = rec.begin, cnt = rec.count;
+    const uint32_t n = min(n0 + rr, N - 1);
+    const uint8_t* arow = nullptr;
+    const float* ascale = nullptr;
+    if (rr < cnt) {
+        const uint32_t row = A.seg_list[begin + rr] / A.a_row_div;
+        arow = A.aq + (uint64_t)row * K;
+        ascale = A.as + (uint64_t)row * nch;
+    }
+    const uint32_t per = (nch + 3) / 4;
+    const uint32_t c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
+    v4f acc[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = c0; c < c1; c++) {
+        const uint32_t kb = c * 128 + g * 32;
+        const bool kv = kb < K;
+        if (fmt == 0) {
+            v8i a;
+            uint32_t sa;
+            load_a(arow, ascale, K, c, g, a, sa);
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                v4i w;
+                uint32_t sw;
+                load_w(rec.w[m] + (uint64_t)n * (K / 2), rec.s[m] + (uint64_t)n * SB, K, c, g, w, sw);
+                acc[m] = mfma_fp8_fp4(a, w, sa, sw, acc[m]);
+            }
+        } else {
+            // Both e4m3 operands in the activation layout (lane group g: k
+            // 16 g.. and 64 + 16 g..); the scale of lane group g is that of
+            // the chunk's 32-column block g, as for the fp4 weights.
+            v8i a;
+            uint32_t sa;
+            load_a(arow, ascale, K, c, g, a, sa);
+            const uint32_t k0 = c * 128 + g * 16;
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                const uint8_t* wr = rec.w[m] + (uint64_t)n * K;
+                v4i wlo = v4i{0, 0, 0, 0}, whi = v4i{0, 0, 0, 0};
+                if (k0 < K) wlo = *reinterpret_cast<const v4i*>(wr + k0);
+                if (k0 + 64 < K) whi = *reinterpret_cast<const v4i*>(wr + k0 + 64);
+                uint32_t sw = 127;
+                if (fmt == 2) {
+                    // One byte per 128 x 128 block; 0 is the scale 0.0.
+                    sw = rec.s[m][(uint64_t)(n / 128) * nch + c];
+                    if (sw == 0u) wlo = whi = v4i{0, 0, 0, 0};
+                } else if (kv) {
+                    sw = rec.s[m][(uint64_t)n * SB + kb / 32];
+                }
+                acc[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    a, v8i{wlo.x, wlo.y, wlo.z, wlo.w, whi.x, whi.y, whi.z, whi.w}, acc[m], 0, 0, 0, (int)sa, 0,
+                    (int)sw);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) red[wave][m][lane] = acc[m];
+    __syncthreads();
+    if (wave != 0) return;
+    v4f tsum[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) tsum[m] = ((red[0][m][lane] + red[1][m][lane]) + red[2][m][lane]) + red[3][m][lane];
+    const uint32_t nn = n0 + rr;
+    if (nn >= N) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t tl = 4 * g + i;
+        if (tl >= cnt) continue;
+        const uint32_t r = A.seg_list[begin + tl];
+        if (MODE == SPAN_GATE_UP) {
+            float gv = round_bf16(tsum[0][i]);
+            float uv = round_bf16(tsum[NMAT - 1][i]);
+            if (A.limit > 0.0f) {
+                gv = fminf(gv, A.limit);
+                uv = fminf(fmaxf(uv, -A.limit), A.limit);
+            }
+            const float h = (gv / (1.0f + expf(-gv))) * uv;
+            A.out16[(uint64_t)(r / A.k) * A.frame_elems + (uint64_t)(r % A.k) * N + nn] = (uint16_t)f32_to_bf16(h);
+        } else {
+            const float wr = bf16_to_f32(A.routes[r] >> 16);
+            A.out16[(uint64_t)r * N + nn] = (uint16_t)f32_to_bf16(tsum[0][i] * wr);
         }
     }
 }
@@ -2984,7 +3116,12 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     // Decode-shaped batches stream each expert's weights once per <= 16
     // routes; prefill-shaped batches use the LDS-staged grouped GEMM with
     // 64-route tiles.
-    const bool grouped = cap >= 512 || K > 4096;
+    // Banks with e4m3 weights (pre-expanded or native FP8 experts) take the
+    // preparation launch and mx_wfmt_kernel at every batch size.
+    const bool wf = ms.weight_repr != 0 || ms.native_fp8_start >= 0;
+    if (wf && (E > 1024 || ms.input_block_major))
+        return nh::fail(NERVE_HIP_UNSUPPORTED, "e4m3 expert banks are supported for E <= 1024, row-major layout");
+    const bool grouped = !wf && (cap >= 512 || K > 4096);
     // Persistent grouped GEMM: enough chunks per item for the descriptor
     // prefetch rounds.
     const bool persistent = grouped && (K + 127) / 128 >= PG_MIN_CHUNKS;
@@ -3046,6 +3183,10 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.n_slot_words = slot_words;
     ta.P = gate_up ? 4 : 2;
     ta.req_w = (uint64_t)N * K / 2;
+    ta.wmode = (uint32_t)ms.weight_repr;
+    ta.native_start = ms.native_fp8_start >= 0 ? (uint32_t)ms.native_fp8_start : 0xffffffffu;
+    ta.req_w8 = (uint64_t)N * K;
+    ta.req_sn = (uint64_t)((N + 127) / 128) * ((K + 127) / 128);
     ta.req_s = (uint64_t)N * K / 32;
     ta.TM = TM;
     ta.max_tiles = max_tiles;
@@ -3058,7 +3199,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.a_row_div = gate_up ? k : 1;
     // Decode-shaped batches: one streaming launch that builds its own tiles
     // and quantizes its own activation chunks (no preparation launch).
-    if (!grouped && !(gate_up && ms.prequant)) {
+    if (!wf && !grouped && !(gate_up && ms.prequant)) {
         StreamArgs fa{};
         fa.K = K;
         fa.N = N;
@@ -3124,6 +3265,30 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ea.n_tiles = ta.n_tiles;
     ea.frame_elems = frame_words * 2;
     ea.limit = ms.limit;
+    if (wf) {
+        SpanArgs wa{};
+        wa.aq = aq;
+        wa.as = as;
+        wa.a_row_div = ea.a_row_div;
+        wa.K = K;
+        wa.N = N;
+        wa.k = k;
+        wa.routes = ea.routes;
+        wa.seg_list = ea.seg_list;
+        wa.recs = ea.recs;
+        wa.n_tiles = ea.n_tiles;
+        wa.frame_elems = ea.frame_elems;
+        wa.limit = ea.limit;
+        const dim3 wgrid((N + 15) / 16, max_tiles);
+        if (gate_up) {
+            wa.out16 = static_cast<uint16_t*>(intermediates);
+            mx_wfmt_kernel<SPAN_GATE_UP, 2><<<wgrid, 256, 0, stream>>>(wa);
+        } else {
+            wa.out16 = static_cast<uint16_t*>(expert_outputs);
+            mx_wfmt_kernel<SPAN_DOWN, 1><<<wgrid, 256, 0, stream>>>(wa);
+        }
+        return nh::check_launch("mx_wfmt_kernel");
+    }
     if (persistent) {
         PgArgs pa;
         pa.aq = aq;

@@ -62,7 +62,12 @@ def test_null_context_is_rejected():
     ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_g32_h2880_i2880_e32_k4.comp", 2),
     # families outside this build
     ("independent_sparse_moe_down_batch1_tensor_parallel_input_block_major_b128_mxfp4_e2m1_g32_h128_i128_e2_k1.comp", 3),
-    ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_resident_fp8_e4m3_g32_h128_i128_e2_k1_limit7.comp", 3),
+    # e4m3 expert banks (resident / adaptive pre-expanded, native FP8 experts)
+    ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_resident_fp8_e4m3_g32_h128_i128_e2_k1_limit7.comp", 0),
+    ("independent_sparse_moe_down_batch1_mxfp4_e2m1_adaptive_fp8_e4m3_g32_h128_i128_e2_k1.comp", 0),
+    ("independent_sparse_moe_down_batch1_mxfp4_e2m1_g32_native_fp8_e4m3_se8m0_b128_nf1_h128_i128_e2_k1.comp", 0),
+    ("independent_sparse_moe_down_batch1_mxfp4_e2m1_g32_native_fp8_e4m3_se8m0_b128_nf2_h128_i128_e2_k1.comp", 2),
+    ("independent_sparse_moe_down_batch1_mxfp4_e2m1_g32_native_fp8_e4m3_se8m0_b128_nf0_h128_i128_e2_k1.comp", 2),
     (topk_spec(32, 4), 0),
     ("moe_topk_batch1_sigmoid_bf16_e256_k8_norm1_cap0_biasf32.comp", 0),
     ("moe_topk_batch4_softmax_bf16_e32_k4_norm1_cap0_nobias.comp", 2),

@@ -365,6 +365,105 @@ def test_down_input_block_major_refused_for_prefill(ctx, dev):
     assert ei.value.status == 3
 
 
+_E2M1_E4M3 = np.array([0x00, 0x30, 0x38, 0x3C, 0x40, 0x44, 0x48, 0x4C], np.uint8)
+
+
+def _expand_e4m3(w):
+    """Compact MXFP4 bytes [..., K/2] -> the e4m3 bytes [..., K] of the same
+    values (mxfp4_e4m3_bits, …gate_up_batch1_mxfp4.comp.template:246-248)."""
+    lo, hi = w & 0x0F, w >> 4
+    out = np.empty(w.shape[:-1] + (2 * w.shape[-1],), np.uint8)
+    out[..., 0::2] = _E2M1_E4M3[lo & 7] | ((lo & 8) << 4)
+    out[..., 1::2] = _E2M1_E4M3[hi & 7] | ((hi & 8) << 4)
+    return out
+
+
+def _bank_tables(dev, per_expert):
+    """Address table and slots from per-expert (tensor, representation)
+    lists: gate_up slots (gw, gs, uw, us) and down slots (dw, ds)."""
+    recs, gate_slots, down_slots = [], [], []
+    keep = []
+    for gate, down in per_expert:
+        for tt, rep in gate:
+            gate_slots.append(len(recs) // 8)
+            recs += address_record(tt, representation=rep)
+            keep.append(tt)
+        for tt, rep in down:
+            down_slots.append(len(recs) // 8)
+            recs += address_record(tt, representation=rep)
+            keep.append(tt)
+    return u32_tensor(recs, dev), u32_tensor(gate_slots, dev), u32_tensor(down_slots, dev), keep
+
+
+@pytest.mark.parametrize("mode", ["resident", "adaptive", "native"])
+@pytest.mark.parametrize("E,k,B,H,I", [(8, 4, 16, 512, 256), (8, 2, 40, 384, 640), (32, 4, 16, 2880, 2880)])
+def test_e4m3_expert_banks(ctx, dev, mode, E, k, B, H, I):
+    """Resident / adaptive pre-expanded MXFP4 and native FP8 experts
+    (…gate_up_batch1_mxfp4.comp.template:173-229, :299-355): the same values
+    as a compact bank give the compact bank's outputs.  Native experts get
+    128 x 128 scale blocks (the compact twin repeats each block's scale) and
+    one all-zero scale block, whose weights count as zero (the compact twin
+    has zero codes there)."""
+    d, routes, hidden = _moe_case(E, k, B, H, I, seed=E + B + H + len(mode))
+    nf = E // 2 if mode == "native" else E
+    orig = {n: d[n].copy() for n in ("gate_w", "up_w", "down_w")}   # native weights keep the zero-scale block's codes
+    if mode == "native":
+        for wn, sn, R, C in (("gate_w", "gate_s", I, H), ("up_w", "up_s", I, H), ("down_w", "down_s", H, I)):
+            s = d[sn].reshape(E, R, C // 32)
+            for e in range(nf, E):
+                blk = s[e, ::128, ::4][:, :(C + 127) // 128].copy()                  # [ceil(R/128), ceil(C/128)]
+                s[e] = np.repeat(np.repeat(blk, 128, 0)[:R], 4, 1)[:, :C // 32]
+            d[wn][nf, :128, :64] = 0                                                  # the zero-scale block
+    rig = MoeRig(dev, d, routes)
+    rig.run(ctx, hidden)
+    ref_h, ref_eo = rig.h_np().copy(), to_np(rig.expert_out, np.uint16).copy()
+
+    exp = {n: to_dev(_expand_e4m3(orig[n] if mode == "native" else d[n]), dev) for n in ("gate_w", "up_w", "down_w")}
+    comp = {n: to_dev(d[n], dev) for n in ("gate_w", "up_w", "down_w", "gate_s", "up_s", "down_s")}
+    nat_s = {}
+    if mode == "native":
+        for sn, R, C in (("gate_s", I, H), ("up_s", I, H), ("down_s", H, I)):
+            s = d[sn].reshape(E, R, C // 32)
+            blk = np.ascontiguousarray(s[:, ::128, ::4][:, :, :(C + 127) // 128])
+            blk[nf, 0, 0] = 0
+            nat_s[sn] = to_dev(blk, dev)
+    per_expert = []
+    for e in range(E):
+        if mode == "native" and e >= nf:
+            g = [(exp["gate_w"][e], 0), (nat_s["gate_s"][e], 0), (exp["up_w"][e], 0), (nat_s["up_s"][e], 0)]
+            dn = [(exp["down_w"][e], 0), (nat_s["down_s"][e], 0)]
+        elif mode == "resident" or (mode == "adaptive" and e % 2 == 1):
+            rep = 1 if mode == "adaptive" else 0
+            g = [(exp["gate_w"][e], rep), (comp["gate_s"][e], 0), (exp["up_w"][e], rep), (comp["up_s"][e], 0)]
+            dn = [(exp["down_w"][e], rep), (comp["down_s"][e], 0)]
+        else:
+            g = [(comp["gate_w"][e], 0), (comp["gate_s"][e], 0), (comp["up_w"][e], 0), (comp["up_s"][e], 0)]
+            dn = [(comp["down_w"][e], 0), (comp["down_s"][e], 0)]
+        per_expert.append((g, dn))
+    addresses, gate_slots, down_slots, _keep = _bank_tables(dev, per_expert)
+    tok = {"resident": "_resident_fp8_e4m3", "adaptive": "_adaptive_fp8_e4m3", "native": ""}[mode]
+    nat = f"_native_fp8_e4m3_se8m0_b128_nf{nf}" if mode == "native" else ""
+    gu = rig.gu.replace("_mxfp4_e2m1_g32_", f"_mxfp4_e2m1{tok}_g32{nat}_")
+    dn = rig.dn.replace("_mxfp4_e2m1_g32_", f"_mxfp4_e2m1{tok}_g32{nat}_")
+    assert check_specialization(gu) == 0 and check_specialization(dn) == 0
+    hidden_d = to_dev(hidden, dev)
+    rig.inter.zero_()
+    rig.expert_out.fill_(0x7F7F)
+    ctx.moe_route_compact(rig.gu, rig.routes, rig.inter, rig.control, B)
+    ctx.mxfp4_moe_gate_up(gu, hidden_d, None, rig.routes, rig.inter, addresses, gate_slots, rig.control, B)
+    h = rig.h_np()
+    ok, worst, exact = bf16_close(h, ref_h)
+    assert ok and exact > 0.97, (worst, exact)
+    # down from the reference h, so its check does not inherit gate_up's rounding
+    fr = rig.frames_np().copy()
+    fr[:, : k * I // 2] = ref_h.reshape(B, k * I).view(np.uint32).reshape(B, k * I // 2)
+    rig.inter.copy_(to_dev(fr.reshape(-1).view(np.int32), dev))
+    ctx.moe_route_compact(rig.dn, rig.routes, None, rig.control, B)
+    ctx.mxfp4_moe_down(dn, rig.inter, rig.routes, rig.expert_out, addresses, down_slots, rig.control, B)
+    ok, worst, exact = bf16_close(to_np(rig.expert_out, np.uint16), ref_eo)
+    assert ok and exact > 0.97, (worst, exact)
+
+
 def test_moe_prefill_config3_subset(ctx, dev):
     """Config 3 (2048 tokens, 128 Zipf-loaded experts, H = I = 2880) on the GPU;
     24 tokens re-computed by the oracle (each token's result depends only on

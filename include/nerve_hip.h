@@ -88,6 +88,22 @@ void nerve_hip_close(nerve_hip_ctx* ctx);
  * 3219-3276, 1513-1545), extended to shapes that are multiples of 32. */
 nerve_hip_status nerve_hip_check_specialization(const char* spec);
 
+/* ---- RMSNorm + FP8 prequantization -------------------------------------- */
+
+/* Replaces rms_norm_quantize[_batch{T}]_fp8_e4m3[_spow2]_b{BLOCK}_h{H}_eps{E}
+ * _offset{O}.comp (rms_norm_quantize_fp8_e4m3.comp.template:70-129; grammar
+ * nerve/model_package_shader_templates.py:3530-3553): per row,
+ * y = bf16(x * inversesqrt(mean(x^2) + eps) * (w + offset)) and, per BLOCK
+ * columns, s = pow2 ("_spow2") or amax/448 scale of max |y|, q = e4m3(y / s).
+ * x, y bf16 [rows, H] (y may be x: the batch form is in place); weight bf16
+ * [H]; q e4m3 [rows, H]; scales f32 [rows, H / BLOCK].  The sum of squares
+ * is a fixed tree of per-thread fma chains, so y can differ from the
+ * shader's (whose order follows its subgroups) in the last bf16 place. */
+nerve_hip_status nerve_hip_rms_norm_quantize_fp8_e4m3(nerve_hip_ctx* ctx, const char* spec,
+                                                     const void* x_bf16, const void* weight_bf16,
+                                                     void* y_bf16, void* q_e4m3, void* scales_f32,
+                                                     uint32_t rows, void* stream);
+
 /* ---- a2: activation block quantization -------------------------------- */
 
 /* Replaces quantize_fp8_e4m3[_spow2]_b128_h{N}.comp

@@ -162,4 +162,12 @@ struct QuantSpec {
 };
 nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out);
 
+struct RmsQuantSpec {
+    int batch_tile = 0;
+    bool pow2 = false;
+    uint32_t block = 0, hidden = 0;
+    float eps = 0.0f, offset = 0.0f;
+};
+nerve_hip_status parse_rms_quant_spec(const char* spec, RmsQuantSpec* out);
+
 }  // namespace nh

@@ -229,6 +229,31 @@ static nerve_hip_status parse_quant_spec_uncached(const char* spec, QuantSpec* o
 }
 
 
+// nerve/model_package_shader_templates.py:3530-3553
+static nerve_hip_status parse_rms_quant_spec_uncached(const char* spec, RmsQuantSpec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex re(
+        "rms_norm_quantize(?:_batch(\\d+))?_fp8_e4m3(?:_(spow2))?_b(\\d+)_h(\\d+)_eps([0-9eE+.-]+)_offset([0-9eE+.-]+)\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("not an RMSNorm FP8 quantizer: ") + spec);
+    RmsQuantSpec s;
+    uint32_t bt = 0;
+    if (m[1].matched) parse_u32(m[1].str(), &bt);
+    s.batch_tile = (int)bt;
+    s.pow2 = m[2].matched;
+    parse_u32(m[3].str(), &s.block);
+    parse_u32(m[4].str(), &s.hidden);
+    if (!parse_float(m[5].str(), &s.eps) || !parse_float(m[6].str(), &s.offset))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("bad eps/offset in ") + spec);
+    // Whole blocks of 32..512 columns (BLOCK_COUNT = HIDDEN / BLOCK_COLUMNS).
+    if ((m[1].matched && bt == 0) || s.hidden == 0 || s.hidden % 32 || s.block < 32 || s.block > 512 ||
+        (s.block & (s.block - 1)) || s.hidden % s.block)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid RMSNorm FP8 quantizer shape ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
 // Specialization strings are parsed once per thread: a dispatch looks its
 // string up here (a hash of ~60 bytes) instead of running the grammar again,
 // which costs more host time than a decode-sized kernel takes on the device.
@@ -265,6 +290,9 @@ nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out) {
 }
 nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out) {
     return parse_cached<QuantSpec, parse_quant_spec_uncached>(spec, out);
+}
+nerve_hip_status parse_rms_quant_spec(const char* spec, RmsQuantSpec* out) {
+    return parse_cached<RmsQuantSpec, parse_rms_quant_spec_uncached>(spec, out);
 }
 
 }  // namespace nh
@@ -310,6 +338,10 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
     if (s.rfind("tied_output_projection", 0) == 0) {
         nh::Fp8HeadSpec f;
         return nh::parse_fp8_head_spec(spec, &f);
+    }
+    if (s.rfind("rms_norm_quantize", 0) == 0) {
+        nh::RmsQuantSpec r;
+        return nh::parse_rms_quant_spec(spec, &r);
     }
     if (s.rfind("quantize", 0) == 0) {
         nh::QuantSpec q;

@@ -21,6 +21,7 @@ EXPORTS = (
     "nerve_hip_close",
     "nerve_hip_check_specialization",
     "nerve_hip_quantize_fp8_e4m3",
+    "nerve_hip_rms_norm_quantize_fp8_e4m3",
     "nerve_hip_mxfp4_gemv",
     "nerve_hip_router_linear_bf16",
     "nerve_hip_moe_router_topk",
@@ -75,6 +76,7 @@ def _declare(lib) -> None:
         "nerve_hip_close": (None, [P]),
         "nerve_hip_check_specialization": (ctypes.c_int, [S]),
         "nerve_hip_quantize_fp8_e4m3": (ctypes.c_int, [P, S, P, U32, P, P, P]),
+        "nerve_hip_rms_norm_quantize_fp8_e4m3": (ctypes.c_int, [P, S, P, P, P, P, P, U32, P]),
         "nerve_hip_mxfp4_gemv": (ctypes.c_int, [P, P, P, U32, U32, P, P, U32, P, P]),
         "nerve_hip_router_linear_bf16": (ctypes.c_int, [P, P, P, P, U32, U32, U32, P]),
         "nerve_hip_moe_router_topk": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
@@ -169,6 +171,11 @@ class Context:
     def quantize_fp8_e4m3(self, spec, x, rows, q, scales, stream=None):
         _check(self.lib.nerve_hip_quantize_fp8_e4m3(self.handle, _spec(spec), ptr(x), rows, ptr(q), ptr(scales),
                                                     _stream(stream)))
+
+    # ---- RMSNorm + FP8 prequantization
+    def rms_norm_quantize_fp8_e4m3(self, spec, x, weight, y, q, scales, rows, stream=None):
+        _check(self.lib.nerve_hip_rms_norm_quantize_fp8_e4m3(self.handle, _spec(spec), ptr(x), ptr(weight), ptr(y),
+                                                             ptr(q), ptr(scales), rows, _stream(stream)))
 
     # ---- raw MXFP4 GEMV
     def mxfp4_gemv(self, q, scales, M, K, weight, weight_scale, N, y, stream=None):

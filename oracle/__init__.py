@@ -54,6 +54,7 @@ def _declare(l) -> None:
         "o_pow2_fp8_scale": (F, [F]),
         "o_amax_fp8_scale": (F, [F]),
         "o_quantize_blocks": (None, [P, L, I, I, I, P, P]),
+        "o_rms_norm_quantize": (None, [P, P, I, I, I, I, F, F, P, P, P]),
         "o_mxfp4_gemv": (None, [P, P, I, I, P, P, I, P]),
         "o_mxfp4_gemv_f64": (None, [P, P, I, I, P, P, I, P]),
         "o_router_linear": (None, [P, P, I, I, I, P]),
@@ -134,6 +135,10 @@ def pow2_fp8_scale(amax: float) -> float:
     return lib().o_pow2_fp8_scale(amax)
 
 
+def amax_fp8_scale(amax: float) -> float:
+    return lib().o_amax_fp8_scale(amax)
+
+
 # --------------------------------------------------------------------------
 # a2 .. a11
 # --------------------------------------------------------------------------
@@ -147,6 +152,19 @@ def quantize_blocks(x_bf16: np.ndarray, pow2: bool):
     s = np.zeros((rows, nblk), np.float32)
     lib().o_quantize_blocks(_p(x), cols, rows, cols, int(pow2), _p(q), _p(s))
     return q, s
+
+
+def rms_norm_quantize(x_bf16: np.ndarray, w_bf16: np.ndarray, block: int, pow2: bool, eps: float, offset: float):
+    """RMSNorm + blockwise e4m3 quantization (rms_norm_quantize_fp8_e4m3.comp.template:70-129).
+    Returns (y bf16 bits [R, H], q u8 [R, H], s f32 [R, H/block])."""
+    x = _c(x_bf16, np.uint16)
+    w = _c(w_bf16, np.uint16)
+    rows, H = x.shape
+    y = np.zeros((rows, H), np.uint16)
+    q = np.zeros((rows, H), np.uint8)
+    s = np.zeros((rows, H // block), np.float32)
+    lib().o_rms_norm_quantize(_p(x), _p(w), rows, H, block, int(pow2), float(eps), float(offset), _p(y), _p(q), _p(s))
+    return y, q, s
 
 
 def mxfp4_gemv(q, s, W, S) -> np.ndarray:

@@ -147,6 +147,40 @@ void o_quantize_blocks(const uint16_t* x, long x_stride, int rows, int cols,
     }
 }
 
+/* RMSNorm + blockwise e4m3 quantization of bf16 rows
+ * (rms_norm_quantize_fp8_e4m3.comp.template:70-129): sum of squares by
+ * fma, inv_rms = 1 / sqrt(sum / H + eps) (the shader's inversesqrt, taken
+ * as the correctly rounded form), y = bf16(x * inv_rms * (w + offset)),
+ * then per `block` columns s = pow2 / amax/448 scale of max |y| and
+ * q = e4m3(y / s).  The sum is taken in index order here; the shader's
+ * order is its subgroup layout's, so y may differ in the last bf16 place. */
+void o_rms_norm_quantize(const uint16_t* x, const uint16_t* w, int rows, int H, int block, int pow2, float eps,
+                         float offset, uint16_t* y, uint8_t* q, float* s) {
+    int nblk = H / block;
+    for (int r = 0; r < rows; r++) {
+        const uint16_t* xr = x + (long)r * H;
+        float ss = 0.0f;
+        for (int c = 0; c < H; c++) {
+            float v = o_bf16_to_f32(xr[c]);
+            ss = fmaf(v, v, ss);
+        }
+        float inv = 1.0f / sqrtf(ss / (float)H + eps);
+        for (int b = 0; b < nblk; b++) {
+            float amax = 0.0f;
+            for (int c = b * block; c < (b + 1) * block; c++) {
+                float v = o_bf16_to_f32(xr[c]) * inv * (o_bf16_to_f32(w[c]) + offset);
+                uint16_t yb = o_f32_to_bf16(v);
+                y[(long)r * H + c] = yb;
+                amax = fmaxf(amax, fabsf(o_bf16_to_f32(yb)));
+            }
+            float sc = pow2 ? o_pow2_fp8_scale(amax) : o_amax_fp8_scale(amax);
+            s[(long)r * nblk + b] = sc;
+            for (int c = b * block; c < (b + 1) * block; c++)
+                q[(long)r * H + c] = o_f32_to_e4m3(o_bf16_to_f32(y[(long)r * H + c]) / sc);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* Shared MXFP4 dot: one output row, emulating the shader's lane loop.  */
 /* ------------------------------------------------------------------ */

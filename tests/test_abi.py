@@ -81,7 +81,8 @@ def test_null_context_is_rejected():
     ("tied_output_projection_batch4_fp8_e4m3_b128x128_151936x4096_scale0.0333333351_to_f32.comp", 0),
     ("tied_output_projection_fp8_e4m3_b1x64_201088x2880_scale1_to_f32.comp", 2),
     ("quantize_fp8_e4m3_spow2_b128_h2880.comp", 0),
-    ("rms_norm_quantize_fp8_e4m3_spow2_b128_h2880_eps1e-05_offset1.comp", 0),
+    ("rms_norm_quantize_fp8_e4m3_spow2_b64_h2880_eps1e-05_offset1.comp", 0),
+    ("rms_norm_quantize_fp8_e4m3_spow2_b128_h2880_eps1e-05_offset1.comp", 2),
     ("rms_norm_quantize_batch16_fp8_e4m3_b32_h4096_eps1e-06_offset0.comp", 0),
     ("rms_norm_quantize_fp8_e4m3_b100_h2800_eps1e-05_offset1.comp", 2),
     ("quantize_batch4_fp8_e4m3_b128_h4096.comp", 0),

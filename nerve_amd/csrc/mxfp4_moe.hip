@@ -985,7 +985,7 @@ __global__ __launch_bounds__(256) void moe_grouped_async_kernel(ExpertArgs A) {
 // e8m0 scale span straight into LDS with global_load_lds (1 KB per wave
 // instruction, all issued up front), while each lane also prefetches its
 // activation operands.  DRAM therefore sees long sequential runs instead of
-// one 64-byte stream per weight row.  After a single wait the 4 waves split
+// one 64-byte stream per weight row.  After a single wait the NWS waves split
 // the K chunks, contract from LDS on the scaled MFMA, and reduce through LDS.
 // ---------------------------------------------------------------------------
 enum SpanMode { SPAN_RAW = 0, SPAN_GATE_UP = 1, SPAN_DOWN = 2 };
@@ -1015,8 +1015,8 @@ struct SpanArgs {
 __host__ __device__ inline uint32_t span_w_region(uint32_t rows, uint32_t K) { return (rows * (K / 2) + 1023) / 1024 * 1024; }
 __host__ __device__ inline uint32_t span_s_region(uint32_t rows, uint32_t K) { return (rows * (K / 32) + 255) / 256 * 256; }
 
-template <int MODE, int NMAT, int NSUB>
-__global__ __launch_bounds__(256) void mx_span_kernel(SpanArgs A) {
+template <int MODE, int NMAT, int NSUB, int NWS = 4>
+__global__ __launch_bounds__(64 * NWS) void mx_span_kernel(SpanArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t span_lds[];
     constexpr uint32_t R = 16 * NSUB;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1048,20 +1048,20 @@ __global__ __launch_bounds__(256) void mx_span_kernel(SpanArgs A) {
         const uint8_t* wsrc = wb + (uint64_t)n0 * RB;
         const uint32_t wbytes = rows * RB;
         uint8_t* wdst = span_lds + m * A.w_region;
-        for (uint32_t pc = wave; pc * 1024 < wbytes; pc += 4) {
+        for (uint32_t pc = wave; pc * 1024 < wbytes; pc += NWS) {
             uint32_t off = pc * 1024 + lane * 16;
             __builtin_amdgcn_global_load_lds(wsrc + (off < wbytes ? off : 0), wdst + pc * 1024, 16, 0, 0);
         }
         const uint8_t* ssrc = sb + (uint64_t)n0 * SB;
         const uint32_t sbytes = rows * SB;
         uint8_t* sdst = span_lds + NMAT * A.w_region + m * A.s_region;
-        for (uint32_t pc = wave; pc * 256 < sbytes; pc += 4) {
+        for (uint32_t pc = wave; pc * 256 < sbytes; pc += NWS) {
             uint32_t off = pc * 256 + lane * 4;
             __builtin_amdgcn_global_load_lds(ssrc + (off < sbytes ? off : 0), sdst + pc * 256, 4, 0, 0);
         }
     }
     // ---- activation operands of this wave's chunks, prefetched to registers
-    const uint32_t per = (nch + 3) / 4;
+    const uint32_t per = (nch + NWS - 1) / NWS;
     const uint32_t c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
     const uint8_t* arow = nullptr;
     const float* ascale = nullptr;
@@ -1115,16 +1115,16 @@ __global__ __launch_bounds__(256) void mx_span_kernel(SpanArgs A) {
 #pragma unroll
         for (int j = 0; j < NSUB; j++) red[((wave * NMAT + m) * NSUB + j) * 64 + lane] = acc[m][j];
     __syncthreads();
-    // Wave w finalizes the sub-tiles j with j % 4 == w (all matrices).
+    // Wave w finalizes the sub-tiles j with j % NWS == w (all matrices).
 #pragma unroll
     for (int j = 0; j < NSUB; j++) {
-        if ((uint32_t)(j % 4) != wave) continue;
+        if ((uint32_t)(j % NWS) != wave) continue;
         v4f t[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             t[m] = red[((0 * NMAT + m) * NSUB + j) * 64 + lane];
 #pragma unroll
-            for (int w = 1; w < 4; w++) t[m] += red[((w * NMAT + m) * NSUB + j) * 64 + lane];
+            for (int w = 1; w < NWS; w++) t[m] += red[((w * NMAT + m) * NSUB + j) * 64 + lane];
         }
         const uint32_t n = n0 + j * 16 + rr;
         if (n >= N) continue;
@@ -1263,22 +1263,22 @@ __global__ __launch_bounds__(256) void mx_wfmt_kernel(SpanArgs A) {
     }
 }
 
-template <int MODE, int NMAT, int NSUB>
+template <int MODE, int NMAT, int NSUB, int NWS = 4>
 nerve_hip_status launch_span(SpanArgs A, uint32_t tiles, hipStream_t st) {
     constexpr uint32_t R = 16 * NSUB;
     A.w_region = span_w_region(R, A.K);
     A.s_region = span_s_region(R, A.K);
     size_t lds = (size_t)NMAT * (A.w_region + A.s_region);
-    size_t red = (size_t)4 * NMAT * NSUB * 64 * sizeof(v4f);
+    size_t red = (size_t)NWS * NMAT * NSUB * 64 * sizeof(v4f);
     if (red > lds) lds = red;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)mx_span_kernel<MODE, NMAT, NSUB>,
+        (void)hipFuncSetAttribute((const void*)mx_span_kernel<MODE, NMAT, NSUB, NWS>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
     dim3 grid((A.N + R - 1) / R, tiles);
-    mx_span_kernel<MODE, NMAT, NSUB><<<grid, 256, lds, st>>>(A);
+    mx_span_kernel<MODE, NMAT, NSUB, NWS><<<grid, 64 * NWS, lds, st>>>(A);
     return nh::check_launch("mx_span_kernel");
 }
 
@@ -3083,7 +3083,7 @@ nerve_hip_status nerve_hip_mxfp4_gemv(nerve_hip_ctx* ctx, const void* q_e4m3, co
         sa.w_direct = static_cast<const uint8_t*>(weight);
         sa.s_direct = static_cast<const uint8_t*>(weight_scale);
         sa.out32 = static_cast<float*>(y_f32);
-        return launch_span<SPAN_RAW, 1, 1>(sa, (M + 15) / 16, (hipStream_t)stream);
+        return launch_span<SPAN_RAW, 1, 1, 8>(sa, (M + 15) / 16, (hipStream_t)stream);
     }
     mxfp4_gemv_kernel<8><<<N / 16, 512, 0, (hipStream_t)stream>>>(
         static_cast<const uint8_t*>(q_e4m3), static_cast<const float*>(scales_f32), M, K,

@@ -299,7 +299,7 @@ def mxfp4_gemv(args, ctx, dev):
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "e4m3xe2m1->f32",
                     {"workload": "mxfp4_gemv_m1_k2880_n5760", "weight_copies_rotated": copies})
-    out["roofline"] = {"bound": "hbm", "kernel": "mx_span_kernel<0,1,1>", "achieved": gbs, "peak": HBM_PEAK_GBS,
+    out["roofline"] = {"bound": "hbm", "kernel": "mx_span_kernel<0,1,1,8>", "achieved": gbs, "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                        "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
     return out

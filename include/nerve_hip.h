@@ -287,6 +287,31 @@ nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char* spec,
                                        const void* aux_bf16, void* y_bf16,
                                        uint32_t batch_width, void* stream);
 
+/* ---- pair-packed INT8 x INT4 (the int8-prequant GPTQ linear) ------------ */
+
+/* Replaces quantize[_batch{T}]_int8_symmetric_pairpacked_b32_h{N}.comp
+ * (quantize_int8_symmetric_pairpacked.comp.template:22-72; grammar
+ * nerve/model_package_shader_templates.py:1440-1474): per 32 columns
+ * s = amax > 0 ? amax / 127 : 1, q = round(clamp(x / s, -127, 127)) (round
+ * half to even), sums = the block's sum of q; columns c..c+7 become the words
+ * (q[c], q[c+2], q[c+4], q[c+6]), (q[c+1], q[c+3], q[c+5], q[c+7]).
+ * x bf16 [rows, N]; q int8 [rows, N]; scales f32 and sums i32 [rows, N/32]. */
+nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
+                                                   void* q_i8, void* scales_f32, void* sums_i32, uint32_t rows,
+                                                   void* stream);
+
+/* Replaces {linear,linear_bias,linear_residual}_prequant_pairpacked[_batch{T}]
+ * _int4_gptq_s{f16,bf16}_g{G}_{K}x{N}.comp
+ * (linear_prequant_pairpacked_int4_gptq.comp.template:56-128): y = bf16 of
+ * sum over groups and 32-column blocks of fma(-8 sums + sum_k q (code),
+ * s_x * s_w), with the bias / residual finalize of nerve_hip_int4_linear.
+ * q, scales_f32, sums as nerve_hip_quantize_int8_pairpacked writes them;
+ * qweight u32 [K/8, N], scales [K/G, N]. */
+nerve_hip_status nerve_hip_int4_linear_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* q_i8,
+                                                 const void* scales_f32, const void* sums_i32,
+                                                 const void* qweight, const void* scales, const void* aux_bf16,
+                                                 void* y_bf16, uint32_t batch_width, void* stream);
+
 /* ---- a10+a11: FP8 output projection + fused argmax ----------------------- */
 
 /* Replaces tied_output_projection[_batch{T}]_fp8_e4m3_b{BR}x128_{N}x{K}_

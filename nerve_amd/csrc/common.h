@@ -144,9 +144,16 @@ struct Int4Spec {
     int batch_tile = 0;         // 0 = unbatched form
     int layout = 0;             // 0 gptq, 1 ct
     int scale_bf16 = 0;
+    int input = 0;              // 0 bf16, 1 "_prequant" int8, 2 "_prequant_pairpacked" int8
     uint32_t group = 0, in = 0, out = 0;
 };
 nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out);
+
+struct QuantI8Spec {
+    int batch_tile = 0;
+    uint32_t block = 0, elements = 0;
+};
+nerve_hip_status parse_quant_i8_spec(const char* spec, QuantI8Spec* out);
 
 struct Fp8HeadSpec {
     int batch_tile = 0;

@@ -164,23 +164,28 @@ static nerve_hip_status parse_topk_spec_uncached(const char* spec, TopkSpec* out
 static nerve_hip_status parse_int4_spec_uncached(const char* spec, Int4Spec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re(
-        "(linear|linear_bias|linear_residual)(?:_batch(\\d+))?_int4_(gptq|ct)_s(f16|bf16)_g(\\d+)_(\\d+)x(\\d+)\\.comp");
+        "(linear|linear_bias|linear_residual)(_prequant_pairpacked|_prequant)?(?:_batch(\\d+))?_int4_(gptq|ct)_s(f16|bf16)_g(\\d+)_"
+        "(\\d+)x(\\d+)\\.comp");
     std::cmatch m;
     if (!std::regex_match(spec, m, re)) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an INT4 linear kernel: ") + spec);
     Int4Spec s;
     std::string op = m[1].str();
     s.op = op == "linear" ? 0 : (op == "linear_bias" ? 1 : 2);
+    s.input = !m[2].matched ? 0 : (m[2].str() == "_prequant" ? 1 : 2);
     uint32_t bt = 0;
-    if (m[2].matched) parse_u32(m[2].str(), &bt);
+    if (m[3].matched) parse_u32(m[3].str(), &bt);
     s.batch_tile = (int)bt;
-    s.layout = m[3].str() == "gptq" ? 0 : 1;
-    s.scale_bf16 = m[4].str() == "bf16";
-    parse_u32(m[5].str(), &s.group);
-    parse_u32(m[6].str(), &s.in);
-    parse_u32(m[7].str(), &s.out);
+    s.layout = m[4].str() == "gptq" ? 0 : 1;
+    s.scale_bf16 = m[5].str() == "bf16";
+    parse_u32(m[6].str(), &s.group);
+    parse_u32(m[7].str(), &s.in);
+    parse_u32(m[8].str(), &s.out);
     if (s.group == 0 || s.group % 32 || s.in == 0 || s.in % s.group || s.out == 0 || s.out % 2 ||
-        (m[2].matched && bt == 0))
+        (m[3].matched && bt == 0))
         return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid native INT4 shape ") + spec);
+    // nerve/model_package_shader_templates.py:3231-3235
+    if (s.input == 2 && s.layout != 0)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("pair-packed INT8 input requires GPTQ weights: ") + spec);
     *out = s;
     return NERVE_HIP_OK;
 }
@@ -254,6 +259,25 @@ static nerve_hip_status parse_rms_quant_spec_uncached(const char* spec, RmsQuant
     return NERVE_HIP_OK;
 }
 
+// nerve/model_package_shader_templates.py:1440-1474 (Q8_0 groups of 32)
+static nerve_hip_status parse_quant_i8_spec_uncached(const char* spec, QuantI8Spec* out) {
+    if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    static const std::regex re("quantize(?:_batch(\\d+))?_int8_symmetric_pairpacked_b(\\d+)_h(\\d+)\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("not a pair-packed INT8 quantizer: ") + spec);
+    QuantI8Spec s;
+    uint32_t bt = 0;
+    if (m[1].matched) parse_u32(m[1].str(), &bt);
+    s.batch_tile = (int)bt;
+    parse_u32(m[2].str(), &s.block);
+    parse_u32(m[3].str(), &s.elements);
+    if ((m[1].matched && bt == 0) || s.block != 32 || s.elements == 0 || s.elements % 32)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid pair-packed INT8 quantizer shape ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
 // Specialization strings are parsed once per thread: a dispatch looks its
 // string up here (a hash of ~60 bytes) instead of running the grammar again,
 // which costs more host time than a decode-sized kernel takes on the device.
@@ -290,6 +314,9 @@ nerve_hip_status parse_fp8_head_spec(const char* spec, Fp8HeadSpec* out) {
 }
 nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out) {
     return parse_cached<QuantSpec, parse_quant_spec_uncached>(spec, out);
+}
+nerve_hip_status parse_quant_i8_spec(const char* spec, QuantI8Spec* out) {
+    return parse_cached<QuantI8Spec, parse_quant_i8_spec_uncached>(spec, out);
 }
 nerve_hip_status parse_rms_quant_spec(const char* spec, RmsQuantSpec* out) {
     return parse_cached<RmsQuantSpec, parse_rms_quant_spec_uncached>(spec, out);
@@ -343,6 +370,10 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
         nh::RmsQuantSpec r;
         return nh::parse_rms_quant_spec(spec, &r);
     }
+    if (s.rfind("quantize", 0) == 0 && s.find("_int8_symmetric_pairpacked_") != std::string::npos) {
+        nh::QuantI8Spec q;
+        return nh::parse_quant_i8_spec(spec, &q);
+    }
     if (s.rfind("quantize", 0) == 0) {
         nh::QuantSpec q;
         return nh::parse_quant_spec(spec, &q);
@@ -351,6 +382,7 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
         nh::Int4Spec i;
         nerve_hip_status st = nh::parse_int4_spec(spec, &i);
         if (st) return st;
+        if (i.input == 1) return nh::fail(NERVE_HIP_UNSUPPORTED, "the unpaired INT8-prequant INT4 input is not built");
         if (i.layout == 1 && i.group % 128)
             return nh::fail(NERVE_HIP_UNSUPPORTED, "CT INT4 kernel needs group % 128 == 0");
         if (i.layout == 0 && i.out % 16) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 16 == 0");

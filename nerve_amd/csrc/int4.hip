@@ -467,6 +467,101 @@ __global__ __launch_bounds__(64 * KS) void int4_ct_kernel(Int4Args A) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Pair-packed INT8 activations (quantize_int8_symmetric_pairpacked.comp.
+// template:22-72): per 32 columns s = amax > 0 ? amax / 127 : 1,
+// q = round-half-even(clamp(x / s, -127, 127)) and the block sum of q.  A
+// thread owns 8 columns c..c+7 and writes the words (q[c], q[c+2], q[c+4],
+// q[c+6]) and (q[c+1], q[c+3], q[c+5], q[c+7]); the 4 threads of a block are
+// consecutive lanes.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_i8pp_kernel(const uint16_t* __restrict__ x, uint32_t rows, uint32_t cols,
+                                                         uint32_t* __restrict__ q, float* __restrict__ s,
+                                                         int32_t* __restrict__ sums) {
+    const uint32_t oct = blockIdx.x * 256 + threadIdx.x, per_row = cols / 8;
+    const bool ok = oct < rows * per_row;
+    const uint32_t o = ok ? oct : 0u;
+    const v4i v = *reinterpret_cast<const v4i*>(x + (uint64_t)o * 8);
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[2 * e] = bf16_to_f32((uint32_t)v[e]);
+        f[2 * e + 1] = bf16_to_f32((uint32_t)v[e] >> 16);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(f[e]));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+    int iv[8], sum = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        iv[e] = (int)__builtin_rintf(fminf(fmaxf(f[e] / sc, -127.0f), 127.0f));
+        sum += iv[e];
+    }
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    if (!ok) return;
+    const uint32_t even = (uint32_t)(iv[0] & 255) | ((uint32_t)(iv[2] & 255) << 8) | ((uint32_t)(iv[4] & 255) << 16) |
+                          ((uint32_t)(iv[6] & 255) << 24);
+    const uint32_t odd = (uint32_t)(iv[1] & 255) | ((uint32_t)(iv[3] & 255) << 8) | ((uint32_t)(iv[5] & 255) << 16) |
+                         ((uint32_t)(iv[7] & 255) << 24);
+    *reinterpret_cast<uint2*>(q + (uint64_t)o * 2) = uint2{even, odd};
+    if ((o & 3u) == 0) {
+        s[o / 4] = sc;
+        sums[o / 4] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pair-packed INT8 x GPTQ INT4 linear (linear_prequant_pairpacked_int4_gptq.
+// comp.template:56-95).  Lane = output column (64 per block), the 4 waves
+// split the weight groups; per 32-column block the integer dot is exact
+// (v_dot4_i32_i8 on the bytes (q - 0) of the packed word's low and high
+// nibbles against the even and odd activation words, minus 8 times the block
+// sum), then acc = fma(dot, s_x * s_w, acc).  Only the f32 accumulation order
+// differs from the shader (per-wave partials added in wave order).
+// ---------------------------------------------------------------------------
+struct PpArgs {
+    const uint32_t* q;          // int8 words [B, K/4], pair-packed
+    const float* s;             // [B, K/32]
+    const int32_t* sums;        // [B, K/32]
+    Int4Args L;                 // qweight, scales, aux, y, shapes
+};
+
+__global__ __launch_bounds__(256) void int4_pp_kernel(PpArgs P) {
+    __shared__ float red[4][64];
+    const Int4Args& A = P.L;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint32_t K = A.K, N = A.N, G = A.G, ngroups = K / G, bpg = G / 32, nblk = K / 32;
+    const uint32_t n = blockIdx.x * 64 + lane;
+    const uint32_t nc = n < N ? n : N - 1;
+    const uint32_t per = (ngroups + 3) / 4, g0 = min(ngroups, wave * per), g1 = min(ngroups, g0 + per);
+    for (uint32_t t = 0; t < A.B; t++) {
+        const uint32_t* qt = P.q + (uint64_t)t * (K / 4);
+        float acc = 0.0f;
+        for (uint32_t g = g0; g < g1; g++) {
+            const float sw = decode_scale(A.scales[(uint64_t)g * N + nc], A.scale_bf16);
+            for (uint32_t b = g * bpg; b < (g + 1) * bpg; b++) {
+                int dot = -8 * P.sums[(uint64_t)t * nblk + b];
+#pragma unroll
+                for (uint32_t p = 0; p < 4; p++) {
+                    const uint32_t word = A.qw[(uint64_t)(b * 4 + p) * N + nc];
+                    dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2], (int)(word & 0x0f0f0f0fu), dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2 + 1], (int)((word >> 4) & 0x0f0f0f0fu), dot,
+                                                 false);
+                }
+                acc = fmaf((float)dot, P.s[(uint64_t)t * nblk + b] * sw, acc);
+            }
+        }
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0 && n < N) finalize_store(A, t, n, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
+        __syncthreads();
+    }
+}
+
 }  // namespace
 
 extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
@@ -477,6 +572,10 @@ extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char
     if (st) return st;
     nh::Int4Spec s;
     if ((st = nh::parse_int4_spec(spec, &s))) return st;
+    if (s.input != 0)
+        return nh::fail(s.input == 2 ? NERVE_HIP_INVALID_SPEC : NERVE_HIP_UNSUPPORTED,
+                        s.input == 2 ? "pair-packed INT8 input goes through nerve_hip_int4_linear_pairpacked"
+                                     : "the unpaired INT8-prequant INT4 input is not built");
     if (!x_bf16 || !qweight || !scales || !y_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (s.op != 0 && !aux_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "bias/residual specialization needs aux");
     if (s.batch_tile == 0 && batch_width > 1)
@@ -540,4 +639,62 @@ extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char
     dim3 grid(A.N / 16, (batch_width + 15) / 16);
     int4_ct_kernel<8><<<grid, 512, 0, strm>>>(A);
     return nh::check_launch("int4_linear_ct");
+}
+
+extern "C" nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
+                                                              void* q_i8, void* scales_f32, void* sums_i32,
+                                                              uint32_t rows, void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::QuantI8Spec qs;
+    if ((st = nh::parse_quant_i8_spec(spec, &qs))) return st;
+    if (!x_bf16 || !q_i8 || !scales_f32 || !sums_i32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (qs.batch_tile == 0 && rows > 1)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "unbatched pair-packed quantizer takes one row");
+    if (((uintptr_t)x_bf16 & 15) || ((uintptr_t)q_i8 & 7))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "x must be 16-byte and q 8-byte aligned");
+    if (rows == 0) return nh::ok();
+    const uint64_t octs = (uint64_t)rows * qs.elements / 8;
+    quant_i8pp_kernel<<<(uint32_t)((octs + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(x_bf16), rows, qs.elements, static_cast<uint32_t*>(q_i8),
+        static_cast<float*>(scales_f32), static_cast<int32_t*>(sums_i32));
+    return nh::check_launch("quantize_int8_pairpacked");
+}
+
+extern "C" nerve_hip_status nerve_hip_int4_linear_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* q_i8,
+                                                            const void* scales_f32, const void* sums_i32,
+                                                            const void* qweight, const void* scales,
+                                                            const void* aux_bf16, void* y_bf16, uint32_t batch_width,
+                                                            void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::Int4Spec s;
+    if ((st = nh::parse_int4_spec(spec, &s))) return st;
+    if (s.input != 2) return nh::fail(NERVE_HIP_INVALID_SPEC, "not a _prequant_pairpacked INT4 specialization");
+    if (!q_i8 || !scales_f32 || !sums_i32 || !qweight || !scales || !y_bf16)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (s.op != 0 && !aux_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "bias/residual specialization needs aux");
+    if (s.batch_tile == 0 && batch_width > 1)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "unbatched INT4 specialization takes batch_width 1");
+    if (((uintptr_t)q_i8 & 3) || ((uintptr_t)qweight & 3))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "q and qweight must be 4-byte aligned");
+    if (batch_width == 0) return nh::ok();
+    PpArgs P;
+    P.q = static_cast<const uint32_t*>(q_i8);
+    P.s = static_cast<const float*>(scales_f32);
+    P.sums = static_cast<const int32_t*>(sums_i32);
+    P.L.x = nullptr;
+    P.L.qw = static_cast<const uint32_t*>(qweight);
+    P.L.scales = static_cast<const uint16_t*>(scales);
+    P.L.qzeros = nullptr;
+    P.L.aux = static_cast<const uint16_t*>(aux_bf16);
+    P.L.y = static_cast<uint16_t*>(y_bf16);
+    P.L.B = batch_width;
+    P.L.K = s.in;
+    P.L.N = s.out;
+    P.L.G = s.group;
+    P.L.scale_bf16 = s.scale_bf16;
+    P.L.finalize = s.op;
+    int4_pp_kernel<<<(s.out + 63) / 64, 256, 0, (hipStream_t)stream>>>(P);
+    return nh::check_launch("int4_linear_pairpacked");
 }

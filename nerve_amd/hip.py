@@ -32,6 +32,8 @@ EXPORTS = (
     "nerve_hip_mxfp4_moe_down_counted",
     "nerve_hip_moe_reduce",
     "nerve_hip_int4_linear",
+    "nerve_hip_quantize_int8_pairpacked",
+    "nerve_hip_int4_linear_pairpacked",
     "nerve_hip_fp8_output_projection",
     "nerve_hip_argmax_f32",
 )
@@ -87,6 +89,8 @@ def _declare(lib) -> None:
         "nerve_hip_mxfp4_moe_down_counted": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_moe_reduce": (ctypes.c_int, [P, P, P, U32, U32, U32, ctypes.c_float, P]),
         "nerve_hip_int4_linear": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
+        "nerve_hip_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
+        "nerve_hip_int4_linear_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, P, U32, P]),
         "nerve_hip_fp8_output_projection": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_argmax_f32": (ctypes.c_int, [P, P, U32, U32, P, P]),
     }
@@ -234,6 +238,16 @@ class Context:
             self.handle, _spec(spec), ptr(intermediates), ptr(routes), ptr(expert_outputs), ptr(addresses),
             addresses.numel() // 8, ptr(param_slots), param_slots.numel(), ptr(control), batch_width,
             _stream(stream)))
+
+    # ---- pair-packed INT8 x INT4
+    def quantize_int8_pairpacked(self, spec, x, q, scales, sums, rows, stream=None):
+        _check(self.lib.nerve_hip_quantize_int8_pairpacked(self.handle, _spec(spec), ptr(x), ptr(q), ptr(scales),
+                                                           ptr(sums), rows, _stream(stream)))
+
+    def int4_linear_pairpacked(self, spec, q, scales_f32, sums, qweight, scales, aux, y, batch_width, stream=None):
+        _check(self.lib.nerve_hip_int4_linear_pairpacked(self.handle, _spec(spec), ptr(q), ptr(scales_f32), ptr(sums),
+                                                         ptr(qweight), ptr(scales), ptr(aux), ptr(y), batch_width,
+                                                         _stream(stream)))
 
     # ---- a8
     def moe_reduce(self, expert_outputs, out, batch_width, hidden, experts_per_token, routed_scale=1.0, stream=None):

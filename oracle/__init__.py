@@ -64,6 +64,8 @@ def _declare(l) -> None:
         "o_moe_down": (None, [P, P, P, I, I, I, I, I, I, P, P, P]),
         "o_moe_reduce": (None, [P, I, I, I, F, P]),
         "o_int4_linear": (None, [I, P, P, P, I, P, I, I, I, I, I, P, P]),
+        "o_quantize_i8_pairpacked": (None, [P, I, I, P, P, P]),
+        "o_int4_linear_pairpacked": (None, [P, P, P, P, P, I, I, I, I, I, I, P, P]),
         "o_fp8_output_projection": (None, [P, I, I, P, P, I, I, F, P]),
         "o_argmax": (None, [P, I, I, P]),
     }
@@ -268,6 +270,31 @@ def int4_linear(layout, x_bf16, qweight, scales, group, *, scale_bf16=False, zer
     lib().o_int4_linear(lay, _p(x), _p(qw), _p(_c(scales, np.uint16)), int(scale_bf16),
                         _p(None if zeros is None else _c(zeros, np.uint32)), group, K, N, B,
                         finalize, _p(None if aux is None else _c(aux, np.uint16)), _p(y))
+    return y
+
+
+def quantize_i8_pairpacked(x_bf16):
+    """Pair-packed symmetric INT8 activations per 32 columns.
+    Returns (q u8 [R, C] in pair-packed byte order, s f32 [R, C/32], sums i32 [R, C/32])."""
+    x = _c(x_bf16, np.uint16)
+    rows, cols = x.shape
+    q = np.zeros((rows, cols), np.uint8)
+    s = np.zeros((rows, cols // 32), np.float32)
+    sums = np.zeros((rows, cols // 32), np.int32)
+    lib().o_quantize_i8_pairpacked(_p(x), rows, cols, _p(q), _p(s), _p(sums))
+    return q, s, sums
+
+
+def int4_linear_pairpacked(q, s, sums, qweight, scales, group, *, scale_bf16=False, finalize=0, aux=None):
+    """Pair-packed INT8 x GPTQ INT4 (qweight [K/8, N], scales [K/G, N])."""
+    q = _c(q, np.uint8)
+    B, K = q.shape
+    qw = _c(qweight, np.uint32)
+    N = qw.shape[1]
+    y = np.zeros((B, N), np.uint16)
+    lib().o_int4_linear_pairpacked(_p(q), _p(_c(s, np.float32)), _p(_c(sums, np.int32)), _p(qw),
+                                   _p(_c(scales, np.uint16)), int(scale_bf16), group, K, N, B, finalize,
+                                   _p(None if aux is None else _c(aux, np.uint16)), _p(y))
     return y
 
 

@@ -612,6 +612,73 @@ void o_int4_linear(int layout, const uint16_t* x, const uint32_t* qw, const uint
     }
 }
 
+/* Pair-packed symmetric INT8 activations (quantize_int8_symmetric_pairpacked.
+ * comp.template:22-72): per 32-column block s = amax > 0 ? amax / 127 : 1,
+ * q = round(clamp(x / s, -127, 127)) (GLSL round, taken here as round half
+ * to even), sum = sum of the block's q.  Each 8 columns c..c+7 become two
+ * words: bytes (q[c], q[c+2], q[c+4], q[c+6]) then (q[c+1], q[c+3], q[c+5],
+ * q[c+7]), low byte first. */
+void o_quantize_i8_pairpacked(const uint16_t* x, int rows, int cols, uint8_t* q, float* s, int32_t* sums) {
+    int nblk = cols / 32;
+    for (int r = 0; r < rows; r++) {
+        const uint16_t* xr = x + (long)r * cols;
+        for (int b = 0; b < nblk; b++) {
+            float amax = 0.0f;
+            for (int c = b * 32; c < b * 32 + 32; c++) amax = fmaxf(amax, fabsf(o_bf16_to_f32(xr[c])));
+            float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+            int sum = 0;
+            for (int e = 0; e < 32; e++) {
+                int c = b * 32 + e;
+                float v = o_bf16_to_f32(xr[c]) / sc;
+                v = v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v);
+                int iv = (int)rintf(v);
+                sum += iv;
+                int oct = e / 8, j = e % 8;
+                int pos = b * 32 + oct * 8 + (j % 2) * 4 + j / 2;
+                q[(long)r * cols + pos] = (uint8_t)(iv & 255);
+            }
+            s[(long)r * nblk + b] = sc;
+            sums[(long)r * nblk + b] = sum;
+        }
+    }
+}
+
+/* Pair-packed INT8 x GPTQ INT4 linear (linear_prequant_pairpacked_int4_gptq.
+ * comp.template:56-95): per output row, for each weight group and each
+ * 32-column block of it, block_dot = -8 * sum + sum of the exact int8 x u4
+ * products, then sum = fma(block_dot, s_x * s_w, sum) in group, block order. */
+void o_int4_linear_pairpacked(const uint8_t* q, const float* s, const int32_t* sums, const uint32_t* qw,
+                              const uint16_t* scales, int scale_bf16, int group, int K, int N, int B, int finalize,
+                              const uint16_t* aux, uint16_t* y) {
+    int nblk = K / 32;
+    #pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; n++) {
+        for (int b = 0; b < B; b++) {
+            const int8_t* qb = (const int8_t*)(q + (size_t)b * K);
+            float sum = 0.0f;
+            for (int g = 0; g < K / group; g++) {
+                uint16_t sr = scales[(size_t)g * N + n];
+                float sw = scale_bf16 ? o_bf16_to_f32(sr) : f16_to_f32(sr);
+                for (int blk = g * (group / 32); blk < (g + 1) * (group / 32); blk++) {
+                    int dot = -8 * sums[(size_t)b * nblk + blk];
+                    for (int p = blk * 4; p < blk * 4 + 4; p++) {
+                        uint32_t word = qw[(size_t)p * N + n];
+                        for (int j = 0; j < 8; j++) {
+                            int pos = p * 8 + (j % 2) * 4 + j / 2;   /* pair-packed position of column 8p + j */
+                            dot += (int)qb[pos] * (int)((word >> (4 * j)) & 15u);
+                        }
+                    }
+                    sum = fmaf((float)dot, s[(size_t)b * nblk + blk] * sw, sum);
+                }
+            }
+            float v = sum;
+            if (finalize == 1) v = o_bf16_to_f32(aux[n]) + sum;
+            else if (finalize == 2) v = o_bf16_to_f32(aux[(size_t)b * N + n]) + round_bf16(sum);
+            y[(size_t)b * N + n] = o_f32_to_bf16(v);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* a10 / a11: FP8 output projection + argmax                             */
 /* ------------------------------------------------------------------ */

@@ -1,0 +1,65 @@
+"""GPU parity: pair-packed INT8 activations and the INT8 x GPTQ INT4 linear
+(quantize_int8_symmetric_pairpacked.comp.template:22-72,
+linear_prequant_pairpacked_int4_gptq.comp.template:56-128) through the C ABI,
+against the CPU oracle: the quantizer bit-exact, the linear within bf16
+tolerance (only the f32 accumulation order differs)."""
+import numpy as np
+import pytest
+
+import oracle
+from nerve_amd import workloads as wl
+
+from helpers import bf16_close, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _quant(ctx, dev, x):
+    import torch
+
+    B, K = x.shape
+    q = torch.zeros(B, K, dtype=torch.uint8, device=dev)
+    s = torch.zeros(B, K // 32, dtype=torch.float32, device=dev)
+    sums = torch.zeros(B, K // 32, dtype=torch.int32, device=dev)
+    spec = f"quantize{'_batch%d' % B if B > 1 else ''}_int8_symmetric_pairpacked_b32_h{K}.comp"
+    ctx.quantize_int8_pairpacked(spec, to_dev(x, dev), q, s, sums, B)
+    return q, s, sums
+
+
+@pytest.mark.parametrize("B,K", [(1, 4096), (5, 2880), (16, 96)])
+def test_quantize_int8_pairpacked_bit_exact(ctx, dev, B, K):
+    rng = np.random.default_rng(B + K)
+    x = wl.bf16_normal(rng, (B, K))
+    x[0, 32:64] = 0
+    q, s, sums = _quant(ctx, dev, x)
+    qr, sr, sumr = oracle.quantize_i8_pairpacked(x)
+    assert np.array_equal(to_np(q, np.uint8), qr)
+    assert np.array_equal(to_np(s, np.float32), sr)
+    assert np.array_equal(to_np(sums, np.int32), sumr)
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 4096, 14336, 128), (4, 1024, 512, 32), (16, 512, 96, 256)])
+@pytest.mark.parametrize("finalize", [0, 2])
+@pytest.mark.parametrize("bf16_scales", [False, True])
+def test_int4_linear_pairpacked(ctx, dev, M, K, N, G, finalize, bf16_scales):
+    import torch
+
+    rng = np.random.default_rng(M + K + N + finalize + bf16_scales)
+    d = wl.int4_gptq(rng, K, N, G, True)
+    sc = d["scales"].view(np.uint16)
+    if bf16_scales:
+        sc = wl.f32_to_bf16_bits(d["scales"].astype(np.float32))
+    x = wl.bf16_normal(rng, (M, K))
+    aux = wl.bf16_normal(rng, (M, N)) if finalize == 2 else None
+    q, s, sums = _quant(ctx, dev, x)
+    y = torch.zeros(M, N, dtype=torch.int16, device=dev)
+    op = ["linear", "linear_bias", "linear_residual"][finalize]
+    spec = (f"{op}_prequant_pairpacked{'_batch%d' % M if M > 1 else ''}_int4_gptq_s{'bf16' if bf16_scales else 'f16'}"
+            f"_g{G}_{K}x{N}.comp")
+    ctx.int4_linear_pairpacked(spec, q, s, sums, to_dev(d["qweight"], dev), to_dev(sc, dev),
+                               None if aux is None else to_dev(aux, dev), y, M)
+    qr, sr, sumr = oracle.quantize_i8_pairpacked(x)
+    ref = oracle.int4_linear_pairpacked(qr, sr, sumr, d["qweight"], sc, G, scale_bf16=bf16_scales,
+                                        finalize=finalize, aux=aux)
+    ok, worst, exact = bf16_close(to_np(y, np.uint16), ref)
+    assert ok and exact > 0.9, (worst, exact)

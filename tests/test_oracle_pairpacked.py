@@ -1,0 +1,52 @@
+"""CPU checks of the pair-packed INT8 x INT4 oracle
+(quantize_int8_symmetric_pairpacked.comp.template:22-72,
+linear_prequant_pairpacked_int4_gptq.comp.template:56-95) against what the
+mathematics fixes: the quantized codes dequantize to x within half a step,
+the block sums are the sums of the codes, the byte order pairs column 8p + j
+with nibble j, and the INT4 product equals the bf16 INT4 oracle (itself
+pinned) applied to the dequantized activations, up to f32 rounding."""
+import numpy as np
+
+import oracle
+from nerve_amd import workloads as wl
+
+
+def _unpack(q):
+    """Pair-packed bytes -> int8 codes in column order."""
+    R, C = q.shape
+    v = q.view(np.int8).reshape(R, C // 8, 2, 4)           # [.., even/odd word, byte]
+    out = np.empty((R, C // 8, 8), np.int8)
+    out[:, :, 0::2] = v[:, :, 0, :]
+    out[:, :, 1::2] = v[:, :, 1, :]
+    return out.reshape(R, C)
+
+
+def test_quantizer_codes_sums_and_order():
+    rng = np.random.default_rng(1)
+    x = wl.bf16_normal(rng, (3, 256))
+    x[0, :32] = 0                                    # an all-zero block: scale 1, codes 0
+    q, s, sums = oracle.quantize_i8_pairpacked(x)
+    codes = _unpack(q).astype(np.int64)
+    xf = wl.bf16_bits_to_f32(x).astype(np.float64)
+    step = np.repeat(s.astype(np.float64), 32, axis=1)
+    assert np.all(np.abs(codes * step - xf) <= step / 2 + 1e-12)
+    assert np.array_equal(sums, codes.reshape(3, 8, 32).sum(axis=2))
+    assert s[0, 0] == 1.0 and np.all(codes[0, :32] == 0)
+    assert np.max(np.abs(codes)) == 127                # the block max maps to +-127
+
+
+def test_linear_matches_bf16_oracle_on_dequantized_input():
+    rng = np.random.default_rng(2)
+    K, N, G, B = 512, 64, 128, 3
+    d = wl.int4_gptq(rng, K, N, G, True)
+    x = wl.bf16_normal(rng, (B, K))
+    q, s, sums = oracle.quantize_i8_pairpacked(x)
+    y = oracle.int4_linear_pairpacked(q, s, sums, d["qweight"], d["scales"].view(np.uint16), G)
+    # dequantized activations are exact bf16 values here only approximately, so
+    # compare in f64 against the closed form sum_k x_q s (q - 8) s_w
+    codes = _unpack(q).astype(np.float64) * np.repeat(s.astype(np.float64), 32, axis=1)
+    wq = d["q"].astype(np.float64) - 8.0                                   # [K, N]
+    sw = np.repeat(d["scales"].astype(np.float64), G, axis=0)
+    ref = codes @ (wq * sw)
+    got = wl.bf16_bits_to_f32(y).astype(np.float64)
+    assert np.max(np.abs(got - ref) / (np.abs(ref) + np.sqrt(np.mean(ref ** 2)))) < 1e-2

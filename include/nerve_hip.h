@@ -231,9 +231,9 @@ nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spe
  * [B, k, H] = bf16(y * route_weight); param_slots u32 [2 * E]
  * (down_w, down_s).  With an input_block_major_b128 spec the down
  * parameters are W [I/128, H, 64] and S [I/128, H, 4] bytes
- * (…down_batch1_mxfp4.comp.template:229-233, :260-263); that layout is
- * streamed for decode-sized batches (B k < 512, 256 <= I <= 4096) and
- * returns NERVE_HIP_UNSUPPORTED otherwise. */
+ * (…down_batch1_mxfp4.comp.template:229-233, :260-263); decode-sized
+ * batches stream that layout, larger ones read it through the preparation
+ * launch and a register-fed kernel (E <= 1024). */
 nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec,
                                           const void* intermediates, const void* routes_u32,
                                           void* expert_outputs,

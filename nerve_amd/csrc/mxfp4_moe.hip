@@ -1010,6 +1010,7 @@ struct SpanArgs {
     uint64_t frame_elems;
     float limit;
     uint32_t w_region, s_region;   // LDS bytes per matrix (padded)
+    uint32_t block_major;          // mx_wfmt_kernel: compact weights in the input-block-major layout
 };
 
 __host__ __device__ inline uint32_t span_w_region(uint32_t rows, uint32_t K) { return (rows * (K / 2) + 1023) / 1024 * 1024; }
@@ -1200,9 +1201,18 @@ __global__ __launch_bounds__(256) void mx_wfmt_kernel(SpanArgs A) {
             load_a(arow, ascale, K, c, g, a, sa);
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
-                v4i w;
-                uint32_t sw;
-                load_w(rec.w[m] + (uint64_t)n * (K / 2), rec.s[m] + (uint64_t)n * SB, K, c, g, w, sw);
+                v4i w = v4i{0, 0, 0, 0};
+                uint32_t sw = 127;
+                if (A.block_major) {
+                    // W [K/128, N, 64], S [K/128, N, 4]: chunk c of row n is
+                    // 64 contiguous bytes, its 4 scales one dword.
+                    if (kv) {
+                        w = *reinterpret_cast<const v4i*>(rec.w[m] + ((uint64_t)c * N + n) * 64 + g * 16);
+                        sw = rec.s[m][((uint64_t)c * N + n) * 4 + g];
+                    }
+                } else {
+                    load_w(rec.w[m] + (uint64_t)n * (K / 2), rec.s[m] + (uint64_t)n * SB, K, c, g, w, sw);
+                }
                 acc[m] = mfma_fp8_fp4(a, w, sa, sw, acc[m]);
             }
         } else {
@@ -3118,9 +3128,12 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     // 64-route tiles.
     // Banks with e4m3 weights (pre-expanded or native FP8 experts) take the
     // preparation launch and mx_wfmt_kernel at every batch size.
-    const bool wf = ms.weight_repr != 0 || ms.native_fp8_start >= 0;
-    if (wf && (E > 1024 || ms.input_block_major))
-        return nh::fail(NERVE_HIP_UNSUPPORTED, "e4m3 expert banks are supported for E <= 1024, row-major layout");
+    // The block-major down layout is streamed by the decode kernel and
+    // otherwise takes the same register-fed kernel.
+    const bool banks = ms.weight_repr != 0 || ms.native_fp8_start >= 0;
+    const bool wf = banks || ms.input_block_major;
+    if (wf && E > 1024)
+        return nh::fail(NERVE_HIP_UNSUPPORTED, "e4m3 expert banks and block-major weights are supported for E <= 1024");
     const bool grouped = !wf && (cap >= 512 || K > 4096);
     // Persistent grouped GEMM: enough chunks per item for the descriptor
     // prefetch rounds.
@@ -3199,7 +3212,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.a_row_div = gate_up ? k : 1;
     // Decode-shaped batches: one streaming launch that builds its own tiles
     // and quantizes its own activation chunks (no preparation launch).
-    if (!wf && !grouped && !(gate_up && ms.prequant)) {
+    if (!banks && !grouped && !(gate_up && ms.prequant)) {
         StreamArgs fa{};
         fa.K = K;
         fa.N = N;
@@ -3229,10 +3242,6 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         }
         if (st != NERVE_HIP_UNSUPPORTED) return st;
     }
-    if (ms.input_block_major)
-        return nh::fail(NERVE_HIP_UNSUPPORTED,
-                        "input_block_major_b128 down weights are supported on the decode streaming path only (B k < "
-                        "512, 256 <= I <= 4096, intermediate frames of whole 16-byte pieces)");
     if (count_control) {
         // Count stage as its own launch (its one changed word, computed the
         // same way) for the other down paths.
@@ -3279,6 +3288,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         wa.n_tiles = ea.n_tiles;
         wa.frame_elems = ea.frame_elems;
         wa.limit = ea.limit;
+        wa.block_major = ms.input_block_major ? 1u : 0u;
         const dim3 wgrid((N + 15) / 16, max_tiles);
         if (gate_up) {
             wa.out16 = static_cast<uint16_t*>(intermediates);

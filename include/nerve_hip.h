@@ -104,6 +104,17 @@ nerve_hip_status nerve_hip_rms_norm_quantize_fp8_e4m3(nerve_hip_ctx* ctx, const 
                                                      void* y_bf16, void* q_e4m3, void* scales_f32,
                                                      uint32_t rows, void* stream);
 
+/* Replaces rms_norm_quantize[_batch{T}]_int8_pairpacked_b32_h{H}_eps{E}
+ * _offset{O}.comp (rms_norm_quantize_int8_pairpacked.comp.template:60-151;
+ * grammar nerve/model_package_shader_templates.py:3357-3375): the same y as
+ * above, then the pair-packed INT8 quantization of
+ * nerve_hip_quantize_int8_pairpacked applied to y (q int8 [rows, H], scales
+ * f32 and sums i32 [rows, H/32]), feeding nerve_hip_int4_linear_pairpacked. */
+nerve_hip_status nerve_hip_rms_norm_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec,
+                                                            const void* x_bf16, const void* weight_bf16,
+                                                            void* y_bf16, void* q_i8, void* scales_f32,
+                                                            void* sums_i32, uint32_t rows, void* stream);
+
 /* ---- a2: activation block quantization -------------------------------- */
 
 /* Replaces quantize_fp8_e4m3[_spow2]_b128_h{N}.comp

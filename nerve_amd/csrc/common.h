@@ -171,6 +171,7 @@ nerve_hip_status parse_quant_spec(const char* spec, QuantSpec* out);
 
 struct RmsQuantSpec {
     int batch_tile = 0;
+    bool int8pp = false;        // int8_pairpacked output instead of fp8_e4m3
     bool pow2 = false;
     uint32_t block = 0, hidden = 0;
     float eps = 0.0f, offset = 0.0f;

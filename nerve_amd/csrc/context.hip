@@ -238,7 +238,8 @@ static nerve_hip_status parse_quant_spec_uncached(const char* spec, QuantSpec* o
 static nerve_hip_status parse_rms_quant_spec_uncached(const char* spec, RmsQuantSpec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re(
-        "rms_norm_quantize(?:_batch(\\d+))?_fp8_e4m3(?:_(spow2))?_b(\\d+)_h(\\d+)_eps([0-9eE+.-]+)_offset([0-9eE+.-]+)\\.comp");
+        "rms_norm_quantize(?:_batch(\\d+))?_(?:fp8_e4m3(?:_(spow2))?|(int8_pairpacked))_b(\\d+)_h(\\d+)_eps([0-9eE+.-]+)"
+        "_offset([0-9eE+.-]+)\\.comp");
     std::cmatch m;
     if (!std::regex_match(spec, m, re))
         return fail(NERVE_HIP_INVALID_SPEC, std::string("not an RMSNorm FP8 quantizer: ") + spec);
@@ -247,10 +248,14 @@ static nerve_hip_status parse_rms_quant_spec_uncached(const char* spec, RmsQuant
     if (m[1].matched) parse_u32(m[1].str(), &bt);
     s.batch_tile = (int)bt;
     s.pow2 = m[2].matched;
-    parse_u32(m[3].str(), &s.block);
-    parse_u32(m[4].str(), &s.hidden);
-    if (!parse_float(m[5].str(), &s.eps) || !parse_float(m[6].str(), &s.offset))
+    s.int8pp = m[3].matched;
+    parse_u32(m[4].str(), &s.block);
+    parse_u32(m[5].str(), &s.hidden);
+    if (!parse_float(m[6].str(), &s.eps) || !parse_float(m[7].str(), &s.offset))
         return fail(NERVE_HIP_INVALID_SPEC, std::string("bad eps/offset in ") + spec);
+    // The pair-packed INT8 output feeds the INT4 linear's 32-column blocks.
+    if (s.int8pp && s.block != 32)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("pair-packed INT8 RMSNorm quantizer needs b32: ") + spec);
     // Whole blocks of 32..512 columns (BLOCK_COUNT = HIDDEN / BLOCK_COLUMNS).
     if ((m[1].matched && bt == 0) || s.hidden == 0 || s.hidden % 32 || s.block < 32 || s.block > 512 ||
         (s.block & (s.block - 1)) || s.hidden % s.block)

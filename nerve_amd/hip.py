@@ -22,6 +22,7 @@ EXPORTS = (
     "nerve_hip_check_specialization",
     "nerve_hip_quantize_fp8_e4m3",
     "nerve_hip_rms_norm_quantize_fp8_e4m3",
+    "nerve_hip_rms_norm_quantize_int8_pairpacked",
     "nerve_hip_mxfp4_gemv",
     "nerve_hip_router_linear_bf16",
     "nerve_hip_moe_router_topk",
@@ -79,6 +80,7 @@ def _declare(lib) -> None:
         "nerve_hip_check_specialization": (ctypes.c_int, [S]),
         "nerve_hip_quantize_fp8_e4m3": (ctypes.c_int, [P, S, P, U32, P, P, P]),
         "nerve_hip_rms_norm_quantize_fp8_e4m3": (ctypes.c_int, [P, S, P, P, P, P, P, U32, P]),
+        "nerve_hip_rms_norm_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_mxfp4_gemv": (ctypes.c_int, [P, P, P, U32, U32, P, P, U32, P, P]),
         "nerve_hip_router_linear_bf16": (ctypes.c_int, [P, P, P, P, U32, U32, U32, P]),
         "nerve_hip_moe_router_topk": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
@@ -180,6 +182,11 @@ class Context:
     def rms_norm_quantize_fp8_e4m3(self, spec, x, weight, y, q, scales, rows, stream=None):
         _check(self.lib.nerve_hip_rms_norm_quantize_fp8_e4m3(self.handle, _spec(spec), ptr(x), ptr(weight), ptr(y),
                                                              ptr(q), ptr(scales), rows, _stream(stream)))
+
+    def rms_norm_quantize_int8_pairpacked(self, spec, x, weight, y, q, scales, sums, rows, stream=None):
+        _check(self.lib.nerve_hip_rms_norm_quantize_int8_pairpacked(self.handle, _spec(spec), ptr(x), ptr(weight),
+                                                                    ptr(y), ptr(q), ptr(scales), ptr(sums), rows,
+                                                                    _stream(stream)))
 
     # ---- raw MXFP4 GEMV
     def mxfp4_gemv(self, q, scales, M, K, weight, weight_scale, N, y, stream=None):

@@ -91,6 +91,8 @@ def test_null_context_is_rejected():
     ("rms_norm_quantize_fp8_e4m3_spow2_b128_h2880_eps1e-05_offset1.comp", 2),
     ("rms_norm_quantize_batch16_fp8_e4m3_b32_h4096_eps1e-06_offset0.comp", 0),
     ("rms_norm_quantize_fp8_e4m3_b100_h2800_eps1e-05_offset1.comp", 2),
+    ("rms_norm_quantize_batch8_int8_pairpacked_b32_h4096_eps1e-06_offset0.comp", 0),
+    ("rms_norm_quantize_int8_pairpacked_b64_h4096_eps1e-06_offset0.comp", 2),
     ("quantize_batch4_fp8_e4m3_b128_h4096.comp", 0),
     ("quantize_fp8_e4m3_b64_h4096.comp", 2),
     ("rms_norm_bf16_h4096.comp", 2),

@@ -311,6 +311,15 @@ nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const ch
                                                    void* q_i8, void* scales_f32, void* sums_i32, uint32_t rows,
                                                    void* stream);
 
+/* Replaces silu_multiply_quantize[_batch{T}]_int8_pairpacked_b32_h{N}.comp
+ * (silu_multiply_quantize_int8_pairpacked.comp.template): y = bf16(bf16(
+ * g / (1 + exp(-g))) * u) for gate and up bf16 [rows, N], written to y, and
+ * the pair-packed INT8 quantization of y as above. */
+nerve_hip_status nerve_hip_silu_multiply_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec,
+                                                                 const void* gate_bf16, const void* up_bf16,
+                                                                 void* y_bf16, void* q_i8, void* scales_f32,
+                                                                 void* sums_i32, uint32_t rows, void* stream);
+
 /* Replaces {linear,linear_bias,linear_residual}_prequant_pairpacked[_batch{T}]
  * _int4_gptq_s{f16,bf16}_g{G}_{K}x{N}.comp
  * (linear_prequant_pairpacked_int4_gptq.comp.template:56-128): y = bf16 of

@@ -151,6 +151,7 @@ nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out);
 
 struct QuantI8Spec {
     int batch_tile = 0;
+    bool silu = false;          // silu_multiply_quantize_* (two bf16 inputs, bf16 output)
     uint32_t block = 0, elements = 0;
 };
 nerve_hip_status parse_quant_i8_spec(const char* spec, QuantI8Spec* out);

@@ -267,17 +267,23 @@ static nerve_hip_status parse_rms_quant_spec_uncached(const char* spec, RmsQuant
 // nerve/model_package_shader_templates.py:1440-1474 (Q8_0 groups of 32)
 static nerve_hip_status parse_quant_i8_spec_uncached(const char* spec, QuantI8Spec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
-    static const std::regex re("quantize(?:_batch(\\d+))?_int8_symmetric_pairpacked_b(\\d+)_h(\\d+)\\.comp");
+    // and silu_multiply_quantize[_batch{T}]_int8_pairpacked_b{B}_h{N}
+    // (nerve/model_package_shader_templates.py:3376-3380).
+    static const std::regex re(
+        "(?:quantize(?:_batch(\\d+))?_int8_symmetric|(silu_multiply)_quantize(?:_batch(\\d+))?_int8)_pairpacked_b(\\d+)"
+        "_h(\\d+)\\.comp");
     std::cmatch m;
     if (!std::regex_match(spec, m, re))
         return fail(NERVE_HIP_INVALID_SPEC, std::string("not a pair-packed INT8 quantizer: ") + spec);
     QuantI8Spec s;
     uint32_t bt = 0;
-    if (m[1].matched) parse_u32(m[1].str(), &bt);
+    s.silu = m[2].matched;
+    const int bi = s.silu ? 3 : 1;
+    if (m[bi].matched) parse_u32(m[bi].str(), &bt);
     s.batch_tile = (int)bt;
-    parse_u32(m[2].str(), &s.block);
-    parse_u32(m[3].str(), &s.elements);
-    if ((m[1].matched && bt == 0) || s.block != 32 || s.elements == 0 || s.elements % 32)
+    parse_u32(m[4].str(), &s.block);
+    parse_u32(m[5].str(), &s.elements);
+    if ((m[bi].matched && bt == 0) || s.block != 32 || s.elements == 0 || s.elements % 32)
         return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid pair-packed INT8 quantizer shape ") + spec);
     *out = s;
     return NERVE_HIP_OK;
@@ -375,7 +381,8 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
         nh::RmsQuantSpec r;
         return nh::parse_rms_quant_spec(spec, &r);
     }
-    if (s.rfind("quantize", 0) == 0 && s.find("_int8_symmetric_pairpacked_") != std::string::npos) {
+    if ((s.rfind("quantize", 0) == 0 && s.find("_int8_symmetric_pairpacked_") != std::string::npos) ||
+        s.rfind("silu_multiply_quantize", 0) == 0) {
         nh::QuantI8Spec q;
         return nh::parse_quant_i8_spec(spec, &q);
     }

@@ -475,7 +475,12 @@ __global__ __launch_bounds__(64 * KS) void int4_ct_kernel(Int4Args A) {
 // q[c+6]) and (q[c+1], q[c+3], q[c+5], q[c+7]); the 4 threads of a block are
 // consecutive lanes.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void quant_i8pp_kernel(const uint16_t* __restrict__ x, uint32_t rows, uint32_t cols,
+// SILU: silu_multiply_quantize_int8_pairpacked.comp.template: the values are
+// y = bf16(bf16(g / (1 + exp(-g))) * u) of the gate (x) and up rows, and y is
+// written out as well.
+template <bool SILU>
+__global__ __launch_bounds__(256) void quant_i8pp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ up,
+                                                         uint16_t* __restrict__ y, uint32_t rows, uint32_t cols,
                                                          uint32_t* __restrict__ q, float* __restrict__ s,
                                                          int32_t* __restrict__ sums) {
     const uint32_t oct = blockIdx.x * 256 + threadIdx.x, per_row = cols / 8;
@@ -487,6 +492,19 @@ __global__ __launch_bounds__(256) void quant_i8pp_kernel(const uint16_t* __restr
     for (int e = 0; e < 4; e++) {
         f[2 * e] = bf16_to_f32((uint32_t)v[e]);
         f[2 * e + 1] = bf16_to_f32((uint32_t)v[e] >> 16);
+    }
+    if (SILU) {
+        const v4i uv = *reinterpret_cast<const v4i*>(up + (uint64_t)o * 8);
+        uint32_t yb[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float act = round_bf16(f[e] / (1.0f + expf(-f[e])));
+            yb[e] = f32_to_bf16(act * bf16_to_f32((uint32_t)uv[e / 2] >> (16 * (e & 1)))) & 0xffffu;
+            f[e] = bf16_to_f32(yb[e]);
+        }
+        if (ok)
+            *reinterpret_cast<v4i*>(y + (uint64_t)o * 8) = v4i{(int)(yb[0] | (yb[1] << 16)), (int)(yb[2] | (yb[3] << 16)),
+                                                               (int)(yb[4] | (yb[5] << 16)), (int)(yb[6] | (yb[7] << 16))};
     }
     float m = 0.0f;
 #pragma unroll
@@ -648,6 +666,7 @@ extern "C" nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ct
     if (st) return st;
     nh::QuantI8Spec qs;
     if ((st = nh::parse_quant_i8_spec(spec, &qs))) return st;
+    if (qs.silu) return nh::fail(NERVE_HIP_INVALID_SPEC, "silu_multiply_quantize goes through its own entry point");
     if (!x_bf16 || !q_i8 || !scales_f32 || !sums_i32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (qs.batch_tile == 0 && rows > 1)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "unbatched pair-packed quantizer takes one row");
@@ -655,10 +674,35 @@ extern "C" nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ct
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "x must be 16-byte and q 8-byte aligned");
     if (rows == 0) return nh::ok();
     const uint64_t octs = (uint64_t)rows * qs.elements / 8;
-    quant_i8pp_kernel<<<(uint32_t)((octs + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        static_cast<const uint16_t*>(x_bf16), rows, qs.elements, static_cast<uint32_t*>(q_i8),
+    quant_i8pp_kernel<false><<<(uint32_t)((octs + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(x_bf16), nullptr, nullptr, rows, qs.elements, static_cast<uint32_t*>(q_i8),
         static_cast<float*>(scales_f32), static_cast<int32_t*>(sums_i32));
     return nh::check_launch("quantize_int8_pairpacked");
+}
+
+extern "C" nerve_hip_status nerve_hip_silu_multiply_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec,
+                                                                            const void* gate_bf16, const void* up_bf16,
+                                                                            void* y_bf16, void* q_i8, void* scales_f32,
+                                                                            void* sums_i32, uint32_t rows,
+                                                                            void* stream) {
+    nerve_hip_status st = nh::enter(ctx);
+    if (st) return st;
+    nh::QuantI8Spec qs;
+    if ((st = nh::parse_quant_i8_spec(spec, &qs))) return st;
+    if (!qs.silu) return nh::fail(NERVE_HIP_INVALID_SPEC, "not a silu_multiply_quantize specialization");
+    if (!gate_bf16 || !up_bf16 || !y_bf16 || !q_i8 || !scales_f32 || !sums_i32)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (qs.batch_tile == 0 && rows > 1)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "unbatched pair-packed quantizer takes one row");
+    if ((((uintptr_t)gate_bf16) | ((uintptr_t)up_bf16) | ((uintptr_t)y_bf16)) & 15 || ((uintptr_t)q_i8 & 7))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "gate, up and y must be 16-byte and q 8-byte aligned");
+    if (rows == 0) return nh::ok();
+    const uint64_t octs = (uint64_t)rows * qs.elements / 8;
+    quant_i8pp_kernel<true><<<(uint32_t)((octs + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(gate_bf16), static_cast<const uint16_t*>(up_bf16), static_cast<uint16_t*>(y_bf16),
+        rows, qs.elements, static_cast<uint32_t*>(q_i8), static_cast<float*>(scales_f32),
+        static_cast<int32_t*>(sums_i32));
+    return nh::check_launch("silu_multiply_quantize_int8_pairpacked");
 }
 
 extern "C" nerve_hip_status nerve_hip_int4_linear_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* q_i8,

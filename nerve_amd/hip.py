@@ -34,6 +34,7 @@ EXPORTS = (
     "nerve_hip_moe_reduce",
     "nerve_hip_int4_linear",
     "nerve_hip_quantize_int8_pairpacked",
+    "nerve_hip_silu_multiply_quantize_int8_pairpacked",
     "nerve_hip_int4_linear_pairpacked",
     "nerve_hip_fp8_output_projection",
     "nerve_hip_argmax_f32",
@@ -92,6 +93,7 @@ def _declare(lib) -> None:
         "nerve_hip_moe_reduce": (ctypes.c_int, [P, P, P, U32, U32, U32, ctypes.c_float, P]),
         "nerve_hip_int4_linear": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
+        "nerve_hip_silu_multiply_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_int4_linear_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, P, U32, P]),
         "nerve_hip_fp8_output_projection": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_argmax_f32": (ctypes.c_int, [P, P, U32, U32, P, P]),
@@ -250,6 +252,11 @@ class Context:
     def quantize_int8_pairpacked(self, spec, x, q, scales, sums, rows, stream=None):
         _check(self.lib.nerve_hip_quantize_int8_pairpacked(self.handle, _spec(spec), ptr(x), ptr(q), ptr(scales),
                                                            ptr(sums), rows, _stream(stream)))
+
+    def silu_multiply_quantize_int8_pairpacked(self, spec, gate, up, y, q, scales, sums, rows, stream=None):
+        _check(self.lib.nerve_hip_silu_multiply_quantize_int8_pairpacked(
+            self.handle, _spec(spec), ptr(gate), ptr(up), ptr(y), ptr(q), ptr(scales), ptr(sums), rows,
+            _stream(stream)))
 
     def int4_linear_pairpacked(self, spec, q, scales_f32, sums, qweight, scales, aux, y, batch_width, stream=None):
         _check(self.lib.nerve_hip_int4_linear_pairpacked(self.handle, _spec(spec), ptr(q), ptr(scales_f32), ptr(sums),

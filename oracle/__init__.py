@@ -65,6 +65,7 @@ def _declare(l) -> None:
         "o_moe_reduce": (None, [P, I, I, I, F, P]),
         "o_int4_linear": (None, [I, P, P, P, I, P, I, I, I, I, I, P, P]),
         "o_quantize_i8_pairpacked": (None, [P, I, I, P, P, P]),
+        "o_silu_multiply_bf16": (None, [P, P, L, P]),
         "o_int4_linear_pairpacked": (None, [P, P, P, P, P, I, I, I, I, I, I, P, P]),
         "o_fp8_output_projection": (None, [P, I, I, P, P, I, I, F, P]),
         "o_argmax": (None, [P, I, I, P]),
@@ -283,6 +284,15 @@ def quantize_i8_pairpacked(x_bf16):
     sums = np.zeros((rows, cols // 32), np.int32)
     lib().o_quantize_i8_pairpacked(_p(x), rows, cols, _p(q), _p(s), _p(sums))
     return q, s, sums
+
+
+def silu_multiply_bf16(g_bf16, u_bf16):
+    """y = bf16(bf16(silu(g)) * u), elementwise (bf16 bits in, bf16 bits out)."""
+    g = _c(g_bf16, np.uint16)
+    u = _c(u_bf16, np.uint16)
+    y = np.zeros(g.shape, np.uint16)
+    lib().o_silu_multiply_bf16(_p(g), _p(u), g.size, _p(y))
+    return y
 
 
 def int4_linear_pairpacked(q, s, sums, qweight, scales, group, *, scale_bf16=False, finalize=0, aux=None):

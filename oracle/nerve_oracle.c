@@ -643,6 +643,16 @@ void o_quantize_i8_pairpacked(const uint16_t* x, int rows, int cols, uint8_t* q,
     }
 }
 
+/* silu(g) * u in bf16 (silu_multiply_quantize_int8_pairpacked.comp.template:
+ * rounded_silu and main): y = bf16(bf16(g / (1 + exp(-g))) * u). */
+void o_silu_multiply_bf16(const uint16_t* g, const uint16_t* u, long n, uint16_t* y) {
+    for (long i = 0; i < n; i++) {
+        float gv = o_bf16_to_f32(g[i]);
+        float act = o_bf16_to_f32(o_f32_to_bf16(gv / (1.0f + expf(-gv))));
+        y[i] = o_f32_to_bf16(act * o_bf16_to_f32(u[i]));
+    }
+}
+
 /* Pair-packed INT8 x GPTQ INT4 linear (linear_prequant_pairpacked_int4_gptq.
  * comp.template:56-95): per output row, for each weight group and each
  * 32-column block of it, block_dot = -8 * sum + sum of the exact int8 x u4

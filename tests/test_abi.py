@@ -83,6 +83,8 @@ def test_null_context_is_rejected():
     ("linear_prequant_int4_gptq_sf16_g128_4096x4096.comp", 3),
     ("quantize_batch4_int8_symmetric_pairpacked_b32_h4096.comp", 0),
     ("quantize_int8_symmetric_pairpacked_b64_h4096.comp", 2),
+    ("silu_multiply_quantize_int8_pairpacked_b32_h14336.comp", 0),
+    ("silu_multiply_quantize_batch16_int8_pairpacked_b32_h14336.comp", 0),
     ("tied_output_projection_fp8_e4m3_b1x128_201088x2880_scale1_to_f32.comp", 0),
     ("tied_output_projection_batch4_fp8_e4m3_b128x128_151936x4096_scale0.0333333351_to_f32.comp", 0),
     ("tied_output_projection_fp8_e4m3_b1x64_201088x2880_scale1_to_f32.comp", 2),

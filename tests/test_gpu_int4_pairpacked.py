@@ -63,3 +63,26 @@ def test_int4_linear_pairpacked(ctx, dev, M, K, N, G, finalize, bf16_scales):
                                         finalize=finalize, aux=aux)
     ok, worst, exact = bf16_close(to_np(y, np.uint16), ref)
     assert ok and exact > 0.9, (worst, exact)
+
+
+@pytest.mark.parametrize("B,N", [(1, 14336), (4, 2880), (16, 96)])
+def test_silu_multiply_quantize_int8_pairpacked(ctx, dev, B, N):
+    import torch
+
+    rng = np.random.default_rng(B * 7 + N)
+    g = wl.bf16_normal(rng, (B, N), 2.0)
+    u = wl.bf16_normal(rng, (B, N))
+    y = torch.zeros(B, N, dtype=torch.int16, device=dev)
+    q = torch.zeros(B, N, dtype=torch.uint8, device=dev)
+    s = torch.zeros(B, N // 32, dtype=torch.float32, device=dev)
+    sums = torch.zeros(B, N // 32, dtype=torch.int32, device=dev)
+    spec = f"silu_multiply_quantize{'_batch%d' % B if B > 1 else ''}_int8_pairpacked_b32_h{N}.comp"
+    ctx.silu_multiply_quantize_int8_pairpacked(spec, to_dev(g, dev), to_dev(u, dev), y, q, s, sums, B)
+    yg = to_np(y, np.uint16)
+    yr = oracle.silu_multiply_bf16(g, u)
+    d = np.abs(yg.astype(np.int32) - yr.astype(np.int32))
+    assert d.max() <= 1 and np.mean(d == 0) > 0.99      # exp may differ in its last place
+    qr, sr, sumr = oracle.quantize_i8_pairpacked(yg)
+    assert np.array_equal(to_np(q, np.uint8), qr)
+    assert np.array_equal(to_np(s, np.float32), sr)
+    assert np.array_equal(to_np(sums, np.int32), sumr)

@@ -50,3 +50,18 @@ def test_linear_matches_bf16_oracle_on_dequantized_input():
     ref = codes @ (wq * sw)
     got = wl.bf16_bits_to_f32(y).astype(np.float64)
     assert np.max(np.abs(got - ref) / (np.abs(ref) + np.sqrt(np.mean(ref ** 2)))) < 1e-2
+
+
+def test_silu_multiply_closed_forms():
+    """silu(0) = 0, silu(x) -> x for large x, silu(x) - silu(-x) = x, and the
+    product with u (all up to the two bf16 roundings)."""
+    g = wl.f32_to_bf16_bits(np.array([0.0, 30.0, -30.0, 1.5, -1.5, 3.0, -3.0], np.float32))
+    one = wl.f32_to_bf16_bits(np.ones(7, np.float32))
+    y = wl.bf16_bits_to_f32(oracle.silu_multiply_bf16(g, one)).astype(np.float64)
+    assert y[0] == 0.0 and abs(y[1] - 30.0) <= 30.0 * 2 ** -7 and abs(y[2]) < 1e-9
+    for i in (3, 5):
+        xv = wl.bf16_bits_to_f32(g[i])
+        assert abs((y[i] - y[i + 1]) - xv) <= abs(xv) * 2 ** -6
+    u = wl.f32_to_bf16_bits(np.full(7, -2.0, np.float32))
+    y2 = wl.bf16_bits_to_f32(oracle.silu_multiply_bf16(g, u)).astype(np.float64)
+    assert np.array_equal(y2, -2.0 * y)                   # a power-of-two factor is exact

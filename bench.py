@@ -368,7 +368,7 @@ def fp8_head(args, ctx, dev):
                     {"workload": f"fp8_lm_head_m{M}_k2880_n201088_argmax"})
     mfma_bound = M >= 512
     kname = ("fp8_head_stream_kernel<3> (+ row quantization, argmax of the partials)" if M <= 16
-             else "fp8_head_kernel (+ row quantization, argmax of the partials)")
+             else "fp8_head_gemm_kernel (+ row quantization, scale scan, argmax of the partials)")
     out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": kname,
                        "achieved": tf if mfma_bound else gbs, "peak": FP8_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
                        "unit": "TFLOP/s" if mfma_bound else "GB/s",

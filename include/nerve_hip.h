@@ -314,7 +314,8 @@ nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const ch
 /* Replaces silu_multiply_quantize[_batch{T}]_int8_pairpacked_b32_h{N}.comp
  * (silu_multiply_quantize_int8_pairpacked.comp.template): y = bf16(bf16(
  * g / (1 + exp(-g))) * u) for gate and up bf16 [rows, N], written to y, and
- * the pair-packed INT8 quantization of y as above. */
+ * the pair-packed INT8 quantization of y as above.  y must not overlap gate
+ * or up (NERVE_HIP_INVALID_ARGUMENT otherwise). */
 nerve_hip_status nerve_hip_silu_multiply_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec,
                                                                  const void* gate_bf16, const void* up_bf16,
                                                                  void* y_bf16, void* q_i8, void* scales_f32,

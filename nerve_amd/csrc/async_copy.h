@@ -98,4 +98,30 @@ __device__ __forceinline__ float max_xor32(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// LDS reads at a fixed register plus an immediate offset (< 64 KiB).
+template <uint32_t OFF>
+__device__ __forceinline__ v4i lds_rd128(uint32_t a) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+template <uint32_t OFF>
+__device__ __forceinline__ uint32_t lds_rd32(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+
+template <typename F, uint32_t... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<uint32_t, I...>) {
+    (f(std::integral_constant<uint32_t, I>{}), ...);
+}
+// f(integral_constant<0>), ..., f(integral_constant<N-1>).
+template <uint32_t N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<uint32_t, N>{});
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)(lds_u8*)p; }
+
 }  // namespace

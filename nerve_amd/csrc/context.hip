@@ -242,7 +242,7 @@ static nerve_hip_status parse_rms_quant_spec_uncached(const char* spec, RmsQuant
         "_offset([0-9eE+.-]+)\\.comp");
     std::cmatch m;
     if (!std::regex_match(spec, m, re))
-        return fail(NERVE_HIP_INVALID_SPEC, std::string("not an RMSNorm FP8 quantizer: ") + spec);
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("not an RMSNorm FP8/INT8 quantizer: ") + spec);
     RmsQuantSpec s;
     uint32_t bt = 0;
     if (m[1].matched) parse_u32(m[1].str(), &bt);

@@ -490,6 +490,625 @@ __global__ __launch_bounds__(64 * HS_NW) void fp8_head_stream_kernel(HeadArgs A,
     fp8_head_stream_body<NBUF>(A, S);
 }
 
+// ---------------------------------------------------------------------------
+// Tiled form (M > 16): an LDS-staged FP8 GEMM.
+//
+// Item = (vocabulary tile of TN rows, token tile of TM rows).  Items are
+// listed with token tiles fastest and dealt to the persistent blocks so that
+// consecutive items run on one XCD: the token tiles of one vocabulary tile
+// read the same weight rows while they sit in that XCD's L2, so the weights
+// come from HBM about once.  A block of WM x WN waves (two per SIMD) streams
+// every 128-column chunk of its items through an NS-stage LDS ring with
+// global_load_lds: the chunk's token rows (TM x 128 B), weight rows (TN x
+// 128 B) and token block scales (TM x 4 B); the ring runs across item
+// boundaries.  The tokens are quantized beforehand into a chunk-major
+// workspace layout ([chunk][token][128 B], 16-byte pieces already in their
+// LDS positions), so their copies are contiguous 1 KiB reads, which the
+// texture path serves at twice the rate of the 8-row weight pieces.  Each
+// 16-byte piece p of a row R sits at piece p ^ f(R), f(R) = (R mod 8) ^
+// (bit 3 of R), so the operand reads of 16 lanes hit 16 distinct bank groups.
+// Every wave issues the same number of copies per chunk (plus one at an
+// item's first chunk for the waves that copy the tile's row scales and
+// flags), so "chunk s has landed" is a vmcnt wait for the copies issued
+// after it.
+//
+// Wave (wm, wn) contracts tokens [wm 16 TT, +16 TT) against weight rows
+// [wn 16 NJ, +16 NJ): per chunk, TT x NJ v_mfma_scale 16x16x128 e4m3 x e4m3
+// (unit scales; the weights are the first operand, so a lane holds 4
+// consecutive vocabulary rows of one token), each result accumulated as
+// acc += p * s_x[token, chunk] and, at the end, multiplied by the row's
+// scale: a reassociation of sum_b dot_b * (s_x[b] * s_w[n, b]) that holds
+// when every row of the tile has one scale across K (per-channel grids; a
+// scan before the launch flags the rows that do not).  A tile with any such
+// row takes the general form, acc += p * (s_x * s_w[n, chunk]), with its
+// scale block staged in LDS.  The epilogue writes logits and one (max, id)
+// per token and tile for the argmax pass.
+// ---------------------------------------------------------------------------
+struct HeadGemmArgs {
+    const uint8_t* xq;            // e4m3 [nblk][Mpad][128], pieces swizzled per row
+    const float* xs;              // f32 [nblk][Mpad]
+    const uint8_t* W;             // e4m3 [N, K]
+    const uint16_t* scale_inv;    // bf16 [ceil(N/BR), nblk]
+    const float* sw_row;          // f32 [N]: each row's first-block scale
+    const uint8_t* nonuni;        // u8 [nvt * TN]: 1 = the row's scale varies along K
+    uint32_t M, Mpad, K, N, BR, nblk;
+    uint32_t ntt, n_items, nvt;
+    float out_scale;
+    float* logits_f32;            // [M, N] or null
+    uint16_t* logits_bf16;        // [M, N] or null
+    float* part_val;              // [M, nvt] or null
+    uint32_t* part_idx;
+};
+
+__device__ __attribute__((aligned(16))) const uint8_t kHeadZero[1024] = {0};
+
+template <int WM, int WN, int TT, int NJ, int NS>
+struct HgLayout {
+    static constexpr uint32_t NW = WM * WN;
+    static constexpr uint32_t TM = 16 * WM * TT, TN = 16 * WN * NJ;
+    static constexpr uint32_t A_BYTES = TM * 128, B_BYTES = TN * 128, SX_BYTES = TM * 4;
+    static constexpr uint32_t STAGE = A_BYTES + B_BYTES + SX_BYTES;
+    static constexpr uint32_t SWROW = NS * STAGE;           // [2][TN] f32, by item parity
+    static constexpr uint32_t FLAGS = SWROW + 2 * TN * 4;   // [2][TN] u8, by item parity
+    // [nblk <= 32][TN] bf16 scale block of a general-form tile; in the
+    // epilogue, the argmax exchange [WN][TM] {f32, u32}
+    static constexpr uint32_t SWB = FLAGS + 2 * TN;
+    static constexpr uint32_t SWB_BYTES = 32 * TN * 2 > WN * TM * 8 ? 32 * TN * 2 : WN * TM * 8;
+    static constexpr uint32_t BYTES = SWB + SWB_BYTES;
+    static constexpr uint32_t AC = TM / 8 / NW;             // token copies per wave per chunk (1 KiB each)
+    static constexpr uint32_t BC = TN / 8 / NW;             // weight copies per wave per chunk
+    static constexpr uint32_t CB = AC + BC;                 // (+ 1 for wave 0: the block scales)
+    static constexpr uint32_t XW = TN / 64 + 1;             // waves with an item-start copy
+    static constexpr uint32_t F32_STRIDE = NJ * 64 + 16, BF16_STRIDE = NJ * 32 + 16;   // epilogue staging rows
+    static_assert(AC * 8 * NW == TM && BC * 8 * NW == TN && AC >= 1 && BC >= 1, "copy split");
+    static_assert(NW * 16 * F32_STRIDE <= STAGE, "staging fits a stage");
+    static_assert(XW <= NW && TM % 64 == 0, "item-start copies");
+};
+
+// Piece swizzle of row r: (r mod 8) ^ bit 3 of r.  Rows 16 apart share it
+// (the operand reads of tile t are those of tile 0 plus an immediate), and
+// the 16 rows a read touches land on 16 distinct 16-byte bank groups.
+__host__ __device__ __forceinline__ uint32_t hg_swz(uint32_t r) { return (r & 7u) ^ ((r >> 3) & 1u); }
+
+template <int WM, int WN, int TT, int NJ, int NS>
+__device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
+    using L = HgLayout<WM, WN, TT, NJ, NS>;
+    constexpr uint32_t TM = L::TM, TN = L::TN, NW = L::NW;
+    extern __shared__ __attribute__((aligned(16))) uint8_t hg_lds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, M = A.M, N = A.N, nblk = A.nblk, Mpad = A.Mpad;
+    const uint32_t G = gridDim.x;
+    const uint32_t ring = lds_addr(hg_lds);
+    // Slot q of the item list; the hardware deals consecutive blocks to the
+    // 8 XCDs in turn, so slot (b % 8) (G / 8) + b / 8 puts consecutive items
+    // on one XCD.
+    const uint32_t slot = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    const uint32_t n_my = (A.n_items - slot + G - 1) / G;     // >= 1: G <= n_items
+    const uint32_t tail_cols = K - (nblk - 1) * 128;          // columns of the last chunk (32..128)
+
+    // ---- issue side --------------------------------------------------------
+    // Weight copy j of a wave fills 8 rows (group wave BC + j) with 8 pieces
+    // each: lane l copies piece (l & 7) ^ f(row) of row l >> 3, where
+    // f(row) = (l >> 3) ^ (group parity), so the lane part of every weight
+    // copy address is one of two values; rows past N (last tile) are
+    // redirected to the tile's first row.  Token copies are contiguous.
+    const uint32_t lr = lane >> 3, sp0 = (lane & 7u) ^ lr;
+    const uint32_t lane_off[2] = {lr * K + sp0 * 16, lr * K + (sp0 ^ 1u) * 16};
+    const bool tail_ok[2] = {sp0 * 16 < tail_cols, (sp0 ^ 1u) * 16 < tail_cols};
+    uint32_t i_item = slot, i_ord = 0, ic = 0, i_t0 = 0, i_n0 = 0;
+    bool issuing = true;
+    auto setup_issue = [&]() __attribute__((always_inline)) {
+        i_t0 = (i_item % A.ntt) * TM;
+        i_n0 = (i_item / A.ntt) * TN;
+    };
+    auto issue_chunk = [&](uint32_t ST) __attribute__((always_inline)) {
+        uint8_t* const dA = hg_lds + ST * L::STAGE + wave * L::AC * 1024;
+        uint8_t* const dB = hg_lds + ST * L::STAGE + L::A_BYTES + wave * L::BC * 1024;
+        uint8_t* const dS = hg_lds + ST * L::STAGE + L::A_BYTES + L::B_BYTES;
+        const bool last = ic + 1 == nblk;
+        const uint8_t* a = A.xq + ((uint64_t)ic * Mpad + i_t0) * 128 + wave * L::AC * 1024 + lane * 16;
+        const uint8_t* w = A.W + (uint64_t)(i_n0 + wave * L::BC * 8) * K + ic * 128;
+        const bool wpart = i_n0 + TN > N;                        // last vocabulary tile
+        static_for<L::AC>([&](auto ji) __attribute__((always_inline)) {
+            constexpr uint32_t j = decltype(ji)::value;
+            __builtin_amdgcn_global_load_lds(a + j * 1024, dA + j * 1024, 16, 0, 0);
+        });
+        static_for<L::BC>([&](auto ji) __attribute__((always_inline)) {
+            constexpr uint32_t j = decltype(ji)::value;
+            const uint8_t* src = w + j * 8 * K + lane_off[j & 1];
+            if (wpart && i_n0 + (wave * L::BC + j) * 8 + lr >= N) src = A.W + (uint64_t)i_n0 * K + ic * 128;
+            __builtin_amdgcn_global_load_lds((!last || tail_ok[j & 1]) ? src : kHeadZero, dB + j * 1024, 16, 0, 0);
+        });
+        if (wave == 0 && lane < TM / 4)   // the chunk's TM block scales: one 16-byte piece per lane
+            __builtin_amdgcn_global_load_lds(A.xs + (uint64_t)ic * Mpad + i_t0 + lane * 4, dS, 16, 0, 0);
+        if (ic == 0 && wave < L::XW) {
+            // Item start: the tile's row scales (waves 0 .. TN/64 - 1) or its
+            // row flags (wave TN/64), into the slot of the item's parity.
+            const uint32_t par = i_ord & 1u;
+            if (wave < TN / 64) {
+                const uint32_t row = i_n0 + 64 * wave + lane;
+                __builtin_amdgcn_global_load_lds(A.sw_row + (row < N ? row : N - 1),
+                                                 hg_lds + L::SWROW + par * TN * 4 + 64 * wave * 4, 4, 0, 0);
+            } else if (lane < TN / 4) {
+                __builtin_amdgcn_global_load_lds(A.nonuni + i_n0 + 4 * lane, hg_lds + L::FLAGS + par * TN, 4, 0, 0);
+            }
+        }
+    };
+    auto issue_next = [&](uint32_t ST) __attribute__((always_inline)) {
+        if (!issuing) return;
+        issue_chunk(ST);
+        if (++ic == nblk) {
+            ic = 0;
+            i_ord++;
+            i_item += G;
+            issuing = i_ord < n_my;
+            if (issuing) setup_issue();
+        }
+    };
+
+    // ---- compute side --------------------------------------------------------
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    const uint32_t RA = wm * 16 * TT + rr, RB = wn * 16 * NJ + rr;
+    const uint32_t LA_lo = ring + RA * 128 + (((2 * g) ^ hg_swz(RA)) * 16);
+    const uint32_t LA_hi = ring + RA * 128 + (((2 * g + 1) ^ hg_swz(RA)) * 16);
+    const uint32_t LB_lo = ring + L::A_BYTES + RB * 128 + (((2 * g) ^ hg_swz(RB)) * 16);
+    const uint32_t LB_hi = ring + L::A_BYTES + RB * 128 + (((2 * g + 1) ^ hg_swz(RB)) * 16);
+    const uint32_t LSX = ring + L::A_BYTES + L::B_BYTES + RA * 4;
+    uint32_t c = 0, c_ord = 0, c_item = slot;
+    bool general = false;
+    v4f acc[TT][NJ];
+
+    auto start_item = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        // Row flags of the tile (landed with chunk 0): one ballot per wave,
+        // the same decision in every wave.
+        uint32_t f = 0;
+        if (lane < TN / 4) f = lds_read_b32(hg_lds + L::FLAGS + (c_ord & 1u) * TN + 4 * lane);
+        lds_drain();
+        asm volatile("" : "+v"(f));
+        general = __ballot(f != 0u) != 0ull;
+        if (general) {
+            // The tile's scale block, transposed to [chunk][row] bf16.  Plain
+            // loads: the compiler drains the copies in flight before their use
+            // (a pipeline bubble on this form only).
+            const uint32_t n0 = (c_item / A.ntt) * TN;
+            for (uint32_t e = tid; e < nblk * TN; e += 64 * NW) {
+                const uint32_t ch = e / TN, R = e % TN, n = n0 + R < N ? n0 + R : N - 1;
+                const uint32_t v = A.scale_inv[(uint64_t)(n / A.BR) * nblk + ch];
+                const uint32_t a = ring + L::SWB + e * 2;
+                asm volatile("ds_write_b16 %0, %1" : : "v"(a), "v"(v) : "memory");
+            }
+            lds_drain();
+            __builtin_amdgcn_s_barrier();
+        }
+    };
+
+    auto compute = [&](uint32_t stb, auto gen_tag) __attribute__((always_inline)) {
+        constexpr bool general = decltype(gen_tag)::value;
+        v4i blo[NJ], bhi[NJ], alo[2], ahi[2];
+        uint32_t sxv[2];
+        v2i swp[NJ];
+        static_for<NJ>([&](auto ji) __attribute__((always_inline)) {
+            constexpr uint32_t j = decltype(ji)::value;
+            blo[j] = lds_rd128<j * 2048>(LB_lo + stb);
+            bhi[j] = lds_rd128<j * 2048>(LB_hi + stb);
+        });
+        if constexpr (general) {
+            // scales of rows 4 g .. 4 g + 3 of each weight tile at this chunk
+            const uint32_t a = ring + L::SWB + (c * TN + wn * 16 * NJ + 4 * g) * 2;
+            v2i* sp = swp;
+            static_for<NJ>([&](auto ji) __attribute__((always_inline)) {
+                constexpr uint32_t j = decltype(ji)::value;
+                v2i r;
+                asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(j * 32));
+                sp[j] = r;
+            });
+        }
+        alo[0] = lds_rd128<0>(LA_lo + stb);
+        ahi[0] = lds_rd128<0>(LA_hi + stb);
+        sxv[0] = lds_rd32<0>(LSX + stb);
+        // Software pipeline over the token tiles: each inline-asm group issues
+        // the MFMA of (tile t, weight tile j) and then the scale-and-accumulate
+        // of (tile t - 1, weight tile j), whose MFMA result was produced NJ
+        // MFMAs earlier (past its latency), so the vector ALU works while the
+        // matrix core is busy.  (Compiler scheduling placed each accumulate
+        // right behind its own MFMA and waited for it.)
+        v4f pr[2][NJ];             // general form: results of tiles t, t - 1
+        v4f pring[NJ + 1];         // fast form: ring of MFMA results
+        float sxp[2];
+        const uint32_t unit = 127u;                 // e8m0 1.0: unscaled e4m3 x e4m3
+        static_for<TT + 1>([&](auto ti) __attribute__((always_inline)) {
+            constexpr uint32_t t = decltype(ti)::value;
+            constexpr uint32_t cur = t & 1u, nxt = cur ^ 1u;
+            if constexpr (t < (uint32_t)TT) {
+                if constexpr (t + 1 < (uint32_t)TT) {
+                    alo[nxt] = lds_rd128<(t + 1) * 2048>(LA_lo + stb);
+                    ahi[nxt] = lds_rd128<(t + 1) * 2048>(LA_hi + stb);
+                    sxv[nxt] = lds_rd32<(t + 1) * 64>(LSX + stb);
+                    asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(alo[cur]), "+v"(ahi[cur]), "+v"(sxv[cur]) : : "memory");
+                } else {
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(alo[cur]), "+v"(ahi[cur]), "+v"(sxv[cur]) : : "memory");
+                }
+                if constexpr (t == 0) {
+#pragma unroll
+                    for (uint32_t j = 0; j < (uint32_t)NJ; j++) asm volatile("" : "+v"(blo[j]), "+v"(bhi[j]));
+                    if constexpr (general) {
+#pragma unroll
+                        for (uint32_t j = 0; j < (uint32_t)NJ; j++) asm volatile("" : "+v"(swp[j]));
+                    }
+                }
+                const v8i bt = v8i{alo[cur].x, alo[cur].y, alo[cur].z, alo[cur].w,
+                                   ahi[cur].x, ahi[cur].y, ahi[cur].z, ahi[cur].w};
+                sxp[cur] = __uint_as_float(sxv[cur]);
+#pragma unroll
+                for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                    const v8i bw = v8i{blo[j].x, blo[j].y, blo[j].z, blo[j].w, bhi[j].x, bhi[j].y, bhi[j].z, bhi[j].w};
+                    // MFMA number m = t NJ + j writes ring slot m % (NJ + 1); the
+                    // accumulate reads the slot of MFMA m - NJ.
+                    const uint32_t m = t * NJ + j, wslot = m % (NJ + 1), rslot = (m + 1) % (NJ + 1);
+                    if constexpr (!general && t >= 1) {
+                        v4f& a4 = acc[t - 1][j];
+                        const v4f po = pring[rslot];
+                        asm volatile(
+                            "v_mfma_scale_f32_16x16x128_f8f6f4 %0, %5, %6, 0, %7, %7 op_sel_hi:[0,0,0]\n\t"
+                            "v_fmac_f32 %1, %8, %12\n\t"
+                            "v_fmac_f32 %2, %9, %12\n\t"
+                            "v_fmac_f32 %3, %10, %12\n\t"
+                            "v_fmac_f32 %4, %11, %12"
+                            : "=&v"(pring[wslot]), "+v"(a4[0]), "+v"(a4[1]), "+v"(a4[2]), "+v"(a4[3])
+                            : "v"(bw), "v"(bt), "v"(unit), "v"(po[0]), "v"(po[1]), "v"(po[2]), "v"(po[3]),
+                              "v"(sxp[cur ^ 1u])
+                            : );
+                    } else if constexpr (!general) {
+                        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0]"
+                                     : "=&v"(pring[wslot])
+                                     : "v"(bw), "v"(bt), "v"(unit));
+                    } else {
+                        pr[cur][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bw, bt, v4f{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                                      0, 0, 127, 0, 127);
+                    }
+                }
+            }
+            if constexpr (general && t >= 1) {
+                constexpr uint32_t tp = t - 1, pp = tp & 1u;
+                const float sx = sxp[pp];
+#pragma unroll
+                for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                    const v4f p = pr[pp][j];
+                    const uint32_t w0 = (uint32_t)swp[j].x, w1 = (uint32_t)swp[j].y;
+                    const float s0 = sx * __uint_as_float(w0 << 16), s1 = sx * __uint_as_float(w0 & 0xffff0000u);
+                    const float s2 = sx * __uint_as_float(w1 << 16), s3 = sx * __uint_as_float(w1 & 0xffff0000u);
+                    acc[tp][j][0] = fmaf(p[0], s0, acc[tp][j][0]);
+                    acc[tp][j][1] = fmaf(p[1], s1, acc[tp][j][1]);
+                    acc[tp][j][2] = fmaf(p[2], s2, acc[tp][j][2]);
+                    acc[tp][j][3] = fmaf(p[3], s3, acc[tp][j][3]);
+                }
+            }
+            if constexpr (!general && t == (uint32_t)TT) {
+                // The last tile's accumulate: its MFMAs were the last issued, so
+                // wait out their latency first (inline-asm results get no
+                // compiler-inserted wait states).
+                constexpr uint32_t pp = (TT - 1) & 1u;
+                asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                             : "+v"(pring[(TT * NJ - 1) % (NJ + 1)]), "+v"(pring[(TT * NJ - NJ) % (NJ + 1)]));
+#pragma unroll
+                for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                    v4f& a4 = acc[TT - 1][j];
+                    const v4f po = pring[((TT - 1) * NJ + j) % (NJ + 1)];
+                    asm volatile(
+                        "v_fmac_f32 %0, %4, %8\n\t"
+                        "v_fmac_f32 %1, %5, %8\n\t"
+                        "v_fmac_f32 %2, %6, %8\n\t"
+                        "v_fmac_f32 %3, %7, %8"
+                        : "+v"(a4[0]), "+v"(a4[1]), "+v"(a4[2]), "+v"(a4[3])
+                        : "v"(po[0]), "v"(po[1]), "v"(po[2]), "v"(po[3]), "v"(sxp[pp]));
+                }
+            }
+        });
+    };
+
+    // Epilogue of the item: logits and the per-token (max, id) of the tile.
+    // After a barrier (every wave done with stage ST and the scale block),
+    // stage ST stages each wave's 16-token slices so the stores write whole
+    // row segments, 16 bytes per lane, and the scale-block region carries
+    // the argmax exchange between the WN waves of a token range.
+    auto epilogue = [&](uint32_t ST) __attribute__((always_inline)) {
+        const uint32_t vt = c_item / A.ntt, t0 = (c_item % A.ntt) * TM, n0 = vt * TN;
+        const uint32_t nw0 = n0 + wn * 16 * NJ;                  // first vocabulary row of this wave
+        if (!general) {
+            v4i r[NJ];
+            const uint32_t a = ring + L::SWROW + (c_ord & 1u) * TN * 4 + (wn * 16 * NJ + 4 * g) * 4;
+            static_for<NJ>([&](auto ji) __attribute__((always_inline)) {
+                constexpr uint32_t j = decltype(ji)::value;
+                r[j] = lds_rd128<j * 64>(a);
+            });
+            lds_drain();
+#pragma unroll
+            for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                asm volatile("" : "+v"(r[j]));
+#pragma unroll
+                for (uint32_t t = 0; t < (uint32_t)TT; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][j][i] *= __int_as_float(r[j][i]) * A.out_scale;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t t = 0; t < (uint32_t)TT; t++)
+#pragma unroll
+                for (uint32_t j = 0; j < (uint32_t)NJ; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][j][i] *= A.out_scale;
+        }
+        lds_drain();
+        __builtin_amdgcn_s_barrier();        // stage ST and the scale block are free
+        if (A.part_val) {
+            const bool whole = nw0 + 16 * NJ <= N;
+#pragma unroll
+            for (uint32_t t = 0; t < (uint32_t)TT; t++) {
+                // A lane's 4 NJ candidates in ascending row order: a strictly
+                // larger value wins, so ties keep the lower row.
+                float bv = -INFINITY;
+                uint32_t bi = 0xffffffffu;
+#pragma unroll
+                for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                    const uint32_t n = nw0 + j * 16 + 4 * g;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float v = acc[t][j][i];
+                        const bool take = (v > bv || bi == 0xffffffffu) && (whole || n + i < N);
+                        bv = take ? v : bv;
+                        bi = take ? n + i : bi;
+                    }
+                }
+                // lanes rr, rr + 16, rr + 32, rr + 48 hold one token: combine
+                // them with row swaps (vector ALU; an LDS-routed shuffle would
+                // queue behind the ring's copies)
+                {
+                    const auto v16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+                    const auto i16 = __builtin_amdgcn_permlane16_swap(bi, bi, false, false);
+                    const float ov = __uint_as_float((lane & 16u) ? v16[0] : v16[1]);
+                    const uint32_t oi = (lane & 16u) ? i16[0] : i16[1];
+                    if (better(ov, oi, bv, bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                    const auto v32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+                    const auto i32 = __builtin_amdgcn_permlane32_swap(bi, bi, false, false);
+                    const float ov2 = __uint_as_float((lane & 32u) ? v32[0] : v32[1]);
+                    const uint32_t oi2 = (lane & 32u) ? i32[0] : i32[1];
+                    if (better(ov2, oi2, bv, bi)) {
+                        bv = ov2;
+                        bi = oi2;
+                    }
+                }
+                if (g == 0) {
+                    const uint32_t a = ring + L::SWB + (wn * TM + wm * 16 * TT + t * 16 + rr) * 8;
+                    asm volatile("ds_write_b64 %0, %1" : : "v"(a), "v"(v2i{(int)__float_as_uint(bv), (int)bi}) : "memory");
+                }
+            }
+        }
+        // Whole slices with 16-byte-aligned rows go through the stage; the
+        // last tile's partial slice and N not a multiple of 8 (4 for f32) are
+        // stored from registers.
+        const bool full = nw0 + 16 * NJ <= N;
+        const uint32_t sbase = ring + ST * L::STAGE + wave * 16 * L::F32_STRIDE;
+        if (A.logits_bf16) {
+            if (full && (N & 7u) == 0) {
+                constexpr uint32_t LPR = 2 * NJ, RPR = 64 / LPR;     // lanes per row, rows per read
+#pragma unroll
+                for (uint32_t t = 0; t < (uint32_t)TT; t++) {
+#pragma unroll
+                    for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                        const v2i w = v2i{(int)(f32_to_bf16(acc[t][j][0]) | (f32_to_bf16(acc[t][j][1]) << 16)),
+                                          (int)(f32_to_bf16(acc[t][j][2]) | (f32_to_bf16(acc[t][j][3]) << 16))};
+                        asm volatile("ds_write_b64 %0, %1" : : "v"(sbase + rr * L::BF16_STRIDE + (j * 16 + 4 * g) * 2), "v"(w) : "memory");
+                    }
+                    v4i r[16 / RPR];
+                    const uint32_t ra = sbase + (lane / LPR) * L::BF16_STRIDE + (lane % LPR) * 16;
+                    static_for<16 / RPR>([&](auto hi) __attribute__((always_inline)) {
+                        constexpr uint32_t h = decltype(hi)::value;
+                        r[h] = lds_rd128<h * RPR * L::BF16_STRIDE>(ra);
+                    });
+                    lds_drain();
+                    const uint32_t col = nw0 + (lane % LPR) * 8;
+#pragma unroll
+                    for (uint32_t h = 0; h < 16 / RPR; h++) {
+                        asm volatile("" : "+v"(r[h]));
+                        const uint32_t tk = t0 + wm * 16 * TT + t * 16 + h * RPR + lane / LPR;
+                        if (tk < M) *reinterpret_cast<v4i*>(A.logits_bf16 + (uint64_t)tk * N + col) = r[h];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t t = 0; t < (uint32_t)TT; t++) {
+                    const uint32_t tok = t0 + wm * 16 * TT + t * 16 + rr;
+                    if (tok >= M) continue;
+#pragma unroll
+                    for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                        const uint32_t n = nw0 + j * 16 + 4 * g;
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (n + i < N) A.logits_bf16[(uint64_t)tok * N + n + i] = (uint16_t)f32_to_bf16(acc[t][j][i]);
+                    }
+                }
+            }
+        }
+        if (A.logits_f32) {
+            if (full && (N & 3u) == 0) {
+                constexpr uint32_t LPR = 4 * NJ, RPR = 64 / LPR;
+#pragma unroll
+                for (uint32_t t = 0; t < (uint32_t)TT; t++) {
+#pragma unroll
+                    for (uint32_t j = 0; j < (uint32_t)NJ; j++)
+                        asm volatile("ds_write_b128 %0, %1" : : "v"(sbase + rr * L::F32_STRIDE + (j * 16 + 4 * g) * 4), "v"(acc[t][j]) : "memory");
+                    v4i r[16 / RPR];
+                    const uint32_t ra = sbase + (lane / LPR) * L::F32_STRIDE + (lane % LPR) * 16;
+                    static_for<16 / RPR>([&](auto hi) __attribute__((always_inline)) {
+                        constexpr uint32_t h = decltype(hi)::value;
+                        r[h] = lds_rd128<h * RPR * L::F32_STRIDE>(ra);
+                    });
+                    lds_drain();
+                    const uint32_t col = nw0 + (lane % LPR) * 4;
+#pragma unroll
+                    for (uint32_t h = 0; h < 16 / RPR; h++) {
+                        asm volatile("" : "+v"(r[h]));
+                        const uint32_t tk = t0 + wm * 16 * TT + t * 16 + h * RPR + lane / LPR;
+                        if (tk < M) *reinterpret_cast<v4i*>(A.logits_f32 + (uint64_t)tk * N + col) = r[h];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t t = 0; t < (uint32_t)TT; t++) {
+                    const uint32_t tok = t0 + wm * 16 * TT + t * 16 + rr;
+                    if (tok >= M) continue;
+#pragma unroll
+                    for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                        const uint32_t n = nw0 + j * 16 + 4 * g;
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (n + i < N) A.logits_f32[(uint64_t)tok * N + n + i] = acc[t][j][i];
+                    }
+                }
+            }
+        }
+        if (A.part_val) {
+            lds_drain();
+            __builtin_amdgcn_s_barrier();    // the exchange is complete
+            // waves wn == 0: the best of the WN entries of each token
+            if (wn == 0 && lane < 16 * TT) {
+                const uint32_t tl = wm * 16 * TT + lane, tok = t0 + tl;
+                float bv = -INFINITY;
+                uint32_t bi = 0xffffffffu;
+#pragma unroll
+                for (uint32_t w2 = 0; w2 < (uint32_t)WN; w2++) {
+                    v2i o;
+                    asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(o) : "v"(ring + L::SWB + (w2 * TM + tl) * 8));
+                    if (better(__uint_as_float((uint32_t)o.x), (uint32_t)o.y, bv, bi)) {
+                        bv = __uint_as_float((uint32_t)o.x);
+                        bi = (uint32_t)o.y;
+                    }
+                }
+                if (tok < M) {
+                    A.part_val[(uint64_t)tok * A.nvt + vt] = bv;
+                    A.part_idx[(uint64_t)tok * A.nvt + vt] = bi;
+                }
+            }
+        }
+    };
+
+    // ---- pipeline ----------------------------------------------------------------
+    // Chunk s of the block's sequence sits in stage s % NS.  Before
+    // contracting chunk s, the copies of chunks s + 1 .. s + NS - 2 may still
+    // be in flight: CB copies each, plus one at an item's first chunk for
+    // waves below XW.
+    const uint32_t total = n_my * nblk;
+    setup_issue();
+    for (uint32_t k = 0; k + 1 < (uint32_t)NS; k++) issue_next(k);
+    uint32_t st = 0;
+    for (uint32_t sidx = 0;; sidx++) {
+        uint32_t x = 0;
+        for (uint32_t k = 1; k + 1 < (uint32_t)NS; k++) {
+            const uint32_t s2 = sidx + k;
+            if (s2 < total) x += L::CB + (wave == 0 ? 1u : 0u) + ((s2 % nblk == 0 && wave < L::XW) ? 1u : 0u);
+        }
+        wait_vm(x);
+        __builtin_amdgcn_s_barrier();
+        // Half the waves issue their copies before contracting, half after:
+        // the copies queue at the texture unit, and a wave waiting to issue
+        // them leaves its SIMD to the other wave, which is contracting.
+        const bool early = wave < NW / 2;
+        if (early) issue_next(st == 0 ? NS - 1 : st - 1);
+        if (c == 0) start_item();
+        const uint32_t stb = __builtin_amdgcn_readfirstlane(st * L::STAGE);
+        if (general) compute(stb, std::true_type{});
+        else compute(stb, std::false_type{});
+        if (!early) issue_next(st == 0 ? NS - 1 : st - 1);
+        if (++c == nblk) {
+            epilogue(st);
+            if (++c_ord == n_my) break;
+            c = 0;
+            c_item += G;
+        }
+        st = st + 1 == (uint32_t)NS ? 0 : st + 1;
+    }
+}
+
+template <int WM, int WN, int TT, int NJ, int NS>
+__global__ __launch_bounds__(64 * WM * WN, 1) void fp8_head_gemm_kernel(HeadGemmArgs A) {
+    fp8_head_gemm_body<WM, WN, TT, NJ, NS>(A);
+}
+
+// Activation quantization for the tiled form (tied_output_projection_batch_
+// fp8_e4m3.comp.template:94-120: per 128-column block s = amax > 0 ?
+// amax / 448 : 1, q = e4m3(x / s)), written chunk-major for the GEMM's
+// contiguous copies: q[chunk][row][128 B] with 16-byte piece p of row r at
+// piece p ^ f(r), s[chunk][row]; rows M .. Mpad are zeros.  One 32-lane
+// cluster per (row, chunk), 4 columns per lane.
+__global__ __launch_bounds__(256) void head_quant_kernel(const uint16_t* __restrict__ x, uint32_t M, uint32_t Mpad,
+                                                         uint32_t K, uint8_t* __restrict__ q, float* __restrict__ s) {
+    const uint32_t nblk = (K + 127) / 128;
+    const uint32_t unit = blockIdx.x * 8 + (threadIdx.x >> 5), cl = threadIdx.x & 31;
+    const uint32_t row = unit / nblk, blk = unit % nblk;
+    if (row >= Mpad) return;                     // uniform per cluster
+    const uint32_t col = blk * 128 + cl * 4;
+    const bool valid = row < M && col < K;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(x + (uint64_t)row * K + col);
+        const uint32_t w0 = p[0], w1 = p[1];
+        v[0] = bf16_to_f32(w0); v[1] = bf16_to_f32(w0 >> 16);
+        v[2] = bf16_to_f32(w1); v[3] = bf16_to_f32(w1 >> 16);
+    }
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = wave_max32(m);
+    const float sc = amax_fp8_scale(m);
+    uint32_t packed = 0;
+    if (valid)
+        packed = f32_to_e4m3(v[0] / sc) | (f32_to_e4m3(v[1] / sc) << 8) | (f32_to_e4m3(v[2] / sc) << 16) |
+                 (f32_to_e4m3(v[3] / sc) << 24);
+    const uint32_t piece = (cl >> 2) ^ hg_swz(row), within = (cl & 3u) * 4;
+    *reinterpret_cast<uint32_t*>(q + ((uint64_t)blk * Mpad + row) * 128 + piece * 16 + within) = packed;
+    if (cl == 0) s[(uint64_t)blk * Mpad + row] = row < M ? sc : 0.0f;
+}
+
+// Per vocabulary row: its first-block scale as f32 and whether its scale
+// varies across the K blocks (rows of the last tile past N: flag 0).  A block
+// covers 256 rows; their scale rows are one contiguous span, read coalesced
+// into LDS and checked there (nblk <= 32).
+__global__ __launch_bounds__(256) void head_scale_scan_kernel(const uint16_t* __restrict__ scale_inv, uint32_t N,
+                                                              uint32_t rows_pad, uint32_t BR, uint32_t nblk,
+                                                              float* __restrict__ sw_row, uint8_t* __restrict__ nonuni) {
+    __shared__ uint16_t sh[256 * 32];
+    const uint32_t n0 = blockIdx.x * 256, tid = threadIdx.x;
+    if (n0 >= N) {
+        if (n0 + tid < rows_pad) nonuni[n0 + tid] = 0;
+        return;
+    }
+    const uint32_t last = min(n0 + 255, N - 1);
+    const uint32_t r0 = n0 / BR, r1 = last / BR;
+    const uint32_t elems = (r1 - r0 + 1) * nblk;           // <= 256 * 32
+    const uint16_t* src = scale_inv + (uint64_t)r0 * nblk;
+    for (uint32_t e = tid; e < elems; e += 256) sh[e] = src[e];
+    __syncthreads();
+    const uint32_t n = n0 + tid;
+    if (n >= rows_pad) return;
+    if (n >= N) {
+        nonuni[n] = 0;
+        return;
+    }
+    const uint16_t* row = sh + (n / BR - r0) * nblk;
+    const uint32_t s0 = row[0];
+    uint32_t diff = 0;
+    for (uint32_t c = 1; c < nblk; c++) diff |= row[c] ^ s0;
+    sw_row[n] = bf16_to_f32(s0);
+    nonuni[n] = diff ? 1 : 0;
+}
+
 // Second pass: one block per row over the partials (argmax_candidate_reduce.
 // comp.template:10-37).
 __global__ __launch_bounds__(256) void argmax_partials_kernel(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
@@ -544,6 +1163,34 @@ __global__ __launch_bounds__(1024) void argmax_f32_kernel(const float* __restric
     if (lane == 0) out[row] = si[0];
 }
 
+template <int WM, int WN, int TT, int NJ, int NS>
+nerve_hip_status launch_head_gemm_t(const HeadGemmArgs& G, uint32_t grid, hipStream_t st) {
+    constexpr uint32_t lds = HgLayout<WM, WN, TT, NJ, NS>::BYTES;
+    static_assert(lds <= 160 * 1024, "LDS");
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)fp8_head_gemm_kernel<WM, WN, TT, NJ, NS>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+            return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for fp8_head_gemm_kernel");
+        attr_set = true;
+    }
+    fp8_head_gemm_kernel<WM, WN, TT, NJ, NS><<<grid, 64 * WM * WN, lds, st>>>(G);
+    return nh::check_launch("fp8_head_gemm_kernel");
+}
+
+// Tiled-form configurations: token tiles of 64 / 128 / 256 rows, 128
+// vocabulary rows per tile, 8 waves.
+struct HgConfig {
+    uint32_t tm, tn, ns;
+};
+constexpr HgConfig kHgConfigs[3] = {{64, 128, 5}, {128, 128, 4}, {256, 128, 3}};
+
+nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid, hipStream_t st) {
+    if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 2, 5>(G, grid, st);
+    if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4>(G, grid, st);
+    return launch_head_gemm_t<4, 2, 4, 4, 3>(G, grid, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -584,12 +1231,25 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
                              ((uintptr_t)scale_inv_bf16 & 3) == 0 && hs.lw <= HS_LWMAX &&
                              hs_nbuf * (size_t)hs.slot_bytes + hs_red <= 160 * 1024 && hs.cpi * hs_nbuf <= 63;
     const uint32_t hs_grid = (uint32_t)ctx->cu_count;
-    const uint32_t nparts = stream_form ? hs_grid : skinny ? sk_grid : nblocks;
+    // Tiled GEMM form (M > 16): token tiles of 64 / 128 / 256 rows, 128
+    // vocabulary rows per tile; K <= 4096 (the general form's scale block
+    // fits its LDS region) with at least NS chunks.
+    const int hg_cfg = M <= 64 ? 0 : M <= 128 ? 1 : 2;
+    const uint32_t hg_tm = kHgConfigs[hg_cfg].tm, hg_ns = kHgConfigs[hg_cfg].ns, hg_tn = kHgConfigs[hg_cfg].tn;
+    const bool gemm_form = !skinny && K <= 4096 && K % 32 == 0 && nblk >= hg_ns;
+    const uint32_t hg_nvt = (N + hg_tn - 1) / hg_tn, hg_ntt = (M + hg_tm - 1) / hg_tm;
+    const uint32_t hg_items = hg_nvt * hg_ntt;
+    const uint32_t hg_grid = std::min<uint32_t>(hg_items, (uint32_t)ctx->cu_count);
+    const uint32_t nparts = stream_form ? hs_grid : skinny ? sk_grid : gemm_form ? hg_nvt : nblocks;
     nh::Carver cv;
-    size_t o_q = cv.take<uint8_t>((size_t)M * K);
-    size_t o_s = cv.take<float>((size_t)M * nblk);
+    // The GEMM form reads whole token tiles: rows up to the padded count.
+    const size_t m_rows = gemm_form ? (size_t)hg_ntt * hg_tm : M;
+    size_t o_q = cv.take<uint8_t>(gemm_form ? m_rows * nblk * 128 : m_rows * K);   // chunk-major pads K to 128
+    size_t o_s = cv.take<float>(m_rows * nblk);
     size_t o_pv = cv.take<float>(argmax_u32 ? (size_t)M * nparts : 0);
     size_t o_pi = cv.take<uint32_t>(argmax_u32 ? (size_t)M * nparts : 0);
+    size_t o_swr = cv.take<float>(gemm_form ? (size_t)N : 0);
+    size_t o_nu = cv.take<uint8_t>(gemm_form ? (size_t)hg_nvt * hg_tn : 0);
     void* ws = nullptr;
     if ((st = nh::workspace(ctx, cv.offset, &ws))) return st;
     uint8_t* base = static_cast<uint8_t*>(ws);
@@ -597,9 +1257,16 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
     HeadArgs A;
     A.xq = base + o_q;
     A.xs = reinterpret_cast<float*>(base + o_s);
-    if ((st = nh::quantize_rows(static_cast<const uint16_t*>(x_bf16), K, M, false, const_cast<uint8_t*>(A.xq),
-                                const_cast<float*>(A.xs), strm)))
+    if (gemm_form) {
+        // chunk-major, swizzled token rows padded to whole tiles
+        const uint32_t mpad = hg_ntt * hg_tm;
+        head_quant_kernel<<<(uint32_t)(((uint64_t)mpad * nblk + 7) / 8), 256, 0, strm>>>(
+            static_cast<const uint16_t*>(x_bf16), M, mpad, K, const_cast<uint8_t*>(A.xq), const_cast<float*>(A.xs));
+        if ((st = nh::check_launch("head_quant"))) return st;
+    } else if ((st = nh::quantize_rows(static_cast<const uint16_t*>(x_bf16), K, M, false, const_cast<uint8_t*>(A.xq),
+                                       const_cast<float*>(A.xs), strm))) {
         return st;
+    }
     A.W = static_cast<const uint8_t*>(weight_e4m3);
     A.scale_inv = static_cast<const uint16_t*>(scale_inv_bf16);
     A.M = M;
@@ -635,6 +1302,34 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
         else if (per <= 4) fp8_head_skinny_kernel<4><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
         else if (per <= 6) fp8_head_skinny_kernel<6><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
         else fp8_head_skinny_kernel<8><<<grid, 64 * SK_WAVES, lds, strm>>>(A, groups);
+    } else if (gemm_form) {
+        HeadGemmArgs G;
+        G.xq = A.xq;
+        G.xs = A.xs;
+        G.W = A.W;
+        G.scale_inv = A.scale_inv;
+        G.sw_row = reinterpret_cast<const float*>(base + o_swr);
+        G.nonuni = base + o_nu;
+        G.M = M;
+        G.Mpad = hg_ntt * hg_tm;
+        G.K = K;
+        G.N = N;
+        G.BR = s.block_rows;
+        G.nblk = nblk;
+        G.ntt = hg_ntt;
+        G.n_items = hg_items;
+        G.nvt = hg_nvt;
+        G.out_scale = s.output_scale;
+        G.logits_f32 = A.logits_f32;
+        G.logits_bf16 = A.logits_bf16;
+        G.part_val = A.part_val;
+        G.part_idx = A.part_idx;
+        A.nblocks = hg_nvt;
+        const uint32_t rows_pad = hg_nvt * hg_tn;
+        head_scale_scan_kernel<<<(rows_pad + 255) / 256, 256, 0, strm>>>(
+            A.scale_inv, N, rows_pad, s.block_rows, nblk, reinterpret_cast<float*>(base + o_swr), base + o_nu);
+        if ((st = nh::check_launch("head_scale_scan"))) return st;
+        if ((st = launch_head_gemm(hg_cfg, G, hg_grid, strm))) return st;
     } else {
         dim3 grid(nblocks, (M + 16 * HEAD_MT - 1) / (16 * HEAD_MT));
         fp8_head_kernel<<<grid, 64 * HEAD_WAVES, 0, strm>>>(A);

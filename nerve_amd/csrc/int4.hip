@@ -697,6 +697,12 @@ extern "C" nerve_hip_status nerve_hip_silu_multiply_quantize_int8_pairpacked(ner
     if ((((uintptr_t)gate_bf16) | ((uintptr_t)up_bf16) | ((uintptr_t)y_bf16)) & 15 || ((uintptr_t)q_i8 & 7))
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "gate, up and y must be 16-byte and q 8-byte aligned");
     if (rows == 0) return nh::ok();
+    // The kernel reads gate and up through restrict pointers while it writes
+    // y: y may not overlap either input.
+    const uintptr_t bytes = (uintptr_t)rows * qs.elements * 2, yb = (uintptr_t)y_bf16;
+    auto overlaps = [&](const void* p) { const uintptr_t a = (uintptr_t)p; return a < yb + bytes && yb < a + bytes; };
+    if (overlaps(gate_bf16) || overlaps(up_bf16))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "y must not overlap gate or up");
     const uint64_t octs = (uint64_t)rows * qs.elements / 8;
     quant_i8pp_kernel<true><<<(uint32_t)((octs + 255) / 256), 256, 0, (hipStream_t)stream>>>(
         static_cast<const uint16_t*>(gate_bf16), static_cast<const uint16_t*>(up_bf16), static_cast<uint16_t*>(y_bf16),

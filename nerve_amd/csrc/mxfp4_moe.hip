@@ -2265,7 +2265,8 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (wave != 0) {
+    const bool preq = A.aq != nullptr;   // wave-uniform: prequantized e4m3 rows + pow2 block scales
+    if (wave != 0 && !preq) {
         const uint16_t* xr = A.x16 + (uint64_t)(row_ok ? rr : 0u) * A.x_frame;
 #pragma unroll
         for (uint32_t q = 0; q < CH; q++) {
@@ -2275,6 +2276,20 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
                 const uint32_t off = (c0 + q) * 128 + g * 16 + (h >= 2 ? 64u : 0u) + (h & 1 ? 8u : 0u);
                 xb[q][h] = gload16_untracked(xr + (piece_ok(q, h) ? off : 0u));
             }
+        }
+    } else if (wave != 0) {
+        // Prequantized hidden rows (PREQUANTIZED_INPUT): the operand pieces
+        // are the e4m3 bytes k = 16 g.. and 64 + 16 g.. of the chunk, the
+        // scale is the row's f32 block scale (its exponent is the e8m0).
+        const uint8_t* xr = A.aq + (uint64_t)(row_ok ? rr : 0u) * K;
+        const float* sr = A.as + (uint64_t)(row_ok ? rr : 0u) * nch;
+#pragma unroll
+        for (uint32_t q = 0; q < CH; q++) {
+            if (c0 + q >= c1) continue;
+            const uint32_t off = (c0 + q) * 128 + g * 16;
+            xb[q][0] = gload16_untracked(xr + (piece_ok(q, 0) ? off : 0u));
+            xb[q][1] = gload16_untracked(xr + (piece_ok(q, 2) ? off + 64u : 0u));
+            xb[q][2].x = (int)gload4_untracked(sr + c0 + q);
         }
     }
     v8i av[CH];
@@ -2434,6 +2449,14 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
             if (c0 + q >= c1) {
                 av[q] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
                 sa[q] = 127u;
+                continue;
+            }
+            if (preq) {
+                asm volatile("" : "+v"(xb[q][0]), "+v"(xb[q][1]), "+v"(xb[q][2]));
+                const v4i lo = piece_ok(q, 0) ? xb[q][0] : v4i{0, 0, 0, 0};
+                const v4i hi = piece_ok(q, 2) ? xb[q][1] : v4i{0, 0, 0, 0};
+                av[q] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                sa[q] = row_ok ? pow2_to_e8m0(__int_as_float(xb[q][2].x)) : 127u;
                 continue;
             }
 #pragma unroll
@@ -2629,18 +2652,6 @@ __device__ __forceinline__ uint32_t pg_swz_a(uint32_t t) { return (t & 7u) ^ ((t
 __device__ __forceinline__ uint32_t pg_swz_b(uint32_t r) { return (r ^ (r >> 2)) & 3u; }
 
 template <uint32_t OFF>
-__device__ __forceinline__ v4i lds_rd128(uint32_t a) {
-    v4i r;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
-    return r;
-}
-template <uint32_t OFF>
-__device__ __forceinline__ uint32_t lds_rd32(uint32_t a) {
-    uint32_t r;
-    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
-    return r;
-}
-template <uint32_t OFF>
 __device__ __forceinline__ uint32_t lds_rd8(uint32_t a) {
     uint32_t r;
     asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
@@ -2650,15 +2661,6 @@ __device__ __forceinline__ uint32_t lds_rd8(uint32_t a) {
 template <int NMAT>
 __host__ __device__ constexpr uint32_t pg_jrow(uint32_t j) { return NMAT == 2 ? (j >> 1) * 128 + (j & 1) * 16 : j * 16; }
 
-template <typename F, uint32_t... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<uint32_t, I...>) {
-    (f(std::integral_constant<uint32_t, I>{}), ...);
-}
-// f(integral_constant<0>), ..., f(integral_constant<N-1>).
-template <uint32_t N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<uint32_t, N>{});
-}
 
 // LDS dword read that waits for itself inside the same asm statement, so
 // no use of the result can be scheduled ahead of the wait.
@@ -2669,7 +2671,6 @@ __device__ __forceinline__ uint32_t lds_rd32_sync(uint32_t a) {
     return r;
 }
 
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)(lds_u8*)p; }
 
 // Issue-side state of the item whose chunks are being copied.
 struct PgIssue {
@@ -3212,7 +3213,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     ta.a_row_div = gate_up ? k : 1;
     // Decode-shaped batches: one streaming launch that builds its own tiles
     // and quantizes its own activation chunks (no preparation launch).
-    if (!banks && !grouped && !(gate_up && ms.prequant)) {
+    if (!banks && !grouped) {
         StreamArgs fa{};
         fa.K = K;
         fa.N = N;
@@ -3227,8 +3228,16 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
             fa.x_frame = H;
             fa.x_seg = 0;
             fa.out16 = static_cast<uint16_t*>(intermediates);
-            st = launch_tokens<3, 8>(fa, ctx, stream);
-            if (st == NERVE_HIP_UNSUPPORTED) st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1, true>(fa, ctx, stream);
+            if (ms.prequant) {
+                // Only the token form reads prequantized rows in its fused
+                // set-up; other decode shapes take the preparation launch.
+                fa.aq = static_cast<const uint8_t*>(pre_q);
+                fa.as = static_cast<const float*>(pre_s);
+                st = launch_tokens<3, 8>(fa, ctx, stream);
+            } else {
+                st = launch_tokens<3, 8>(fa, ctx, stream);
+                if (st == NERVE_HIP_UNSUPPORTED) st = launch_stream<SPAN_GATE_UP, 2, 3, 8, 1, true>(fa, ctx, stream);
+            }
         } else {
             fa.x16 = frames16;
             fa.x_frame = frame_words * 2;
@@ -3394,6 +3403,7 @@ nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spe
         (ms.prequant && !hidden_scales))
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (ms.prequant && ((uintptr_t)hidden & 15)) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "prequantized hidden must be 16-byte aligned");
+    if (ms.prequant && ((uintptr_t)hidden_scales & 3)) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "hidden scales must be 4-byte aligned");
     return moe_common(ctx, ms, true, hidden, hidden, hidden_scales, routes_u32, intermediates, nullptr, addresses_u32,
                       address_records, param_slots_u32, param_slot_words, control_u32, batch_width,
                       (hipStream_t)stream);

@@ -71,7 +71,7 @@ def test_int4_gptq_group_lengths(ctx, dev, G, N, M):
     assert ok and exact > 0.9, (worst, exact)
 
 
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 4, 16])
 def test_int4_config1_full_size(ctx, dev, M):
     d = wl.config1(M=M)
     K, N, G = d["K"], d["N"], d["group"]
@@ -139,9 +139,14 @@ def _argmax_ok(ids, ref_logits, tol):
 # M <= 16 with per-row scales takes the LDS-ring stream kernel (two ring
 # slots at K = 4096, a partial last 16-row group at N % 16 != 0, fewer groups
 # than blocks at small N); an odd N * nblk falls back to the register form;
-# M > 16 takes the tiled kernel.
+# M > 16 takes the LDS-staged GEMM (token tiles of 64 / 128 / 256 rows;
+# partial token and vocabulary tiles, N % 4 != 0, the 64-column K tail,
+# K = 4096) or, with fewer K chunks than its ring has stages, the register
+# form.
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (7, 4096, 2880), (64, 2048, 512), (130, 600, 384),
-                                   (16, 2000, 4096), (2, 777, 64), (5, 1001, 384), (3, 30010, 2880)])
+                                   (16, 2000, 4096), (2, 777, 64), (5, 1001, 384), (3, 30010, 2880),
+                                   (20, 1000, 2880), (64, 4099, 640), (100, 777, 1024), (128, 3000, 2880),
+                                   (300, 1300, 640), (257, 2051, 4096), (512, 5000, 2880)])
 def test_fp8_head_parity(ctx, dev, M, N, K):
     rng = np.random.default_rng(M * N + K)
     d = wl.fp8_head(rng, N, K, M)
@@ -157,13 +162,17 @@ def test_fp8_head_parity(ctx, dev, M, N, K):
     assert _argmax_ok(am, ref, 2e-3 * np.max(np.abs(ref)))
 
 
-def test_fp8_head_block_rows_and_output_scale(ctx, dev):
-    M, N, K, BR = 3, 1024, 640, 128
+# M = 3: the register form; M = 50 / 200: the GEMM's general form (scales
+# that vary along K, staged per tile), with one tile of uniform rows.
+@pytest.mark.parametrize("M", [3, 50, 200])
+def test_fp8_head_block_rows_and_output_scale(ctx, dev, M):
+    N, K, BR = 1024, 640, 128
     rng = np.random.default_rng(5)
     d = wl.fp8_head(rng, N, K, M)
     nblk = K // 128
     grid = wl.bf16_normal(rng, ((N + BR - 1) // BR, nblk), 0.001)
     grid = wl.f32_to_bf16_bits(np.abs(wl.bf16_bits_to_f32(grid)) + np.float32(1e-4))
+    grid[2, :] = grid[2, 0]          # rows 256..383 (one GEMM tile): one scale along K
     d["scale_inv"] = grid
     spec = f"tied_output_projection_batch4_fp8_e4m3_b{BR}x128_{N}x{K}_scale0.5_to_f32.comp"
     lf, _, am = _head(ctx, dev, d, spec, want_bf16=False)

@@ -39,7 +39,7 @@ def test_quantize_int8_pairpacked_bit_exact(ctx, dev, B, K):
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 4096, 14336, 128), (4, 1024, 512, 32), (16, 512, 96, 256)])
-@pytest.mark.parametrize("finalize", [0, 2])
+@pytest.mark.parametrize("finalize", [0, 1, 2])
 @pytest.mark.parametrize("bf16_scales", [False, True])
 def test_int4_linear_pairpacked(ctx, dev, M, K, N, G, finalize, bf16_scales):
     import torch
@@ -50,7 +50,7 @@ def test_int4_linear_pairpacked(ctx, dev, M, K, N, G, finalize, bf16_scales):
     if bf16_scales:
         sc = wl.f32_to_bf16_bits(d["scales"].astype(np.float32))
     x = wl.bf16_normal(rng, (M, K))
-    aux = wl.bf16_normal(rng, (M, N)) if finalize == 2 else None
+    aux = wl.bf16_normal(rng, (M, N)) if finalize == 2 else wl.bf16_normal(rng, (N,)) if finalize == 1 else None
     q, s, sums = _quant(ctx, dev, x)
     y = torch.zeros(M, N, dtype=torch.int16, device=dev)
     op = ["linear", "linear_bias", "linear_residual"][finalize]
@@ -86,3 +86,23 @@ def test_silu_multiply_quantize_int8_pairpacked(ctx, dev, B, N):
     assert np.array_equal(to_np(q, np.uint8), qr)
     assert np.array_equal(to_np(s, np.float32), sr)
     assert np.array_equal(to_np(sums, np.int32), sumr)
+
+
+def test_silu_multiply_quantize_rejects_aliased_output(ctx, dev):
+    """y written over gate or up is refused on the host (the kernel reads its
+    inputs through restrict pointers)."""
+    import torch
+
+    from nerve_amd.hip import NerveHipError
+
+    B, N = 2, 256
+    rng = np.random.default_rng(11)
+    gd = to_dev(wl.bf16_normal(rng, (B, N)), dev)
+    ud = to_dev(wl.bf16_normal(rng, (B, N)), dev)
+    q = torch.zeros(B, N, dtype=torch.uint8, device=dev)
+    s = torch.zeros(B, N // 32, dtype=torch.float32, device=dev)
+    sums = torch.zeros(B, N // 32, dtype=torch.int32, device=dev)
+    spec = f"silu_multiply_quantize_batch{B}_int8_pairpacked_b32_h{N}.comp"
+    for y in (gd, ud, gd[1:]):
+        with pytest.raises(NerveHipError):
+            ctx.silu_multiply_quantize_int8_pairpacked(spec, gd, ud, y, q, s, sums, B)

@@ -349,6 +349,23 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
                                                  void* logits_bf16, void* argmax_u32,
                                                  uint32_t batch_width, void* stream);
 
+/* No counterpart in the reference: the FP8 output projection of
+ * nerve_hip_fp8_output_projection (same arguments, same results, same
+ * kernels) for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * scratch (quantized activations, per-row scale flags, argmax partials) is a
+ * file-scope device array of 4 MiB per GPU, resolved once per device by
+ * nerve_hip_open; it calls no hipMalloc/hipFree.  A call whose scratch would
+ * exceed 4 MiB returns NERVE_HIP_INVALID_ARGUMENT without launching (e.g.
+ * N = 201088, K = 2880 fits up to M = 128).  Calls on one GPU share the array:
+ * two that overlap (other streams, other contexts on the same device) race;
+ * nothing is kept between calls. */
+nerve_hip_status nerve_hip_fp8_output_projection_noalloc(nerve_hip_ctx* ctx, const char* spec,
+                                                         const void* x_bf16, const void* weight_e4m3,
+                                                         const void* scale_inv_bf16, void* logits_f32,
+                                                         void* logits_bf16, void* argmax_u32,
+                                                         uint32_t batch_width, void* stream);
+
 /* Standalone greedy argmax over f32 logits [B, N] (greedy_sampler_f32.comp.
  * template:25-109 without its stream-control bookkeeping). */
 nerve_hip_status nerve_hip_argmax_f32(nerve_hip_ctx* ctx, const void* logits_f32,

@@ -83,9 +83,13 @@ struct nerve_hip_ctx {
     int cu_count;
     void* workspace;
     size_t workspace_bytes;
+    void* static_scratch;         // device address of this device's static scratch array
 };
 
 namespace nh {
+
+// Size of the file-scope device array behind the no-allocation entry point.
+constexpr size_t kStaticScratchBytes = 4u << 20;
 
 nerve_hip_status fail(nerve_hip_status code, const std::string& msg);
 nerve_hip_status ok();

@@ -12,6 +12,12 @@ namespace {
 thread_local std::string g_last_error;
 }
 
+// Scratch of nerve_hip_fp8_output_projection_noalloc: every device holds its
+// own copy of this array until the process ends.  In host code the name is
+// only a stand-in; nerve_hip_open resolves each device's copy to a device
+// address with hipGetSymbolAddress, and only that address is ever used.
+static __device__ __align__(256) uint8_t scratch[nh::kStaticScratchBytes];
+
 namespace nh {
 
 nerve_hip_status fail(nerve_hip_status code, const std::string& msg) {
@@ -353,11 +359,20 @@ nerve_hip_status nerve_hip_open(int device_ordinal, nerve_hip_ctx** out) {
     if (e != hipSuccess) return nh::fail(NERVE_HIP_DEVICE_ERROR, std::string("hipGetDeviceProperties: ") + hipGetErrorString(e));
     if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
         return nh::fail(NERVE_HIP_UNSUPPORTED, std::string("libnerve_hip is built for gfx950, device is ") + prop.gcnArchName);
+    // The no-allocation entry point's scratch: this device's copy of the
+    // array, resolved with the device current (once per context).
+    e = hipSetDevice(device_ordinal);
+    if (e != hipSuccess) return nh::fail(NERVE_HIP_DEVICE_ERROR, std::string("hipSetDevice: ") + hipGetErrorString(e));
+    void* scratch_ptr = nullptr;
+    e = hipGetSymbolAddress(&scratch_ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !scratch_ptr)
+        return nh::fail(NERVE_HIP_DEVICE_ERROR, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
     nerve_hip_ctx* ctx = new nerve_hip_ctx();
     ctx->device = device_ordinal;
     ctx->cu_count = prop.multiProcessorCount;
     ctx->workspace = nullptr;
     ctx->workspace_bytes = 0;
+    ctx->static_scratch = scratch_ptr;
     *out = ctx;
     return NERVE_HIP_OK;
 }

@@ -1195,10 +1195,15 @@ nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid,
 
 extern "C" {
 
-nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
-                                                 const void* weight_e4m3, const void* scale_inv_bf16, void* logits_f32,
-                                                 void* logits_bf16, void* argmax_u32, uint32_t batch_width,
-                                                 void* stream) {
+}  // extern "C"
+
+namespace {
+// The projection with its scratch either from the context workspace
+// (fixed == nullptr; may grow it with hipMalloc) or from `fixed`, a buffer of
+// `fixed_bytes` that is never resized (calls needing more are refused).
+nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16, const void* weight_e4m3,
+                                const void* scale_inv_bf16, void* logits_f32, void* logits_bf16, void* argmax_u32,
+                                uint32_t batch_width, void* stream, void* fixed, size_t fixed_bytes) {
     nerve_hip_status st = nh::enter(ctx);
     if (st) return st;
     nh::Fp8HeadSpec s;
@@ -1250,8 +1255,15 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
     size_t o_pi = cv.take<uint32_t>(argmax_u32 ? (size_t)M * nparts : 0);
     size_t o_swr = cv.take<float>(gemm_form ? (size_t)N : 0);
     size_t o_nu = cv.take<uint8_t>(gemm_form ? (size_t)hg_nvt * hg_tn : 0);
-    void* ws = nullptr;
-    if ((st = nh::workspace(ctx, cv.offset, &ws))) return st;
+    void* ws = fixed;
+    if (fixed) {
+        if (cv.offset > fixed_bytes)
+            return nh::fail(NERVE_HIP_INVALID_ARGUMENT,
+                            "FP8 projection needs " + std::to_string(cv.offset) + " bytes of scratch; the static scratch holds " +
+                                std::to_string(fixed_bytes));
+    } else if ((st = nh::workspace(ctx, cv.offset, &ws))) {
+        return st;
+    }
     uint8_t* base = static_cast<uint8_t*>(ws);
     hipStream_t strm = (hipStream_t)stream;
     HeadArgs A;
@@ -1340,6 +1352,28 @@ nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char*
         return nh::check_launch("fp8_output_projection_argmax");
     }
     return nh::ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+nerve_hip_status nerve_hip_fp8_output_projection(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
+                                                 const void* weight_e4m3, const void* scale_inv_bf16, void* logits_f32,
+                                                 void* logits_bf16, void* argmax_u32, uint32_t batch_width,
+                                                 void* stream) {
+    return fp8_projection(ctx, spec, x_bf16, weight_e4m3, scale_inv_bf16, logits_f32, logits_bf16, argmax_u32,
+                          batch_width, stream, nullptr, 0);
+}
+
+nerve_hip_status nerve_hip_fp8_output_projection_noalloc(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
+                                                         const void* weight_e4m3, const void* scale_inv_bf16,
+                                                         void* logits_f32, void* logits_bf16, void* argmax_u32,
+                                                         uint32_t batch_width, void* stream) {
+    if (!ctx) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null nerve_hip_ctx");
+    if (!ctx->static_scratch) return nh::fail(NERVE_HIP_DEVICE_ERROR, "the static scratch of this device was not resolved");
+    return fp8_projection(ctx, spec, x_bf16, weight_e4m3, scale_inv_bf16, logits_f32, logits_bf16, argmax_u32,
+                          batch_width, stream, ctx->static_scratch, nh::kStaticScratchBytes);
 }
 
 nerve_hip_status nerve_hip_argmax_f32(nerve_hip_ctx* ctx, const void* logits_f32, uint32_t batch_width, uint32_t vocab,

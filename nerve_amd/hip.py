@@ -37,6 +37,7 @@ EXPORTS = (
     "nerve_hip_silu_multiply_quantize_int8_pairpacked",
     "nerve_hip_int4_linear_pairpacked",
     "nerve_hip_fp8_output_projection",
+    "nerve_hip_fp8_output_projection_noalloc",
     "nerve_hip_argmax_f32",
 )
 
@@ -96,6 +97,7 @@ def _declare(lib) -> None:
         "nerve_hip_silu_multiply_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_int4_linear_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, P, U32, P]),
         "nerve_hip_fp8_output_projection": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
+        "nerve_hip_fp8_output_projection_noalloc": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_argmax_f32": (ctypes.c_int, [P, P, U32, U32, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -279,6 +281,13 @@ class Context:
         _check(self.lib.nerve_hip_fp8_output_projection(self.handle, _spec(spec), ptr(x), ptr(weight), ptr(scale_inv),
                                                         ptr(logits_f32), ptr(logits_bf16), ptr(argmax), batch_width,
                                                         _stream(stream)))
+
+    def fp8_output_projection_noalloc(self, spec, x, weight, scale_inv, logits_f32, logits_bf16, argmax, batch_width,
+                                      stream=None):
+        """The projection with the library's static per-GPU scratch: no device allocation."""
+        _check(self.lib.nerve_hip_fp8_output_projection_noalloc(self.handle, _spec(spec), ptr(x), ptr(weight),
+                                                                ptr(scale_inv), ptr(logits_f32), ptr(logits_bf16),
+                                                                ptr(argmax), batch_width, _stream(stream)))
 
     def argmax_f32(self, logits, batch_width, vocab, out, stream=None):
         _check(self.lib.nerve_hip_argmax_f32(self.handle, ptr(logits), batch_width, vocab, ptr(out), _stream(stream)))

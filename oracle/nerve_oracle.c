@@ -63,7 +63,7 @@ float o_e4m3_to_f32(uint8_t b) {
  * comp.template:103).  The quantizers never feed it |x| > 448 (the scale is
  * chosen so that |x/s| <= 448), so the saturation rule is only reached by the
  * weight producer (nerve/model_package_tensors.py:1044-1075), whose subnormal
- * quirk is restated separately in tests/golden/producers.py. */
+ * quirk is restated separately in nerve_amd/workloads.py (f32_to_e4m3fn_producer). */
 uint8_t o_f32_to_e4m3(float x) {
     uint32_t b = f2u(x);
     uint8_t sign = (uint8_t)((b >> 24) & 0x80u);

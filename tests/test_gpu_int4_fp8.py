@@ -195,3 +195,25 @@ def test_argmax_ties_lower_id(ctx, dev):
     got = to_np(out, np.uint32)
     assert list(got) == [5, 0, V - 2, 123456]
     assert np.array_equal(got, oracle.argmax(lg))
+
+
+@pytest.mark.parametrize("layout", ["gptq", "ct"])
+def test_int4_finalize_rounding_closed_form(ctx, dev, layout):
+    """The GPU finalize forms by closed form: bias rounds once (0x3F81),
+    residual rounds the sum first and ties to even (0x3F80); see the CPU
+    twin in test_oracle_paths.py for the derivation."""
+    K, N, G, M = 128, 16, 128, 2
+    x = np.zeros((M, K), np.uint16)
+    x[:, 0], x[:, 1], x[:, 2] = 0x3F80, 0x3B00, 0x3A80
+    if layout == "gptq":
+        qw = np.full((K // 8, N), 0x99999999, np.uint32)
+        sc = np.full((K // G, N), 0x3C00, np.uint16)
+    else:
+        qw = np.full((N, K // 8), 0x99999999, np.uint32)
+        sc = np.full((N, K // G), 0x3C00, np.uint16)
+    b = np.full((N,), 0x3B80, np.uint16)
+    r = np.full((M, N), 0x3B80, np.uint16)
+    for op, aux, want in (("linear", None, 0x3F80), ("linear_bias", b, 0x3F81), ("linear_residual", r, 0x3F80)):
+        spec = f"{op}_batch16_int4_{layout}_sf16_g{G}_{K}x{N}.comp"
+        y = _run_int4(ctx, dev, spec, x, qw, sc, None, aux, M, N)
+        assert np.all(y == want), (op, y[0, :4])

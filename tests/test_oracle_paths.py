@@ -320,3 +320,32 @@ def test_fp8_head_float64_and_one_hot():
 def test_argmax_tie_rule():
     lg = np.array([[1, 3, 3, 2], [-np.inf, -np.inf, -np.inf, -np.inf], [0, 0, 5, 5]], np.float32)
     assert list(oracle.argmax(lg)) == [1, 0, 2]
+
+
+def test_int4_finalize_rounding_closed_form():
+    """The INT4 finalize forms by closed form
+    (nerve/model_package_shader_selection.py:2504-2525): bias adds to the f32
+    sum and rounds once, y = bf16(b + S); residual rounds the sum first,
+    y = bf16(r + bf16(S)).  With every code 9 (weight 1), scale 1 and
+    x = (1, 2^-9, 2^-10, 0, ...) the sum is exactly S = 1 + 2^-9 + 2^-10, so
+    bf16(S) = 1; with b = r = 2^-8 the single rounding gives 1 + 2^-7
+    (0x3F81) and the double rounding ties to even at 1.0 (0x3F80)."""
+    K, N, G = 128, 16, 128
+    x = np.zeros((1, K), np.uint16)
+    x[0, 0] = 0x3F80                       # 1.0
+    x[0, 1] = 0x3B00                       # 2^-9
+    x[0, 2] = 0x3A80                       # 2^-10
+    qw = np.full((K // 8, N), 0x99999999, np.uint32)
+    sc = np.full((K // G, N), 0x3C00, np.uint16)          # f16 1.0
+    b = np.full((N,), 0x3B80, np.uint16)                  # 2^-8
+    y0 = oracle.int4_linear("gptq", x, qw, sc, G)
+    assert np.all(y0 == 0x3F80)                            # bf16(S) = 1.0
+    y1 = oracle.int4_linear("gptq", x, qw, sc, G, finalize=1, aux=b)
+    assert np.all(y1 == 0x3F81)
+    y2 = oracle.int4_linear("gptq", x, qw, sc, G, finalize=2, aux=np.tile(b, (1, 1)))
+    assert np.all(y2 == 0x3F80)
+    # the CT layout of the same codes gives the same bits
+    qct = np.full((N, K // 8), 0x99999999, np.uint32)
+    sct = np.full((N, K // G), 0x3C00, np.uint16)
+    assert np.array_equal(oracle.int4_linear("ct", x, qct, sct, G, finalize=1, aux=b), y1)
+    assert np.array_equal(oracle.int4_linear("ct", x, qct, sct, G, finalize=2, aux=np.tile(b, (1, 1))), y2)

@@ -291,7 +291,12 @@ nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_out
  * (ct); zeros: NULL for the reference's symmetric code-8 ABI, or (gptq only,
  * an extension outside the reference ABI) AutoGPTQ qzeros u32 [K/G, N/8];
  * aux: bias bf16 [N] (linear_bias) or residual bf16 [B, N] (linear_residual),
- * else NULL; y: bf16 [B, N]. */
+ * else NULL; y: bf16 [B, N].  Also replaces {op}_batch64_cooperative_int4_
+ * {gptq|ct}_s{f16|bf16}_g{G}_{K}x{N}.comp (linear_batch_cooperative_int4.
+ * comp.template:85-233; grammar nerve/model_package_shader_templates.py:
+ * 3148-3215): per group, the bf16 MFMA sum of (code - 8) x, then
+ * fma(group_sum, scale, acc), any batch_width (the CT layout with group % 128
+ * != 0 returns NERVE_HIP_UNSUPPORTED). */
 nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char* spec,
                                        const void* x_bf16, const void* qweight,
                                        const void* scales, const void* zeros,
@@ -306,7 +311,11 @@ nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char* spec,
  * s = amax > 0 ? amax / 127 : 1, q = round(clamp(x / s, -127, 127)) (round
  * half to even), sums = the block's sum of q; columns c..c+7 become the words
  * (q[c], q[c+2], q[c+4], q[c+6]), (q[c+1], q[c+3], q[c+5], q[c+7]).
- * x bf16 [rows, N]; q int8 [rows, N]; scales f32 and sums i32 [rows, N/32]. */
+ * x bf16 [rows, N]; q int8 [rows, N]; scales f32 and sums i32 [rows, N/32].
+ * Also replaces the unpaired quantize[_batch{T}]_int8_symmetric_b32_h{N}.comp
+ * (quantize_int8_symmetric.comp.template:38-58; grammar :1478-1506): the same
+ * codes and scales with q in column order; sums may then be NULL (written
+ * when given). */
 nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16,
                                                    void* q_i8, void* scales_f32, void* sums_i32, uint32_t rows,
                                                    void* stream);
@@ -327,7 +336,13 @@ nerve_hip_status nerve_hip_silu_multiply_quantize_int8_pairpacked(nerve_hip_ctx*
  * sum over groups and 32-column blocks of fma(-8 sums + sum_k q (code),
  * s_x * s_w), with the bias / residual finalize of nerve_hip_int4_linear.
  * q, scales_f32, sums as nerve_hip_quantize_int8_pairpacked writes them;
- * qweight u32 [K/8, N], scales [K/G, N]. */
+ * qweight u32 [K/8, N], scales [K/G, N].
+ * Also replaces the unpaired {linear,linear_bias,linear_residual}_prequant
+ * [_batch{T}]_int4_{gptq,ct}_s{f16,bf16}_g{G}_{K}x{N}.comp
+ * (linear_prequant_int4_gptq.comp.template:65-103, linear_prequant_int4_ct.
+ * comp.template:66-108): q in column order (the unpaired quantizer), sums
+ * unused (NULL), block_dot = sum_k q (code - 8); the CT layout takes qweight
+ * u32 [N, K/8] and scales [N, K/G]. */
 nerve_hip_status nerve_hip_int4_linear_pairpacked(nerve_hip_ctx* ctx, const char* spec, const void* q_i8,
                                                  const void* scales_f32, const void* sums_i32,
                                                  const void* qweight, const void* scales, const void* aux_bf16,

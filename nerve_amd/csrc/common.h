@@ -149,12 +149,14 @@ struct Int4Spec {
     int layout = 0;             // 0 gptq, 1 ct
     int scale_bf16 = 0;
     int input = 0;              // 0 bf16, 1 "_prequant" int8, 2 "_prequant_pairpacked" int8
+    bool cooperative = false;   // "_batch64_cooperative_" (batch-64 tiles of group sums)
     uint32_t group = 0, in = 0, out = 0;
 };
 nerve_hip_status parse_int4_spec(const char* spec, Int4Spec* out);
 
 struct QuantI8Spec {
     int batch_tile = 0;
+    bool paired = true;         // pair-packed byte order (with block sums) vs columns in order
     bool silu = false;          // silu_multiply_quantize_* (two bf16 inputs, bf16 output)
     uint32_t block = 0, elements = 0;
 };

@@ -166,13 +166,32 @@ static nerve_hip_status parse_topk_spec_uncached(const char* spec, TopkSpec* out
     return NERVE_HIP_OK;
 }
 
-// nerve/model_package_shader_templates.py:3219-3276
+// nerve/model_package_shader_templates.py:3219-3276, and the batch-64
+// cooperative form (:3148-3215), which computes the same group sums.
 static nerve_hip_status parse_int4_spec_uncached(const char* spec, Int4Spec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     static const std::regex re(
         "(linear|linear_bias|linear_residual)(_prequant_pairpacked|_prequant)?(?:_batch(\\d+))?_int4_(gptq|ct)_s(f16|bf16)_g(\\d+)_"
         "(\\d+)x(\\d+)\\.comp");
+    static const std::regex coop(
+        "(linear|linear_bias|linear_residual)_batch64_cooperative_int4_(gptq|ct)_s(f16|bf16)_g(\\d+)_(\\d+)x(\\d+)\\.comp");
     std::cmatch m;
+    if (std::regex_match(spec, m, coop)) {
+        Int4Spec s;
+        std::string op = m[1].str();
+        s.op = op == "linear" ? 0 : (op == "linear_bias" ? 1 : 2);
+        s.batch_tile = 64;
+        s.cooperative = true;
+        s.layout = m[2].str() == "gptq" ? 0 : 1;
+        s.scale_bf16 = m[3].str() == "bf16";
+        parse_u32(m[4].str(), &s.group);
+        parse_u32(m[5].str(), &s.in);
+        parse_u32(m[6].str(), &s.out);
+        if (s.group == 0 || s.group % 32 || s.in == 0 || s.in % s.group || s.out == 0 || s.out % 2)
+            return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid cooperative INT4 shape ") + spec);
+        *out = s;
+        return NERVE_HIP_OK;
+    }
     if (!std::regex_match(spec, m, re)) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an INT4 linear kernel: ") + spec);
     Int4Spec s;
     std::string op = m[1].str();
@@ -275,22 +294,26 @@ static nerve_hip_status parse_quant_i8_spec_uncached(const char* spec, QuantI8Sp
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
     // and silu_multiply_quantize[_batch{T}]_int8_pairpacked_b{B}_h{N}
     // (nerve/model_package_shader_templates.py:3376-3380).
+    // and quantize[_batch{T}]_int8_symmetric_b{B}_h{N}, the unpaired form
+    // (nerve/model_package_shader_templates.py:1478-1506).
     static const std::regex re(
-        "(?:quantize(?:_batch(\\d+))?_int8_symmetric|(silu_multiply)_quantize(?:_batch(\\d+))?_int8)_pairpacked_b(\\d+)"
+        "(?:quantize(?:_batch(\\d+))?_int8_symmetric|(silu_multiply)_quantize(?:_batch(\\d+))?_int8)(_pairpacked)?_b(\\d+)"
         "_h(\\d+)\\.comp");
     std::cmatch m;
     if (!std::regex_match(spec, m, re))
-        return fail(NERVE_HIP_INVALID_SPEC, std::string("not a pair-packed INT8 quantizer: ") + spec);
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("not an INT8 activation quantizer: ") + spec);
     QuantI8Spec s;
     uint32_t bt = 0;
     s.silu = m[2].matched;
+    s.paired = m[4].matched;
+    if (s.silu && !s.paired) return fail(NERVE_HIP_INVALID_SPEC, std::string("not an INT8 activation quantizer: ") + spec);
     const int bi = s.silu ? 3 : 1;
     if (m[bi].matched) parse_u32(m[bi].str(), &bt);
     s.batch_tile = (int)bt;
-    parse_u32(m[4].str(), &s.block);
-    parse_u32(m[5].str(), &s.elements);
+    parse_u32(m[5].str(), &s.block);
+    parse_u32(m[6].str(), &s.elements);
     if ((m[bi].matched && bt == 0) || s.block != 32 || s.elements == 0 || s.elements % 32)
-        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid pair-packed INT8 quantizer shape ") + spec);
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid INT8 quantizer shape ") + spec);
     *out = s;
     return NERVE_HIP_OK;
 }
@@ -396,7 +419,7 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
         nh::RmsQuantSpec r;
         return nh::parse_rms_quant_spec(spec, &r);
     }
-    if ((s.rfind("quantize", 0) == 0 && s.find("_int8_symmetric_pairpacked_") != std::string::npos) ||
+    if ((s.rfind("quantize", 0) == 0 && s.find("_int8_symmetric_") != std::string::npos) ||
         s.rfind("silu_multiply_quantize", 0) == 0) {
         nh::QuantI8Spec q;
         return nh::parse_quant_i8_spec(spec, &q);
@@ -409,7 +432,7 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
         nh::Int4Spec i;
         nerve_hip_status st = nh::parse_int4_spec(spec, &i);
         if (st) return st;
-        if (i.input == 1) return nh::fail(NERVE_HIP_UNSUPPORTED, "the unpaired INT8-prequant INT4 input is not built");
+        if (i.input != 0) return NERVE_HIP_OK;   // INT8-prequant inputs: any group of 32k columns, N even
         if (i.layout == 1 && i.group % 128)
             return nh::fail(NERVE_HIP_UNSUPPORTED, "CT INT4 kernel needs group % 128 == 0");
         if (i.layout == 0 && i.out % 16) return nh::fail(NERVE_HIP_UNSUPPORTED, "GPTQ INT4 kernel needs N % 16 == 0");

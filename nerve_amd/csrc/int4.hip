@@ -478,7 +478,7 @@ __global__ __launch_bounds__(64 * KS) void int4_ct_kernel(Int4Args A) {
 // SILU: silu_multiply_quantize_int8_pairpacked.comp.template: the values are
 // y = bf16(bf16(g / (1 + exp(-g))) * u) of the gate (x) and up rows, and y is
 // written out as well.
-template <bool SILU>
+template <bool SILU, bool PAIRED = true>
 __global__ __launch_bounds__(256) void quant_i8pp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ up,
                                                          uint16_t* __restrict__ y, uint32_t rows, uint32_t cols,
                                                          uint32_t* __restrict__ q, float* __restrict__ s,
@@ -521,14 +521,18 @@ __global__ __launch_bounds__(256) void quant_i8pp_kernel(const uint16_t* __restr
     sum += __shfl_xor(sum, 1);
     sum += __shfl_xor(sum, 2);
     if (!ok) return;
-    const uint32_t even = (uint32_t)(iv[0] & 255) | ((uint32_t)(iv[2] & 255) << 8) | ((uint32_t)(iv[4] & 255) << 16) |
-                          ((uint32_t)(iv[6] & 255) << 24);
-    const uint32_t odd = (uint32_t)(iv[1] & 255) | ((uint32_t)(iv[3] & 255) << 8) | ((uint32_t)(iv[5] & 255) << 16) |
-                         ((uint32_t)(iv[7] & 255) << 24);
-    *reinterpret_cast<uint2*>(q + (uint64_t)o * 2) = uint2{even, odd};
+    // pair-packed: (q[c], q[c+2], q[c+4], q[c+6]), (q[c+1], ...); unpaired:
+    // the 8 codes in column order
+    const int a0 = PAIRED ? 0 : 0, a1 = PAIRED ? 2 : 1, a2 = PAIRED ? 4 : 2, a3 = PAIRED ? 6 : 3;
+    const int b0 = PAIRED ? 1 : 4, b1 = PAIRED ? 3 : 5, b2 = PAIRED ? 5 : 6, b3 = PAIRED ? 7 : 7;
+    const uint32_t w0 = (uint32_t)(iv[a0] & 255) | ((uint32_t)(iv[a1] & 255) << 8) | ((uint32_t)(iv[a2] & 255) << 16) |
+                        ((uint32_t)(iv[a3] & 255) << 24);
+    const uint32_t w1 = (uint32_t)(iv[b0] & 255) | ((uint32_t)(iv[b1] & 255) << 8) | ((uint32_t)(iv[b2] & 255) << 16) |
+                        ((uint32_t)(iv[b3] & 255) << 24);
+    *reinterpret_cast<uint2*>(q + (uint64_t)o * 2) = uint2{w0, w1};
     if ((o & 3u) == 0) {
         s[o / 4] = sc;
-        sums[o / 4] = sum;
+        if (sums) sums[o / 4] = sum;
     }
 }
 
@@ -548,6 +552,16 @@ struct PpArgs {
     Int4Args L;                 // qweight, scales, aux, y, shapes
 };
 
+// Unpaired input (linear_prequant_int4_{gptq,ct}.comp.template): the int8
+// words hold columns in order, so each packed weight word becomes the signed
+// bytes (code - 8) of nibbles 0..3 and 4..7 for two v_dot4_i32_i8.
+__device__ __forceinline__ int nibbles_to_i8x4(uint32_t t16) {
+    uint32_t b = (t16 & 0xFu) | ((t16 & 0xF0u) << 4) | ((t16 & 0xF00u) << 8) | ((t16 & 0xF000u) << 12);
+    b ^= 0x08080808u;                       // code - 8 as a 4-bit two's complement value
+    return (int)(b | ((b & 0x08080808u) * 0x1Eu));   // sign-extend each byte
+}
+
+template <bool PAIRED, bool CT>
 __global__ __launch_bounds__(256) void int4_pp_kernel(PpArgs P) {
     __shared__ float red[4][64];
     const Int4Args& A = P.L;
@@ -560,15 +574,21 @@ __global__ __launch_bounds__(256) void int4_pp_kernel(PpArgs P) {
         const uint32_t* qt = P.q + (uint64_t)t * (K / 4);
         float acc = 0.0f;
         for (uint32_t g = g0; g < g1; g++) {
-            const float sw = decode_scale(A.scales[(uint64_t)g * N + nc], A.scale_bf16);
+            const float sw = decode_scale(CT ? A.scales[(uint64_t)nc * ngroups + g] : A.scales[(uint64_t)g * N + nc],
+                                          A.scale_bf16);
             for (uint32_t b = g * bpg; b < (g + 1) * bpg; b++) {
-                int dot = -8 * P.sums[(uint64_t)t * nblk + b];
+                int dot = PAIRED ? -8 * P.sums[(uint64_t)t * nblk + b] : 0;
 #pragma unroll
                 for (uint32_t p = 0; p < 4; p++) {
-                    const uint32_t word = A.qw[(uint64_t)(b * 4 + p) * N + nc];
-                    dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2], (int)(word & 0x0f0f0f0fu), dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2 + 1], (int)((word >> 4) & 0x0f0f0f0fu), dot,
-                                                 false);
+                    const uint32_t word = CT ? A.qw[(uint64_t)nc * (K / 8) + b * 4 + p] : A.qw[(uint64_t)(b * 4 + p) * N + nc];
+                    if (PAIRED) {
+                        dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2], (int)(word & 0x0f0f0f0fu), dot, false);
+                        dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2 + 1], (int)((word >> 4) & 0x0f0f0f0fu), dot,
+                                                     false);
+                    } else {
+                        dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2], nibbles_to_i8x4(word & 0xffffu), dot, false);
+                        dot = __builtin_amdgcn_sdot4((int)qt[(b * 4 + p) * 2 + 1], nibbles_to_i8x4(word >> 16), dot, false);
+                    }
                 }
                 acc = fmaf((float)dot, P.s[(uint64_t)t * nblk + b] * sw, acc);
             }
@@ -591,9 +611,7 @@ extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char
     nh::Int4Spec s;
     if ((st = nh::parse_int4_spec(spec, &s))) return st;
     if (s.input != 0)
-        return nh::fail(s.input == 2 ? NERVE_HIP_INVALID_SPEC : NERVE_HIP_UNSUPPORTED,
-                        s.input == 2 ? "pair-packed INT8 input goes through nerve_hip_int4_linear_pairpacked"
-                                     : "the unpaired INT8-prequant INT4 input is not built");
+        return nh::fail(NERVE_HIP_INVALID_SPEC, "INT8-prequantized input goes through nerve_hip_int4_linear_pairpacked");
     if (!x_bf16 || !qweight || !scales || !y_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (s.op != 0 && !aux_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "bias/residual specialization needs aux");
     if (s.batch_tile == 0 && batch_width > 1)
@@ -667,17 +685,24 @@ extern "C" nerve_hip_status nerve_hip_quantize_int8_pairpacked(nerve_hip_ctx* ct
     nh::QuantI8Spec qs;
     if ((st = nh::parse_quant_i8_spec(spec, &qs))) return st;
     if (qs.silu) return nh::fail(NERVE_HIP_INVALID_SPEC, "silu_multiply_quantize goes through its own entry point");
-    if (!x_bf16 || !q_i8 || !scales_f32 || !sums_i32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (!x_bf16 || !q_i8 || !scales_f32 || (qs.paired && !sums_i32))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (qs.batch_tile == 0 && rows > 1)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "unbatched pair-packed quantizer takes one row");
     if (((uintptr_t)x_bf16 & 15) || ((uintptr_t)q_i8 & 7))
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "x must be 16-byte and q 8-byte aligned");
     if (rows == 0) return nh::ok();
     const uint64_t octs = (uint64_t)rows * qs.elements / 8;
-    quant_i8pp_kernel<false><<<(uint32_t)((octs + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        static_cast<const uint16_t*>(x_bf16), nullptr, nullptr, rows, qs.elements, static_cast<uint32_t*>(q_i8),
-        static_cast<float*>(scales_f32), static_cast<int32_t*>(sums_i32));
-    return nh::check_launch("quantize_int8_pairpacked");
+    const uint32_t grid = (uint32_t)((octs + 255) / 256);
+    if (qs.paired)
+        quant_i8pp_kernel<false, true><<<grid, 256, 0, (hipStream_t)stream>>>(
+            static_cast<const uint16_t*>(x_bf16), nullptr, nullptr, rows, qs.elements, static_cast<uint32_t*>(q_i8),
+            static_cast<float*>(scales_f32), static_cast<int32_t*>(sums_i32));
+    else
+        quant_i8pp_kernel<false, false><<<grid, 256, 0, (hipStream_t)stream>>>(
+            static_cast<const uint16_t*>(x_bf16), nullptr, nullptr, rows, qs.elements, static_cast<uint32_t*>(q_i8),
+            static_cast<float*>(scales_f32), static_cast<int32_t*>(sums_i32));
+    return nh::check_launch("quantize_int8");
 }
 
 extern "C" nerve_hip_status nerve_hip_silu_multiply_quantize_int8_pairpacked(nerve_hip_ctx* ctx, const char* spec,
@@ -720,8 +745,9 @@ extern "C" nerve_hip_status nerve_hip_int4_linear_pairpacked(nerve_hip_ctx* ctx,
     if (st) return st;
     nh::Int4Spec s;
     if ((st = nh::parse_int4_spec(spec, &s))) return st;
-    if (s.input != 2) return nh::fail(NERVE_HIP_INVALID_SPEC, "not a _prequant_pairpacked INT4 specialization");
-    if (!q_i8 || !scales_f32 || !sums_i32 || !qweight || !scales || !y_bf16)
+    if (s.input == 0) return nh::fail(NERVE_HIP_INVALID_SPEC, "not a _prequant[_pairpacked] INT4 specialization");
+    const bool paired = s.input == 2;
+    if (!q_i8 || !scales_f32 || (paired && !sums_i32) || !qweight || !scales || !y_bf16)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (s.op != 0 && !aux_bf16) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "bias/residual specialization needs aux");
     if (s.batch_tile == 0 && batch_width > 1)
@@ -745,6 +771,10 @@ extern "C" nerve_hip_status nerve_hip_int4_linear_pairpacked(nerve_hip_ctx* ctx,
     P.L.G = s.group;
     P.L.scale_bf16 = s.scale_bf16;
     P.L.finalize = s.op;
-    int4_pp_kernel<<<(s.out + 63) / 64, 256, 0, (hipStream_t)stream>>>(P);
-    return nh::check_launch("int4_linear_pairpacked");
+    const uint32_t grid = (s.out + 63) / 64;
+    hipStream_t strm = (hipStream_t)stream;
+    if (paired) int4_pp_kernel<true, false><<<grid, 256, 0, strm>>>(P);
+    else if (s.layout == 0) int4_pp_kernel<false, false><<<grid, 256, 0, strm>>>(P);
+    else int4_pp_kernel<false, true><<<grid, 256, 0, strm>>>(P);
+    return nh::check_launch("int4_linear_prequant");
 }

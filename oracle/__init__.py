@@ -67,6 +67,8 @@ def _declare(l) -> None:
         "o_quantize_i8_pairpacked": (None, [P, I, I, P, P, P]),
         "o_silu_multiply_bf16": (None, [P, P, L, P]),
         "o_int4_linear_pairpacked": (None, [P, P, P, P, P, I, I, I, I, I, I, P, P]),
+        "o_quantize_i8": (None, [P, I, I, P, P]),
+        "o_int4_linear_prequant": (None, [I, P, P, P, P, I, I, I, I, I, I, P, P]),
         "o_fp8_output_projection": (None, [P, I, I, P, P, I, I, F, P]),
         "o_argmax": (None, [P, I, I, P]),
     }
@@ -327,3 +329,29 @@ def argmax(logits) -> np.ndarray:
     ids = np.zeros(M, np.uint32)
     lib().o_argmax(_p(lg), M, N, _p(ids))
     return ids
+
+
+def quantize_i8(x_bf16):
+    """Symmetric INT8 activations per 32 columns, natural byte order.
+    Returns (q u8 [R, C], s f32 [R, C/32])."""
+    x = _c(x_bf16, np.uint16)
+    rows, cols = x.shape
+    q = np.zeros((rows, cols), np.uint8)
+    s = np.zeros((rows, cols // 32), np.float32)
+    lib().o_quantize_i8(_p(x), rows, cols, _p(q), _p(s))
+    return q, s
+
+
+def int4_linear_prequant(layout, q, s, qweight, scales, group, *, scale_bf16=False, finalize=0, aux=None):
+    """INT8-prequant INT4 linear, unpaired input: layout "gptq" (qweight
+    [K/8, N], scales [K/G, N]) or "ct" (qweight [N, K/8], scales [N, K/G])."""
+    q = _c(q, np.uint8)
+    B, K = q.shape
+    qw = _c(qweight, np.uint32)
+    lay = {"gptq": 0, "ct": 1}[layout]
+    N = qw.shape[1] if lay == 0 else qw.shape[0]
+    y = np.zeros((B, N), np.uint16)
+    lib().o_int4_linear_prequant(lay, _p(q), _p(_c(s, np.float32)), _p(qw), _p(_c(scales, np.uint16)),
+                                 int(scale_bf16), group, K, N, B, finalize,
+                                 _p(None if aux is None else _c(aux, np.uint16)), _p(y))
+    return y

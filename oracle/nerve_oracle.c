@@ -689,6 +689,82 @@ void o_int4_linear_pairpacked(const uint8_t* q, const float* s, const int32_t* s
     }
 }
 
+/* Symmetric INT8 activations in natural byte order (quantize_int8_symmetric.
+ * comp.template:38-58): per 32 columns s = amax > 0 ? amax / 127 : 1,
+ * q = round(clamp(x / s, -127, 127)) (ties to even here; the GLSL round()
+ * leaves the direction of exact .5 ties to the implementation). */
+void o_quantize_i8(const uint16_t* x, int rows, int cols, uint8_t* q, float* s) {
+    int nblk = cols / 32;
+    for (int r = 0; r < rows; r++) {
+        const uint16_t* xr = x + (long)r * cols;
+        for (int b = 0; b < nblk; b++) {
+            float amax = 0.0f;
+            for (int c = b * 32; c < b * 32 + 32; c++) amax = fmaxf(amax, fabsf(o_bf16_to_f32(xr[c])));
+            float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+            for (int c = b * 32; c < b * 32 + 32; c++) {
+                float v = o_bf16_to_f32(xr[c]) / sc;
+                v = v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v);
+                q[(long)r * cols + c] = (uint8_t)((int)rintf(v) & 255);
+            }
+            s[(long)r * nblk + b] = sc;
+        }
+    }
+}
+
+/* INT8-prequant INT4 linear, unpaired input (q in natural byte order).
+ * layout 0, linear_prequant_int4_gptq.comp.template:65-103: per output row,
+ * for each weight group and each 32-column block of it, the exact integer
+ * block_dot = sum of q * (code - 8), then sum = fma(block_dot, s_x * s_w,
+ * sum).  layout 1, linear_prequant_int4_ct.comp.template:66-108: 64 lanes
+ * take packed words (8 columns) lane, lane + 64, ...; each adds
+ * fma(packed_dot, s_x[block] * s_w[group], lane_sum); then a subgroup add.
+ * finalize as o_int4_linear. */
+void o_int4_linear_prequant(int layout, const uint8_t* q, const float* s, const uint32_t* qw,
+                            const uint16_t* scales, int scale_bf16, int group, int K, int N, int B, int finalize,
+                            const uint16_t* aux, uint16_t* y) {
+    int nblk = K / 32, G = K / group;
+    #pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; n++) {
+        for (int b = 0; b < B; b++) {
+            const int8_t* qb = (const int8_t*)(q + (size_t)b * K);
+            float sum = 0.0f;
+            if (layout == 0) {
+                for (int g = 0; g < G; g++) {
+                    uint16_t sr = scales[(size_t)g * N + n];
+                    float sw = scale_bf16 ? o_bf16_to_f32(sr) : f16_to_f32(sr);
+                    for (int blk = g * (group / 32); blk < (g + 1) * (group / 32); blk++) {
+                        int dot = 0;
+                        for (int p = blk * 4; p < blk * 4 + 4; p++) {
+                            uint32_t word = qw[(size_t)p * N + n];
+                            for (int j = 0; j < 8; j++) dot += (int)qb[p * 8 + j] * ((int)((word >> (4 * j)) & 15u) - 8);
+                        }
+                        sum = fmaf((float)dot, s[(size_t)b * nblk + blk] * sw, sum);
+                    }
+                }
+            } else {
+                float lanes[64];
+                for (int lane = 0; lane < 64; lane++) {
+                    float ls = 0.0f;
+                    for (int p = lane; p < K / 8; p += 64) {
+                        uint32_t word = qw[(size_t)n * (K / 8) + p];
+                        int dot = 0;
+                        for (int j = 0; j < 8; j++) dot += (int)qb[p * 8 + j] * ((int)((word >> (4 * j)) & 15u) - 8);
+                        uint16_t sr = scales[(size_t)n * G + (p * 8) / group];
+                        float sw = scale_bf16 ? o_bf16_to_f32(sr) : f16_to_f32(sr);
+                        ls = fmaf((float)dot, s[(size_t)b * nblk + (p * 8) / 32] * sw, ls);
+                    }
+                    lanes[lane] = ls;
+                }
+                sum = subgroup_add(lanes, 64);
+            }
+            float v = sum;
+            if (finalize == 1) v = o_bf16_to_f32(aux[n]) + sum;
+            else if (finalize == 2) v = o_bf16_to_f32(aux[(size_t)b * N + n]) + round_bf16(sum);
+            y[(size_t)b * N + n] = o_f32_to_bf16(v);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* a10 / a11: FP8 output projection + argmax                             */
 /* ------------------------------------------------------------------ */

@@ -80,7 +80,15 @@ def test_null_context_is_rejected():
     ("linear_prequant_pairpacked_batch16_int4_gptq_sf16_g128_4096x14336.comp", 0),
     ("linear_residual_prequant_pairpacked_int4_gptq_sbf16_g32_4096x4096.comp", 0),
     ("linear_prequant_pairpacked_int4_ct_sf16_g128_4096x4096.comp", 2),
-    ("linear_prequant_int4_gptq_sf16_g128_4096x4096.comp", 3),
+    ("linear_prequant_int4_gptq_sf16_g128_4096x4096.comp", 0),
+    ("linear_bias_prequant_batch4_int4_ct_sbf16_g64_4096x4096.comp", 0),
+    ("quantize_batch16_int8_symmetric_b32_h4096.comp", 0),
+    ("linear_batch64_cooperative_int4_gptq_sf16_g128_4096x14336.comp", 0),
+    ("linear_residual_batch64_cooperative_int4_ct_sbf16_g128_4096x4096.comp", 0),
+    ("linear_batch64_cooperative_int4_ct_sf16_g64_4096x4096.comp", 3),
+    ("linear_batch32_cooperative_int4_gptq_sf16_g128_4096x4096.comp", 2),
+    ("quantize_int8_symmetric_b64_h4096.comp", 2),
+    ("silu_multiply_quantize_int8_b32_h4096.comp", 2),
     ("quantize_batch4_int8_symmetric_pairpacked_b32_h4096.comp", 0),
     ("quantize_int8_symmetric_pairpacked_b64_h4096.comp", 2),
     ("silu_multiply_quantize_int8_pairpacked_b32_h14336.comp", 0),

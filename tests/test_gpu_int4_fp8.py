@@ -217,3 +217,26 @@ def test_int4_finalize_rounding_closed_form(ctx, dev, layout):
         spec = f"{op}_batch16_int4_{layout}_sf16_g{G}_{K}x{N}.comp"
         y = _run_int4(ctx, dev, spec, x, qw, sc, None, aux, M, N)
         assert np.all(y == want), (op, y[0, :4])
+
+
+# linear_batch_cooperative_int4.comp.template: batch-64 tiles; one and two
+# tiles of tokens, both layouts, groups of 128 (and 32 for GPTQ).
+@pytest.mark.parametrize("B", [64, 100])
+@pytest.mark.parametrize("layout,G", [("gptq", 128), ("gptq", 32), ("ct", 128)])
+@pytest.mark.parametrize("finalize", [0, 2])
+def test_int4_cooperative_batch64(ctx, dev, B, layout, G, finalize):
+    K, N = 1024, 384
+    rng = np.random.default_rng(B + G + finalize + len(layout))
+    d = wl.int4_gptq(rng, K, N, G, True)
+    x = wl.bf16_normal(rng, (B, K))
+    if layout == "gptq":
+        qw, sc = d["qweight"], d["scales"]
+    else:
+        qw, sc = _ct_from_gptq(d, K, N, G)
+    aux = wl.bf16_normal(rng, (B, N)) if finalize == 2 else None
+    op = ["linear", "linear_bias", "linear_residual"][finalize]
+    spec = f"{op}_batch64_cooperative_int4_{layout}_sf16_g{G}_{K}x{N}.comp"
+    y = _run_int4(ctx, dev, spec, x, qw, sc.view(np.uint16), None, aux, B, N)
+    ref = oracle.int4_linear(layout, x, qw, sc.view(np.uint16), G, finalize=finalize, aux=aux)
+    ok, worst, exact = bf16_close(y, ref)
+    assert ok and exact > 0.9, (worst, exact)

@@ -65,3 +65,60 @@ def test_silu_multiply_closed_forms():
     u = wl.f32_to_bf16_bits(np.full(7, -2.0, np.float32))
     y2 = wl.bf16_bits_to_f32(oracle.silu_multiply_bf16(g, u)).astype(np.float64)
     assert np.array_equal(y2, -2.0 * y)                   # a power-of-two factor is exact
+
+
+# --------------------------------------------------------------------------
+# Unpaired INT8 input (quantize_int8_symmetric.comp.template:38-58,
+# linear_prequant_int4_{gptq,ct}.comp.template)
+# --------------------------------------------------------------------------
+
+def test_unpaired_quantizer_is_the_pairpacked_codes_in_column_order():
+    """Both quantizers apply the same rule per 32 columns; only the byte order
+    differs (the pair-packed one is pinned above)."""
+    rng = np.random.default_rng(3)
+    x = wl.bf16_normal(rng, (4, 384))
+    x[1, 64:96] = 0
+    q, s = oracle.quantize_i8(x)
+    qp, sp, sums = oracle.quantize_i8_pairpacked(x)
+    assert np.array_equal(q.view(np.int8), _unpack(qp))
+    assert np.array_equal(s, sp)
+
+
+def test_unpaired_gptq_linear_equals_pairpacked_on_the_same_codes():
+    """block_dot = sum q (code - 8) = sum q code - 8 sum q: the unpaired and the
+    pair-packed GPTQ forms hold the same integers and the same fma order, so
+    their outputs are bit-identical; finalize forms included."""
+    rng = np.random.default_rng(4)
+    K, N, G, B = 512, 48, 128, 3
+    d = wl.int4_gptq(rng, K, N, G, True)
+    x = wl.bf16_normal(rng, (B, K))
+    q, s = oracle.quantize_i8(x)
+    qp, sp, sums = oracle.quantize_i8_pairpacked(x)
+    sc = d["scales"].view(np.uint16)
+    for fin, aux in ((0, None), (1, wl.bf16_normal(rng, (N,))), (2, wl.bf16_normal(rng, (B, N)))):
+        y = oracle.int4_linear_prequant("gptq", q, s, d["qweight"], sc, G, finalize=fin, aux=aux)
+        yp = oracle.int4_linear_pairpacked(qp, sp, sums, d["qweight"], sc, G, finalize=fin, aux=aux)
+        assert np.array_equal(y, yp), fin
+
+
+def test_unpaired_ct_linear_closed_form():
+    """The CT form against sum_k x_q s_x (code - 8) s_w in float64 (its f32
+    chains differ from the GPTQ order only by rounding), and against the
+    GPTQ form on the same codes in the transposed layout."""
+    rng = np.random.default_rng(5)
+    K, N, G, B = 1024, 32, 128, 2
+    d = wl.int4_gptq(rng, K, N, G, True)
+    x = wl.bf16_normal(rng, (B, K))
+    q, s = oracle.quantize_i8(x)
+    qt = np.ascontiguousarray(d["q"].T)                          # [N, K]
+    qct = np.zeros((N, K // 8), np.uint32)
+    for j in range(8):
+        qct |= qt[:, j::8] << np.uint32(4 * j)
+    sct = np.ascontiguousarray(d["scales"].T).view(np.uint16)
+    y = wl.bf16_bits_to_f32(oracle.int4_linear_prequant("ct", q, s, qct, sct, G)).astype(np.float64)
+    xq = q.view(np.int8).astype(np.float64) * np.repeat(s.astype(np.float64), 32, axis=1)
+    ref = xq @ ((d["q"].astype(np.float64) - 8.0) * np.repeat(d["scales"].astype(np.float64), G, axis=0))
+    assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-3 * np.sqrt(np.mean(ref ** 2)))) <= 2 ** -7
+    yg = wl.bf16_bits_to_f32(oracle.int4_linear_prequant("gptq", q, s, d["qweight"], d["scales"].view(np.uint16),
+                                                          G)).astype(np.float64)
+    assert np.mean(yg == y) > 0.9

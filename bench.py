@@ -40,10 +40,11 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="moe_decode",
-                   choices=["moe_decode", "moe_prefill", "mxfp4_gemv", "int4_gemv", "fp8_head", "hbm_copy"])
+                   choices=["moe_decode", "moe_prefill", "mxfp4_gemv", "int4_gemv", "int4_moe", "fp8_head",
+                            "hbm_copy"])
     p.add_argument("--summarize-traffic", nargs=4, metavar="DIR",
                    help="FETCH_SIZE and WRITE_SIZE rocprofv3 CSV dirs of a run, then of the hbm_copy run")
-    p.add_argument("--m", type=int, default=1, help="batch rows for int4_gemv / fp8_head")
+    p.add_argument("--m", type=int, default=1, help="batch rows for int4_gemv / int4_moe / fp8_head")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -336,6 +337,75 @@ def int4_gemv(args, ctx, dev):
     return out
 
 
+def int4_moe(args, ctx, dev):
+    """Sparse INT4-CT experts at the geometry of the reference's compiler test
+    (h3072 i1024 e256 k10, g32 bf16 scales): one step = route compaction ->
+    gate_up -> count -> down -> reduce for a batch of --m tokens.  The whole
+    256-expert bank (1.36 GB) is drawn on the GPU, and every step routes the
+    tokens to fresh random experts, so weights stream from HBM."""
+    import torch
+
+    from nerve_amd.moe import Int4CtExpertBank, int4_ct_spec
+
+    B, H, I, E, k, G = args.m, 3072, 1024, 256, 10, 32
+    g = torch.Generator(device=dev).manual_seed(20260005)
+
+    def words(*shape):
+        return torch.randint(-2 ** 31, 2 ** 31 - 1, shape, generator=g, device=dev, dtype=torch.int64).to(torch.int32)
+
+    def scales(*shape):
+        return (torch.rand(shape, generator=g, device=dev) * 0.018 + 0.002).to(torch.bfloat16).view(torch.int16)
+
+    bank = Int4CtExpertBank(words(E, 2 * I, H // 8), scales(E, 2 * I, H // G), words(E, H, I // 8),
+                            scales(E, H, I // G))
+    rng = np.random.default_rng(5)
+    R = 64
+    sets = np.stack([np.stack([rng.choice(E, size=k, replace=False) for _ in range(B)]) for _ in range(R)])
+    wbits = np.uint32(0x3DCC) << np.uint32(16)                       # bf16 0.1
+    routes = [to_dev(sets[i].astype(np.uint32) | wbits, dev) for i in range(R)]
+    x = (torch.randn(B, H, generator=g, device=dev)).to(torch.bfloat16).view(torch.int16)
+    gspec = int4_ct_spec("gate_up", H, I, E, k, G)
+    dspec = int4_ct_spec("down", H, I, E, k, G)
+    fw = k * I // 2 + k
+    inter = torch.zeros(B * fw, dtype=torch.int32, device=dev)
+    control = to_dev(np.array([B, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev)
+    eo = torch.zeros(B, k, H, dtype=torch.int16, device=dev)
+    y = torch.zeros(B, H, dtype=torch.int16, device=dev)
+
+    def step(i, st=None):
+        r = routes[i % R]
+        ctx.moe_route_compact(gspec, r, inter, control, B, st)
+        ctx.int4_moe_gate_up(gspec, x, r, inter, bank.addresses, bank.gate_slots, control, B, st)
+        ctx.moe_route_compact(dspec, r, None, control, B, st)
+        ctx.int4_moe_down(dspec, inter, r, eo, bank.addresses, bank.down_slots, control, B, st)
+        ctx.moe_reduce(eo, y, B, H, k, 1.0, st)
+
+    stream = torch.cuda.current_stream()
+    ms = wall_ms(lambda i: step(i, stream), args.steps, args.warmup)
+    step_ms = graph_event_ms(step, R)
+    for i in range(R):
+        ctx.moe_route_compact(gspec, routes[i], inter, control, B, stream)
+    gu_ms = graph_event_ms(lambda i, st: ctx.int4_moe_gate_up(gspec, x, routes[i % R], inter, bank.addresses,
+                                                              bank.gate_slots, control, B, st), R)
+    dn_ms = graph_event_ms(lambda i, st: ctx.int4_moe_down(dspec, inter, routes[i % R], eo, bank.addresses,
+                                                           bank.down_slots, control, B, st), R)
+    distinct = np.mean([len(np.unique(s)) for s in sets])
+    gu_alg = distinct * (2 * I * H // 2 + 2 * I * (H // G) * 2) + B * H * 2 + B * k * I * 2
+    dn_alg = distinct * (H * I // 2 + H * (I // G) * 2) + B * k * I * 2 + B * k * H * 2
+    gu_gbs = gu_alg / (gu_ms * 1e-3) / 1e9
+    dn_gbs = dn_alg / (dn_ms * 1e-3) / 1e9
+    out = base_line(args, B * k / (step_ms * 1e-3), "expert-tokens/s", ms, "bf16xint4->f32",
+                    {"workload": f"int4_ct_sparse_moe_b{B}_h3072_i1024_e256_k10_g32"})
+    out["roofline"] = {"bound": "hbm", "kernel": "sparse_int4_kernel<true, 32, false> (gate_up)", "achieved": gu_gbs,
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gu_gbs / HBM_PEAK_GBS,
+                       "traffic": traffic_for("sparse_int4_kernel<true, 32u, false>"),
+                       "algorithmic_bytes_per_launch": gu_alg, "launch_ms": gu_ms}
+    out["down"] = {"kernel": "sparse_int4_kernel<false, 32, false>", "hbm_gbs": dn_gbs, "frac": dn_gbs / HBM_PEAK_GBS,
+                   "algorithmic_bytes_per_launch": dn_alg, "launch_ms": dn_ms}
+    out["step_ms_graph"] = step_ms
+    return out
+
+
 def fp8_head(args, ctx, dev):
     """Weights are drawn on the GPU (N(0,0.02), per-row bf16 amax/448 scale,
     torch's e4m3fn cast): 579 MB exceeds the Infinity Cache on its own."""
@@ -500,6 +570,8 @@ def main():
         out = mxfp4_gemv(args, ctx, dev)
     elif args.workload == "int4_gemv":
         out = int4_gemv(args, ctx, dev)
+    elif args.workload == "int4_moe":
+        out = int4_moe(args, ctx, dev)
     elif args.workload == "hbm_copy":
         out = hbm_copy(args, ctx, dev)
     else:

@@ -281,6 +281,40 @@ nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_out
                                       uint32_t experts_per_token, float routed_scale,
                                       void* stream);
 
+/* ---- sparse INT4 (compressed-tensors) experts --------------------------- */
+
+/* Replace sparse_moe_gate_up[_batch1]_int4_ct_s{f16|bf16}_g{G}_h{H}_i{I}_e{E}_
+ * k{k}.comp (sparse_moe_gate_up_int4_ct.comp.template:97-227) and
+ * sparse_moe_down[_batch1]_int4_ct_….comp (sparse_moe_down_int4_ct.comp.
+ * template:106-193; grammar and rendering nerve/model_package_sparse_
+ * projection_shaders.py:80-232).  Per expert two parameter slots
+ * (param_slots u32 [2 * E]): CT-packed weights u32 [rows, K/8] (codes low
+ * nibble first, value code - 8) and f16/bf16 scales [rows, K/G]; gate_up rows
+ * are the I gate rows then the I up rows (K = H), down rows are H (K = I).
+ * gate_up writes h = bf16(bf16(silu(bf16 g)) * bf16 u) into the intermediate
+ * slices; down writes expert_outputs bf16 [B, k, H] = bf16(bf16(y) *
+ * route_weight).
+ * "_batch1" (frame-parallel) form: frames [B][k*I/2 + k] with the route map
+ * in the tails (nerve_hip_moe_route_compact with this spec writes it) and
+ * control = BatchControl, exactly as the MXFP4 entry points.  Unbatched form:
+ * batch_width 1, intermediates [k][I/2] words without a map, and control
+ * either NULL (every expert) or a BatchControl whose words 1 and 2 give the
+ * owned expert range (DispatchControl {expert_start, expert_count}).
+ * Slots that are unbound, beyond the table, or whose record has a null or
+ * misaligned address or fewer bytes than the expert's tensor skip the route
+ * (the reference skips unbound slots only).  Needs K % 32 == 0 and
+ * K <= 16384. */
+nerve_hip_status nerve_hip_int4_moe_gate_up(nerve_hip_ctx* ctx, const char* spec, const void* hidden_bf16,
+                                            const void* routes_u32, void* intermediates,
+                                            const void* addresses_u32, uint32_t address_records,
+                                            const void* param_slots_u32, uint32_t param_slot_words,
+                                            const void* control_u32, uint32_t batch_width, void* stream);
+nerve_hip_status nerve_hip_int4_moe_down(nerve_hip_ctx* ctx, const char* spec, const void* intermediates,
+                                         const void* routes_u32, void* expert_outputs,
+                                         const void* addresses_u32, uint32_t address_records,
+                                         const void* param_slots_u32, uint32_t param_slot_words,
+                                         const void* control_u32, uint32_t batch_width, void* stream);
+
 /* ---- a9: group-scaled INT4 linear --------------------------------------- */
 
 /* Replaces {linear|linear_bias|linear_residual}[_batch{T}]_int4_{gptq|ct}_

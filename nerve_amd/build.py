@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libnerve_hip.so")
-SOURCES = ["context.hip", "mxfp4_moe.hip", "routing.hip", "int4.hip", "fp8_head.hip", "rms_quant.hip"]
+SOURCES = ["context.hip", "mxfp4_moe.hip", "routing.hip", "int4.hip", "fp8_head.hip", "rms_quant.hip", "int4_moe.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -128,8 +128,23 @@ struct MoeSpec {
     uint32_t hidden = 0, inter = 0, experts = 0, k = 0;
     bool has_limit = false;
     float limit = 0.0f;
+    // 0: independent_sparse_moe_*_mxfp4 (demand-addressed MXFP4 experts);
+    // 1: sparse_moe_*_int4_ct (compressed-tensors INT4 experts, bf16 or f16
+    //    group scales, 16-row tiles).
+    int family = 0;
+    int scale_bf16 = 0;
+    uint32_t group = 0;
 };
 nerve_hip_status parse_moe_spec(const char* spec, MoeSpec* out);
+
+// TILES_PER_ROUTE of an expert projection: the rows one reference workgroup
+// produces per route (MXFP4: 32-row gate_up and 64-row down tiles,
+// nerve/model_package_shader_templates.py:4836; INT4-CT: 16-row tiles,
+// nerve/model_package_common.py:64).
+inline uint32_t moe_tiles_per_route(const MoeSpec& m) {
+    if (m.family == 1) return ((m.gate_up ? m.inter : m.hidden) + 15) / 16;
+    return m.gate_up ? (m.inter + 31) / 32 : (m.hidden + 63) / 64;
+}
 
 struct TopkSpec {
     int mode = 0;               // 0 moe_topk, 1 moe_router_score_topk

@@ -77,8 +77,37 @@ static bool parse_u32(const std::string& s, uint32_t* out) {
 }
 
 // nerve/model_package_shader_templates.py:4773-4846
+// nerve/model_package_sparse_projection_shaders.py:80-125
+static nerve_hip_status parse_int4_moe_spec(const char* spec, MoeSpec* out) {
+    static const std::regex re(
+        "sparse_moe_(gate_up|down)(?:_batch(\\d+))?_int4_ct_s(f16|bf16)_g(\\d+)_"
+        "h(\\d+)_i(\\d+)_e(\\d+)_k(\\d+)\\.comp");
+    std::cmatch m;
+    if (!std::regex_match(spec, m, re)) return NERVE_HIP_UNSUPPORTED;
+    MoeSpec s;
+    s.family = 1;
+    s.gate_up = m[1].str() == "gate_up";
+    if (m[2].matched && m[2].str() != "1")
+        return fail(NERVE_HIP_INVALID_SPEC, "INT4 sparse experts support only frame-parallel batch tiles");
+    s.batch1 = m[2].matched;
+    s.scale_bf16 = m[3].str() == "bf16";
+    if (!parse_u32(m[4].str(), &s.group) || !parse_u32(m[5].str(), &s.hidden) || !parse_u32(m[6].str(), &s.inter) ||
+        !parse_u32(m[7].str(), &s.experts) || !parse_u32(m[8].str(), &s.k))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("bad shape in ") + spec);
+    const uint32_t in_w = s.gate_up ? s.hidden : s.inter, out_w = s.gate_up ? s.inter : s.hidden;
+    if (s.group == 0 || s.group % 8 || in_w == 0 || in_w % s.group || in_w % 8 || out_w == 0 || out_w % 2 ||
+        !(0 < s.k && s.k <= s.experts && s.experts <= 4096))
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid INT4 sparse expert geometry ") + spec);
+    *out = s;
+    return NERVE_HIP_OK;
+}
+
 static nerve_hip_status parse_moe_spec_uncached(const char* spec, MoeSpec* out) {
     if (!spec) return fail(NERVE_HIP_INVALID_SPEC, "null specialization");
+    {
+        nerve_hip_status st = parse_int4_moe_spec(spec, out);
+        if (st != NERVE_HIP_UNSUPPORTED) return st;
+    }
     static const std::regex re(
         "independent_sparse_moe_(gate_up|down)(?:_(batch1))?"
         "(?:_(tensor_parallel))?"
@@ -406,6 +435,15 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
     if (s.rfind("independent_sparse_moe_", 0) == 0) {
         nh::MoeSpec m;
         return nh::parse_moe_spec(spec, &m);
+    }
+    if (s.rfind("sparse_moe_", 0) == 0) {
+        nh::MoeSpec m;
+        nerve_hip_status st = nh::parse_moe_spec(spec, &m);
+        if (st) return st;
+        if (m.family != 1) return nh::fail(NERVE_HIP_INVALID_SPEC, std::string("not an INT4 sparse expert kernel: ") + spec);
+        if ((m.gate_up ? m.hidden : m.inter) % 32)
+            return nh::fail(NERVE_HIP_UNSUPPORTED, "INT4 sparse experts need an input width that is a multiple of 32");
+        return NERVE_HIP_OK;
     }
     if (s.rfind("moe_topk", 0) == 0 || s.rfind("moe_router", 0) == 0) {
         nh::TopkSpec t;

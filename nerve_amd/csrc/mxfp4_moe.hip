@@ -3398,6 +3398,7 @@ nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spe
     if (st) return st;
     nh::MoeSpec ms;
     if ((st = nh::parse_moe_spec(spec, &ms))) return st;
+    if (ms.family != 0) return nh::fail(NERVE_HIP_INVALID_SPEC, std::string("not an MXFP4 expert kernel: ") + spec);
     if (!ms.gate_up) return nh::fail(NERVE_HIP_INVALID_SPEC, "gate_up entry given a down specialization");
     if (!hidden || !routes_u32 || !intermediates || !addresses_u32 || !param_slots_u32 || !control_u32 ||
         (ms.prequant && !hidden_scales))
@@ -3418,6 +3419,7 @@ nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec, 
     if (st) return st;
     nh::MoeSpec ms;
     if ((st = nh::parse_moe_spec(spec, &ms))) return st;
+    if (ms.family != 0) return nh::fail(NERVE_HIP_INVALID_SPEC, std::string("not an MXFP4 expert kernel: ") + spec);
     if (ms.gate_up) return nh::fail(NERVE_HIP_INVALID_SPEC, "down entry given a gate_up specialization");
     if (!intermediates || !routes_u32 || !expert_outputs || !addresses_u32 || !param_slots_u32 || !control_u32)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
@@ -3435,6 +3437,7 @@ nerve_hip_status nerve_hip_mxfp4_moe_down_counted(nerve_hip_ctx* ctx, const char
     if (st) return st;
     nh::MoeSpec ms;
     if ((st = nh::parse_moe_spec(spec, &ms))) return st;
+    if (ms.family != 0) return nh::fail(NERVE_HIP_INVALID_SPEC, std::string("not an MXFP4 expert kernel: ") + spec);
     if (ms.gate_up) return nh::fail(NERVE_HIP_INVALID_SPEC, "down entry given a gate_up specialization");
     if (!intermediates || !routes_u32 || !expert_outputs || !addresses_u32 || !param_slots_u32 || !control_u32)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");

@@ -831,9 +831,10 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
     if ((st = nh::parse_moe_spec(spec, &ms))) return st;
     if (!routes_u32 || !control_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     const uint32_t n = batch_width * ms.k;
-    // TILES_PER_ROUTE of the consuming projection: 32-row gate_up tiles,
-    // 64-row down tiles (nerve/model_package_shader_templates.py:4836).
-    const uint32_t tiles = ms.gate_up ? (ms.inter + 31) / 32 : (ms.hidden + 63) / 64;
+    if (ms.family == 1 && !ms.batch1)
+        return nh::fail(NERVE_HIP_INVALID_SPEC, "the unbatched INT4 expert form reads no route map");
+    // TILES_PER_ROUTE of the consuming projection.
+    const uint32_t tiles = nh::moe_tiles_per_route(ms);
     const uint64_t frame_words = (uint64_t)ms.k * ms.inter / 2 + ms.k;
     const uint32_t data_words = ms.k * ms.inter / 2;
     CompactArgs A;
@@ -862,6 +863,8 @@ nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_
     nh::MoeSpec ms;
     if ((st = nh::parse_topk_spec(topk_spec, &ts))) return st;
     if ((st = nh::parse_moe_spec(moe_spec, &ms))) return st;
+    if (ms.family == 1 && !ms.batch1)
+        return nh::fail(NERVE_HIP_INVALID_SPEC, "the unbatched INT4 expert form reads no route map");
     if (!x_bf16 || !router_weight_bf16 || !routes_u32 || !control_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (ts.bias != 0 && !bias) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "specialization requires a selection bias");
     if (ts.experts != ms.experts || ts.k + ts.always_count != ms.k)
@@ -908,7 +911,7 @@ nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_
     A.frame_words = (uint64_t)ms.k * ms.inter / 2 + ms.k;
     A.data_words = ms.k * ms.inter / 2;
     A.control = static_cast<uint32_t*>(control_u32);
-    A.tiles_per_route = ms.gate_up ? (ms.inter + 31) / 32 : (ms.hidden + 63) / 64;
+    A.tiles_per_route = nh::moe_tiles_per_route(ms);
     route_fused_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(F);
     return nh::check_launch("moe_route_fused");
 }

@@ -32,6 +32,8 @@ EXPORTS = (
     "nerve_hip_mxfp4_moe_down",
     "nerve_hip_mxfp4_moe_down_counted",
     "nerve_hip_moe_reduce",
+    "nerve_hip_int4_moe_gate_up",
+    "nerve_hip_int4_moe_down",
     "nerve_hip_int4_linear",
     "nerve_hip_quantize_int8_pairpacked",
     "nerve_hip_silu_multiply_quantize_int8_pairpacked",
@@ -92,6 +94,8 @@ def _declare(lib) -> None:
         "nerve_hip_mxfp4_moe_down": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_mxfp4_moe_down_counted": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_moe_reduce": (ctypes.c_int, [P, P, P, U32, U32, U32, ctypes.c_float, P]),
+        "nerve_hip_int4_moe_gate_up": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
+        "nerve_hip_int4_moe_down": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_int4_linear": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
         "nerve_hip_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
         "nerve_hip_silu_multiply_quantize_int8_pairpacked": (ctypes.c_int, [P, S, P, P, P, P, P, P, U32, P]),
@@ -238,6 +242,21 @@ class Context:
     def mxfp4_moe_down(self, spec, intermediates, routes, expert_outputs, addresses, param_slots, control,
                        batch_width, stream=None):
         _check(self.lib.nerve_hip_mxfp4_moe_down(
+            self.handle, _spec(spec), ptr(intermediates), ptr(routes), ptr(expert_outputs), ptr(addresses),
+            addresses.numel() // 8, ptr(param_slots), param_slots.numel(), ptr(control), batch_width,
+            _stream(stream)))
+
+    # ---- sparse INT4-CT experts
+    def int4_moe_gate_up(self, spec, hidden, routes, intermediates, addresses, param_slots, control, batch_width,
+                         stream=None):
+        _check(self.lib.nerve_hip_int4_moe_gate_up(
+            self.handle, _spec(spec), ptr(hidden), ptr(routes), ptr(intermediates), ptr(addresses),
+            addresses.numel() // 8, ptr(param_slots), param_slots.numel(), ptr(control), batch_width,
+            _stream(stream)))
+
+    def int4_moe_down(self, spec, intermediates, routes, expert_outputs, addresses, param_slots, control,
+                      batch_width, stream=None):
+        _check(self.lib.nerve_hip_int4_moe_down(
             self.handle, _spec(spec), ptr(intermediates), ptr(routes), ptr(expert_outputs), ptr(addresses),
             addresses.numel() // 8, ptr(param_slots), param_slots.numel(), ptr(control), batch_width,
             _stream(stream)))

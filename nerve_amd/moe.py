@@ -37,6 +37,14 @@ def down_spec(H: int, I: int, E: int, k: int, batch1: bool = True) -> str:
     return f"independent_sparse_moe_down{'_batch1' if batch1 else ''}_mxfp4_e2m1_g32_h{H}_i{I}_e{E}_k{k}.comp"
 
 
+def int4_ct_spec(stage: str, H: int, I: int, E: int, k: int, group: int, *, scale_bf16: bool = True,
+                 batch1: bool = True) -> str:
+    """sparse_moe_{gate_up|down}[_batch1]_int4_ct_… specialization
+    (nerve/model_package_sparse_projection_shaders.py:80-84)."""
+    return (f"sparse_moe_{stage}{'_batch1' if batch1 else ''}_int4_ct_s{'bf16' if scale_bf16 else 'f16'}"
+            f"_g{group}_h{H}_i{I}_e{E}_k{k}.comp")
+
+
 def topk_spec(E: int, k: int, *, sigmoid: bool = False, normalize: bool = True, softcap: float = 0.0,
               bias: str = "nobias") -> str:
     return (f"moe_topk_batch1_{'sigmoid' if sigmoid else 'softmax'}_bf16_e{E}_k{k}_norm{int(normalize)}"
@@ -99,6 +107,39 @@ class ExpertBank:
         self.addresses = u32_tensor(recs, dev)
         self.gate_slots = u32_tensor(gate_slots, dev)
         self.down_slots = u32_tensor(down_slots, dev)
+
+
+class Int4CtExpertBank:
+    """Sparse INT4-CT expert parameters and their address table.
+
+    gate_up_w: u32 [Eb, 2I, H/8] (as int32), gate_up_s: u16 [Eb, 2I, H/G];
+    down_w: u32 [Eb, H, I/8], down_s: u16 [Eb, H, I/G].  Expert e of an
+    E-expert model reads bank bank_of[e] (default e), so several experts may
+    share one stored tensor; per expert two parameter slots per stage
+    (weight, scales), as the shaders' DYNAMIC_PARAMETER_COUNT = 2.
+    """
+
+    def __init__(self, gate_up_w, gate_up_s, down_w, down_s, experts: int | None = None, bank_of=None):
+        self.gate_up_w, self.gate_up_s, self.down_w, self.down_s = gate_up_w, gate_up_s, down_w, down_s
+        nb = gate_up_w.shape[0]
+        self.experts = nb if experts is None else experts
+        self.bank_of = list(range(self.experts)) if bank_of is None else [int(b) for b in bank_of]
+        dev = gate_up_w.device
+        recs: list[int] = []
+        gu_rec, dn_rec = [], []
+        for b in range(nb):
+            gu_rec.append((len(recs) // 8, len(recs) // 8 + 1))
+            recs += address_record(gate_up_w[b]) + address_record(gate_up_s[b])
+            dn_rec.append((len(recs) // 8, len(recs) // 8 + 1))
+            recs += address_record(down_w[b]) + address_record(down_s[b])
+        gs, ds = [], []
+        for e in range(self.experts):
+            gs += list(gu_rec[self.bank_of[e]])
+            ds += list(dn_rec[self.bank_of[e]])
+        self.records = recs
+        self.addresses = u32_tensor(recs, dev)
+        self.gate_slots = u32_tensor(gs, dev)
+        self.down_slots = u32_tensor(ds, dev)
 
 
 class MoEBlock:

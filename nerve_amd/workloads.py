@@ -117,6 +117,26 @@ def int4_gptq(rng: np.random.Generator, K: int, N: int, group: int, symmetric: b
     return dict(q=q, qweight=qw, scales=scales, zeros=z, qzeros=qz)
 
 
+def int4_ct_experts(rng: np.random.Generator, E: int, rows: int, K: int, group: int, scale_bf16: bool = True,
+                    keep_codes: bool = False):
+    """Sparse INT4-CT expert bank: W u32 [E, rows, K/8] (8 codes along K per
+    word, low nibble first, value code - 8) and scale bits u16 [E, rows,
+    K/group] (bf16 or f16 values in U(0.002, 0.02)); the layout of
+    experts.gate_up / experts.down (tests/test_model_package_moe_components.py:
+    1012-1049 in the reference)."""
+    q = rng.integers(0, 16, size=(E, rows, K), dtype=np.uint8)
+    qq = q.reshape(E, rows, K // 8, 8).astype(np.uint32)
+    W = np.zeros((E, rows, K // 8), np.uint32)
+    for j in range(8):
+        W |= qq[..., j] << np.uint32(4 * j)
+    sv = rng.uniform(0.002, 0.02, size=(E, rows, K // group)).astype(np.float32)
+    S = f32_to_bf16_bits(sv) if scale_bf16 else sv.astype(np.float16).view(np.uint16)
+    d = dict(W=W, S=S)
+    if keep_codes:
+        d["q"] = q
+    return d
+
+
 def config1(M: int = 1, K: int = 4096, N: int = 14336, group: int = 128, symmetric: bool = False):
     rng = rng_for(1)
     d = int4_gptq(rng, K, N, group, symmetric)

@@ -71,6 +71,10 @@ def _declare(l) -> None:
         "o_int4_linear_prequant": (None, [I, P, P, P, P, I, I, I, I, I, I, P, P]),
         "o_fp8_output_projection": (None, [P, I, I, P, P, I, I, F, P]),
         "o_argmax": (None, [P, I, I, P]),
+        "o_sparse_int4_gate_up": (None, [P, P, P, I, I, I, I, I, I, I, I, ctypes.c_uint32, ctypes.c_uint32, P, P, P,
+                                         P]),
+        "o_sparse_int4_down": (None, [P, P, P, I, I, I, I, I, I, I, I, ctypes.c_uint32, ctypes.c_uint32, P, P, P,
+                                      P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(l, name)
@@ -355,3 +359,47 @@ def int4_linear_prequant(layout, q, s, qweight, scales, group, *, scale_bf16=Fal
                                  int(scale_bf16), group, K, N, B, finalize,
                                  _p(None if aux is None else _c(aux, np.uint16)), _p(y))
     return y
+
+
+def _ct_bound(bound, E):
+    return None if bound is None else _c(np.asarray(bound, np.uint8), np.uint8)
+
+
+def sparse_int4_gate_up(hidden, routes, cmap, n_pos, W, S, group, *, scale_bf16=True, expert_start=0,
+                        expert_count=0, bound=None, inter=None):
+    """Sparse INT4-CT gate/up (``sparse_moe_gate_up_int4_ct.comp.template:97-227``).
+    hidden bf16 [B, H]; routes u32 [B, k]; cmap: compacted positions -> route
+    index (None: identity); W u32 [E, 2I, H/8]; S u16 [E, 2I, H/group].
+    Returns bf16 intermediates [B, k, I] (``inter`` supplies the untouched
+    values)."""
+    h = _c(hidden, np.uint16)
+    r = _c(routes, np.uint32)
+    B, H = h.shape
+    k = r.shape[1]
+    E, R2, _ = W.shape
+    I = R2 // 2
+    out = np.zeros((B, k, I), np.uint16) if inter is None else _c(inter, np.uint16).copy()
+    m = None if cmap is None else _c(cmap, np.uint32)
+    bd = _ct_bound(bound, E)
+    lib().o_sparse_int4_gate_up(_p(h), _p(r), None if m is None else _p(m), n_pos, B, k, E, H, I, group,
+                                int(scale_bf16), expert_start, expert_count, None if bd is None else _p(bd),
+                                _p(_c(W, np.uint32)), _p(_c(S, np.uint16)), _p(out))
+    return out
+
+
+def sparse_int4_down(inter, routes, cmap, n_pos, W, S, group, *, scale_bf16=True, expert_start=0,
+                     expert_count=0, bound=None, out=None):
+    """Sparse INT4-CT down (``sparse_moe_down_int4_ct.comp.template:106-193``).
+    inter bf16 [B, k, I]; W u32 [E, H, I/8]; S u16 [E, H, I/group].  Returns
+    bf16 expert outputs [B, k, H]."""
+    it = _c(inter, np.uint16)
+    r = _c(routes, np.uint32)
+    B, k, I = it.shape
+    E, H, _ = W.shape
+    o = np.zeros((B, k, H), np.uint16) if out is None else _c(out, np.uint16).copy()
+    m = None if cmap is None else _c(cmap, np.uint32)
+    bd = _ct_bound(bound, E)
+    lib().o_sparse_int4_down(_p(it), _p(r), None if m is None else _p(m), n_pos, B, k, E, H, I, group,
+                             int(scale_bf16), expert_start, expert_count, None if bd is None else _p(bd),
+                             _p(_c(W, np.uint32)), _p(_c(S, np.uint16)), _p(o))
+    return o

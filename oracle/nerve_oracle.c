@@ -817,3 +817,102 @@ void o_argmax(const float* logits, int M, int N, uint32_t* ids) {
         ids[m] = bi;
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* Sparse INT4 (compressed-tensors) experts                             */
+/* ------------------------------------------------------------------ */
+
+/* project_row (sparse_moe_gate_up_int4_ct.comp.template:124-149; the down
+ * template's inner loop :156-174 is the same): 64 lane-strided chains of
+ * sum = fma(dot(x[8c..8c+3], lo(w)) + dot(x[8c+4..8c+7], hi(w)), scale, sum)
+ * over the packed words c of the row, then subgroupAdd.  lo/hi: codes 0-3 and
+ * 4-7 of the word (low nibble first), each minus 8; scale[row, 8c / G]. */
+static float ct_row_dot(const float* x, const uint32_t* wrow, const uint16_t* srow, int K, int G, int scale_bf16) {
+    float lanes[SUBGROUP];
+    int pc = K / 8;
+    for (int lane = 0; lane < SUBGROUP; lane++) {
+        float sum = 0.0f;
+        for (int c = lane; c < pc; c += SUBGROUP) {
+            uint32_t w = wrow[c];
+            float lo[4], hi[4];
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (float)((int)((w >> (4 * i)) & 15u) - 8);
+                hi[i] = (float)((int)((w >> (16 + 4 * i)) & 15u) - 8);
+            }
+            uint16_t sb = srow[c * 8 / G];
+            float sc = scale_bf16 ? o_bf16_to_f32(sb) : f16_to_f32(sb);
+            sum = fmaf(dot4(x + 8 * c, lo) + dot4(x + 8 * c + 4, hi), sc, sum);
+        }
+        lanes[lane] = sum;
+    }
+    return subgroup_add(lanes, SUBGROUP);
+}
+
+/* Route selection shared by both stages (…gate_up_int4_ct.comp.template:
+ * 142-166): position p < n_pos names route c = map[p] (map NULL: c = p);
+ * routes whose expert is out of range or (expert_count != 0) outside
+ * [expert_start, expert_start + expert_count) are skipped, as are experts
+ * whose bank entry is marked unbound (bound[e] == 0; bound NULL: all bound). */
+static int ct_route(const uint32_t* routes, const uint32_t* map, int p, int cap, int E, uint32_t start,
+                    uint32_t count, const uint8_t* bound, uint32_t* c_out, uint32_t* e_out) {
+    uint32_t c = map ? map[p] : (uint32_t)p;
+    if (c >= (uint32_t)cap) return 0;
+    uint32_t e = routes[c] & 0xffffu;
+    if (e >= (uint32_t)E) return 0;
+    if (count != 0 && (e < start || e - start >= count)) return 0;
+    if (bound && !bound[e]) return 0;
+    *c_out = c;
+    *e_out = e;
+    return 1;
+}
+
+/* Gate/up (…gate_up_int4_ct.comp.template:168-227): W u32 [E, 2I, H/8] (gate
+ * rows then up rows), S [E, 2I, H/G]; inter bf16 [B, k, I] gets
+ * bf16(bf16(silu(bf16 g)) * bf16 u) for each selected route. */
+void o_sparse_int4_gate_up(const uint16_t* hidden, const uint32_t* routes, const uint32_t* map, int n_pos,
+                           int B, int k, int E, int H, int I, int G, int scale_bf16, uint32_t start,
+                           uint32_t count, const uint8_t* bound, const uint32_t* W, const uint16_t* S,
+                           uint16_t* inter) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)H);
+    for (int p = 0; p < n_pos; p++) {
+        uint32_t c, e;
+        if (!ct_route(routes, map, p, B * k, E, start, count, bound, &c, &e)) continue;
+        int b = (int)(c / (uint32_t)k);
+        for (int j = 0; j < H; j++) x[j] = o_bf16_to_f32(hidden[(size_t)b * H + j]);
+        const uint32_t* we = W + (size_t)e * 2 * I * (H / 8);
+        const uint16_t* se = S + (size_t)e * 2 * I * (H / G);
+        #pragma omp parallel for schedule(static)
+        for (int i = 0; i < I; i++) {
+            float g = ct_row_dot(x, we + (size_t)i * (H / 8), se + (size_t)i * (H / G), H, G, scale_bf16);
+            float u = ct_row_dot(x, we + (size_t)(I + i) * (H / 8), se + (size_t)(I + i) * (H / G), H, G,
+                                 scale_bf16);
+            g = round_bf16(g);
+            u = round_bf16(u);
+            inter[(size_t)c * I + i] = o_f32_to_bf16(round_bf16(g / (1.0f + expf(-g))) * u);
+        }
+    }
+    free(x);
+}
+
+/* Down (…down_int4_ct.comp.template:131-193): W u32 [E, H, I/8], S [E, H,
+ * I/G]; out bf16 [B, k, H] = bf16(bf16(y) * route_weight) for each selected
+ * route, reading that route's intermediate slice inter [B, k, I]. */
+void o_sparse_int4_down(const uint16_t* inter, const uint32_t* routes, const uint32_t* map, int n_pos, int B,
+                        int k, int E, int H, int I, int G, int scale_bf16, uint32_t start, uint32_t count,
+                        const uint8_t* bound, const uint32_t* W, const uint16_t* S, uint16_t* out) {
+    float* x = (float*)malloc(sizeof(float) * (size_t)I);
+    for (int p = 0; p < n_pos; p++) {
+        uint32_t c, e;
+        if (!ct_route(routes, map, p, B * k, E, start, count, bound, &c, &e)) continue;
+        for (int j = 0; j < I; j++) x[j] = o_bf16_to_f32(inter[(size_t)c * I + j]);
+        float wr = o_bf16_to_f32((uint16_t)(routes[c] >> 16));
+        const uint32_t* we = W + (size_t)e * H * (I / 8);
+        const uint16_t* se = S + (size_t)e * H * (I / G);
+        #pragma omp parallel for schedule(static)
+        for (int j = 0; j < H; j++) {
+            float y = ct_row_dot(x, we + (size_t)j * (I / 8), se + (size_t)j * (I / G), I, G, scale_bf16);
+            out[(size_t)c * H + j] = o_f32_to_bf16(round_bf16(round_bf16(y) * wr));
+        }
+    }
+    free(x);
+}

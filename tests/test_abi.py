@@ -54,6 +54,18 @@ def test_null_context_is_rejected():
     (gate_up_spec(2880, 2880, 32, 4, 7.0), 0),
     (down_spec(2880, 2880, 128, 4), 0),
     ("independent_sparse_moe_gate_up_batch1_prequant_mxfp4_e2m1_g32_h4096_i2048_e256_k6_limit7.comp", 0),
+    # sparse INT4-CT experts (nerve/model_package_sparse_projection_shaders.py:80-125)
+    ("sparse_moe_gate_up_int4_ct_sbf16_g32_h3072_i1024_e256_k10.comp", 0),
+    ("sparse_moe_down_batch1_int4_ct_sf16_g32_h3072_i1024_e256_k10.comp", 0),
+    ("sparse_moe_gate_up_batch1_int4_ct_sbf16_g8_h256_i96_e4_k2.comp", 0),
+    ("sparse_moe_gate_up_batch2_int4_ct_sbf16_g32_h3072_i1024_e256_k10.comp", 2),
+    ("sparse_moe_gate_up_int4_ct_sbf16_g12_h96_i96_e4_k2.comp", 2),
+    ("sparse_moe_down_int4_ct_sbf16_g32_h64_i16_e4_k2.comp", 2),
+    ("sparse_moe_gate_up_int4_ct_sbf16_g32_h64_i15_e4_k2.comp", 2),
+    ("sparse_moe_gate_up_int4_ct_sbf16_g32_h64_i16_e5000_k2.comp", 2),
+    ("sparse_moe_gate_up_int4_ct_sbf16_g32_h64_i16_e4_k5.comp", 2),
+    ("sparse_moe_gate_up_int4_ct_sbf16_g16_h48_i16_e4_k2.comp", 3),
+    ("sparse_moe_gate_up_int4_ct_sbf8_g32_h64_i16_e4_k2.comp", 2),
     ("independent_sparse_moe_gate_up_mxfp4_e2m1_g32_h128_i128_e1_k1_limit10.comp", 0),
     # shape rules (the 128 rule relaxed to 32)
     ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_g32_h2890_i2880_e32_k4_limit7.comp", 2),

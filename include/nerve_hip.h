@@ -168,14 +168,15 @@ nerve_hip_status nerve_hip_moe_router_topk(nerve_hip_ctx* ctx, const char* spec,
 
 /* ---- a5 + a6 + a7 in one launch (decode-sized batches) ------------------- */
 
-/* Two launches in place of the router linear (linear_bf16.comp.template:
+/* One launch in place of the router linear (linear_bf16.comp.template:
  * 47-68), the top-k (moe_topk_routed_batch1_bf16.comp.template:71-182 or
  * moe_router_score_topk_batch1_bf16.comp.template:109-219) and the route
  * compaction for `moe_spec`'s projection (moe_route_compact_batch1.comp.
  * template:26-106): the node pair linear -> moe_route of
  * nerve/circuit_lowering_sparse_experts.py:82-88 plus the route-scheduling
  * stage before gate_up (nerve/model_package_batching.py:265-284).  The
- * logits (f32 sums over 16 K slices added in slice order, rounded to bf16)
+ * logits (f32 sums over up to 16 K slices added in slice order, rounded to
+ * bf16; the last block of the launch to finish its slice does the rest)
  * are within one bf16 ulp of nerve_hip_router_linear_bf16's; routes,
  * telemetry, the route map and the control words are exactly what
  * nerve_hip_moe_router_topk + nerve_hip_moe_route_compact produce from

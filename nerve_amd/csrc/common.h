@@ -84,6 +84,7 @@ struct nerve_hip_ctx {
     void* workspace;
     size_t workspace_bytes;
     void* static_scratch;         // device address of this device's static scratch array
+    uint32_t* sync_words;         // arrival counters of single-launch reductions (zeroed at open)
 };
 
 namespace nh {

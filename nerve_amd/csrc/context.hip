@@ -419,8 +419,20 @@ nerve_hip_status nerve_hip_open(int device_ordinal, nerve_hip_ctx** out) {
     e = hipGetSymbolAddress(&scratch_ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !scratch_ptr)
         return nh::fail(NERVE_HIP_DEVICE_ERROR, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    // Arrival counters of launches whose last block finishes the work; zeroed
+    // once here, each launch leaves its counter at zero.
+    uint32_t* sync_words = nullptr;
+    e = hipMalloc(&sync_words, 256);
+    if (e != hipSuccess) return nh::fail(NERVE_HIP_OUT_OF_MEMORY, std::string("hipMalloc: ") + hipGetErrorString(e));
+    e = hipMemset(sync_words, 0, 256);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(sync_words);
+        return nh::fail(NERVE_HIP_DEVICE_ERROR, std::string("hipMemset: ") + hipGetErrorString(e));
+    }
     nerve_hip_ctx* ctx = new nerve_hip_ctx();
     ctx->device = device_ordinal;
+    ctx->sync_words = sync_words;
     ctx->cu_count = prop.multiProcessorCount;
     ctx->workspace = nullptr;
     ctx->workspace_bytes = 0;
@@ -482,11 +494,10 @@ nerve_hip_status nerve_hip_check_specialization(const char* spec) {
 
 void nerve_hip_close(nerve_hip_ctx* ctx) {
     if (!ctx) return;
-    if (ctx->workspace) {
-        (void)hipSetDevice(ctx->device);
-        (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->workspace);
-    }
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();
+    if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->sync_words) (void)hipFree(ctx->sync_words);
     delete ctx;
 }
 

@@ -1183,10 +1183,10 @@ nerve_hip_status launch_head_gemm_t(const HeadGemmArgs& G, uint32_t grid, hipStr
 struct HgConfig {
     uint32_t tm, tn, ns;
 };
-constexpr HgConfig kHgConfigs[3] = {{64, 128, 5}, {128, 128, 4}, {256, 128, 3}};
+constexpr HgConfig kHgConfigs[3] = {{64, 256, 3}, {128, 128, 4}, {256, 128, 3}};
 
 nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid, hipStream_t st) {
-    if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 2, 5>(G, grid, st);
+    if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 4, 3>(G, grid, st);
     if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4>(G, grid, st);
     return launch_head_gemm_t<4, 2, 4, 4, 3>(G, grid, st);
 }

@@ -1083,7 +1083,7 @@ __global__ __launch_bounds__(256) void head_quant_kernel(const uint16_t* __restr
 __global__ __launch_bounds__(256) void head_scale_scan_kernel(const uint16_t* __restrict__ scale_inv, uint32_t N,
                                                               uint32_t rows_pad, uint32_t BR, uint32_t nblk,
                                                               float* __restrict__ sw_row, uint8_t* __restrict__ nonuni) {
-    __shared__ uint16_t sh[256 * 32];
+    __shared__ __attribute__((aligned(16))) uint16_t sh[256 * 32];
     const uint32_t n0 = blockIdx.x * 256, tid = threadIdx.x;
     if (n0 >= N) {
         if (n0 + tid < rows_pad) nonuni[n0 + tid] = 0;
@@ -1093,7 +1093,16 @@ __global__ __launch_bounds__(256) void head_scale_scan_kernel(const uint16_t* __
     const uint32_t r0 = n0 / BR, r1 = last / BR;
     const uint32_t elems = (r1 - r0 + 1) * nblk;           // <= 256 * 32
     const uint16_t* src = scale_inv + (uint64_t)r0 * nblk;
-    for (uint32_t e = tid; e < elems; e += 256) sh[e] = src[e];
+    if ((((uintptr_t)src) & 15) == 0) {
+        // 16-byte pieces (a few per thread), then the ragged tail
+        const uint32_t nv = elems / 8;
+        const v4i* s4 = reinterpret_cast<const v4i*>(src);
+        v4i* d4 = reinterpret_cast<v4i*>(sh);
+        for (uint32_t e = tid; e < nv; e += 256) d4[e] = s4[e];
+        for (uint32_t e = nv * 8 + tid; e < elems; e += 256) sh[e] = src[e];
+    } else {
+        for (uint32_t e = tid; e < elems; e += 256) sh[e] = src[e];
+    }
     __syncthreads();
     const uint32_t n = n0 + tid;
     if (n >= rows_pad) return;

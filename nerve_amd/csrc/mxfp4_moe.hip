@@ -2597,48 +2597,55 @@ nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
 // ---------------------------------------------------------------------------
 // Persistent grouped GEMM for prefill-shaped batches.
 //
-// Work item = (tile of <= 128 routes of one expert, block of 256 weight rows).
-// For gate_up the 256 rows are 128 gate and 128 up rows of the same channels,
+// Work item = (tile of <= 128 routes of one expert, block of 128 weight rows).
+// For gate_up the 128 rows are 64 gate and 64 up rows of the same channels,
 // so SwiGLU runs on the accumulators.  The preparation launch lists the items
 // as (expert, row block, tile) with tiles fastest; every block takes every
 // G-th item, with consecutive items on blocks of one XCD, so the tiles of one
 // expert at one row block run side by side and read the same weight rows
-// while they are in that XCD's L2.  One 512-thread block per CU streams every 128-k chunk of
-// its items (activations 128 x 128 B e4m3, weights 256 x 64 B e2m1, their
-// scales) global -> LDS with global_load_lds into a 4-stage ring that runs
-// across item boundaries: the copies of the next item are in flight while
-// the last chunks of the current one are contracted.
+// while they are in that XCD's L2.
 //
-// The loop is built for few instructions per chunk: every wave issues the
-// same 6 copies per stage (an SGPR base advanced per chunk plus a fixed
-// 32-bit lane offset), so the vmcnt waits are compile-time constants; one
-// barrier per chunk; the step body is unrolled over the 4 stages so every
-// LDS operand read is a fixed register plus an immediate offset.  The next
-// item's descriptor (item record, then its tile's route list) also arrives
-// by LDS copies issued by wave 0 inside the same pipeline.
+// One 512-thread block per CU streams every 256-k chunk of its items global
+// -> LDS with global_load_lds into a 3-stage ring that runs across item
+// boundaries: activations 128 x 256 B e4m3, weights 128 x 128 B e2m1 (each
+// weight row's piece of a chunk is one whole 128-byte line: with 128-k chunks
+// the two halves of every line arrive as separate requests, which measured
+// ~20% slower at the same bytes), their scales.  The copies of the next item
+// are in flight while the last chunks of the current one are contracted.
 //
-// Wave (wm, wn) contracts routes [64 wm, 64 wm + 64) against 64 weight rows
+// Every wave issues a fixed set of copies per stage (an SGPR base advanced
+// per chunk plus a fixed 32-bit lane offset), so the vmcnt waits count
+// copies per stage; one barrier per chunk; the step body is unrolled over the
+// 3 stages so every LDS operand read is a fixed register plus an immediate
+// offset.  The next item's descriptor (item record, then its tile's route
+// list) also arrives by LDS copies issued by wave 0 inside the same pipeline.
+//
+// Wave (wm, wn) contracts routes [32 wm, 32 wm + 32) against 64 weight rows
 // (gate_up: 32 gate + the same 32 up channels).
 // ---------------------------------------------------------------------------
 constexpr uint32_t PG_TM = PG_TILE;
-constexpr uint32_t PG_ROWS = 256;
-constexpr uint32_t PG_NST = 4;
+constexpr uint32_t PG_ROWS = 128;
+constexpr uint32_t PG_NST = 3;
+constexpr uint32_t PG_KC = 256;           // k per chunk
 // LDS map (bytes).  Regions are grouped by kind so a stage is an immediate.
-constexpr uint32_t PG_A_OFF = 0;          // [4][128 routes][128 B], 16-byte pieces XOR-swizzled
-constexpr uint32_t PG_B_OFF = 65536;      // [4][256 rows][64 B], swizzled
-constexpr uint32_t PG_SB_OFF = 131072;    // [4][256 rows][8 B]: the aligned dword pair holding 4 e8m0 bytes
-constexpr uint32_t PG_SA_OFF = 139264;    // [4][128 routes] f32 block scales
-constexpr uint32_t PG_REC_OFF = 141568;   // [2][256 B] item records (48 B used); 141312.. unused
-constexpr uint32_t PG_LIST_OFF = 142080;  // [2][2 KB] tile route lists
-constexpr uint32_t PG_LDS = 146176;
-constexpr uint32_t PG_COPIES = 6;         // copy slots per wave per stage
-constexpr uint32_t PG_MIN_CHUNKS = 10;    // descriptor copies ride on chunks 3 and 6; the list is read at nch - 4
+constexpr uint32_t PG_A_OFF = 0;          // [3][128 routes][256 B], 16-byte pieces XOR-swizzled by route
+constexpr uint32_t PG_B_OFF = 98304;      // [3][128 rows][128 B], pieces XOR-swizzled by row pair
+constexpr uint32_t PG_SB_OFF = 147456;    // [3][128 rows][16 B]: 3 aligned dwords holding the row's 8 e8m0 bytes
+constexpr uint32_t PG_SA_OFF = 153600;    // [3][4 wm][16 r][2 a][2 h] f32 block scales
+constexpr uint32_t PG_REC_OFF = 156672;   // [2][256 B] item records (48 B used)
+constexpr uint32_t PG_LIST_OFF = 157184;  // [2][2 KB] tile route lists
+constexpr uint32_t PG_LDS = 161280;
+constexpr uint32_t PG_COPIES = 8;         // copy slots per wave per stage
+// The item record rides on chunk 2's copies, the route list on chunk 4's,
+// and the next item's copies are set up when chunk nch - 1 is issued (at
+// chunk nch - 3), so an item needs at least 7 chunks.
+constexpr uint32_t PG_MIN_CHUNKS = 7;
 
 __device__ __attribute__((aligned(16))) const uint8_t kZeroPage[1024] = {0};
 
 struct PgArgs {
     const uint8_t* aq;          // e4m3 activations, row stride K
-    const float* as;            // pow2 scales, row stride nch
+    const float* as;            // pow2 scales, row stride ceil(K / 128)
     uint32_t K, N, k;
     const ItemRec* items;
     const PgList* lists;
@@ -2648,8 +2655,7 @@ struct PgArgs {
     float limit;
 };
 
-__device__ __forceinline__ uint32_t pg_swz_a(uint32_t t) { return (t & 7u) ^ ((t >> 3) & 1u); }
-__device__ __forceinline__ uint32_t pg_swz_b(uint32_t r) { return (r ^ (r >> 2)) & 3u; }
+__device__ __forceinline__ uint32_t pg_swz_b(uint32_t r) { return (r >> 1) & 7u; }
 
 template <uint32_t OFF>
 __device__ __forceinline__ uint32_t lds_rd8(uint32_t a) {
@@ -2657,9 +2663,15 @@ __device__ __forceinline__ uint32_t lds_rd8(uint32_t a) {
     asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
     return r;
 }
-// Row of weight tile j inside a wave's 64 rows (gate_up: gate 0, 16, up 128, 144).
+// 16-byte LDS read at any offset below 128 KiB (the immediate field holds 16 bits).
+template <uint32_t OFF>
+__device__ __forceinline__ v4i lds_rd128_far(uint32_t a) {
+    if constexpr (OFF >= 65536u) return lds_rd128<OFF - 65536u>(a + 65536u);
+    else return lds_rd128<OFF>(a);
+}
+// Item row of weight tile j inside a wave's 64 rows (gate_up: gate 0, 16, up 64, 80).
 template <int NMAT>
-__host__ __device__ constexpr uint32_t pg_jrow(uint32_t j) { return NMAT == 2 ? (j >> 1) * 128 + (j & 1) * 16 : j * 16; }
+__host__ __device__ constexpr uint32_t pg_jrow(uint32_t j) { return NMAT == 2 ? (j >> 1) * 64 + (j & 1) * 16 : j * 16; }
 
 
 // LDS dword read that waits for itself inside the same asm statement, so
@@ -2674,10 +2686,8 @@ __device__ __forceinline__ uint32_t lds_rd32_sync(uint32_t a) {
 
 // Issue-side state of the item whose chunks are being copied.
 struct PgIssue {
-    const uint8_t* a_base;      // uniform: activations (chunk 0)
-    const uint8_t* b_base[2];   // uniform: weight matrices of copy slots 2, 3
-    const uint8_t* sb_base;     // uniform: scale matrix of slot 4
-    const uint8_t* sa_base;     // uniform: activation scales (or the zero page)
+    const uint8_t* b_base[2];   // uniform: weight matrices of slots 4, 5
+    const uint8_t* sb_base;     // uniform: scale matrix of slot 6
     uint32_t off[PG_COPIES];    // per lane
     uint32_t tail_ok;           // per lane: bit i = slot i's piece lies inside K in the last chunk
     uint32_t on;                // uniform: bit i = slot i is copied (routes / rows that exist)
@@ -2690,7 +2700,8 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t g = lane >> 4, rr = lane & 15;
-    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + PG_KC - 1) / PG_KC;
+    const uint32_t nsa = (K + 127) / 128;             // activation scales per row
     constexpr uint32_t RPM = PG_ROWS / NMAT;           // rows per matrix in an item
     const uint32_t nrb = (N + RPM - 1) / RPM;
     const uint32_t n_items = __builtin_amdgcn_readfirstlane(*A.n_tiles) * nrb;
@@ -2719,67 +2730,63 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     };
 
     // ---- issue side: set-up of an item's copies (after its descriptor landed) ----
-    // Slots: 0, 1 = activations of routes 8w.., 64+8w..; 2, 3 = weight rows
-    // 16w.., 128+16w..; 4 = scale dword pairs of rows 32w..; 5 = activation
-    // scales of routes 64w.. (waves 0, 1; a padding copy elsewhere).
+    // Slots: 0-3 = activations of routes 32 i + 4 w.. (four 256-byte rows per
+    // copy); 4, 5 = weight rows 64 i + 8 w.. (eight 128-byte rows per copy);
+    // 6 = scale dwords of rows 16 w..; 7 = activation scales of routes
+    // 32 w.. (waves 0-3).
     auto setup_issue = [&](uint32_t par, PgIssue& S) __attribute__((always_inline)) {
         const uint32_t rb = rec_word(par, 0), count = rec_word(par, 1);
         const uint8_t* wp[2] = {rec_ptr(par, 4), rec_ptr(par, 6)};
         const uint8_t* sp[2] = {rec_ptr(par, 8), rec_ptr(par, 10)};
         const uint32_t list = ring + PG_LIST_OFF + par * 2048;
         const uint32_t last = nch - 1;
-        uint32_t tail = 0;
+        uint32_t tail = 0, on = 0;
         // activations
-        for (uint32_t h = 0; h < 2; h++) {
-            const uint32_t t = 64 * h + 8 * wave + (lane >> 3);
-            const uint32_t p = (lane & 7) ^ pg_swz_a(t);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t t = 32 * i + 4 * wave + (lane >> 4);
+            const uint32_t p = (lane & 15) ^ (t & 15);
             const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
-            S.off[h] = row * K + p * 16;
-            tail |= (last * 128 + p * 16 < K ? 1u : 0u) << h;
+            S.off[i] = row * K + p * 16;
+            tail |= (last * PG_KC + p * 16 < K ? 1u : 0u) << i;
+            on |= (32 * i + 4 * wave < count ? 1u : 0u) << i;
         }
-        S.a_base = A.aq;
         // weight rows
-        for (uint32_t h = 0; h < 2; h++) {
-            const uint32_t r = 128 * h + 16 * wave + (lane >> 2);
-            const uint32_t p = (lane & 3) ^ pg_swz_b(r);
-            const uint32_t mat = r / RPM, n = rb * RPM + r % RPM;
-            S.off[2 + h] = (n < N ? n : 0) * RB + p * 16;
-            S.b_base[h] = wp[(128 * h) / RPM];
-            (void)mat;
-            tail |= (last * 128 + p * 32 < K ? 1u : 0u) << (2 + h);
+#pragma unroll
+        for (uint32_t i = 0; i < 2; i++) {
+            const uint32_t r = 64 * i + 8 * wave + (lane >> 3);
+            const uint32_t p = (lane & 7) ^ pg_swz_b(r);
+            const uint32_t n = rb * RPM + r % RPM;
+            S.off[4 + i] = (n < N ? n : 0) * RB + p * 16;
+            S.b_base[i] = wp[(64 * i) / RPM];
+            tail |= (last * (PG_KC / 2) + p * 16 < RB ? 1u : 0u) << (4 + i);
+            on |= (rb * RPM + (64 * i + 8 * wave) % RPM < N ? 1u : 0u) << (4 + i);
         }
-        // weight scale dword pairs
+        // weight scale dwords: 3 aligned dwords cover a row's 8 bytes of a
+        // chunk (its row offset is even); the fourth slot repeats the third
         {
-            const uint32_t r = 32 * wave + (lane >> 1), hh = lane & 1;
+            const uint32_t r = 16 * wave + (lane >> 2), d = lane & 3;
             const uint32_t n = rb * RPM + r % RPM;
             const uint32_t rowoff = (n < N ? n : 0) * SB;
-            S.off[4] = (rowoff & ~3u) + 4 * hh;
-            S.sb_base = sp[(32 * wave) / RPM];
-            const uint32_t a_last = (rowoff & ~3u) + 4 * last;
-            tail |= (hh == 0 || a_last + 4 < rowoff + SB ? 1u : 0u) << 4;
+            S.off[6] = (rowoff & ~3u) + 4 * (d < 3 ? d : 2u);
+            S.sb_base = sp[(16 * wave) / RPM];
+            tail |= (d < 3 && (rowoff & ~3u) + 8 * last + 4 * d < rowoff + SB ? 1u : 0u) << 6;
+            on |= (rb * RPM + (16 * wave) % RPM < N ? 1u : 0u) << 6;
         }
-        // activation scales, stored so that LDS word 4 rr + a of half p holds
-        // route 64 p + 16 a + rr: a lane reads its 4 subtiles' scales at once
-        if (wave < 2) {
-            const uint32_t t = 64 * wave + 16 * (lane & 3) + (lane >> 2);
+        // activation scales, stored so that LDS word 4 r + 2 a + h of route
+        // group w holds route 32 w + 16 a + r, block 2 c + h: a lane reads its
+        // 2 subtiles x 2 halves at once
+        if (wave < 4) {
+            const uint32_t r = lane >> 2, a = (lane >> 1) & 1u, h = lane & 1u;
+            const uint32_t t = 32 * wave + 16 * a + r;
             const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
-            S.off[5] = row * nch * 4;
-            S.sa_base = reinterpret_cast<const uint8_t*>(A.as);
+            S.off[7] = row * nsa * 4 + h * 4;
+            tail |= (2 * last + h < nsa ? 1u : 0u) << 7;
+            on |= (32 * wave < count ? 1u : 0u) << 7;
         } else {
-            S.off[5] = 0;
-            S.sa_base = kZeroPage;
+            S.off[7] = 0;
         }
-        tail |= 1u << 5;
         S.tail_ok = tail;
-        // Slots with nothing to copy: route groups past the count, weight
-        // rows past N, the activation scales outside waves 0-1.
-        uint32_t on = 0;
-        on |= (8 * wave < count ? 1u : 0u) << 0;
-        on |= (64 + 8 * wave < count ? 1u : 0u) << 1;
-        on |= (rb * RPM + (16 * wave) % RPM < N ? 1u : 0u) << 2;
-        on |= (rb * RPM + (128 + 16 * wave) % RPM < N ? 1u : 0u) << 3;
-        on |= (rb * RPM + (32 * wave) % RPM < N ? 1u : 0u) << 4;
-        on |= (wave < 2 && 64 * wave < count ? 1u : 0u) << 5;
         S.on = on;
         S.n = __builtin_popcount(on);
     };
@@ -2787,34 +2794,27 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     // Copies of chunk c of the issue item into stage ST.
     auto issue_chunk = [&](const PgIssue& S, uint32_t c, auto st_tag) __attribute__((always_inline)) {
         constexpr uint32_t ST = decltype(st_tag)::value;
-        uint8_t* const dA = pg_ring + PG_A_OFF + ST * 16384 + wave * 1024;
+        uint8_t* const dA = pg_ring + PG_A_OFF + ST * 32768 + wave * 1024;
         uint8_t* const dB = pg_ring + PG_B_OFF + ST * 16384 + wave * 1024;
         uint8_t* const dS = pg_ring + PG_SB_OFF + ST * 2048 + wave * 256;
-        uint8_t* const dT = pg_ring + PG_SA_OFF + ST * 512 + (wave & 1) * 256;
+        uint8_t* const dT = pg_ring + PG_SA_OFF + ST * 1024 + (wave & 3) * 256;
         const uint32_t on = S.on;
-        if (c + 1 < nch) {
-            const uint8_t* a = S.a_base + c * 128;
-            if (on & 1) __builtin_amdgcn_global_load_lds(a + S.off[0], dA, 16, 0, 0);
-            if (on & 2) __builtin_amdgcn_global_load_lds(a + S.off[1], dA + 8192, 16, 0, 0);
-            if (on & 4) __builtin_amdgcn_global_load_lds(S.b_base[0] + c * 64 + S.off[2], dB, 16, 0, 0);
-            if (on & 8) __builtin_amdgcn_global_load_lds(S.b_base[1] + c * 64 + S.off[3], dB + 8192, 16, 0, 0);
-            if (on & 16) __builtin_amdgcn_global_load_lds(S.sb_base + c * 4 + S.off[4], dS, 4, 0, 0);
-            if (on & 32) __builtin_amdgcn_global_load_lds(S.sa_base + c * 4 + S.off[5], dT, 4, 0, 0);
-        } else {
-            // Last chunk: pieces past K (and the scale dword past a row's
-            // end) come from the zero page.
-            const uint32_t ok = S.tail_ok;
-            const uint8_t* a = S.a_base + c * 128;
-            if (on & 1) __builtin_amdgcn_global_load_lds((ok & 1) ? a + S.off[0] : kZeroPage, dA, 16, 0, 0);
-            if (on & 2) __builtin_amdgcn_global_load_lds((ok & 2) ? a + S.off[1] : kZeroPage, dA + 8192, 16, 0, 0);
-            if (on & 4)
-                __builtin_amdgcn_global_load_lds((ok & 4) ? S.b_base[0] + c * 64 + S.off[2] : kZeroPage, dB, 16, 0, 0);
-            if (on & 8)
-                __builtin_amdgcn_global_load_lds((ok & 8) ? S.b_base[1] + c * 64 + S.off[3] : kZeroPage, dB + 8192, 16,
-                                                 0, 0);
-            if (on & 16) __builtin_amdgcn_global_load_lds((ok & 16) ? S.sb_base + c * 4 + S.off[4] : kZeroPage, dS, 4, 0, 0);
-            if (on & 32) __builtin_amdgcn_global_load_lds(S.sa_base + c * 4 + S.off[5], dT, 4, 0, 0);
-        }
+        const uint8_t* a = A.aq + c * PG_KC;
+        const uint8_t* b0 = S.b_base[0] + c * (PG_KC / 2);
+        const uint8_t* b1 = S.b_base[1] + c * (PG_KC / 2);
+        const uint8_t* sb = S.sb_base + c * (PG_KC / 32);
+        const uint8_t* sa = reinterpret_cast<const uint8_t*>(A.as) + c * 8;
+        // In the last chunk, pieces past K (and scale dwords past a row's
+        // end) come from the zero page.
+        const uint32_t ok = c + 1 < nch ? 0xffu : S.tail_ok;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++)
+            if (on & (1u << i))
+                __builtin_amdgcn_global_load_lds((ok & (1u << i)) ? a + S.off[i] : kZeroPage, dA + i * 8192, 16, 0, 0);
+        if (on & 16) __builtin_amdgcn_global_load_lds((ok & 16) ? b0 + S.off[4] : kZeroPage, dB, 16, 0, 0);
+        if (on & 32) __builtin_amdgcn_global_load_lds((ok & 32) ? b1 + S.off[5] : kZeroPage, dB + 8192, 16, 0, 0);
+        if (on & 64) __builtin_amdgcn_global_load_lds((ok & 64) ? sb + S.off[6] : kZeroPage, dS, 4, 0, 0);
+        if (on & 128) __builtin_amdgcn_global_load_lds((ok & 128) ? sa + S.off[7] : kZeroPage, dT, 4, 0, 0);
     };
 
     // ---- first item: descriptor copied synchronously ----
@@ -2835,16 +2835,15 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     setup_issue(0, S);
     uint32_t ic = 0, ipar = 0, iitem = item;   // issue item: next chunk, descriptor slot, index
     bool issuing = true;
-    // Issues the next chunk group (one per stage) and moves to the next item
-    // after the last chunk of the current one.
-    uint32_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;   // copies this wave issued into each stage
+    // Issues the next chunk (one per stage) and moves to the next item after
+    // the last chunk of the current one.
+    uint32_t q0 = 0, q1 = 0, q2 = 0;   // copies this wave issued into each stage
     auto issue_next = [&](auto st_tag) __attribute__((always_inline)) {
         constexpr uint32_t ST = decltype(st_tag)::value;
         const uint32_t nq = issuing ? S.n : 0u;
         if (ST == 0) q0 = nq;
         if (ST == 1) q1 = nq;
         if (ST == 2) q2 = nq;
-        if (ST == 3) q3 = nq;
         if (issuing) {
             issue_chunk(S, ic, st_tag);
             if (++ic == nch) {
@@ -2858,33 +2857,38 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     };
     issue_next(std::integral_constant<uint32_t, 0>{});
     issue_next(std::integral_constant<uint32_t, 1>{});
-    issue_next(std::integral_constant<uint32_t, 2>{});
 
     // ---- compute side ----
-    const uint32_t wm = wave >> 2, wn = wave & 3;
+    const uint32_t wm = wave >> 1, wn = wave & 1;
     const uint32_t brow0 = NMAT == 2 ? wn * 32 : wn * 64;
     auto jrow = [](int j) __attribute__((always_inline)) -> uint32_t { return pg_jrow<NMAT>((uint32_t)j); };
-    const uint32_t ta = 64 * wm + rr, fa = pg_swz_a(rr);
-    const uint32_t LA_lo = ring + PG_A_OFF + ta * 128 + (g ^ fa) * 16;
-    const uint32_t LA_hi = ring + PG_A_OFF + ta * 128 + ((g ^ fa) ^ 4u) * 16;
+    // Activation operand of lane (g, r): route 32 wm + 16 a + r, k 16 g.. and
+    // 64 + 16 g.. of each 128-k half h, at pieces (8 h + g) ^ r, (8 h + 4 + g) ^ r.
+    const uint32_t ta = 32 * wm + rr;
+    uint32_t LA[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) LA[q] = ring + PG_A_OFF + ta * 256 + (((4 * q) + g) ^ rr) * 16;
     const uint32_t LSA = ring + PG_SA_OFF + wm * 256 + rr * 16;
-    const uint32_t LB = ring + PG_B_OFF + (brow0 + rr) * 64 + (g ^ pg_swz_b(rr)) * 16;
+    // Weight operand of lane (g, r): row r of the tile, bytes 64 h + 16 g.
+    const uint32_t sw = pg_swz_b(rr);
+    const uint32_t LB0 = ring + PG_B_OFF + (brow0 + rr) * 128 + ((g ^ sw) * 16);
+    const uint32_t LB1 = ring + PG_B_OFF + (brow0 + rr) * 128 + (((4 + g) ^ sw) * 16);
 
     uint32_t cpar = 0, c = 0;              // compute item descriptor slot, chunk
     uint32_t count = 0, rb = 0, alim = 0;
     uint32_t LSB[4];
-    v4f acc[4][4];
+    v4f acc[2][4];
     auto start_item = [&]() __attribute__((always_inline)) {
         rb = rec_word(cpar, 0);
         count = rec_word(cpar, 1);
-        alim = count > 64 * wm ? min(4u, (count - 64 * wm + 15) / 16) : 0u;
+        alim = count > 32 * wm ? min(2u, (count - 32 * wm + 15) / 16) : 0u;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t r = brow0 + jrow(j) + rr, n = rb * RPM + r % RPM;
-            LSB[j] = ring + PG_SB_OFF + r * 8 + (((n < N ? n : 0) * SB) & 3u) + g;
+            LSB[j] = ring + PG_SB_OFF + r * 16 + (((n < N ? n : 0) * SB) & 3u) + g;
         }
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < 2; a++)
 #pragma unroll
             for (int j = 0; j < 4; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
     };
@@ -2894,11 +2898,11 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     auto epilogue = [&]() __attribute__((always_inline)) {
         const uint32_t list = ring + PG_LIST_OFF + cpar * 2048;
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
+        for (int a = 0; a < 2; a++) {
             if ((uint32_t)a >= alim) continue;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t t = 64 * wm + 16 * a + 4 * g + i;
+                const uint32_t t = 32 * wm + 16 * a + 4 * g + i;
                 const uint32_t r = lds_rd32_sync<0>(list + 4 * t);
                 const uint32_t wrb = lds_rd32_sync<1024>(list + 4 * t);
                 if (t >= count) continue;
@@ -2930,61 +2934,76 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     };
 
     // One pipeline step on stage ST: wait for this chunk, barrier, issue the
-    // chunk three ahead (and the descriptor copies riding on chunks 3 and 6),
-    // contract, and on the item's last chunk write it out and switch items.
-    // Returns false when the block has no more work.
+    // chunk two ahead (wave 0 first copies the next item's record at chunk 0
+    // and its route list at chunk 2), contract, and on the item's last chunk
+    // write it out and switch items.  Returns false when the block has no
+    // more work.
     auto step = [&](auto st_tag) __attribute__((always_inline)) -> bool {
         constexpr uint32_t ST = decltype(st_tag)::value;
-        // Copies issued after this chunk's: those of the next two chunks
-        // (counted per stage when issued), plus wave 0's descriptor copies
-        // riding on them.
-        const uint32_t l1 = c + 1 < nch ? c + 1 : c + 1 - nch, l2 = c + 2 < nch ? c + 2 : c + 2 - nch;
-        constexpr uint32_t S1 = (ST + 1) % PG_NST, S2 = (ST + 2) % PG_NST;
-        uint32_t x = (S1 == 0 ? q0 : S1 == 1 ? q1 : S1 == 2 ? q2 : q3) + (S2 == 0 ? q0 : S2 == 1 ? q1 : S2 == 2 ? q2 : q3);
-        if (wave == 0) x += (l1 == 3 ? 1u : 0u) + (l1 == 6 ? 2u : 0u) + (l2 == 3 ? 1u : 0u) + (l2 == 6 ? 2u : 0u);
+        // Copies issued after this chunk's: the next chunk's, plus wave 0's
+        // descriptor copies issued in the previous step (record at chunk 0,
+        // list at chunk 2).
+        constexpr uint32_t S1 = (ST + 1) % PG_NST;
+        uint32_t x = S1 == 0 ? q0 : S1 == 1 ? q1 : q2;
+        if (wave == 0) x += (c == 1 ? 1u : 0u) + (c == 3 ? 2u : 0u);
         wait_vm(x);
         __builtin_amdgcn_s_barrier();
-        // Chunk c + 3 (of this item or the next) goes into stage ST + 3.
-        issue_next(std::integral_constant<uint32_t, (ST + 3) % PG_NST>{});
         if (wave == 0) {
             if (c == 0) copy_rec(item + G, cpar ^ 1u);
-            else if (c == 3) copy_list(cpar ^ 1u);
+            else if (c == 2) copy_list(cpar ^ 1u);
         }
+        // Chunk c + 2 (of this item or the next) goes into stage ST + 2.
+        issue_next(std::integral_constant<uint32_t, (ST + 2) % PG_NST>{});
         // ---- contract chunk c from stage ST (waves without routes skip it) ----
         if (alim != 0) {
-            v4i lo[4], hi[4], w[4];
+            v4i lo[2][2], hi[2][2], w[4][2];
             v4i sa4;
-            uint32_t sbv[4];
+            uint32_t sbv[4][2];
             static_for<4>([&](auto ji) __attribute__((always_inline)) {
                 constexpr uint32_t j = decltype(ji)::value;
-                w[j] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 64>(LB);
+                w[j][0] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 128>(LB0);
+                w[j][1] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 128>(LB1);
             });
 #pragma unroll
-            for (int j = 0; j < 4; j++) sbv[j] = lds_rd8<ST * 2048>(LSB[j]);
-            sa4 = lds_rd128<ST * 512>(LSA);
-            static_for<4>([&](auto ai) __attribute__((always_inline)) {
+            for (int j = 0; j < 4; j++) {
+                sbv[j][0] = lds_rd8<ST * 2048>(LSB[j]);
+                sbv[j][1] = lds_rd8<ST * 2048 + 4>(LSB[j]);
+            }
+            sa4 = lds_rd128<ST * 1024>(LSA);
+            static_for<2>([&](auto ai) __attribute__((always_inline)) {
                 constexpr uint32_t a = decltype(ai)::value;
                 if (a < alim) {
-                    lo[a] = lds_rd128<ST * 16384 + a * 2048>(LA_lo);
-                    hi[a] = lds_rd128<ST * 16384 + a * 2048>(LA_hi);
+                    lo[a][0] = lds_rd128_far<ST * 32768 + a * 4096>(LA[0]);
+                    hi[a][0] = lds_rd128_far<ST * 32768 + a * 4096>(LA[1]);
+                    lo[a][1] = lds_rd128_far<ST * 32768 + a * 4096>(LA[2]);
+                    hi[a][1] = lds_rd128_far<ST * 32768 + a * 4096>(LA[3]);
                 }
             });
             asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]), "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]),
-                           "+v"(hi[3]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(sa4), "+v"(sbv[0]),
-                           "+v"(sbv[1]), "+v"(sbv[2]), "+v"(sbv[3]));
+                         : "+v"(lo[0][0]), "+v"(lo[0][1]), "+v"(lo[1][0]), "+v"(lo[1][1]), "+v"(hi[0][0]),
+                           "+v"(hi[0][1]), "+v"(hi[1][0]), "+v"(hi[1][1]), "+v"(w[0][0]), "+v"(w[0][1]),
+                           "+v"(w[1][0]), "+v"(w[1][1]), "+v"(w[2][0]), "+v"(w[2][1]), "+v"(w[3][0]),
+                           "+v"(w[3][1]), "+v"(sa4), "+v"(sbv[0][0]), "+v"(sbv[0][1]), "+v"(sbv[1][0]),
+                           "+v"(sbv[1][1]), "+v"(sbv[2][0]), "+v"(sbv[2][1]), "+v"(sbv[3][0]), "+v"(sbv[3][1]));
             // Scale blocks past K (last chunk) read bytes beyond the row.
-            const bool bvalid = c * 4 + g < SB;
 #pragma unroll
-            for (int j = 0; j < 4; j++) sbv[j] = bvalid ? sbv[j] : 127u;
-            const uint32_t sav[4] = {(uint32_t)sa4.x, (uint32_t)sa4.y, (uint32_t)sa4.z, (uint32_t)sa4.w};
+            for (int h = 0; h < 2; h++) {
+                const bool bvalid = c * 8 + 4 * h + g < SB;
 #pragma unroll
-            for (int a = 0; a < 4; a++) {
+                for (int j = 0; j < 4; j++) sbv[j][h] = bvalid ? sbv[j][h] : 127u;
+            }
+            const uint32_t sav[2][2] = {{(uint32_t)sa4.x, (uint32_t)sa4.y}, {(uint32_t)sa4.z, (uint32_t)sa4.w}};
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
                 if ((uint32_t)a >= alim) continue;
-                const v8i av = v8i{lo[a].x, lo[a].y, lo[a].z, lo[a].w, hi[a].x, hi[a].y, hi[a].z, hi[a].w};
-                const uint32_t se = (sav[a] >> 23) & 0xffu;
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[a][j] = mfma_fp8_fp4(av, w[j], se, sbv[j], acc[a][j]);
+                for (int h = 0; h < 2; h++) {
+                    const v8i av = v8i{lo[a][h].x, lo[a][h].y, lo[a][h].z, lo[a][h].w,
+                                       hi[a][h].x, hi[a][h].y, hi[a][h].z, hi[a][h].w};
+                    const uint32_t se = (sav[a][h] >> 23) & 0xffu;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[a][j] = mfma_fp8_fp4(av, w[j][h], se, sbv[j][h], acc[a][j]);
+                }
             }
         }
         if (++c < nch) return true;
@@ -3002,7 +3021,6 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
         if (!step(std::integral_constant<uint32_t, 0>{})) break;
         if (!step(std::integral_constant<uint32_t, 1>{})) break;
         if (!step(std::integral_constant<uint32_t, 2>{})) break;
-        if (!step(std::integral_constant<uint32_t, 3>{})) break;
     }
 }
 
@@ -3138,7 +3156,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     const bool grouped = !wf && (cap >= 512 || K > 4096);
     // Persistent grouped GEMM: enough chunks per item for the descriptor
     // prefetch rounds.
-    const bool persistent = grouped && (K + 127) / 128 >= PG_MIN_CHUNKS;
+    const bool persistent = grouped && (K + PG_KC - 1) / PG_KC >= PG_MIN_CHUNKS;
     const uint32_t TM = persistent ? PG_TM : grouped ? 64 : 16;
     const uint32_t max_tiles = (cap + TM - 1) / TM + (E < cap ? E : cap);
     nh::Carver cv;

@@ -169,9 +169,11 @@ def _moe_case(E, k, B, H, I, seed):
                                        (8, 2, 6, 1024, 512), (12, 3, 9, 4096, 1024),
                                        # >= 512 routes: the LDS-staged grouped GEMM path
                                        (16, 4, 160, 512, 384), (8, 2, 300, 2880, 160), (64, 8, 70, 224, 288),
-                                       # persistent grouped GEMM on both stages: K tail of 64,
-                                       # partial row blocks, experts with several 128-route tiles
-                                       (16, 4, 140, 1344, 1408), (4, 2, 300, 1344, 1408)])
+                                       # grouped GEMM at K = 1344 / 1408 (below the persistent kernel's 7 chunks)
+                                       (16, 4, 140, 1344, 1408),
+                                       # persistent grouped GEMM on both stages: K tails of 64 / 128 and
+                                       # 32 / 32 bytes, partial row blocks, experts with several 128-route tiles
+                                       (16, 4, 140, 1856, 1664), (4, 2, 300, 1856, 1664), (8, 2, 280, 2080, 1568)])
 def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
     d, routes, hidden = _moe_case(E, k, B, H, I, seed=E * 100 + B)
     rig = MoeRig(dev, d, routes)

@@ -323,6 +323,32 @@ __device__ __forceinline__ bool record_valid(uint32_t slot, uint32_t n_records, 
 constexpr uint32_t PREP_R = 8;                 // slots per thread whose route ids stay in registers
 constexpr uint16_t NO_EXPERT = 0xffffu;
 
+// atomicAdd(&cnt[e], 1) for every lane of the wave with e != NO_EXPERT,
+// one LDS atomic per distinct expert of the wave (routes come in expert
+// order from the compaction, so a wave mostly holds one or two experts and
+// the hot experts' counters would otherwise serialize 64-way).  Returns the
+// lane's old count plus its rank among the wave's lanes of the same expert.
+__device__ __forceinline__ uint32_t wave_add_one(uint32_t* cnt, uint32_t e, bool want_old) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint64_t todo = __ballot(e != NO_EXPERT);
+    uint32_t mine = 0;
+    while (todo) {
+        const uint32_t leader = (uint32_t)__ffsll((unsigned long long)todo) - 1u;
+        const uint32_t el = __shfl(e, leader);
+        const uint64_t m = __ballot(e == el);
+        uint32_t base = 0;
+        if (lane == leader) {
+            if (want_old) base = atomicAdd(&cnt[el], (uint32_t)__popcll(m));
+            else atomicAdd(&cnt[el], (uint32_t)__popcll(m));
+        }
+        if (want_old) base = __shfl(base, leader);
+        if (e == el) mine = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+        todo &= ~m;
+    }
+    return mine;
+}
+
+
 // Latency matters here (decode runs this once per projection), so the block
 // needs only two rounds of dependent global loads: (1) slot words of every
 // expert's parameters, the compacted route map entries and the control
@@ -338,6 +364,10 @@ __device__ void build_tiles(const TileArgs& A) {
     __shared__ uint8_t valid[MAXE];
     __shared__ uint32_t wave_tot[16];
     __shared__ uint32_t total;
+    // Expert pointers (w0, s0, w1, s1) for the work-item expansion, when
+    // every expert has its own thread.
+    constexpr bool EPTR = MAXE <= 1024;
+    __shared__ const uint8_t* eptr[EPTR ? MAXE : 1][4];
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
     const uint32_t cap = A.batch_width * A.k;
     const uint32_t P = A.P;   // 4 (gate, gate scales, up, up scales) or 2 (down, down scales)
@@ -351,8 +381,16 @@ __device__ void build_tiles(const TileArgs& A) {
             if (p < P && idx < A.n_slot_words) slot[p] = A.slots[idx];
         }
     }
-    uint32_t rword = 0xffffffffu;
-    if (tid < cap) rword = A.frames[(uint64_t)(tid / A.k) * A.frame_words + A.data_words + tid % A.k];
+    // Slots c = tid + i nt for i < PREP_R keep their route index and route
+    // word in registers, loaded in these two rounds.  (Slots beyond PREP_R nt
+    // take a plain loop.)
+    uint32_t rw_r[PREP_R], rt_r[PREP_R];
+#pragma unroll
+    for (uint32_t i = 0; i < PREP_R; i++) {
+        const uint32_t c = tid + i * nt;
+        rw_r[i] = c < cap ? A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k] : 0xffffffffu;
+    }
+    const uint32_t rword = rw_r[0];
     const uint32_t c2 = A.control[2], c3 = A.control[3];
     // ---- round 2: address records, route word
     uint32_t rec[4][8];
@@ -362,8 +400,12 @@ __device__ void build_tiles(const TileArgs& A) {
 #pragma unroll
         for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? A.addr[(uint64_t)slot[p] * 8 + j] : 0u;
     }
-    uint32_t route = 0;
-    if (rword < cap) route = A.routes[rword];
+#pragma unroll
+    for (uint32_t i = 0; i < PREP_R; i++) {
+        const uint32_t c = tid + i * nt;
+        rt_r[i] = (c < cap && rw_r[i] < cap) ? A.routes[rw_r[i]] : 0u;
+    }
+    const uint32_t route = rt_r[0];
 
     uint32_t n = c2 != 0u ? c3 : cap;
     if (n > cap) n = cap;
@@ -396,6 +438,12 @@ __device__ void build_tiles(const TileArgs& A) {
             my_w[m] = reinterpret_cast<const uint8_t*>((uint64_t)rec[2 * m][0] | ((uint64_t)rec[2 * m][1] << 32));
             my_s[m] = reinterpret_cast<const uint8_t*>((uint64_t)rec[2 * m + 1][0] | ((uint64_t)rec[2 * m + 1][1] << 32));
         }
+        if constexpr (EPTR) {
+            eptr[tid][0] = my_w[0];
+            eptr[tid][1] = my_s[0];
+            eptr[tid][2] = my_w[1];
+            eptr[tid][3] = my_s[1];
+        }
     }
     // Experts beyond the block size (E > 1024) take the plain path (compact
     // MXFP4 only: the host sends the other representations here only with
@@ -417,37 +465,21 @@ __device__ void build_tiles(const TileArgs& A) {
         const uint32_t e = rt & 0xffffu;
         return (e < A.E && valid[e]) ? e : NO_EXPERT;
     };
-    if (tid < cap) {
-        const uint32_t e = slot_expert(tid, rword, route);
-        if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
-    }
-    // Slots c = tid + i nt for i < PREP_R keep their route index and route
-    // word in registers: two batched rounds of loads instead of a dependent
-    // pair per slot.  (Slots beyond PREP_R nt take the plain loop.)
-    uint32_t rw_r[PREP_R], rt_r[PREP_R];
-    rw_r[0] = rword;
-    rt_r[0] = route;
+    wave_add_one(cnt, tid < cap ? slot_expert(tid, rword, route) : NO_EXPERT, false);
 #pragma unroll
     for (uint32_t i = 1; i < PREP_R; i++) {
         const uint32_t c = tid + i * nt;
-        rw_r[i] = c < cap ? A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k] : 0xffffffffu;
+        if (c - tid >= cap) break;   // uniform: no lane of the block has slots this far
+        wave_add_one(cnt, c < cap ? slot_expert(c, rw_r[i], rt_r[i]) : NO_EXPERT, false);
     }
-#pragma unroll
-    for (uint32_t i = 1; i < PREP_R; i++) {
-        const uint32_t c = tid + i * nt;
-        rt_r[i] = (c < cap && rw_r[i] < cap) ? A.routes[rw_r[i]] : 0u;
-    }
-#pragma unroll
-    for (uint32_t i = 1; i < PREP_R; i++) {
-        const uint32_t c = tid + i * nt;
-        if (c >= cap) continue;
-        const uint32_t e = slot_expert(c, rw_r[i], rt_r[i]);
-        if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
-    }
-    for (uint32_t c = tid + PREP_R * nt; c < cap; c += nt) {
-        const uint32_t rw = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-        const uint32_t e = slot_expert(c, rw, rw < cap ? A.routes[rw] : 0u);
-        if (e != NO_EXPERT) atomicAdd(&cnt[e], 1u);
+    for (uint32_t c0 = PREP_R * nt; c0 < cap; c0 += nt) {
+        const uint32_t c = c0 + tid;
+        uint32_t e = NO_EXPERT;
+        if (c < cap) {
+            const uint32_t rw = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+            e = slot_expert(c, rw, rw < cap ? A.routes[rw] : 0u);
+        }
+        wave_add_one(cnt, e, false);
     }
     __syncthreads();
     // Exclusive scans of route counts and tile counts over experts.
@@ -499,8 +531,10 @@ __device__ void build_tiles(const TileArgs& A) {
     // Route slots in expert order.  For the persistent grouped GEMM the slot
     // also goes into its tile's route list (position rank % TM of tile
     // tst[e] + rank / TM), with its activation row and route weight.
+    // Called by every lane of the wave (e = NO_EXPERT places nothing).
     auto place = [&](uint32_t e, uint32_t r, uint32_t rt) {
-        const uint32_t pos = atomicAdd(&cur[e], 1u);
+        const uint32_t pos = wave_add_one(cur, e, true);
+        if (e == NO_EXPERT) return;
         A.seg_list[pos] = r;
         if (A.lists) {
             const uint32_t rank = pos - est[e], t = tst[e] + rank / A.TM, j = rank % A.TM;
@@ -515,15 +549,18 @@ __device__ void build_tiles(const TileArgs& A) {
 #pragma unroll
     for (uint32_t i = 0; i < PREP_R; i++) {
         const uint32_t c = tid + i * nt;
-        if (c >= n) continue;
-        const uint32_t e = slot_expert(c, rw_r[i], rt_r[i]);
-        if (e != NO_EXPERT) place(e, rw_r[i], rt_r[i]);
+        if (c - tid >= n) break;     // uniform
+        place(c < n ? slot_expert(c, rw_r[i], rt_r[i]) : NO_EXPERT, rw_r[i], rt_r[i]);
     }
-    for (uint32_t c = tid + PREP_R * nt; c < n; c += nt) {
-        const uint32_t r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
-        const uint32_t rt = r < cap ? A.routes[r] : 0u;
-        const uint32_t e = slot_expert(c, r, rt);
-        if (e != NO_EXPERT) place(e, r, rt);
+    for (uint32_t c0 = PREP_R * nt; c0 < n; c0 += nt) {
+        const uint32_t c = c0 + tid;
+        uint32_t r = 0, rt = 0, e = NO_EXPERT;
+        if (c < n) {
+            r = A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k];
+            rt = r < cap ? A.routes[r] : 0u;
+            e = slot_expert(c, r, rt);
+        }
+        place(e, r, rt);
     }
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
     if (A.items) {
@@ -549,10 +586,17 @@ __device__ void build_tiles(const TileArgs& A) {
             o.count = min(A.TM, cnt[e] - kk * A.TM);
             o.tile = t;
             o.pad = 0;
-            o.w[0] = A.recs[t].w[0];
-            o.w[1] = A.recs[t].w[1];
-            o.s[0] = A.recs[t].s[0];
-            o.s[1] = A.recs[t].s[1];
+            if constexpr (EPTR) {
+                o.w[0] = eptr[e][0];
+                o.s[0] = eptr[e][1];
+                o.w[1] = eptr[e][2];
+                o.s[1] = eptr[e][3];
+            } else {
+                o.w[0] = A.recs[t].w[0];
+                o.w[1] = A.recs[t].w[1];
+                o.s[0] = A.recs[t].s[0];
+                o.s[1] = A.recs[t].s[1];
+            }
             A.items[i] = o;
         }
     }

@@ -309,6 +309,31 @@ __global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* __restrict_
     out[idx] = (uint16_t)f32_to_bf16(acc * routed_scale);
 }
 
+// The same combine, 8 columns per thread with 16-byte loads and stores
+// (H % 8 == 0, 16-byte aligned buffers).
+__global__ __launch_bounds__(256) void reduce8_kernel(const uint16_t* __restrict__ eo, uint16_t* __restrict__ out,
+                                                      uint32_t B, uint32_t H, uint32_t k, float routed_scale) {
+    const uint32_t H8 = H / 8;
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)B * H8) return;
+    const uint32_t b = (uint32_t)(idx / H8), j = (uint32_t)(idx % H8) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (uint32_t r = 0; r < k; r++) {
+        const v4i v = *reinterpret_cast<const v4i*>(eo + ((uint64_t)b * k + r) * H + j);
+        const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            acc[2 * q] = round_bf16(acc[2 * q] + bf16_to_f32(w[q] & 0xffffu));
+            acc[2 * q + 1] = round_bf16(acc[2 * q + 1] + bf16_to_f32(w[q] >> 16));
+        }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        o[q] = f32_to_bf16(acc[2 * q] * routed_scale) | (f32_to_bf16(acc[2 * q + 1] * routed_scale) << 16);
+    *reinterpret_cast<v4i*>(out + (uint64_t)b * H + j) = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+}
+
 
 }  // namespace
 
@@ -466,9 +491,14 @@ nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_out
     if (experts_per_token == 0) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "experts_per_token must be positive");
     const uint64_t total = (uint64_t)batch_width * hidden;
     if (total == 0) return nh::ok();
-    reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        static_cast<const uint16_t*>(expert_outputs), static_cast<uint16_t*>(out_bf16), batch_width, hidden,
-        experts_per_token, routed_scale);
+    if (hidden % 8 == 0 && (((uintptr_t)expert_outputs | (uintptr_t)out_bf16) & 15) == 0)
+        reduce8_kernel<<<(unsigned)((total / 8 + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+            static_cast<const uint16_t*>(expert_outputs), static_cast<uint16_t*>(out_bf16), batch_width, hidden,
+            experts_per_token, routed_scale);
+    else
+        reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+            static_cast<const uint16_t*>(expert_outputs), static_cast<uint16_t*>(out_bf16), batch_width, hidden,
+            experts_per_token, routed_scale);
     return nh::check_launch("moe_reduce");
 }
 

@@ -493,12 +493,16 @@ __device__ bool compact_counting(const CompactArgs& A, uint32_t* cnt, uint32_t* 
         const uint32_t i = base + lane;
         const bool valid = i < s1;
         const uint32_t e = valid ? (A.routes[i] & 0xffffu) : 0xffffffffu;
-        uint32_t before = 0, after = 0;
-        for (uint32_t j = 0; j < 64; j++) {
-            const uint32_t ej = __shfl(e, j);
-            before += (j < lane && ej == e) ? 1u : 0u;
-            after += (j > lane && ej == e) ? 1u : 0u;
+        // Lanes holding the same expert, from one ballot per key bit (E <= 512).
+        uint64_t eq = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 9; bit++) {
+            const bool one = (e >> bit) & 1u;
+            const uint64_t m = __ballot(one);
+            eq &= one ? m : ~m;
         }
+        const uint32_t before = (uint32_t)__popcll(eq & ((1ull << lane) - 1ull));
+        const uint32_t after = (uint32_t)__popcll(eq >> lane) - 1u;
         if (valid) {
             const uint32_t pos = cnt[wave * E + e] + before;
             put_map(A, pos, i);

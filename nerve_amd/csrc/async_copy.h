@@ -75,6 +75,19 @@ __device__ __forceinline__ v4i gload16_untracked(const void* p) {
     return v;
 }
 
+// Nontemporal forms (streamed once: whole-line reads at ~7 TB/s over the chip).
+__device__ __forceinline__ v4i gload16_nt_untracked(const void* p) {
+    v4i v;
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(p));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t gload4_nt_untracked(const void* p) {
+    uint32_t v;
+    asm volatile("global_load_dword %0, %1, off nt" : "=v"(v) : "v"(p));
+    return v;
+}
+
 __device__ __forceinline__ uint32_t gload4_untracked(const void* p) {
     uint32_t v;
     asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p));

@@ -1513,7 +1513,7 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
     // Ranges run back to back in one block: every wave has finished the
     // previous one (ring slots and the reduction area are reused).
     __builtin_amdgcn_s_barrier();
-    uint8_t* red = ring + NBUF * A.slot_bytes;   // [wave][NMAT * NSUB][lane] v4f partial sums
+    uint8_t* red = ring + 2 * A.slot_bytes;   // [wave][NMAT * NSUB][lane] v4f partial sums
     const uint32_t npw = (RI * RB + 1023) / 1024, nps = (RI * SB + 255) / 256;
 
     // ---- copy plan, fixed for the range: piece t of this wave starts at
@@ -1550,27 +1550,41 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         ssrc[t] = A.block_major ? ((soff[t] % SB) / 4) * N * 4 + (soff[t] / SB) * 4 : soff[t];
     const uint32_t wrow = A.block_major ? 64u : RB, srow = A.block_major ? 4u : SB;
 
-    // ---- issue side: copies of item `item` into ring slot `slot`
+    // ---- issue side: item `item`'s pieces are loaded with nontemporal
+    // loads into a register set and written to an LDS slot when the item
+    // comes up (streaming reads from registers sustain ~7 TB/s over the chip
+    // where copies straight into LDS sustain ~6.1).
     const uint32_t tile_base = (i0 / nrb) * nrb;
-    auto issue = [&](uint32_t item, uint32_t slot) {
+    struct ItemRegs {
+        v4i w[NMAT][LWMAX];
+        uint32_t s[NMAT][LSMAX];
+    };
+    auto load_item = [&](uint32_t item, ItemRegs& R) __attribute__((always_inline)) {
         const uint32_t n0 = (item - tile_base) * RI;
         const uint32_t rows = min(RI, N - n0);
         const uint32_t wbytes = rows * RB, sbytes = rows * SB;
-        uint8_t* dst = ring + slot * A.slot_bytes;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             const uint8_t* ws = ts.w[m] + (uint64_t)n0 * wrow;
 #pragma unroll
             for (uint32_t t = 0; t < LWMAX; t++)
-                if (t < lw)
-                    __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? wsrc[t] : 0),
-                                                     dst + m * A.w_region + wpos[t], 16, 0, 0);
+                if (t < lw) R.w[m][t] = gload16_nt_untracked(ws + (woff[t] < wbytes ? wsrc[t] : 0));
             const uint8_t* ss = ts.s[m] + (uint64_t)n0 * srow;
 #pragma unroll
             for (uint32_t t = 0; t < LSMAX; t++)
-                if (t < ls)
-                    __builtin_amdgcn_global_load_lds(ss + (soff[t] < sbytes ? ssrc[t] : 0),
-                                                     dst + NMAT * A.w_region + m * A.s_region + spos[t], 4, 0, 0);
+                if (t < ls) R.s[m][t] = gload4_nt_untracked(ss + (soff[t] < sbytes ? ssrc[t] : 0));
+        }
+    };
+    auto store_item = [&](const ItemRegs& R, uint32_t slot) __attribute__((always_inline)) {
+        uint8_t* dst = ring + slot * A.slot_bytes;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+#pragma unroll
+            for (uint32_t t = 0; t < LWMAX; t++)
+                if (t < lw) *reinterpret_cast<v4i*>(dst + m * A.w_region + woff[t]) = R.w[m][t];
+#pragma unroll
+            for (uint32_t t = 0; t < LSMAX; t++)
+                if (t < ls) *reinterpret_cast<uint32_t*>(dst + NMAT * A.w_region + m * A.s_region + soff[t]) = R.s[m][t];
         }
     };
 
@@ -1679,31 +1693,40 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
         obase = (uint64_t)ts.out_route * N;
     const float wr = bf16_to_f32(ts.out_word >> 16);
 
-    // Prologue: the tile's activations, then the first item's copies.  Loads
-    // retire in issue order, so waiting until only that item's copies are in
+    // Prologue: the tile's activations, then the first item's loads.  Loads
+    // retire in issue order, so waiting until only that item's loads are in
     // flight lands the activations, which are quantized while the item
-    // streams; the other ring slots are filled after that (issuing them
-    // first would stall this wave until the CU's miss queue drains).  The
-    // loop's first iteration would issue into the last slot; that copy is
-    // already in flight.
+    // streams; the second item is loaded after that (issuing it first would
+    // stall this wave until the CU's miss queue drains).
     act_request();
     // Every wave's activation loads enter the CU's memory pipeline before
-    // any copy: behind the copies they would wait for HBM-bound traffic.
+    // any weight load: behind those they would wait for HBM-bound traffic.
     __builtin_amdgcn_s_barrier();
-    const uint32_t pro = min((uint32_t)NBUF, i1 - i0);
-    issue(i0, 0);
+    ItemRegs R0{}, R1{};
+    load_item(i0, R0);
     wait_vm(A.copies_per_item);
     act_finish();
-#pragma unroll
-    for (uint32_t j = 1; j < NBUF; j++)
-        if (j < pro) issue(i0 + j, j);
+    if (i0 + 1 < i1) load_item(i0 + 1, R1);
 
-    for (uint32_t i = i0; i < i1; i++) {
-        const uint32_t slot = (i - i0) % NBUF;
-        if (i > i0 && i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
+    // One item: its registers go to LDS slot (i - i0) % 2 (last read by the
+    // item two back, whose reduction barrier every wave has passed), the
+    // item two ahead is loaded into the same registers, a barrier, then the
+    // contraction and the cross-wave reduction.
+    auto item_step = [&](uint32_t i, ItemRegs& R) __attribute__((always_inline)) {
+        const uint32_t slot = (i - i0) & 1u;
+        // With only the next item's loads allowed in flight this item's have landed.
+        wait_vm(i + 1 < i1 ? A.copies_per_item : 0u);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+#pragma unroll
+            for (uint32_t t = 0; t < LWMAX; t++) asm volatile("" : "+v"(R.w[m][t]));
+#pragma unroll
+            for (uint32_t t = 0; t < LSMAX; t++) asm volatile("" : "+v"(R.s[m][t]));
+        }
+        store_item(R, slot);
+        if (i + 2 < i1) load_item(i + 2, R);
+        __syncthreads();
         const uint32_t n0 = (i - tile_base) * RI;
-        wait_vm(A.copies_per_item * min((uint32_t)(NBUF - 1), i1 - 1 - i));
-        __builtin_amdgcn_s_barrier();
         // ---- contract this wave's chunks of the slot
         const uint8_t* buf = ring + slot * A.slot_bytes;
         v4f acc[NMAT][NSUB];
@@ -1766,7 +1789,7 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
                 lds_write16(red + ((wave * NMAT * NSUB + m * NSUB + j) * 64 + lane) * 16, acc[m][j]);
         lds_drain();
         __builtin_amdgcn_s_barrier();
-        if (wave >= 4) continue;
+        if (wave >= 4) return;
 #pragma unroll
         for (int j = 0; j < NSUB; j++) {
             float t[NMAT];
@@ -1801,6 +1824,10 @@ __device__ __forceinline__ void stream_range(const StreamArgs& A, uint32_t i0, u
                 }
             }
         }
+    };
+    for (uint32_t i = i0; i < i1; i += 2) {
+        item_step(i, R0);
+        if (i + 1 < i1) item_step(i + 1, R1);
     }
 }
 
@@ -2200,13 +2227,13 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.lw = (npw + NW - 1) / NW;
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = NMAT * (A.lw + A.ls);
-    size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
+    size_t lds = (size_t)2 * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
     // The set-up tables and the staged address table share the ring's LDS
     // (short rings are extended to hold them).
     const size_t tables = (sizeof(FusedTables) + 15) / 16 * 16 + (size_t)A.T.n_records * 32;
     if (FUSED && lds < tables) lds = tables;
     A.addr_lds_records = FUSED ? (uint32_t)((lds - (sizeof(FusedTables) + 15) / 16 * 16) / 32) : 0u;
-    if (lds > 160 * 1024 || A.copies_per_item * NBUF > 63) return NERVE_HIP_UNSUPPORTED;
+    if (lds > 160 * 1024 || A.copies_per_item * 2 > 63) return NERVE_HIP_UNSUPPORTED;
     A.small_plan = FUSED && A.T.E <= 64 && A.T.batch_width * A.T.k <= 64 && ctx->cu_count >= 64 ? 1u : 0u;
     if (FUSED) {
         // Every compacted slot needs a thread in the tables, and activation
@@ -2426,7 +2453,7 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     lds_drain();   // the plan is read before any copy can overwrite it
     __builtin_amdgcn_s_barrier();
 
-    uint8_t* red = ring + NBUF * A.slot_bytes;   // [wave][NMAT][lane] v4f partial sums
+    uint8_t* red = ring + 2 * A.slot_bytes;   // [wave][NMAT][lane] v4f partial sums
     const uint32_t npw = (RI * RB + 1023) / 1024, nps = (RI * SB + 255) / 256;
     const uint32_t lw = A.lw, ls = A.ls;
     uint32_t wpos[LWMAX], spos[LSMAX], woff[LWMAX], soff[LSMAX];
@@ -2445,26 +2472,42 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
         soff[q] = spos[q] + lane * 4;
     }
     // Item i: expert index i / nrb (u0 or u0 + 1), rows (i % nrb) * 16.
-    auto issue = [&](uint32_t item, uint32_t slot) __attribute__((always_inline)) {
+    // Its weight and scale bytes are loaded with nontemporal loads into a
+    // register set (the same 1 KB / 256 B pieces per wave as a ring slot's
+    // layout) and written to an LDS slot when the item comes up: streaming
+    // reads from registers sustain ~7 TB/s over the chip where copies
+    // straight into LDS (global_load_lds) sustain ~6.1.
+    struct ItemRegs {
+        v4i w[NMAT][LWMAX];
+        uint32_t s[NMAT][LSMAX];
+    };
+    auto load_item = [&](uint32_t item, ItemRegs& R) __attribute__((always_inline)) {
         const uint32_t second = item / nrb != u0 ? 1u : 0u;
         const uint32_t n0 = (item - (u0 + second) * nrb) * RI;
         const uint32_t rows = min(RI, N - n0);
         const uint32_t wbytes = rows * RB, sbytes = rows * SB;
-        uint8_t* dst = ring + slot * A.slot_bytes;
 #pragma unroll
         for (uint32_t m = 0; m < NMAT; m++) {
             const uint8_t* ws = (second ? wp[1][m] : wp[0][m]) + (uint64_t)n0 * RB;
 #pragma unroll
             for (uint32_t q = 0; q < LWMAX; q++)
-                if (q < lw)
-                    __builtin_amdgcn_global_load_lds(ws + (woff[q] < wbytes ? woff[q] : 0),
-                                                     dst + m * A.w_region + wpos[q], 16, 0, 0);
+                if (q < lw) R.w[m][q] = gload16_nt_untracked(ws + (woff[q] < wbytes ? woff[q] : 0));
             const uint8_t* ss = (second ? sp[1][m] : sp[0][m]) + (uint64_t)n0 * SB;
 #pragma unroll
             for (uint32_t q = 0; q < LSMAX; q++)
-                if (q < ls)
-                    __builtin_amdgcn_global_load_lds(ss + (soff[q] < sbytes ? soff[q] : 0),
-                                                     dst + NMAT * A.w_region + m * A.s_region + spos[q], 4, 0, 0);
+                if (q < ls) R.s[m][q] = gload4_nt_untracked(ss + (soff[q] < sbytes ? soff[q] : 0));
+        }
+    };
+    auto store_item = [&](const ItemRegs& R, uint32_t slot) __attribute__((always_inline)) {
+        uint8_t* dst = ring + slot * A.slot_bytes;
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) {
+#pragma unroll
+            for (uint32_t q = 0; q < LWMAX; q++)
+                if (q < lw) *reinterpret_cast<v4i*>(dst + m * A.w_region + woff[q]) = R.w[m][q];
+#pragma unroll
+            for (uint32_t q = 0; q < LSMAX; q++)
+                if (q < ls) *reinterpret_cast<uint32_t*>(dst + NMAT * A.w_region + m * A.s_region + soff[q]) = R.s[m][q];
         }
     };
     uint32_t rw[CH], rs[CH];
@@ -2478,14 +2521,14 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
         rs[q] = NMAT * A.w_region + rr * SB + kk / 32;
     }
 
-    // Prologue: the first item's copies, then the quantization while it
-    // streams, then the other ring slots (issuing every slot up front stalls
-    // the wave at issue until the CU's miss queue drains).
-    const uint32_t pro = min((uint32_t)NBUF, i1 - i0);
-    issue(i0, 0);
+    // Prologue: the first item's loads, then the quantization while they
+    // stream, then the second item's (issuing more up front stalls the wave
+    // at issue until the CU's miss queue drains).
+    ItemRegs R0{}, R1{};
+    load_item(i0, R0);
     if (wave != 0) {
         // ---- quantize this wave's chunks of all tokens: loads retire in
-        // issue order, so once only the first item's copies are in flight
+        // issue order, so once only the first item's loads are in flight
         // the activations have landed.
         wait_vm(A.copies_per_item);
 #pragma unroll
@@ -2513,17 +2556,30 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
             sa[q] = row_ok ? e8 : 127u;
         }
     }
-#pragma unroll
-    for (uint32_t j = 1; j < NBUF; j++)
-        if (j < pro) issue(i0 + j, j);
+    if (i0 + 1 < i1) load_item(i0 + 1, R1);
 
-    for (uint32_t i = i0; i < i1; i++) {
-        const uint32_t slot = (i - i0) % NBUF;
-        if (i > i0 && i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
+    // One item: its registers go to LDS slot `slot` (last read by the item
+    // two back, whose reduction barrier every wave has passed), the item two
+    // ahead is loaded into the same registers, a barrier, then the
+    // contraction and the cross-wave reduction.  (Three items in flight
+    // measured slower: 49.3 against 47.8 us at config 2.)
+    auto item_step = [&](uint32_t i, ItemRegs& R) __attribute__((always_inline)) {
+        const uint32_t slot = (i - i0) & 1u;
+        // Loads retire in issue order: with only the next item's loads
+        // allowed in flight this item's have landed.
+        wait_vm(i + 1 < i1 ? A.copies_per_item : 0u);
+#pragma unroll
+        for (uint32_t m = 0; m < NMAT; m++) {
+#pragma unroll
+            for (uint32_t q = 0; q < LWMAX; q++) asm volatile("" : "+v"(R.w[m][q]));
+#pragma unroll
+            for (uint32_t q = 0; q < LSMAX; q++) asm volatile("" : "+v"(R.s[m][q]));
+        }
+        store_item(R, slot);
+        if (i + 2 < i1) load_item(i + 2, R);
+        __syncthreads();
         const uint32_t second = i / nrb != u0 ? 1u : 0u;
         const uint32_t n0 = (i - (u0 + second) * nrb) * RI;
-        wait_vm(A.copies_per_item * min((uint32_t)(NBUF - 1), i1 - 1 - i));
-        __builtin_amdgcn_s_barrier();
         const uint8_t* buf = ring + slot * A.slot_bytes;
         v4f acc[NMAT];
 #pragma unroll
@@ -2567,37 +2623,43 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
         for (uint32_t m = 0; m < NMAT; m++) lds_write16(red + ((wave * NMAT + m) * 64 + lane) * 16, acc[m]);
         lds_drain();
         __builtin_amdgcn_s_barrier();
-        if (wave >= 4) continue;
-        const uint32_t om = second ? om1 : om0;
-        float tsum[NMAT];
+        if (wave < 4) {
+            const uint32_t om = second ? om1 : om0;
+            float tsum[NMAT];
 #pragma unroll
-        for (uint32_t m = 0; m < NMAT; m++) {
-            uint32_t v[NW];
+            for (uint32_t m = 0; m < NMAT; m++) {
+                uint32_t v[NW];
 #pragma unroll
-            for (uint32_t w2 = 0; w2 < NW; w2++) v[w2] = lds_read_b32(red + ((w2 * NMAT + m) * 64 + lane) * 16 + 4 * wave);
-            lds_drain();
-            float sum = 0.0f;
+                for (uint32_t w2 = 0; w2 < NW; w2++)
+                    v[w2] = lds_read_b32(red + ((w2 * NMAT + m) * 64 + lane) * 16 + 4 * wave);
+                lds_drain();
+                float sum = 0.0f;
 #pragma unroll
-            for (uint32_t w2 = 0; w2 < NW; w2++) {
-                asm volatile("" : "+v"(v[w2]));
-                sum += __uint_as_float(v[w2]);
+                for (uint32_t w2 = 0; w2 < NW; w2++) {
+                    asm volatile("" : "+v"(v[w2]));
+                    sum += __uint_as_float(v[w2]);
+                }
+                tsum[m] = sum;
             }
-            tsum[m] = sum;
+            const uint32_t nrow = n0 + rr;
+            if (om != 0u && nrow < N) {
+                float gv = round_bf16(tsum[0]);
+                float uv = round_bf16(tsum[1]);
+                if (A.limit > 0.0f) {
+                    gv = fminf(gv, A.limit);
+                    uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                }
+                const uint16_t h = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
+                for (uint32_t bits = om; bits; bits &= bits - 1u) {
+                    const uint32_t j = (uint32_t)__builtin_ctz(bits);
+                    A.out16[(uint64_t)tok * A.frame_elems + (uint64_t)j * N + nrow] = h;
+                }
+            }
         }
-        const uint32_t nrow = n0 + rr;
-        if (om != 0u && nrow < N) {
-            float gv = round_bf16(tsum[0]);
-            float uv = round_bf16(tsum[1]);
-            if (A.limit > 0.0f) {
-                gv = fminf(gv, A.limit);
-                uv = fminf(fmaxf(uv, -A.limit), A.limit);
-            }
-            const uint16_t h = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
-            for (uint32_t bits = om; bits; bits &= bits - 1u) {
-                const uint32_t j = (uint32_t)__builtin_ctz(bits);
-                A.out16[(uint64_t)tok * A.frame_elems + (uint64_t)j * N + nrow] = h;
-            }
-        }
+    };
+    for (uint32_t i = i0; i < i1; i += 2) {
+        item_step(i, R0);
+        if (i + 1 < i1) item_step(i + 1, R1);
     }
 }
 
@@ -2624,9 +2686,9 @@ nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.lw = (npw + NW - 1) / NW;
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = 2 * (A.lw + A.ls);
-    const size_t lds = (size_t)NBUF * A.slot_bytes + (size_t)NW * 2 * 64 * 16;
+    const size_t lds = (size_t)2 * A.slot_bytes + (size_t)NW * 2 * 64 * 16;
     const size_t plan = (sizeof(TokPlan) + 15) / 16 * 16 + (size_t)A.T.n_records * 32;
-    if (lds > 160 * 1024 || plan > lds || A.copies_per_item * NBUF > 63) return NERVE_HIP_UNSUPPORTED;
+    if (lds > 160 * 1024 || plan > lds || A.copies_per_item * 2 > 63) return NERVE_HIP_UNSUPPORTED;
     static bool attr_set = false;
     if (!attr_set) {
         if (hipFuncSetAttribute((const void*)mx_tokens_kernel<NBUF, NW>, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -75,6 +75,18 @@ __device__ __forceinline__ v4i gload16_untracked(const void* p) {
     return v;
 }
 
+// Nontemporal global loads the compiler tracks (it waits for them itself);
+// the explicit global address space keeps them off the FLAT path, whose
+// loads also count against the LDS counter.
+typedef __attribute__((address_space(1))) const v4i global_v4i;
+typedef __attribute__((address_space(1))) const uint32_t global_u32;
+__device__ __forceinline__ v4i gload16_nt(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<global_v4i*>(reinterpret_cast<uintptr_t>(p)));
+}
+__device__ __forceinline__ uint32_t gload4_nt(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<global_u32*>(reinterpret_cast<uintptr_t>(p)));
+}
+
 // Nontemporal forms (streamed once: whole-line reads at ~7 TB/s over the chip).
 __device__ __forceinline__ v4i gload16_nt_untracked(const void* p) {
     v4i v;

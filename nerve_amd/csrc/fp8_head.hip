@@ -279,16 +279,17 @@ __global__ __launch_bounds__(64 * SK_WAVES) void fp8_head_skinny_kernel(HeadArgs
 // Stream form (M <= 16, per-row weight scales): one 8-wave block per CU over
 // a contiguous range of 16-row vocabulary groups.  A group's weights are one
 // contiguous 16 K-byte span of W and its scales one contiguous 32 nblk-byte
-// span of scale_inv; both are copied into an NBUF-slot LDS ring by
-// global_load_lds (1 KiB and 256 B per wave instruction), so every wave keeps
-// NBUF - 1 groups of copies in flight while it contracts the current one.
+// span of scale_inv; both are read with nontemporal loads (1 KiB and 256 B
+// per wave instruction) into a register set, written to one of two LDS slots
+// when the group comes up, and every wave keeps the next group's loads in
+// flight while it contracts the current one.
 // The tokens are the MFMA A operand and stay in registers for the whole
 // range; each wave contracts its share of the K chunks of every group and the
 // 8 partial sums meet in LDS, where waves 0..3 finalize token 4 g + wave.
 // ---------------------------------------------------------------------------
 constexpr int HS_NW = 8;
 constexpr uint32_t HS_CH = 4;        // K chunks per wave (K <= 4096; the LDS wait below names 4)
-constexpr uint32_t HS_LWMAX = 8;     // weight copies per wave per group (16 K <= 64 KiB)
+constexpr uint32_t HS_LWMAX = 6;     // weight pieces per wave per group (16 K <= 48 KiB: K <= 3072)
 
 struct HeadStream {
     uint32_t groups;
@@ -305,7 +306,7 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
     const uint32_t K = A.K, M = A.M, N = A.N, nblk = (K + 127) / 128;
     const uint32_t G = gridDim.x, b = blockIdx.x;
     const uint32_t i0 = (uint32_t)((uint64_t)S.groups * b / G), i1 = (uint32_t)((uint64_t)S.groups * (b + 1) / G);
-    uint8_t* red = ring + NBUF * S.slot_bytes;      // [wave][lane] v4f partial sums
+    uint8_t* red = ring + 2 * S.slot_bytes;         // [wave][lane] v4f partial sums
 
     // ---- copy plan: piece t of this wave starts at byte wpos[t] of the
     // group's span (waves past the last piece repeat their first one, so
@@ -325,17 +326,34 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
     const uint32_t spos = sspan >= 256 ? min(spc * 256, sspan - 256) : 0u;
     const uint32_t soff = spos + lane * 4;
 
-    auto issue = [&](uint32_t item, uint32_t slot) __attribute__((always_inline)) {
+    // Group `item`'s pieces are loaded with nontemporal loads into a register
+    // set and written to an LDS slot when the group comes up (streaming
+    // reads from registers sustain ~7 TB/s over the chip where copies
+    // straight into LDS sustain ~6.1).
+    struct GroupRegs {
+        v4i w[HS_LWMAX];
+        uint32_t s;
+    };
+    // The loads are tracked by the compiler, which waits for each before its
+    // LDS store.  Every wave issues HS_LWMAX + 1 per group on every path
+    // (groups past the block's range re-read one of it, L2-resident), so
+    // those waits count the other register set's loads rather than draining.
+    auto load_group = [&](uint32_t item, GroupRegs& R) __attribute__((always_inline)) {
+        item = item < i1 ? item : i1 > i0 ? i1 - 1 : S.groups - 1;
         const uint32_t n0 = item * 16, rows = min(16u, N - n0);
         const uint32_t wbytes = rows * K, sbytes = (rows * nblk * 2 + 3) & ~3u;
         const uint8_t* ws = A.W + (uint64_t)n0 * K;
-        uint8_t* dst = ring + slot * S.slot_bytes;
 #pragma unroll
         for (uint32_t t = 0; t < HS_LWMAX; t++)
-            if (t < S.lw)
-                __builtin_amdgcn_global_load_lds(ws + (woff[t] < wbytes ? woff[t] : 0u), dst + wpos[t], 16, 0, 0);
+            R.w[t] = gload16_nt(ws + (woff[t] < wbytes ? woff[t] : 0u));
         const uint8_t* ss = reinterpret_cast<const uint8_t*>(A.scale_inv) + (uint64_t)n0 * nblk * 2;
-        __builtin_amdgcn_global_load_lds(ss + (soff < sbytes ? soff : 0u), dst + S.s_off + spos, 4, 0, 0);
+        R.s = gload4_nt(ss + (soff < sbytes ? soff : 0u));
+    };
+    auto store_group = [&](const GroupRegs& R, uint32_t slot) __attribute__((always_inline)) {
+        uint8_t* dst = ring + slot * S.slot_bytes;
+#pragma unroll
+        for (uint32_t t = 0; t < HS_LWMAX; t++) *reinterpret_cast<v4i*>(dst + woff[t]) = R.w[t];
+        *reinterpret_cast<uint32_t*>(dst + S.s_off + soff) = R.s;
     };
 
     // ---- this wave's K chunks and their LDS offsets
@@ -351,9 +369,8 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
         rs[q] = S.s_off + (rr * nblk + (c < c1 ? c : 0u)) * 2;
     }
 
-    // ---- tokens: e4m3 operand pieces and block scales, loaded with
-    // untracked loads before the first copies and waited for together with
-    // the first group's copies (loads retire in issue order).  Quantizing
+    // ---- tokens: e4m3 operand pieces and block scales, loaded before the
+    // first group's weights.  Quantizing
     // the tokens here instead would repeat the whole M x K quantization in
     // every block, vector-ALU work that outlasts the ring's first groups.
     const bool arow = rr < M;
@@ -365,21 +382,17 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
         for (uint32_t q = 0; q < HS_CH; q++) {
             if (c0 + q >= c1) continue;                 // wave-uniform
             const uint32_t kb = kvalid[q] ? (c0 + q) * 128 + g * 32 : 0u;
-            xlo[q] = gload16_untracked(xr + kb);
-            xhi[q] = gload16_untracked(xr + kb + 16);
+            xlo[q] = *reinterpret_cast<const v4i*>(xr + kb);
+            xhi[q] = *reinterpret_cast<const v4i*>(xr + kb + 16);
 #pragma unroll
             for (uint32_t i = 0; i < 4; i++) {
                 const uint32_t tk = 4 * g + i;
-                sxr[q][i] = gload4_untracked(A.xs + (tk < M ? tk * nblk + c0 + q : 0u));
+                sxr[q][i] = __float_as_uint(A.xs[tk < M ? tk * nblk + c0 + q : 0u]);
             }
         }
     }
-    if (i0 >= i1) {
-        wait_vm_imm<0>();
-    } else {
-        issue(i0, 0);
-        wait_vm(S.cpi);
-    }
+    GroupRegs R0, R1;
+    load_group(i0, R0);
     v8i av[HS_CH];
     float sx[HS_CH][4];
 #pragma unroll
@@ -388,44 +401,38 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) sx[q][i] = 0.0f;
         if (c0 + q >= c1) continue;
-        asm volatile("" : "+v"(xlo[q]), "+v"(xhi[q]));
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++) asm volatile("" : "+v"(sxr[q][i]));
         if (arow && kvalid[q])
             av[q] = v8i{xlo[q].x, xlo[q].y, xlo[q].z, xlo[q].w, xhi[q].x, xhi[q].y, xhi[q].z, xhi[q].w};
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) sx[q][i] = 4 * g + i < M ? __uint_as_float(sxr[q][i]) : 0.0f;
     }
-    const uint32_t pro = min((uint32_t)NBUF, i1 - i0);
-#pragma unroll
-    for (uint32_t j = 1; j < NBUF; j++)
-        if (j < pro) issue(i0 + j, j);
+    load_group(i0 + 1, R1);
 
     const uint32_t tok = 4 * g + wave;                  // finalized token (waves 0..3)
     float best_v = -INFINITY;
     uint32_t best_i = 0xffffffffu;
-    for (uint32_t i = i0; i < i1; i++) {
-        const uint32_t slot = (i - i0) % NBUF;
-        if (i > i0 && i + NBUF - 1 < i1) issue(i + NBUF - 1, (i - i0 + NBUF - 1) % NBUF);
-        wait_vm(S.cpi * min((uint32_t)(NBUF - 1), i1 - 1 - i));
-        __builtin_amdgcn_s_barrier();
+    // One group: its registers go to LDS slot (i - i0) % 2 (last read by the
+    // group two back, whose reduction barrier every wave has passed), the
+    // group two ahead is loaded into the same registers, a barrier, then the
+    // contraction, the cross-wave reduction and the finalization.
+    auto group_step = [&](uint32_t i, GroupRegs& R) __attribute__((always_inline)) {
+        const uint32_t slot = (i - i0) & 1u;
+        store_group(R, slot);
+        load_group(i + 2, R);
+        __syncthreads();
+        // Plain LDS reads: nothing but ds_writes fills the slots, so the
+        // compiler's own waits cover them (inline-asm reads would leave it
+        // free to copy their results before the wait).
         const uint8_t* buf = ring + slot * S.slot_bytes;
         v4i w0[HS_CH], w1[HS_CH];
         uint32_t sw[HS_CH];
 #pragma unroll
         for (uint32_t q = 0; q < HS_CH; q++) {
             if (c0 + q >= c1) continue;
-            w0[q] = lds_read16(buf + rw[q]);
-            w1[q] = lds_read16(buf + rw[q] + 16);
-            sw[q] = lds_read_u16(buf + rs[q]);
+            w0[q] = *reinterpret_cast<const v4i*>(buf + rw[q]);
+            w1[q] = *reinterpret_cast<const v4i*>(buf + rw[q] + 16);
+            sw[q] = *reinterpret_cast<const uint16_t*>(buf + rs[q]);
         }
-        // The wait takes the read results as operands, so no copy of them
-        // is scheduled in front of it.
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(w0[0]), "+v"(w1[0]), "+v"(sw[0]), "+v"(w0[1]), "+v"(w1[1]), "+v"(sw[1]), "+v"(w0[2]),
-                       "+v"(w1[2]), "+v"(sw[2]), "+v"(w0[3]), "+v"(w1[3]), "+v"(sw[3])
-                     :
-                     : "memory");
         v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t q = 0; q < HS_CH; q++) {
@@ -440,23 +447,12 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[e] = fmaf(p[e], sx[q][e] * s, acc[e]);
         }
-        // An MFMA result read by inline asm needs software wait states the
-        // compiler does not add: the nops take the sums as operands.
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(acc));
-        lds_write16(red + (wave * 64 + lane) * 16, acc);
-        lds_drain();
-        __builtin_amdgcn_s_barrier();
-        if (wave >= 4) continue;
-        uint32_t v[HS_NW];
-#pragma unroll
-        for (int w2 = 0; w2 < HS_NW; w2++) v[w2] = lds_read_b32(red + (w2 * 64 + lane) * 16 + 4 * wave);
-        lds_drain();
+        *reinterpret_cast<v4f*>(red + (wave * 64 + lane) * 16) = acc;
+        __syncthreads();
+        if (wave >= 4) return;
         float sum = 0.0f;
 #pragma unroll
-        for (int w2 = 0; w2 < HS_NW; w2++) {
-            asm volatile("" : "+v"(v[w2]));
-            sum += __uint_as_float(v[w2]);
-        }
+        for (int w2 = 0; w2 < HS_NW; w2++) sum += *reinterpret_cast<const float*>(red + (w2 * 64 + lane) * 16 + 4 * wave);
         const float val = sum * A.out_scale;
         const uint32_t n = i * 16 + rr;
         const bool cv = n < N;
@@ -478,7 +474,16 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
                 best_i = bi;
             }
         }
+    };
+    // Both register sets are stepped on every path back to the loop head, so
+    // the compiler's waits before the stores count the other set's loads.
+    for (uint32_t i = i0; i < i1;) {
+        group_step(i, R0);
+        if (++i >= i1) break;
+        group_step(i, R1);
+        ++i;
     }
+    wait_vm_imm<0>();   // the last re-read groups
     if (A.part_val && wave < 4 && rr == 0 && tok < M) {
         A.part_val[(uint64_t)tok * G + b] = best_v;
         A.part_idx[(uint64_t)tok * G + b] = best_i;
@@ -1238,9 +1243,9 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
     const uint32_t sspan = 32 * nblk;
     hs.slot_bytes = hs.s_off + ((sspan < 256 ? 256 : sspan) + 15) / 16 * 16;
     hs.lw = (16 * K + 1023) / 1024 / HS_NW + ((16 * K + 1023) / 1024 % HS_NW ? 1 : 0);
-    hs.cpi = hs.lw + 1;
+    hs.cpi = HS_LWMAX + 1;   // every wave loads HS_LWMAX pieces (repeats past lw) and one scale dword
     const size_t hs_red = HS_NW * 64 * 16;
-    const int hs_nbuf = (3 * (size_t)hs.slot_bytes + hs_red <= 160 * 1024) ? 3 : 2;
+    const int hs_nbuf = 2;   // LDS slots; one more group is in flight in registers
     const bool stream_form = skinny && s.block_rows == 1 && K >= 64 && ((uint64_t)N * nblk) % 2 == 0 &&
                              ((uintptr_t)scale_inv_bf16 & 3) == 0 && hs.lw <= HS_LWMAX &&
                              hs_nbuf * (size_t)hs.slot_bytes + hs_red <= 160 * 1024 && hs.cpi * hs_nbuf <= 63;

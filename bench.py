@@ -437,7 +437,7 @@ def fp8_head(args, ctx, dev):
     out = base_line(args, M / (kms * 1e-3), "tokens/s", ms, "e4m3xe4m3->f32",
                     {"workload": f"fp8_lm_head_m{M}_k2880_n201088_argmax"})
     mfma_bound = M >= 512
-    kname = ("fp8_head_stream_kernel<3> (+ row quantization, argmax of the partials)" if M <= 16
+    kname = ("fp8_head_stream_kernel<2> (+ row quantization, argmax of the partials)" if M <= 16
              else "fp8_head_gemm_kernel (+ row quantization, scale scan, argmax of the partials)")
     out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": kname,
                        "achieved": tf if mfma_bound else gbs, "peak": FP8_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,

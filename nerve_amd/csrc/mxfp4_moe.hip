@@ -564,40 +564,73 @@ __device__ void build_tiles(const TileArgs& A) {
     }
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
     if (A.items) {
-        // Work items (expert, row block, tile) with tiles fastest, decoded
-        // from the LDS tables; the tile records written above by this block
-        // are visible after the barrier.
+        // Work items (expert, row block, tile) with tiles fastest, grouped by
+        // the expert's route count: experts with more than 64 routes, 33-64,
+        // then 1-32 (the grouped GEMM contracts 128, 64 or 32 routes per tile
+        // for them).  est[] (free now) takes each expert's first tile among
+        // its group's tiles; n_tiles[1], n_tiles[2] the first two groups' tile
+        // counts.  The tile records written above are visible after the
+        // barrier.
         __syncthreads();
-        const uint32_t nrb = A.item_nrb, n_t = min(tiles_total, A.max_tiles), n_items = n_t * nrb;
-        for (uint32_t i = tid; i < n_items; i += nt) {
-            const uint32_t tp = i / nrb;
-            // Expert of tile tp: the last e with tst[e] <= tp (experts without
-            // tiles share their successor's start, so it has tiles).
-            uint32_t lo = 0, hi = A.E;
-            while (hi - lo > 1) {
-                const uint32_t mid = (lo + hi) / 2;
-                if (tst[mid] <= tp) lo = mid;
-                else hi = mid;
-            }
-            const uint32_t e = lo, first = tst[e], nte = (cnt[e] + A.TM - 1) / A.TM;
-            const uint32_t local = i - first * nrb, kk = local % nte, t = first + kk;
-            ItemRec o;
-            o.rb = local / nte;
-            o.count = min(A.TM, cnt[e] - kk * A.TM);
-            o.tile = t;
-            o.pad = 0;
-            if constexpr (EPTR) {
-                o.w[0] = eptr[e][0];
-                o.s[0] = eptr[e][1];
-                o.w[1] = eptr[e][2];
-                o.s[1] = eptr[e][3];
+        auto group_of = [](uint32_t c) -> uint32_t { return c > 64 ? 0u : c > 32 ? 1u : 2u; };
+        uint32_t l01 = 0, l2 = 0;
+        for (uint32_t e = e0; e < e1; e++) {
+            const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM, gr = group_of(cnt[e]);
+            if (gr == 0) l01 += nte;
+            else if (gr == 1) l01 += nte << 16;
+            else l2 += nte;
+        }
+        uint32_t o01 = block_exclusive_scan(l01, wave_tot, &total);
+        const uint32_t t01 = total;
+        uint32_t o2 = block_exclusive_scan(l2, wave_tot, &total);
+        for (uint32_t e = e0; e < e1; e++) {
+            const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM, gr = group_of(cnt[e]);
+            if (gr == 0) {
+                est[e] = o01 & 0xffffu;
+                o01 += nte;
+            } else if (gr == 1) {
+                est[e] = o01 >> 16;
+                o01 += nte << 16;
             } else {
-                o.w[0] = A.recs[t].w[0];
-                o.w[1] = A.recs[t].w[1];
-                o.s[0] = A.recs[t].s[0];
-                o.s[1] = A.recs[t].s[1];
+                est[e] = o2;
+                o2 += nte;
             }
-            A.items[i] = o;
+        }
+        const uint32_t nt0 = t01 & 0xffffu, nt1 = t01 >> 16;
+        if (tid == 0) {
+            A.n_tiles[1] = nt0;
+            A.n_tiles[2] = nt1;
+        }
+        __syncthreads();
+        // One thread per (expert, row block): its tiles' items.
+        const uint32_t nrb = A.item_nrb;
+        for (uint32_t pr = tid; pr < A.E * nrb; pr += nt) {
+            const uint32_t e = pr / nrb, rb = pr % nrb;
+            const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM;
+            if (nte == 0) continue;
+            const uint32_t gr = group_of(cnt[e]);
+            const uint32_t gbase = gr == 0 ? 0u : gr == 1 ? nt0 * nrb : (nt0 + nt1) * nrb;
+            const uint32_t base = gbase + est[e] * nrb + rb * nte;
+            for (uint32_t kk = 0; kk < nte; kk++) {
+                const uint32_t t = tst[e] + kk;
+                ItemRec o;
+                o.rb = rb;
+                o.count = min(A.TM, cnt[e] - kk * A.TM);
+                o.tile = t;
+                o.pad = 0;
+                if constexpr (EPTR) {
+                    o.w[0] = eptr[e][0];
+                    o.s[0] = eptr[e][1];
+                    o.w[1] = eptr[e][2];
+                    o.s[1] = eptr[e][3];
+                } else {
+                    o.w[0] = A.recs[t].w[0];
+                    o.w[1] = A.recs[t].w[1];
+                    o.s[0] = A.recs[t].s[0];
+                    o.s[1] = A.recs[t].s[1];
+                }
+                A.items[base + kk] = o;
+            }
         }
     }
 }
@@ -2703,45 +2736,48 @@ nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
 // ---------------------------------------------------------------------------
 // Persistent grouped GEMM for prefill-shaped batches.
 //
-// Work item = (tile of <= 128 routes of one expert, block of 128 weight rows).
-// For gate_up the 128 rows are 64 gate and 64 up rows of the same channels,
+// Work item = (tile of <= 128 routes of one expert, block of 256 weight rows).
+// For gate_up the 256 rows are 128 gate and 128 up rows of the same channels,
 // so SwiGLU runs on the accumulators.  The preparation launch lists the items
 // as (expert, row block, tile) with tiles fastest; every block takes every
 // G-th item, with consecutive items on blocks of one XCD, so the tiles of one
 // expert at one row block run side by side and read the same weight rows
 // while they are in that XCD's L2.
 //
-// One 512-thread block per CU streams every 256-k chunk of its items global
-// -> LDS with global_load_lds into a 3-stage ring that runs across item
-// boundaries: activations 128 x 256 B e4m3, weights 128 x 128 B e2m1 (each
-// weight row's piece of a chunk is one whole 128-byte line: with 128-k chunks
-// the two halves of every line arrive as separate requests, which measured
-// ~20% slower at the same bytes), their scales.  The copies of the next item
-// are in flight while the last chunks of the current one are contracted.
+// One 512-thread block per CU.  Each wave owns 32 of the item's weight rows
+// (gate_up: 16 gate + the same 16 up channels) and contracts them against
+// all of the tile's routes, so a weight byte is used by one wave only: the
+// weights go from global memory straight into that wave's registers (16-byte
+// loads in the MFMA's operand layout, three chunks in flight per wave), with
+// no LDS round trip.  The activations (128 routes x 256 B
+// e4m3 per 256-k chunk), the rows' e8m0 scale bytes and the routes' block
+// scales are shared by all waves: they go global -> LDS with global_load_lds
+// into a 3-stage ring that runs across item boundaries.  Per CU that keeps
+// ~130 KB of weight and activation bytes in flight, and 256-row items read
+// each route's activations once per 256 rows.
 //
-// Every wave issues a fixed set of copies per stage (an SGPR base advanced
-// per chunk plus a fixed 32-bit lane offset), so the vmcnt waits count
-// copies per stage; one barrier per chunk; the step body is unrolled over the
-// 3 stages so every LDS operand read is a fixed register plus an immediate
-// offset.  The next item's descriptor (item record, then its tile's route
-// list) also arrives by LDS copies issued by wave 0 inside the same pipeline.
-//
-// Wave (wm, wn) contracts routes [32 wm, 32 wm + 32) against 64 weight rows
-// (gate_up: 32 gate + the same 32 up channels).
+// Every wave issues a fixed set of copies and loads per stage (an SGPR base
+// advanced per chunk plus fixed 32-bit lane offsets), so the vmcnt waits
+// count them per stage; one barrier per chunk; the step body is unrolled
+// over the 3 stages so every LDS operand read is a fixed register plus an
+// immediate offset and every weight register set is a fixed variable.  The
+// next item's descriptor (item record, then its tile's route list) also
+// arrives by LDS copies issued by wave 0 inside the same pipeline.
 // ---------------------------------------------------------------------------
 constexpr uint32_t PG_TM = PG_TILE;
-constexpr uint32_t PG_ROWS = 128;
+constexpr uint32_t PG_ROWS = 256;         // weight rows per item (gate_up: 128 gate + 128 up)
 constexpr uint32_t PG_NST = 3;
 constexpr uint32_t PG_KC = 256;           // k per chunk
 // LDS map (bytes).  Regions are grouped by kind so a stage is an immediate.
 constexpr uint32_t PG_A_OFF = 0;          // [3][128 routes][256 B], 16-byte pieces XOR-swizzled by route
-constexpr uint32_t PG_B_OFF = 98304;      // [3][128 rows][128 B], pieces XOR-swizzled by row pair
-constexpr uint32_t PG_SB_OFF = 147456;    // [3][128 rows][16 B]: 3 aligned dwords holding the row's 8 e8m0 bytes
-constexpr uint32_t PG_SA_OFF = 153600;    // [3][4 wm][16 r][2 a][2 h] f32 block scales
-constexpr uint32_t PG_REC_OFF = 156672;   // [2][256 B] item records (48 B used)
-constexpr uint32_t PG_LIST_OFF = 157184;  // [2][2 KB] tile route lists
-constexpr uint32_t PG_LDS = 161280;
-constexpr uint32_t PG_COPIES = 8;         // copy slots per wave per stage
+constexpr uint32_t PG_SA_OFF = 98304;     // [3][128 routes][2] f32 block scales
+constexpr uint32_t PG_REC_OFF = 101376;   // [2][256 B] item records (48 B used)
+constexpr uint32_t PG_LIST_OFF = 101888;  // [2][2 KB] tile route lists
+constexpr uint32_t PG_SPAN_OFF = 105984;  // [2][256 rows][K / 32 B]: the item's e8m0 scale rows, by item parity
+// LDS bytes of a launch for contraction length K (the scale spans grow with K).
+__host__ __device__ constexpr uint32_t pg_lds_bytes(uint32_t K) { return PG_SPAN_OFF + 2 * PG_ROWS * (K / 32); }
+constexpr uint32_t PG_COPIES = 5;         // per-chunk LDS copy slots per wave
+constexpr uint32_t PG_WLOADS = 4;         // weight register loads per wave per stage
 // The item record rides on chunk 2's copies, the route list on chunk 4's,
 // and the next item's copies are set up when chunk nch - 1 is issued (at
 // chunk nch - 3), so an item needs at least 7 chunks.
@@ -2761,24 +2797,33 @@ struct PgArgs {
     float limit;
 };
 
-__device__ __forceinline__ uint32_t pg_swz_b(uint32_t r) { return (r >> 1) & 7u; }
-
 template <uint32_t OFF>
 __device__ __forceinline__ uint32_t lds_rd8(uint32_t a) {
     uint32_t r;
     asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
     return r;
 }
+template <uint32_t OFF>
+__device__ __forceinline__ v2i lds_rd64(uint32_t a) {
+    v2i r;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+
 // 16-byte LDS read at any offset below 128 KiB (the immediate field holds 16 bits).
 template <uint32_t OFF>
 __device__ __forceinline__ v4i lds_rd128_far(uint32_t a) {
     if constexpr (OFF >= 65536u) return lds_rd128<OFF - 65536u>(a + 65536u);
     else return lds_rd128<OFF>(a);
 }
-// Item row of weight tile j inside a wave's 64 rows (gate_up: gate 0, 16, up 64, 80).
-template <int NMAT>
-__host__ __device__ constexpr uint32_t pg_jrow(uint32_t j) { return NMAT == 2 ? (j >> 1) * 64 + (j & 1) * 16 : j * 16; }
 
+// Item row of a wave's weight subtile j (16 rows): gate_up waves take gate
+// rows 16 w.. and the same up channels (item rows 128 + 16 w..), down waves
+// rows 32 w + 16 j...
+template <int NMAT>
+__host__ __device__ constexpr uint32_t pg_irow(uint32_t wave, uint32_t j) {
+    return NMAT == 2 ? j * 128 + 16 * wave : 32 * wave + 16 * j;
+}
 
 // LDS dword read that waits for itself inside the same asm statement, so
 // no use of the result can be scheduled ahead of the wait.
@@ -2789,19 +2834,29 @@ __device__ __forceinline__ uint32_t lds_rd32_sync(uint32_t a) {
     return r;
 }
 
-
-// Issue-side state of the item whose chunks are being copied.
+// Issue-side state of the item whose chunks are being copied and loaded.
 struct PgIssue {
-    const uint8_t* b_base[2];   // uniform: weight matrices of slots 4, 5
-    const uint8_t* sb_base;     // uniform: scale matrix of slot 6
-    uint32_t off[PG_COPIES];    // per lane
-    uint32_t tail_ok;           // per lane: bit i = slot i's piece lies inside K in the last chunk
-    uint32_t on;                // uniform: bit i = slot i is copied (routes / rows that exist)
-    uint32_t n;                 // uniform: copies per chunk
+    const uint8_t* sp[2];       // uniform: scale span of each matrix part of the item
+    const uint8_t* wb[2];       // uniform: weight matrices of the wave's subtiles
+    uint32_t off[PG_COPIES];    // per lane: copy source offsets
+    uint32_t woff[2];           // per lane: weight row offset of subtile j (+ 16 g)
+    uint32_t tail_ok;           // per lane: bit i = copy slot i lies inside K in the last chunk;
+                                //   bits 8 + 2 j + h: weight piece (j, h) does
+    uint32_t on;                // uniform: bit i = copy slot i is issued (routes that exist)
+    uint32_t n;                 // uniform: copies + loads per chunk
+    uint32_t slen[2];           // uniform: scale span bytes of each part
+    uint32_t np0;               // uniform: 256-byte span pieces of part 0
+    uint32_t nspan;             // uniform: this wave's span pieces (issued with chunk 0)
 };
 
-template <int NMAT>
-__global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
+// Weight register set of one chunk: subtile j (0, 1), half h (0, 1).
+struct PgW {
+    v4i w[2][2];
+};
+
+// Items [i0, n_items) of one route-count group, NA route subtiles per tile.
+template <int NMAT, int NA>
+__device__ __forceinline__ void pg_range(const PgArgs& A, uint32_t i0, uint32_t n_items) {
     extern __shared__ __attribute__((aligned(16))) uint8_t pg_ring[];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2809,14 +2864,12 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + PG_KC - 1) / PG_KC;
     const uint32_t nsa = (K + 127) / 128;             // activation scales per row
     constexpr uint32_t RPM = PG_ROWS / NMAT;           // rows per matrix in an item
-    const uint32_t nrb = (N + RPM - 1) / RPM;
-    const uint32_t n_items = __builtin_amdgcn_readfirstlane(*A.n_tiles) * nrb;
     const uint32_t G = gridDim.x;
     const uint32_t ring = lds_addr(pg_ring);
 
     // ---- descriptor copies (wave 0): item record, then the tile's list ----
     auto copy_rec = [&](uint32_t item, uint32_t par) __attribute__((always_inline)) {
-        const uint32_t idx = item < n_items ? item : 0u;
+        const uint32_t idx = item < n_items ? item : i0;
         const uint32_t* src = reinterpret_cast<const uint32_t*>(A.items + idx) + (lane < 12 ? lane : 0);
         __builtin_amdgcn_global_load_lds(src, pg_ring + PG_REC_OFF + par * 256, 4, 0, 0);
     };
@@ -2836,10 +2889,10 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     };
 
     // ---- issue side: set-up of an item's copies (after its descriptor landed) ----
-    // Slots: 0-3 = activations of routes 32 i + 4 w.. (four 256-byte rows per
-    // copy); 4, 5 = weight rows 64 i + 8 w.. (eight 128-byte rows per copy);
-    // 6 = scale dwords of rows 16 w..; 7 = activation scales of routes
-    // 32 w.. (waves 0-3).
+    // Copy slots: 0-3 = activations of routes 32 i + 4 w.. (four 256-byte
+    // rows per copy); 4, 5 = scale dwords of the wave's subtiles (16 rows x
+    // 4 dwords); 6 = block scales of routes 32 w.. (waves 0-3).  Loads:
+    // weight pieces (j, h) of the wave's two subtiles.
     auto setup_issue = [&](uint32_t par, PgIssue& S) __attribute__((always_inline)) {
         const uint32_t rb = rec_word(par, 0), count = rec_word(par, 1);
         const uint8_t* wp[2] = {rec_ptr(par, 4), rec_ptr(par, 6)};
@@ -2857,78 +2910,83 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
             tail |= (last * PG_KC + p * 16 < K ? 1u : 0u) << i;
             on |= (32 * i + 4 * wave < count ? 1u : 0u) << i;
         }
-        // weight rows
-#pragma unroll
-        for (uint32_t i = 0; i < 2; i++) {
-            const uint32_t r = 64 * i + 8 * wave + (lane >> 3);
-            const uint32_t p = (lane & 7) ^ pg_swz_b(r);
-            const uint32_t n = rb * RPM + r % RPM;
-            S.off[4 + i] = (n < N ? n : 0) * RB + p * 16;
-            S.b_base[i] = wp[(64 * i) / RPM];
-            tail |= (last * (PG_KC / 2) + p * 16 < RB ? 1u : 0u) << (4 + i);
-            on |= (rb * RPM + (64 * i + 8 * wave) % RPM < N ? 1u : 0u) << (4 + i);
-        }
-        // weight scale dwords: 3 aligned dwords cover a row's 8 bytes of a
-        // chunk (its row offset is even); the fourth slot repeats the third
+        // the item's scale rows: per matrix part, the span of its existing
+        // rows (contiguous in the package layout), copied once per item in
+        // 256-byte pieces, the last one aligned to the span's end
         {
-            const uint32_t r = 16 * wave + (lane >> 2), d = lane & 3;
-            const uint32_t n = rb * RPM + r % RPM;
-            const uint32_t rowoff = (n < N ? n : 0) * SB;
-            S.off[6] = (rowoff & ~3u) + 4 * (d < 3 ? d : 2u);
-            S.sb_base = sp[(16 * wave) / RPM];
-            tail |= (d < 3 && (rowoff & ~3u) + 8 * last + 4 * d < rowoff + SB ? 1u : 0u) << 6;
-            on |= (rb * RPM + (16 * wave) % RPM < N ? 1u : 0u) << 6;
+            uint32_t np = 0;
+#pragma unroll
+            for (uint32_t m = 0; m < (uint32_t)NMAT; m++) {
+                const uint32_t rows = min(RPM, N - rb * RPM);
+                S.sp[m] = sp[m] + (uint64_t)rb * RPM * SB;
+                S.slen[m] = rows * SB;
+                np += (rows * SB + 255) / 256;
+                if (m == 0) S.np0 = np;
+            }
+            S.nspan = np > wave ? (np - wave + 7) / 8 : 0u;
         }
-        // activation scales, stored so that LDS word 4 r + 2 a + h of route
-        // group w holds route 32 w + 16 a + r, block 2 c + h: a lane reads its
-        // 2 subtiles x 2 halves at once
+        // activation block scales: LDS word 2 t + h holds route t, block 2 c + h
         if (wave < 4) {
-            const uint32_t r = lane >> 2, a = (lane >> 1) & 1u, h = lane & 1u;
-            const uint32_t t = 32 * wave + 16 * a + r;
+            const uint32_t t = 32 * wave + (lane >> 1), h = lane & 1u;
             const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
-            S.off[7] = row * nsa * 4 + h * 4;
-            tail |= (2 * last + h < nsa ? 1u : 0u) << 7;
-            on |= (32 * wave < count ? 1u : 0u) << 7;
+            S.off[4] = row * nsa * 4 + h * 4;
+            tail |= (2 * last + h < nsa ? 1u : 0u) << 4;
+            on |= (32 * wave < count ? 1u : 0u) << 4;
         } else {
-            S.off[7] = 0;
+            S.off[4] = 0;
+        }
+        // weights: lane (g, r) of subtile j loads bytes 64 h + 16 g of row r's
+        // chunk piece (rows past N read row 0; pieces past K read the row start)
+#pragma unroll
+        for (uint32_t j = 0; j < 2; j++) {
+            const uint32_t ir = pg_irow<NMAT>(wave, j), m = ir / RPM;
+            const uint32_t n = rb * RPM + ir % RPM + rr;
+            S.woff[j] = (n < N ? n : 0) * RB + 16 * g;
+            S.wb[j] = wp[m];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) tail |= (last * (PG_KC / 2) + 64 * h + 16 * g < RB ? 1u : 0u) << (8 + 2 * j + h);
         }
         S.tail_ok = tail;
         S.on = on;
-        S.n = __builtin_popcount(on);
+        S.n = __builtin_popcount(on) + PG_WLOADS;
     };
 
-    // Copies of chunk c of the issue item into stage ST.
-    auto issue_chunk = [&](const PgIssue& S, uint32_t c, auto st_tag) __attribute__((always_inline)) {
-        constexpr uint32_t ST = decltype(st_tag)::value;
-        uint8_t* const dA = pg_ring + PG_A_OFF + ST * 32768 + wave * 1024;
-        uint8_t* const dB = pg_ring + PG_B_OFF + ST * 16384 + wave * 1024;
-        uint8_t* const dS = pg_ring + PG_SB_OFF + ST * 2048 + wave * 256;
-        uint8_t* const dT = pg_ring + PG_SA_OFF + ST * 1024 + (wave & 3) * 256;
-        const uint32_t on = S.on;
-        const uint8_t* a = A.aq + c * PG_KC;
-        const uint8_t* b0 = S.b_base[0] + c * (PG_KC / 2);
-        const uint8_t* b1 = S.b_base[1] + c * (PG_KC / 2);
-        const uint8_t* sb = S.sb_base + c * (PG_KC / 32);
-        const uint8_t* sa = reinterpret_cast<const uint8_t*>(A.as) + c * 8;
-        // In the last chunk, pieces past K (and scale dwords past a row's
-        // end) come from the zero page.
-        const uint32_t ok = c + 1 < nch ? 0xffu : S.tail_ok;
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++)
-            if (on & (1u << i))
-                __builtin_amdgcn_global_load_lds((ok & (1u << i)) ? a + S.off[i] : kZeroPage, dA + i * 8192, 16, 0, 0);
-        if (on & 16) __builtin_amdgcn_global_load_lds((ok & 16) ? b0 + S.off[4] : kZeroPage, dB, 16, 0, 0);
-        if (on & 32) __builtin_amdgcn_global_load_lds((ok & 32) ? b1 + S.off[5] : kZeroPage, dB + 8192, 16, 0, 0);
-        if (on & 64) __builtin_amdgcn_global_load_lds((ok & 64) ? sb + S.off[6] : kZeroPage, dS, 4, 0, 0);
-        if (on & 128) __builtin_amdgcn_global_load_lds((ok & 128) ? sa + S.off[7] : kZeroPage, dT, 4, 0, 0);
+    // Issue unit U (0..7) of chunk c of the issue item into stage ST / set W:
+    // units 0-3 load weight pieces (j, h) = (U / 2, U % 2), units 4-7 copy
+    // activation rows 32 (U - 4) + 4 w.., unit 7 also the block scales.  The
+    // loads are inline asm the compiler does not count (its wait pass would
+    // otherwise wait for them, and for every copy in flight, before the next
+    // LDS read): they are waited for by the per-stage vmcnt count and
+    // laundered through an empty asm before use.  In the last chunk, pieces
+    // past K come from the zero page (copies) or the row start (loads).
+    auto issue_unit = [&](const PgIssue& S, uint32_t c, auto st_tag, PgW& W, auto u_tag) __attribute__((always_inline)) {
+        constexpr uint32_t ST = decltype(st_tag)::value, U = decltype(u_tag)::value;
+        const uint32_t ok = c + 1 < nch ? 0xffffu : S.tail_ok;
+        if constexpr (U < 4) {
+            constexpr uint32_t j = U / 2, h = U % 2;
+            const uint32_t bo = (ok & (1u << (8 + 2 * j + h))) ? c * (PG_KC / 2) + 64 * h : 0u;
+            W.w[j][h] = gload16_untracked(S.wb[j] + S.woff[j] + bo);
+        } else {
+            constexpr uint32_t i = U - 4;
+            uint8_t* const dA = pg_ring + PG_A_OFF + ST * 32768 + wave * 1024 + i * 8192;
+            if (S.on & (1u << i))
+                __builtin_amdgcn_global_load_lds((ok & (1u << i)) ? A.aq + c * PG_KC + S.off[i] : kZeroPage, dA, 16, 0, 0);
+            if constexpr (U == 7) {
+                uint8_t* const dT = pg_ring + PG_SA_OFF + ST * 1024 + wave * 256;
+                const uint8_t* sa = reinterpret_cast<const uint8_t*>(A.as) + c * 8;
+                if (S.on & 16) __builtin_amdgcn_global_load_lds((ok & 16) ? sa + S.off[4] : kZeroPage, dT, 4, 0, 0);
+            }
+        }
     };
 
     // ---- first item: descriptor copied synchronously ----
-    // Item s*G + q goes to the block in slot q, and the hardware deals
-    // consecutive blocks to the 8 XCDs in turn: slot q = (b % 8) * (G / 8) +
-    // b / 8 puts consecutive items (the tiles of one expert row block) on
-    // one XCD, where they share its L2 copy of the weight rows.
-    uint32_t item = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    // Item s*G + q (of the whole item list, across the groups) goes to the
+    // block in slot q, and the hardware deals consecutive blocks to the 8
+    // XCDs in turn: slot q = (b % 8) * (G / 8) + b / 8 puts consecutive items
+    // (the tiles of one expert row block) on one XCD, where they share its L2
+    // copy of the weight rows.
+    const uint32_t slot = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    uint32_t item = i0 + (slot + G - i0 % G) % G;
     if (item >= n_items) return;
     if (wave == 0) copy_rec(item, 0);
     wait_vm_imm<0>();
@@ -2941,62 +2999,73 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     setup_issue(0, S);
     uint32_t ic = 0, ipar = 0, iitem = item;   // issue item: next chunk, descriptor slot, index
     bool issuing = true;
-    // Issues the next chunk (one per stage) and moves to the next item after
-    // the last chunk of the current one.
-    uint32_t q0 = 0, q1 = 0, q2 = 0;   // copies this wave issued into each stage
-    auto issue_next = [&](auto st_tag) __attribute__((always_inline)) {
+    // Issues the next chunk (one per stage: the item's scale spans at its
+    // chunk 0, the weight loads, the copies) and moves to the next item after
+    // the last chunk of the current one.  Past the block's last item the
+    // weight loads are still issued (the last chunk again, unused) so every
+    // register set is written on every path.
+    uint32_t q0 = 0, q1 = 0, q2 = 0;   // copies + loads this wave issued into each stage
+    // The item's scale spans, into the span slot of its parity: piece p of
+    // the parts laid back to back (part m at byte m RPM K/32 of the slot).
+    auto issue_span = [&](uint32_t par) __attribute__((always_inline)) {
+        uint8_t* const dst = pg_ring + PG_SPAN_OFF + par * (PG_ROWS * SB);
+        for (uint32_t t = 0; t < S.nspan; t++) {
+            uint32_t q = wave + 8 * t, m = 0;
+            if (NMAT == 2 && q >= S.np0) {
+                m = 1;
+                q -= S.np0;
+            }
+            const uint32_t o = min(q * 256, S.slen[m] - 256);
+            __builtin_amdgcn_global_load_lds(S.sp[m] + o + lane * 4, dst + m * RPM * SB + o, 4, 0, 0);
+        }
+    };
+    auto issue_next = [&](auto st_tag, PgW& W) __attribute__((always_inline)) {
         constexpr uint32_t ST = decltype(st_tag)::value;
-        const uint32_t nq = issuing ? S.n : 0u;
+        if (issuing && ic == 0) issue_span(ipar);
+        const uint32_t nq = issuing ? S.n + (ic == 0 ? S.nspan : 0u) : PG_WLOADS;
         if (ST == 0) q0 = nq;
         if (ST == 1) q1 = nq;
         if (ST == 2) q2 = nq;
-        if (issuing) {
-            issue_chunk(S, ic, st_tag);
-            if (++ic == nch) {
-                ic = 0;
-                ipar ^= 1u;
-                iitem += G;
-                issuing = iitem < n_items;
-                if (issuing) setup_issue(ipar, S);
-            }
+        if (!issuing) S.on = 0;
+        const uint32_t ci = issuing ? ic : nch - 1;
+        static_for<8>([&](auto u) __attribute__((always_inline)) { issue_unit(S, ci, st_tag, W, u); });
+        if (issuing && ++ic == nch) {
+            ic = 0;
+            ipar ^= 1u;
+            iitem += G;
+            issuing = iitem < n_items;
+            if (issuing) setup_issue(ipar, S);
         }
     };
-    issue_next(std::integral_constant<uint32_t, 0>{});
-    issue_next(std::integral_constant<uint32_t, 1>{});
+    PgW W0, W1, W2;
+    issue_next(std::integral_constant<uint32_t, 0>{}, W0);
+    issue_next(std::integral_constant<uint32_t, 1>{}, W1);
 
     // ---- compute side ----
-    const uint32_t wm = wave >> 1, wn = wave & 1;
-    const uint32_t brow0 = NMAT == 2 ? wn * 32 : wn * 64;
-    auto jrow = [](int j) __attribute__((always_inline)) -> uint32_t { return pg_jrow<NMAT>((uint32_t)j); };
-    // Activation operand of lane (g, r): route 32 wm + 16 a + r, k 16 g.. and
+    // Activation operand of lane (g, r): route 16 a + r, k 16 g.. and
     // 64 + 16 g.. of each 128-k half h, at pieces (8 h + g) ^ r, (8 h + 4 + g) ^ r.
-    const uint32_t ta = 32 * wm + rr;
     uint32_t LA[4];
 #pragma unroll
-    for (uint32_t q = 0; q < 4; q++) LA[q] = ring + PG_A_OFF + ta * 256 + (((4 * q) + g) ^ rr) * 16;
-    const uint32_t LSA = ring + PG_SA_OFF + wm * 256 + rr * 16;
-    // Weight operand of lane (g, r): row r of the tile, bytes 64 h + 16 g.
-    const uint32_t sw = pg_swz_b(rr);
-    const uint32_t LB0 = ring + PG_B_OFF + (brow0 + rr) * 128 + ((g ^ sw) * 16);
-    const uint32_t LB1 = ring + PG_B_OFF + (brow0 + rr) * 128 + (((4 + g) ^ sw) * 16);
+    for (uint32_t q = 0; q < 4; q++) LA[q] = ring + PG_A_OFF + rr * 256 + (((4 * q) + g) ^ rr) * 16;
+    const uint32_t LSA = ring + PG_SA_OFF + rr * 8;
 
     uint32_t cpar = 0, c = 0;              // compute item descriptor slot, chunk
     uint32_t count = 0, rb = 0, alim = 0;
-    uint32_t LSB[4];
-    v4f acc[2][4];
+    uint32_t LSB[2];
+    v4f acc[NA][2];
     auto start_item = [&]() __attribute__((always_inline)) {
         rb = rec_word(cpar, 0);
         count = rec_word(cpar, 1);
-        alim = count > 32 * wm ? min(2u, (count - 32 * wm + 15) / 16) : 0u;
+        alim = min((uint32_t)NA, (count + 15) / 16);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t r = brow0 + jrow(j) + rr, n = rb * RPM + r % RPM;
-            LSB[j] = ring + PG_SB_OFF + r * 16 + (((n < N ? n : 0) * SB) & 3u) + g;
+        for (uint32_t j = 0; j < 2; j++) {
+            const uint32_t ir = pg_irow<NMAT>(wave, j);
+            LSB[j] = ring + PG_SPAN_OFF + cpar * (PG_ROWS * SB) + (ir + rr) * SB + g;
         }
 #pragma unroll
-        for (int a = 0; a < 2; a++)
+        for (int a = 0; a < NA; a++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 2; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
     };
     start_item();
     bool cnext = item + G < n_items;        // is there an item after the compute item
@@ -3004,34 +3073,34 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     auto epilogue = [&]() __attribute__((always_inline)) {
         const uint32_t list = ring + PG_LIST_OFF + cpar * 2048;
 #pragma unroll
-        for (int a = 0; a < 2; a++) {
-            if ((uint32_t)a >= alim) continue;
+        for (uint32_t a = 0; a < (uint32_t)NA; a++) {
+            if (a >= alim) continue;
+            // routes 16 a + 4 g .. + 3 (and their weights) in one read each
+            v4i rt, wv;
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(rt), "=&v"(wv)
+                         : "v"(list + (16 * a + 4 * g) * 4));
+            const uint32_t lim = count - 16 * a;   // routes of subtile a (a < alim: > 0)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t t = 32 * wm + 16 * a + 4 * g + i;
-                const uint32_t r = lds_rd32_sync<0>(list + 4 * t);
-                const uint32_t wrb = lds_rd32_sync<1024>(list + 4 * t);
-                if (t >= count) continue;
+                if (4 * g + i >= lim) continue;
+                const uint32_t r = (uint32_t)rt[i];
                 if (NMAT == 2) {
                     const uint64_t ob = (uint64_t)(r / A.k) * A.frame_elems + (uint64_t)(r % A.k) * N;
-#pragma unroll
-                    for (int j2 = 0; j2 < 2; j2++) {
-                        const uint32_t ch = rb * RPM + brow0 + j2 * 16 + rr;
-                        if (ch >= N) continue;
-                        float gv = round_bf16(acc[a][j2][i]);
-                        float uv = round_bf16(acc[a][2 + j2][i]);
-                        if (A.limit > 0.0f) {
-                            gv = fminf(gv, A.limit);
-                            uv = fminf(fmaxf(uv, -A.limit), A.limit);
-                        }
-                        const float h = (gv / (1.0f + expf(-gv))) * uv;
-                        A.out[ob + ch] = (uint16_t)f32_to_bf16(h);
+                    const uint32_t ch = rb * RPM + 16 * wave + rr;
+                    if (ch >= N) continue;
+                    float gv = round_bf16(acc[a][0][i]);
+                    float uv = round_bf16(acc[a][1][i]);
+                    if (A.limit > 0.0f) {
+                        gv = fminf(gv, A.limit);
+                        uv = fminf(fmaxf(uv, -A.limit), A.limit);
                     }
+                    A.out[ob + ch] = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
                 } else {
-                    const float wr = __uint_as_float(wrb);
+                    const float wr = __int_as_float(wv[i]);
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint32_t row = rb * RPM + brow0 + jrow(j) + rr;
+                    for (int j = 0; j < 2; j++) {
+                        const uint32_t row = rb * RPM + 32 * wave + 16 * j + rr;
                         if (row < N) A.out[(uint64_t)r * N + row] = (uint16_t)f32_to_bf16(acc[a][j][i] * wr);
                     }
                 }
@@ -3044,74 +3113,85 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     // and its route list at chunk 2), contract, and on the item's last chunk
     // write it out and switch items.  Returns false when the block has no
     // more work.
-    auto step = [&](auto st_tag) __attribute__((always_inline)) -> bool {
+    auto step = [&](auto st_tag, PgW& Wc, PgW& Wn) __attribute__((always_inline)) -> bool {
         constexpr uint32_t ST = decltype(st_tag)::value;
-        // Copies issued after this chunk's: the next chunk's, plus wave 0's
-        // descriptor copies issued in the previous step (record at chunk 0,
-        // list at chunk 2).
+        // Copies and loads issued after this chunk's: the next chunk's, plus
+        // wave 0's descriptor copies issued in the previous step (record at
+        // chunk 0, list at chunk 2).
         constexpr uint32_t S1 = (ST + 1) % PG_NST;
         uint32_t x = S1 == 0 ? q0 : S1 == 1 ? q1 : q2;
         if (wave == 0) x += (c == 1 ? 1u : 0u) + (c == 3 ? 2u : 0u);
         wait_vm(x);
         __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) asm volatile("" : "+v"(Wc.w[j][h]));
         if (wave == 0) {
             if (c == 0) copy_rec(item + G, cpar ^ 1u);
             else if (c == 2) copy_list(cpar ^ 1u);
         }
         // Chunk c + 2 (of this item or the next) goes into stage ST + 2.
-        issue_next(std::integral_constant<uint32_t, (ST + 2) % PG_NST>{});
-        // ---- contract chunk c from stage ST (waves without routes skip it) ----
-        if (alim != 0) {
-            v4i lo[2][2], hi[2][2], w[4][2];
-            v4i sa4;
-            uint32_t sbv[4][2];
-            static_for<4>([&](auto ji) __attribute__((always_inline)) {
-                constexpr uint32_t j = decltype(ji)::value;
-                w[j][0] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 128>(LB0);
-                w[j][1] = lds_rd128<ST * 16384 + pg_jrow<NMAT>(j) * 128>(LB1);
-            });
+        issue_next(std::integral_constant<uint32_t, (ST + 2) % PG_NST>{}, Wn);
+        // ---- contract chunk c: scales, then the route subtiles two reads ahead ----
+        // Subtiles past the item's routes contract stale LDS rows into
+        // accumulators the epilogue never reads; the three forms (2, 4, 8
+        // subtiles) keep every LDS read unconditional inside a form, so no
+        // read result has to be merged across branches before its wait.
+        auto contract = [&](auto n_tag) __attribute__((always_inline)) {
+            constexpr uint32_t NC = decltype(n_tag)::value;
+            uint32_t sbv[2][2];
+            v2i sav[2];
+            v4i av[2][4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                sbv[j][0] = lds_rd8<ST * 2048>(LSB[j]);
-                sbv[j][1] = lds_rd8<ST * 2048 + 4>(LSB[j]);
+            for (int j = 0; j < 2; j++) {
+                sbv[j][0] = lds_rd8<0>(LSB[j] + 8 * c);
+                sbv[j][1] = lds_rd8<4>(LSB[j] + 8 * c);
             }
-            sa4 = lds_rd128<ST * 1024>(LSA);
-            static_for<2>([&](auto ai) __attribute__((always_inline)) {
+            // Route subtile a's operands: 4 activation pieces and its block scales.
+            auto read_a = [&](auto ai) __attribute__((always_inline)) {
                 constexpr uint32_t a = decltype(ai)::value;
-                if (a < alim) {
-                    lo[a][0] = lds_rd128_far<ST * 32768 + a * 4096>(LA[0]);
-                    hi[a][0] = lds_rd128_far<ST * 32768 + a * 4096>(LA[1]);
-                    lo[a][1] = lds_rd128_far<ST * 32768 + a * 4096>(LA[2]);
-                    hi[a][1] = lds_rd128_far<ST * 32768 + a * 4096>(LA[3]);
+#pragma unroll
+                for (int q = 0; q < 4; q++) av[a % 2][q] = lds_rd128_far<ST * 32768 + a * 4096>(LA[q]);
+                sav[a % 2] = lds_rd64<ST * 1024 + a * 128>(LSA);
+            };
+            read_a(std::integral_constant<uint32_t, 0>{});
+            static_for<NC>([&](auto ai) __attribute__((always_inline)) {
+                constexpr uint32_t a = decltype(ai)::value;
+                // Subtile a's reads are done when at most the next subtile's
+                // five are in flight.
+                if constexpr (a + 1 < NC) {
+                    read_a(std::integral_constant<uint32_t, a + 1>{});
+                    asm volatile("s_waitcnt lgkmcnt(5)"
+                                 : "+v"(av[a % 2][0]), "+v"(av[a % 2][1]), "+v"(av[a % 2][2]), "+v"(av[a % 2][3]),
+                                   "+v"(sav[a % 2]));
+                } else {
+                    asm volatile("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(av[a % 2][0]), "+v"(av[a % 2][1]), "+v"(av[a % 2][2]), "+v"(av[a % 2][3]),
+                                   "+v"(sav[a % 2]));
                 }
-            });
-            asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(lo[0][0]), "+v"(lo[0][1]), "+v"(lo[1][0]), "+v"(lo[1][1]), "+v"(hi[0][0]),
-                           "+v"(hi[0][1]), "+v"(hi[1][0]), "+v"(hi[1][1]), "+v"(w[0][0]), "+v"(w[0][1]),
-                           "+v"(w[1][0]), "+v"(w[1][1]), "+v"(w[2][0]), "+v"(w[2][1]), "+v"(w[3][0]),
-                           "+v"(w[3][1]), "+v"(sa4), "+v"(sbv[0][0]), "+v"(sbv[0][1]), "+v"(sbv[1][0]),
-                           "+v"(sbv[1][1]), "+v"(sbv[2][0]), "+v"(sbv[2][1]), "+v"(sbv[3][0]), "+v"(sbv[3][1]));
-            // Scale blocks past K (last chunk) read bytes beyond the row.
+                if constexpr (a == 0) {
+                    asm volatile("" : "+v"(sbv[0][0]), "+v"(sbv[0][1]), "+v"(sbv[1][0]), "+v"(sbv[1][1]));
+                    // Scale blocks past K (last chunk) read bytes beyond the row.
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const bool bvalid = c * 8 + 4 * h + g < SB;
+                    for (int h = 0; h < 2; h++) {
+                        const bool bvalid = c * 8 + 4 * h + g < SB;
 #pragma unroll
-                for (int j = 0; j < 4; j++) sbv[j][h] = bvalid ? sbv[j][h] : 127u;
-            }
-            const uint32_t sav[2][2] = {{(uint32_t)sa4.x, (uint32_t)sa4.y}, {(uint32_t)sa4.z, (uint32_t)sa4.w}};
-#pragma unroll
-            for (int a = 0; a < 2; a++) {
-                if ((uint32_t)a >= alim) continue;
+                        for (int j = 0; j < 2; j++) sbv[j][h] = bvalid ? sbv[j][h] : 127u;
+                    }
+                }
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const v8i av = v8i{lo[a][h].x, lo[a][h].y, lo[a][h].z, lo[a][h].w,
-                                       hi[a][h].x, hi[a][h].y, hi[a][h].z, hi[a][h].w};
-                    const uint32_t se = (sav[a][h] >> 23) & 0xffu;
+                    const v8i x8 = v8i{av[a % 2][2 * h].x, av[a % 2][2 * h].y, av[a % 2][2 * h].z, av[a % 2][2 * h].w,
+                                       av[a % 2][2 * h + 1].x, av[a % 2][2 * h + 1].y, av[a % 2][2 * h + 1].z,
+                                       av[a % 2][2 * h + 1].w};
+                    const uint32_t se = ((uint32_t)sav[a % 2][h] >> 23) & 0xffu;
 #pragma unroll
-                    for (int j = 0; j < 4; j++) acc[a][j] = mfma_fp8_fp4(av, w[j][h], se, sbv[j][h], acc[a][j]);
+                    for (int j = 0; j < 2; j++) acc[a][j] = mfma_fp8_fp4(x8, Wc.w[j][h], se, sbv[j][h], acc[a][j]);
                 }
-            }
-        }
+            });
+        };
+        contract(std::integral_constant<uint32_t, NA>{});
         if (++c < nch) return true;
         // ---- end of the item ----
         epilogue();
@@ -3124,10 +3204,28 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
         return true;
     };
     while (true) {
-        if (!step(std::integral_constant<uint32_t, 0>{})) break;
-        if (!step(std::integral_constant<uint32_t, 1>{})) break;
-        if (!step(std::integral_constant<uint32_t, 2>{})) break;
+        if (!step(std::integral_constant<uint32_t, 0>{}, W0, W2)) break;
+        if (!step(std::integral_constant<uint32_t, 1>{}, W1, W0)) break;
+        if (!step(std::integral_constant<uint32_t, 2>{}, W2, W1)) break;
     }
+    // Loads past the last item may still be in flight into registers.
+    wait_vm_imm<0>();
+}
+
+template <int NMAT>
+__global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
+    constexpr uint32_t RPM = PG_ROWS / NMAT;
+    const uint32_t nrb = (A.N + RPM - 1) / RPM;
+    const uint32_t nt = __builtin_amdgcn_readfirstlane(A.n_tiles[0]);
+    const uint32_t nt0 = __builtin_amdgcn_readfirstlane(A.n_tiles[1]);
+    const uint32_t nt1 = __builtin_amdgcn_readfirstlane(A.n_tiles[2]);
+    // The groups run one after the other; every wave finishes a group (its
+    // descriptor slots and ring are reused) before the next starts.
+    pg_range<NMAT, 8>(A, 0, nt0 * nrb);
+    __syncthreads();
+    pg_range<NMAT, 4>(A, nt0 * nrb, (nt0 + nt1) * nrb);
+    __syncthreads();
+    pg_range<NMAT, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
 }
 
 template <int NMAT>
@@ -3135,11 +3233,11 @@ nerve_hip_status launch_pgemm(const PgArgs& A, const nerve_hip_ctx* ctx, hipStre
     static bool attr_set = false;
     if (!attr_set) {
         if (hipFuncSetAttribute((const void*)moe_pgemm_kernel<NMAT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                PG_LDS) != hipSuccess)
+                                160 * 1024) != hipSuccess)
             return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for moe_pgemm_kernel");
         attr_set = true;
     }
-    moe_pgemm_kernel<NMAT><<<ctx->cu_count, 512, PG_LDS, st>>>(A);
+    moe_pgemm_kernel<NMAT><<<ctx->cu_count, 512, pg_lds_bytes(A.K), st>>>(A);
     return nh::check_launch("moe_pgemm_kernel");
 }
 
@@ -3261,8 +3359,12 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         return nh::fail(NERVE_HIP_UNSUPPORTED, "e4m3 expert banks and block-major weights are supported for E <= 1024");
     const bool grouped = !wf && (cap >= 512 || K > 4096);
     // Persistent grouped GEMM: enough chunks per item for the descriptor
-    // prefetch rounds.
-    const bool persistent = grouped && (K + PG_KC - 1) / PG_KC >= PG_MIN_CHUNKS;
+    // prefetch rounds, the item's scale spans fit the LDS, and every span is
+    // a whole number of dwords of at least 256 bytes (copied in 256-byte
+    // pieces, the last aligned to the span's end).
+    const uint32_t pg_rpm = gate_up ? PG_ROWS / 2 : PG_ROWS, pg_tail = N % pg_rpm;
+    const bool persistent = grouped && (K + PG_KC - 1) / PG_KC >= PG_MIN_CHUNKS && pg_lds_bytes(K) <= 160 * 1024 &&
+                            (pg_tail * (K / 32)) % 4 == 0 && (pg_tail == 0 || pg_tail * (K / 32) >= 256);
     const uint32_t TM = persistent ? PG_TM : grouped ? 64 : 16;
     const uint32_t max_tiles = (cap + TM - 1) / TM + (E < cap ? E : cap);
     nh::Carver cv;
@@ -3270,7 +3372,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     size_t o_as = cv.take<float>((size_t)arows * nblk);
     size_t o_seg = cv.take<uint32_t>(cap + 16);   // +16: the streaming kernel reads 16 entries at once
     size_t o_rec = cv.take<TileRec>(max_tiles);
-    size_t o_nt = cv.take<uint32_t>(1);
+    size_t o_nt = cv.take<uint32_t>(4);   // tiles; persistent GEMM: tiles of the first two route-count groups
     const uint32_t item_nrb = (N + (gate_up ? PG_ROWS / 2 : PG_ROWS) - 1) / (gate_up ? PG_ROWS / 2 : PG_ROWS);
     size_t o_items = cv.take<ItemRec>(persistent ? (size_t)max_tiles * item_nrb : 0);
     size_t o_lists = cv.take<PgList>(persistent ? max_tiles : 0);

@@ -373,12 +373,17 @@ __device__ void build_tiles(const TileArgs& A) {
     const uint32_t P = A.P;   // 4 (gate, gate scales, up, up scales) or 2 (down, down scales)
 
     // ---- round 1: slot words of expert tid, route map entry tid, control
+    // Every load of the two rounds is issued unconditionally (from a clamped
+    // index, its value discarded where it does not apply): a load under a
+    // lane condition makes the compiler wait for all loads in flight at the
+    // branch's end, which turned the rounds into a dozen round trips.
     uint32_t slot[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
-    if (tid < A.E) {
+    if (A.n_slot_words != 0) {
 #pragma unroll
         for (uint32_t p = 0; p < 4; p++) {
             const uint32_t idx = tid * P + p;
-            if (p < P && idx < A.n_slot_words) slot[p] = A.slots[idx];
+            const uint32_t v = A.slots[min(idx, A.n_slot_words - 1)];
+            if (tid < A.E && p < P && idx < A.n_slot_words) slot[p] = v;
         }
     }
     // Slots c = tid + i nt for i < PREP_R keep their route index and route
@@ -388,22 +393,33 @@ __device__ void build_tiles(const TileArgs& A) {
 #pragma unroll
     for (uint32_t i = 0; i < PREP_R; i++) {
         const uint32_t c = tid + i * nt;
-        rw_r[i] = c < cap ? A.frames[(uint64_t)(c / A.k) * A.frame_words + A.data_words + c % A.k] : 0xffffffffu;
+        const uint32_t cc = c < cap ? c : 0u;
+        const uint32_t v = A.frames[(uint64_t)(cc / A.k) * A.frame_words + A.data_words + cc % A.k];
+        rw_r[i] = c < cap ? v : 0xffffffffu;
     }
     const uint32_t rword = rw_r[0];
     const uint32_t c2 = A.control[2], c3 = A.control[3];
     // ---- round 2: address records, route word
-    uint32_t rec[4][8];
+    uint32_t rec[4][8] = {};
+    if (A.n_records != 0) {
 #pragma unroll
-    for (uint32_t p = 0; p < 4; p++) {
-        const bool has = slot[p] != UNBOUND_SLOT && slot[p] < A.n_records;
+        for (uint32_t p = 0; p < 4; p++) {
+            const bool has = slot[p] != UNBOUND_SLOT && slot[p] < A.n_records;
+            const v4i* r4 = reinterpret_cast<const v4i*>(A.addr + (uint64_t)(has ? slot[p] : 0u) * 8);
+            const v4i lo = r4[0], hi = r4[1];
+            const uint32_t w8[8] = {(uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)lo.z, (uint32_t)lo.w,
+                                    (uint32_t)hi.x, (uint32_t)hi.y, (uint32_t)hi.z, (uint32_t)hi.w};
 #pragma unroll
-        for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? A.addr[(uint64_t)slot[p] * 8 + j] : 0u;
+            for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? w8[j] : 0u;
+        }
     }
+    uint32_t rv[PREP_R];
+#pragma unroll
+    for (uint32_t i = 0; i < PREP_R; i++) rv[i] = A.routes[rw_r[i] < cap ? rw_r[i] : 0u];
 #pragma unroll
     for (uint32_t i = 0; i < PREP_R; i++) {
         const uint32_t c = tid + i * nt;
-        rt_r[i] = (c < cap && rw_r[i] < cap) ? A.routes[rw_r[i]] : 0u;
+        rt_r[i] = (c < cap && rw_r[i] < cap) ? rv[i] : 0u;
     }
     const uint32_t route = rt_r[0];
 

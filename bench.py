@@ -300,8 +300,8 @@ def mxfp4_gemv(args, ctx, dev):
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "e4m3xe2m1->f32",
                     {"workload": "mxfp4_gemv_m1_k2880_n5760", "weight_copies_rotated": copies})
-    out["roofline"] = {"bound": "hbm", "kernel": "mx_span_kernel<0,1,1,8>", "achieved": gbs, "peak": HBM_PEAK_GBS,
-                       "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+    out["roofline"] = {"bound": "hbm", "kernel": "mx_span_kernel<0,1,2,8>", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": traffic_for("mx_span_kernel<0, 1, 2, 8>"),
                        "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
     return out
 
@@ -332,7 +332,7 @@ def int4_gemv(args, ctx, dev):
                     {"workload": f"int4_gptq_g128_asym_m{M}_k4096_n14336", "weight_copies_rotated": copies})
     kname = "int4_gptq_gemv_kernel<16, 128, true>" if M <= 2 else "int4_gptq_fixed_kernel<16, 4, 4>"
     out["roofline"] = {"bound": "hbm", "kernel": kname, "achieved": gbs, "peak": HBM_PEAK_GBS,
-                       "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                       "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": traffic_for(kname),
                        "algorithmic_bytes_per_launch": alg, "launch_ms": kms}
     return out
 
@@ -439,10 +439,13 @@ def fp8_head(args, ctx, dev):
     mfma_bound = M >= 512
     kname = ("fp8_head_stream_kernel<2> (+ row quantization, argmax of the partials)" if M <= 16
              else "fp8_head_gemm_kernel (+ row quantization, scale scan, argmax of the partials)")
+    tkey = ("fp8_head_stream_kernel<2>" if M <= 16 else "fp8_head_gemm_kernel<2, 4, 2, 4, 3>" if M <= 64
+            else "fp8_head_gemm_kernel<2, 4, 4, 2, 4>" if M <= 128 else "fp8_head_gemm_kernel<4, 2, 4, 4, 3>")
     out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": kname,
                        "achieved": tf if mfma_bound else gbs, "peak": FP8_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
                        "unit": "TFLOP/s" if mfma_bound else "GB/s",
-                       "frac": (tf / FP8_PEAK_TFLOPS) if mfma_bound else (gbs / HBM_PEAK_GBS), "traffic": None,
+                       "frac": (tf / FP8_PEAK_TFLOPS) if mfma_bound else (gbs / HBM_PEAK_GBS),
+                       "traffic": traffic_for(tkey),
                        "hbm_gbs": gbs, "tflops": tf, "launch_ms": kms}
     return out
 
@@ -466,13 +469,16 @@ def hbm_copy(args, ctx, dev):
     return out
 
 
-def _pmc_per_dispatch(csv_dir, counter):
-    """{kernel name: mean counter value per dispatch} from rocprofv3 CSVs."""
+def _pmc_per_dispatch(csv_dirs, counter):
+    """{kernel name: mean counter value per dispatch} from rocprofv3 CSVs
+    under the comma-separated directories `csv_dirs`."""
     import csv
     import glob
 
     vals = {}
-    for f in glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True):
+    files = [f for d in csv_dirs.split(",")
+             for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)]
+    for f in files:
         with open(f) as fh:
             for row in csv.DictReader(fh):
                 if row.get("Counter_Name") != counter:
@@ -485,7 +491,8 @@ def _pmc_per_dispatch(csv_dir, counter):
 
 
 def summarize_traffic(dirs):
-    """--summarize-traffic FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR:
+    """--summarize-traffic FETCH_DIRS WRITE_DIRS COPY_FETCH_DIR COPY_WRITE_DIR
+    (FETCH_DIRS / WRITE_DIRS: comma-separated, one run per workload):
     per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of every kernel, scaled by the
     copy calibration (512 MiB read and written per dispatch), written to
     profiles/traffic.json and printed as a markdown table."""

@@ -1104,6 +1104,7 @@ struct SpanArgs {
     float limit;
     uint32_t w_region, s_region;   // LDS bytes per matrix (padded)
     uint32_t block_major;          // mx_wfmt_kernel: compact weights in the input-block-major layout
+    uint32_t rpb;                  // mx_span_kernel: weight rows per block (<= 16 NSUB; 0: 16 NSUB)
 };
 
 __host__ __device__ inline uint32_t span_w_region(uint32_t rows, uint32_t K) { return (rows * (K / 2) + 1023) / 1024 * 1024; }
@@ -1116,8 +1117,10 @@ __global__ __launch_bounds__(64 * NWS) void mx_span_kernel(SpanArgs A) {
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t g = lane >> 4, rr = lane & 15;
     const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
-    const uint32_t n0 = blockIdx.x * R;
+    const uint32_t rpb = A.rpb ? A.rpb : R;
+    const uint32_t n0 = blockIdx.x * rpb;
     if (n0 >= N) return;
+    const uint32_t rows = min(rpb, N - n0);   // rows of this block (the subtiles past them are not stored)
     uint32_t cnt, begin = 0;
     TileRec rec;
     if (MODE == SPAN_RAW) {
@@ -1138,7 +1141,6 @@ __global__ __launch_bounds__(64 * NWS) void mx_span_kernel(SpanArgs A) {
     for (int m = 0; m < NMAT; m++) {
         const uint8_t* wb = rec.w[m];
         const uint8_t* sb = rec.s[m];
-        const uint32_t rows = min(R, N - n0);
         const uint8_t* wsrc = wb + (uint64_t)n0 * RB;
         const uint32_t wbytes = rows * RB;
         uint8_t* wdst = span_lds + m * A.w_region;
@@ -1221,7 +1223,7 @@ __global__ __launch_bounds__(64 * NWS) void mx_span_kernel(SpanArgs A) {
             for (int w = 1; w < NWS; w++) t[m] += red[((w * NMAT + m) * NSUB + j) * 64 + lane];
         }
         const uint32_t n = n0 + j * 16 + rr;
-        if (n >= N) continue;
+        if (j * 16 + rr >= rows) continue;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t tl = 4 * g + i;
@@ -1380,7 +1382,9 @@ nerve_hip_status launch_span(SpanArgs A, uint32_t tiles, hipStream_t st) {
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
-    dim3 grid((A.N + R - 1) / R, tiles);
+    const uint32_t rpb = A.rpb ? A.rpb : R;
+    if (rpb > R) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "span rows per block exceed the kernel's tile");
+    dim3 grid((A.N + rpb - 1) / rpb, tiles);
     mx_span_kernel<MODE, NMAT, NSUB, NWS><<<grid, 64 * NWS, lds, st>>>(A);
     return nh::check_launch("mx_span_kernel");
 }
@@ -3332,6 +3336,16 @@ nerve_hip_status nerve_hip_mxfp4_gemv(nerve_hip_ctx* ctx, const void* q_e4m3, co
         sa.w_direct = static_cast<const uint8_t*>(weight);
         sa.s_direct = static_cast<const uint8_t*>(weight_scale);
         sa.out32 = static_cast<float*>(y_f32);
+        // Rows per block: one block per CU when N allows (a multiple of 8 rows,
+        // so every block's weight and scale spans keep 16- and 4-byte
+        // alignment), 16 to 32 rows; 16-row blocks leave some CUs two blocks
+        // while others have one.
+        const uint32_t cu = (uint32_t)ctx->cu_count;
+        const uint32_t want = ((N + cu - 1) / cu + 7) / 8 * 8;
+        if (want > 16 && want <= 32 && (uint64_t)want * (K / 32) % 4 == 0) {
+            sa.rpb = want;
+            return launch_span<SPAN_RAW, 1, 2, 8>(sa, (M + 15) / 16, (hipStream_t)stream);
+        }
         return launch_span<SPAN_RAW, 1, 1, 8>(sa, (M + 15) / 16, (hipStream_t)stream);
     }
     mxfp4_gemv_kernel<8><<<N / 16, 512, 0, (hipStream_t)stream>>>(

@@ -58,7 +58,10 @@ def test_gemv_config0_parity(ctx, dev):
     assert rel_err_normwise(y, ref) <= 1e-3
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 128, 16), (4, 256, 64), (16, 2880, 256), (33, 4096, 128), (64, 160, 32)])
+@pytest.mark.parametrize("M,K,N", [(1, 128, 16), (4, 256, 64), (16, 2880, 256), (33, 4096, 128), (64, 160, 32),
+                                   # rows per block sized to one block per CU: 24 rows with a 16-row
+                                   # last block, 32 rows
+                                   (3, 2880, 5776), (1, 1024, 7168)])
 def test_gemv_shapes(ctx, dev, M, K, N):
     rng = np.random.default_rng(M * K + N)
     W, S = wl.mxfp4_matrix(rng, N, K, 118, 130)

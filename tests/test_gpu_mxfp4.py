@@ -205,6 +205,32 @@ def test_moe_chain_parity(ctx, dev, E, k, B, H, I):
     assert rel_err_normwise(wl.bf16_bits_to_f32(to_np(rig.out, np.uint16)), out_chain) <= 2e-2
 
 
+@pytest.mark.parametrize("counts", [(1, 32, 33, 64, 65, 128, 129, 260), (200, 300, 3, 17, 0, 45, 60, 91)])
+def test_prefill_route_count_groups(ctx, dev, counts):
+    """Persistent grouped GEMM: experts on both sides of the 32- and 64-route
+    group boundaries, several 128-route tiles (with a short last tile) and an
+    expert without routes, against the oracle on both stages."""
+    E, k, H, I = 8, 2, 1856, 1664
+    rng = np.random.default_rng(sum(counts))
+    ex = np.repeat(np.arange(E), counts)
+    rng.shuffle(ex)
+    B = len(ex) // k
+    assert B * k == len(ex) and B * k >= 512
+    d = wl.moe_experts(rng, E, H, I)
+    d["limit"] = 7.0
+    routes = _route_words(ex.reshape(B, k), rng.uniform(0.05, 1.0, (B, k)).astype(np.float32))
+    hidden = wl.bf16_normal(rng, (B, H))
+    rig = MoeRig(dev, d, routes)
+    rig.run(ctx, hidden)
+    cmap, _ = oracle.route_compact(routes, k, (I + 31) // 32, B)
+    h_ref = oracle.moe_gate_up(hidden, routes, cmap, B * k, k, d["gate_w"], d["gate_s"], d["up_w"], d["up_s"], 7.0)
+    ok, worst, exact = bf16_close(rig.h_np(), h_ref)
+    assert ok and exact > 0.9, (worst, exact)
+    eo_ref = oracle.moe_down(rig.h_np(), routes, cmap, B * k, d["down_w"], d["down_s"])
+    ok, worst, exact = bf16_close(to_np(rig.expert_out, np.uint16), eo_ref)
+    assert ok and exact > 0.9, (worst, exact)
+
+
 # H = 128: the span kernels; H = 512: the token-form gate_up kernel and the
 # streaming down kernel.
 @pytest.mark.parametrize("H,I", [(128, 128), (512, 256)])

@@ -437,9 +437,10 @@ def fp8_head(args, ctx, dev):
     out = base_line(args, M / (kms * 1e-3), "tokens/s", ms, "e4m3xe4m3->f32",
                     {"workload": f"fp8_lm_head_m{M}_k2880_n201088_argmax"})
     mfma_bound = M >= 512
-    kname = ("fp8_head_stream_kernel<2> (+ row quantization, argmax of the partials)" if M <= 16
+    kname = ("fp8_head_stream_kernel<2, 1 or 2> (+ row quantization, argmax of the partials)" if M <= 32
              else "fp8_head_gemm_kernel (+ row quantization, scale scan, argmax of the partials)")
-    tkey = ("fp8_head_stream_kernel<2>" if M <= 16 else "fp8_head_gemm_kernel<2, 4, 2, 4, 3>" if M <= 64
+    tkey = ("fp8_head_stream_kernel<2, 1>" if M <= 16 else "fp8_head_stream_kernel<2, 2>" if M <= 32
+            else "fp8_head_gemm_kernel<2, 4, 2, 4, 3>" if M <= 64
             else "fp8_head_gemm_kernel<2, 4, 4, 2, 4>" if M <= 128 else "fp8_head_gemm_kernel<4, 2, 4, 4, 3>")
     out["roofline"] = {"bound": "mfma" if mfma_bound else "hbm", "kernel": kname,
                        "achieved": tf if mfma_bound else gbs, "peak": FP8_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,

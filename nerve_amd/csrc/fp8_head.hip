@@ -276,7 +276,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void fp8_head_skinny_kernel(HeadArgs
 }
 
 // ---------------------------------------------------------------------------
-// Stream form (M <= 16, per-row weight scales): one 8-wave block per CU over
+// Stream form (M <= 32, per-row weight scales, K <= 3072): one 8-wave block per CU over
 // a contiguous range of 16-row vocabulary groups.  A group's weights are one
 // contiguous 16 K-byte span of W and its scales one contiguous 32 nblk-byte
 // span of scale_inv; both are read with nontemporal loads (1 KiB and 256 B
@@ -285,10 +285,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) void fp8_head_skinny_kernel(HeadArgs
 // flight while it contracts the current one.
 // The tokens are the MFMA A operand and stay in registers for the whole
 // range; each wave contracts its share of the K chunks of every group and the
-// 8 partial sums meet in LDS, where waves 0..3 finalize token 4 g + wave.
+// 8 partial sums meet in LDS, where waves 0..3 finalize token 16 t + 4 g +
+// wave of each token tile t.
 // ---------------------------------------------------------------------------
 constexpr int HS_NW = 8;
-constexpr uint32_t HS_CH = 4;        // K chunks per wave (K <= 4096; the LDS wait below names 4)
+constexpr uint32_t HS_CH = 3;        // K chunks per wave (K <= 3072: 24 chunks over 8 waves)
 constexpr uint32_t HS_LWMAX = 6;     // weight pieces per wave per group (16 K <= 48 KiB: K <= 3072)
 
 struct HeadStream {
@@ -298,7 +299,11 @@ struct HeadStream {
     uint32_t slot_bytes, s_off;      // ring slot size; scale region offset in a slot
 };
 
-template <int NBUF>
+// MT token tiles of 16 (M <= 16 MT): each group's weights are contracted
+// against all of them, so the weight stream is read once for up to 32 tokens.
+// (Four tiles, with the token scales moved to LDS to fit the registers, took
+// 186 us at M = 64 against the tiled GEMM's 161.)
+template <int NBUF, int MT>
 __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const HeadStream& S) {
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -306,7 +311,7 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
     const uint32_t K = A.K, M = A.M, N = A.N, nblk = (K + 127) / 128;
     const uint32_t G = gridDim.x, b = blockIdx.x;
     const uint32_t i0 = (uint32_t)((uint64_t)S.groups * b / G), i1 = (uint32_t)((uint64_t)S.groups * (b + 1) / G);
-    uint8_t* red = ring + 2 * S.slot_bytes;         // [wave][lane] v4f partial sums
+    uint8_t* red = ring + 2 * S.slot_bytes;         // [wave][MT][lane] v4f partial sums
 
     // ---- copy plan: piece t of this wave starts at byte wpos[t] of the
     // group's span (waves past the last piece repeat their first one, so
@@ -370,47 +375,58 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
     }
 
     // ---- tokens: e4m3 operand pieces and block scales, loaded before the
-    // first group's weights.  Quantizing
-    // the tokens here instead would repeat the whole M x K quantization in
-    // every block, vector-ALU work that outlasts the ring's first groups.
-    const bool arow = rr < M;
-    v4i xlo[HS_CH], xhi[HS_CH];
-    uint32_t sxr[HS_CH][4];
-    {
-        const uint8_t* xr = A.xq + (uint64_t)(arow ? rr : 0u) * K;
+    // first group's weights.  Quantizing the tokens here instead would repeat
+    // the whole M x K quantization in every block, vector-ALU work that
+    // outlasts the ring's first groups.
+    v4i xlo[MT][HS_CH], xhi[MT][HS_CH];
+    uint32_t sxr[MT][HS_CH][4];
+#pragma unroll
+    for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) {
+        const bool arow = 16 * mt + rr < M;
+        const uint8_t* xr = A.xq + (uint64_t)(arow ? 16 * mt + rr : 0u) * K;
 #pragma unroll
         for (uint32_t q = 0; q < HS_CH; q++) {
             if (c0 + q >= c1) continue;                 // wave-uniform
             const uint32_t kb = kvalid[q] ? (c0 + q) * 128 + g * 32 : 0u;
-            xlo[q] = *reinterpret_cast<const v4i*>(xr + kb);
-            xhi[q] = *reinterpret_cast<const v4i*>(xr + kb + 16);
+            xlo[mt][q] = *reinterpret_cast<const v4i*>(xr + kb);
+            xhi[mt][q] = *reinterpret_cast<const v4i*>(xr + kb + 16);
 #pragma unroll
             for (uint32_t i = 0; i < 4; i++) {
-                const uint32_t tk = 4 * g + i;
-                sxr[q][i] = __float_as_uint(A.xs[tk < M ? tk * nblk + c0 + q : 0u]);
+                const uint32_t tk = 16 * mt + 4 * g + i;
+                sxr[mt][q][i] = __float_as_uint(A.xs[tk < M ? tk * nblk + c0 + q : 0u]);
             }
         }
     }
     GroupRegs R0, R1;
     load_group(i0, R0);
-    v8i av[HS_CH];
-    float sx[HS_CH][4];
+    v8i av[MT][HS_CH];
+    float sx[MT][HS_CH][4];
 #pragma unroll
-    for (uint32_t q = 0; q < HS_CH; q++) {
-        av[q] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) {
+        const bool arow = 16 * mt + rr < M;
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) sx[q][i] = 0.0f;
-        if (c0 + q >= c1) continue;
-        if (arow && kvalid[q])
-            av[q] = v8i{xlo[q].x, xlo[q].y, xlo[q].z, xlo[q].w, xhi[q].x, xhi[q].y, xhi[q].z, xhi[q].w};
+        for (uint32_t q = 0; q < HS_CH; q++) {
+            av[mt][q] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) sx[q][i] = 4 * g + i < M ? __uint_as_float(sxr[q][i]) : 0.0f;
+            for (uint32_t i = 0; i < 4; i++) sx[mt][q][i] = 0.0f;
+            if (c0 + q >= c1) continue;
+            if (arow && kvalid[q])
+                av[mt][q] = v8i{xlo[mt][q].x, xlo[mt][q].y, xlo[mt][q].z, xlo[mt][q].w,
+                                xhi[mt][q].x, xhi[mt][q].y, xhi[mt][q].z, xhi[mt][q].w};
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) sx[mt][q][i] = 16 * mt + 4 * g + i < M ? __uint_as_float(sxr[mt][q][i]) : 0.0f;
+        }
     }
     load_group(i0 + 1, R1);
 
-    const uint32_t tok = 4 * g + wave;                  // finalized token (waves 0..3)
-    float best_v = -INFINITY;
-    uint32_t best_i = 0xffffffffu;
+    const uint32_t tok = 4 * g + wave;                  // finalized token of tile 0 (waves 0..3)
+    float best_v[MT];
+    uint32_t best_i[MT];
+#pragma unroll
+    for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) {
+        best_v[mt] = -INFINITY;
+        best_i[mt] = 0xffffffffu;
+    }
     // One group: its registers go to LDS slot (i - i0) % 2 (last read by the
     // group two back, whose reduction barrier every wave has passed), the
     // group two ahead is loaded into the same registers, a barrier, then the
@@ -433,45 +449,57 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
             w1[q] = *reinterpret_cast<const v4i*>(buf + rw[q] + 16);
             sw[q] = *reinterpret_cast<const uint16_t*>(buf + rs[q]);
         }
-        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+        v4f acc[MT];
+#pragma unroll
+        for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t q = 0; q < HS_CH; q++) {
             if (c0 + q >= c1) continue;
             v4i b0 = w0[q], b1 = w1[q];
             uint32_t s16 = sw[q];
             if (!kvalid[q]) b0 = b1 = v4i{0, 0, 0, 0};
-            const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                av[q], v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
-                0, 127);
+            const v8i bw = v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
             const float s = bf16_to_f32(s16);
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] = fmaf(p[e], sx[q][e] * s, acc[e]);
+            for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) {
+                const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[mt][q], bw, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                                0, 0, 0, 127, 0, 127);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[mt][e] = fmaf(p[e], sx[mt][q][e] * s, acc[mt][e]);
+            }
         }
-        *reinterpret_cast<v4f*>(red + (wave * 64 + lane) * 16) = acc;
+#pragma unroll
+        for (uint32_t mt = 0; mt < (uint32_t)MT; mt++)
+            *reinterpret_cast<v4f*>(red + ((wave * MT + mt) * 64 + lane) * 16) = acc[mt];
         __syncthreads();
         if (wave >= 4) return;
-        float sum = 0.0f;
-#pragma unroll
-        for (int w2 = 0; w2 < HS_NW; w2++) sum += *reinterpret_cast<const float*>(red + (w2 * 64 + lane) * 16 + 4 * wave);
-        const float val = sum * A.out_scale;
         const uint32_t n = i * 16 + rr;
         const bool cv = n < N;
-        if (tok < M && cv) {
-            if (A.logits_f32) A.logits_f32[(uint64_t)tok * N + n] = val;
-            if (A.logits_bf16) A.logits_bf16[(uint64_t)tok * N + n] = (uint16_t)f32_to_bf16(val);
-        }
-        if (A.part_val) {
-            float bv = cv ? val : -INFINITY;
-            uint32_t bi = cv ? n : 0xffffffffu;
 #pragma unroll
-            for (int d = 1; d < 16; d <<= 1) {
-                const float ov = __shfl_xor(bv, d);
-                const uint32_t oi = __shfl_xor(bi, d);
-                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < HS_NW; w2++)
+                sum += *reinterpret_cast<const float*>(red + ((w2 * MT + mt) * 64 + lane) * 16 + 4 * wave);
+            const float val = sum * A.out_scale;
+            const uint32_t tk = 16 * mt + tok;
+            if (tk < M && cv) {
+                if (A.logits_f32) A.logits_f32[(uint64_t)tk * N + n] = val;
+                if (A.logits_bf16) A.logits_bf16[(uint64_t)tk * N + n] = (uint16_t)f32_to_bf16(val);
             }
-            if (better(bv, bi, best_v, best_i)) {
-                best_v = bv;
-                best_i = bi;
+            if (A.part_val) {
+                float bv = cv ? val : -INFINITY;
+                uint32_t bi = cv ? n : 0xffffffffu;
+#pragma unroll
+                for (int d = 1; d < 16; d <<= 1) {
+                    const float ov = __shfl_xor(bv, d);
+                    const uint32_t oi = __shfl_xor(bi, d);
+                    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                }
+                if (better(bv, bi, best_v[mt], best_i[mt])) {
+                    best_v[mt] = bv;
+                    best_i[mt] = bi;
+                }
             }
         }
     };
@@ -484,19 +512,24 @@ __device__ __forceinline__ void fp8_head_stream_body(const HeadArgs& A, const He
         ++i;
     }
     wait_vm_imm<0>();   // the last re-read groups
-    if (A.part_val && wave < 4 && rr == 0 && tok < M) {
-        A.part_val[(uint64_t)tok * G + b] = best_v;
-        A.part_idx[(uint64_t)tok * G + b] = best_i;
+#pragma unroll
+    for (uint32_t mt = 0; mt < (uint32_t)MT; mt++) {
+        const uint32_t tk = 16 * mt + tok;
+        if (A.part_val && wave < 4 && rr == 0 && tk < M) {
+            A.part_val[(uint64_t)tk * G + b] = best_v[mt];
+            A.part_idx[(uint64_t)tk * G + b] = best_i[mt];
+        }
     }
 }
 
-template <int NBUF>
+template <int NBUF, int MT>
 __global__ __launch_bounds__(64 * HS_NW) void fp8_head_stream_kernel(HeadArgs A, HeadStream S) {
-    fp8_head_stream_body<NBUF>(A, S);
+    fp8_head_stream_body<NBUF, MT>(A, S);
 }
 
 // ---------------------------------------------------------------------------
-// Tiled form (M > 16): an LDS-staged FP8 GEMM.
+// Tiled form (M > 32, or M > 16 where the stream form does not apply): an
+// LDS-staged FP8 GEMM.
 //
 // Item = (vocabulary tile of TN rows, token tile of TM rows).  Items are
 // listed with token tiles fastest and dealt to the persistent blocks so that
@@ -1244,18 +1277,22 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
     hs.slot_bytes = hs.s_off + ((sspan < 256 ? 256 : sspan) + 15) / 16 * 16;
     hs.lw = (16 * K + 1023) / 1024 / HS_NW + ((16 * K + 1023) / 1024 % HS_NW ? 1 : 0);
     hs.cpi = HS_LWMAX + 1;   // every wave loads HS_LWMAX pieces (repeats past lw) and one scale dword
-    const size_t hs_red = HS_NW * 64 * 16;
+    // Up to 32 tokens in 1 or 2 tiles of 16 (the weight stream is read once
+    // for all of them).
+    const uint32_t hs_mt = M <= 16 ? 1u : 2u;
+    const size_t hs_red = (size_t)HS_NW * hs_mt * 64 * 16;
     const int hs_nbuf = 2;   // LDS slots; one more group is in flight in registers
-    const bool stream_form = skinny && s.block_rows == 1 && K >= 64 && ((uint64_t)N * nblk) % 2 == 0 &&
-                             ((uintptr_t)scale_inv_bf16 & 3) == 0 && hs.lw <= HS_LWMAX &&
+    const bool stream_form = M <= 32 && K <= 4096 && K % 32 == 0 && s.block_rows == 1 && K >= 64 &&
+                             ((uint64_t)N * nblk) % 2 == 0 && ((uintptr_t)scale_inv_bf16 & 3) == 0 &&
+                             hs.lw <= HS_LWMAX && (nblk + HS_NW - 1) / HS_NW <= HS_CH &&
                              hs_nbuf * (size_t)hs.slot_bytes + hs_red <= 160 * 1024 && hs.cpi * hs_nbuf <= 63;
     const uint32_t hs_grid = (uint32_t)ctx->cu_count;
-    // Tiled GEMM form (M > 16): token tiles of 64 / 128 / 256 rows, 128
+    // Tiled GEMM form (M > 16 without the stream form): token tiles of 64 / 128 / 256 rows, 128
     // vocabulary rows per tile; K <= 4096 (the general form's scale block
     // fits its LDS region) with at least NS chunks.
     const int hg_cfg = M <= 64 ? 0 : M <= 128 ? 1 : 2;
     const uint32_t hg_tm = kHgConfigs[hg_cfg].tm, hg_ns = kHgConfigs[hg_cfg].ns, hg_tn = kHgConfigs[hg_cfg].tn;
-    const bool gemm_form = !skinny && K <= 4096 && K % 32 == 0 && nblk >= hg_ns;
+    const bool gemm_form = !stream_form && !skinny && K <= 4096 && K % 32 == 0 && nblk >= hg_ns;
     const uint32_t hg_nvt = (N + hg_tn - 1) / hg_tn, hg_ntt = (M + hg_tm - 1) / hg_tm;
     const uint32_t hg_items = hg_nvt * hg_ntt;
     const uint32_t hg_grid = std::min<uint32_t>(hg_items, (uint32_t)ctx->cu_count);
@@ -1310,15 +1347,15 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
         const size_t lds = hs_nbuf * (size_t)hs.slot_bytes + hs_red;
         static bool attr_set = false;
         if (!attr_set) {
-            if (hipFuncSetAttribute((const void*)fp8_head_stream_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize,
+            if (hipFuncSetAttribute((const void*)fp8_head_stream_kernel<2, 1>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     160 * 1024) != hipSuccess ||
-                hipFuncSetAttribute((const void*)fp8_head_stream_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                hipFuncSetAttribute((const void*)fp8_head_stream_kernel<2, 2>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     160 * 1024) != hipSuccess)
                 return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for fp8_head_stream_kernel");
             attr_set = true;
         }
-        if (hs_nbuf == 3) fp8_head_stream_kernel<3><<<hs_grid, 64 * HS_NW, lds, strm>>>(A, hs);
-        else fp8_head_stream_kernel<2><<<hs_grid, 64 * HS_NW, lds, strm>>>(A, hs);
+        if (hs_mt == 1) fp8_head_stream_kernel<2, 1><<<hs_grid, 64 * HS_NW, lds, strm>>>(A, hs);
+        else fp8_head_stream_kernel<2, 2><<<hs_grid, 64 * HS_NW, lds, strm>>>(A, hs);
     } else if (skinny) {
         A.nblocks = sk_grid;
         const uint32_t per = (nblk + SK_WAVES - 1) / SK_WAVES;

@@ -136,17 +136,20 @@ def _argmax_ok(ids, ref_logits, tol):
     return True
 
 
-# M <= 16 with per-row scales takes the LDS-ring stream kernel (two ring
-# slots at K = 4096, a partial last 16-row group at N % 16 != 0, fewer groups
-# than blocks at small N); an odd N * nblk falls back to the register form;
-# M > 16 takes the LDS-staged GEMM (token tiles of 64 / 128 / 256 rows;
+# M <= 32 with per-row scales and K <= 3072 takes the stream kernel (1 or 2
+# token tiles of 16, a partial last 16-row group at N % 16 != 0, fewer
+# groups than blocks at small N); an odd N * nblk or K > 3072 falls back to
+# the register form (M <= 16) or the GEMM; other M > 16 take the LDS-staged
+# GEMM (token tiles of 64 / 128 / 256 rows;
 # partial token and vocabulary tiles, N % 4 != 0, the 64-column K tail,
 # K = 4096) or, with fewer K chunks than its ring has stages, the register
 # form.
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (7, 4096, 2880), (64, 2048, 512), (130, 600, 384),
                                    (16, 2000, 4096), (2, 777, 64), (5, 1001, 384), (3, 30010, 2880),
                                    (20, 1000, 2880), (64, 4099, 640), (100, 777, 1024), (128, 3000, 2880),
-                                   (300, 1300, 640), (257, 2051, 4096), (512, 5000, 2880)])
+                                   (300, 1300, 640), (257, 2051, 4096), (512, 5000, 2880),
+                                   # stream form with 2 token tiles (partial last tile); M = 33: the GEMM
+                                   (17, 2002, 384), (32, 3000, 2880), (33, 1500, 1024)])
 def test_fp8_head_parity(ctx, dev, M, N, K):
     rng = np.random.default_rng(M * N + K)
     d = wl.fp8_head(rng, N, K, M)

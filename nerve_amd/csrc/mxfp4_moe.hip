@@ -2340,7 +2340,7 @@ constexpr uint32_t TOK_MAX_RECORDS = 512;            // address table staged by 
 template <int NBUF, int NW>
 __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     constexpr uint32_t RI = 16, NMAT = 2, NSUB = 1;
-    constexpr uint32_t CH = 32 / NW;                              // chunks per computing wave (K <= (NW-1) CH 128)
+    constexpr uint32_t CH = 24 / NW;                              // chunks per wave (K <= NW CH 128)
     constexpr uint32_t LWMAX = (32 * NSUB + NW - 1) / NW;
     constexpr uint32_t LSMAX = (8 * NSUB + NW - 1) / NW;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
@@ -2352,9 +2352,10 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + 127) / 128;
     const uint32_t nrb = (N + RI - 1) / RI;
     const uint32_t B = T.batch_width, kr = T.k, cap = B * kr, E = T.E, P = T.P;
-    // Waves 1.. split the K chunks; wave 0 builds the plan and contracts nothing.
-    const uint32_t per = (nch + NW - 2) / (NW - 1);
-    const uint32_t c0 = wave == 0 ? nch : min(nch, (wave - 1) * per), c1 = wave == 0 ? nch : min(nch, c0 + per);
+    // All waves split the K chunks; wave 0 also builds the plan (and loads
+    // its activations after it).
+    const uint32_t per = (nch + NW - 1) / NW;
+    const uint32_t c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
     const bool row_ok = rr < B;
 
     // ---- activations: token rr's pieces of this wave's chunks (inline-asm
@@ -2390,7 +2391,8 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     const bool preq = A.aq != nullptr;   // wave-uniform: prequantized e4m3 rows + pow2 block scales
-    if (wave != 0 && !preq) {
+    auto act_loads = [&]() __attribute__((always_inline)) {
+    if (!preq) {
         const uint16_t* xr = A.x16 + (uint64_t)(row_ok ? rr : 0u) * A.x_frame;
 #pragma unroll
         for (uint32_t q = 0; q < CH; q++) {
@@ -2401,7 +2403,7 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
                 xb[q][h] = gload16_untracked(xr + (piece_ok(q, h) ? off : 0u));
             }
         }
-    } else if (wave != 0) {
+    } else {
         // Prequantized hidden rows (PREQUANTIZED_INPUT): the operand pieces
         // are the e4m3 bytes k = 16 g.. and 64 + 16 g.. of the chunk, the
         // scale is the row's f32 block scale (its exponent is the e8m0).
@@ -2416,6 +2418,8 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
             xb[q][2].x = (int)gload4_untracked(sr + c0 + q);
         }
     }
+    };
+    if (wave != 0) act_loads();
     v8i av[CH];
     uint32_t sa[CH];
     if (wave == 0) {
@@ -2481,6 +2485,9 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
             for (uint32_t p = 0; p < 4; p++) S.ptr[u_of_lane][p] = ptr[p];
         }
         if (lane == 0) S.n_act = (uint32_t)__popcll(act);
+        // Wave 0's activation loads go out after the plan's (the compiler's
+        // waits for the plan's loads would otherwise also wait for them).
+        act_loads();
     }
     __syncthreads();
     // ---- this block's share of the items, and the (at most two) experts it spans
@@ -2579,7 +2586,7 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     // at issue until the CU's miss queue drains).
     ItemRegs R0{}, R1{};
     load_item(i0, R0);
-    if (wave != 0) {
+    {
         // ---- quantize this wave's chunks of all tokens: loads retire in
         // issue order, so once only the first item's loads are in flight
         // the activations have landed.
@@ -2725,10 +2732,10 @@ __global__ __launch_bounds__(64 * NW) void mx_tokens_kernel(StreamArgs A) {
 // batch or the shape does not fit it.
 template <int NBUF, int NW>
 nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream_t st) {
-    constexpr uint32_t RI = 16, CH = 32 / NW;
+    constexpr uint32_t RI = 16, CH = 24 / NW;
     const uint32_t nch = (A.K + 127) / 128;
     if (A.T.batch_width > TOK_MAX_TOKENS || A.T.E > TOK_MAX_EXPERTS || A.T.batch_width * A.T.k > 64 || A.T.P != 4 ||
-        A.T.n_records > TOK_MAX_RECORDS || A.K % 32 || A.K > 4096 || (nch + NW - 2) / (NW - 1) > CH || RI * (A.K / 32) < 256 || A.x_seg != 0 ||
+        A.T.n_records > TOK_MAX_RECORDS || A.K % 32 || A.K > 4096 || (nch + NW - 1) / NW > CH || RI * (A.K / 32) < 256 || A.x_seg != 0 ||
         ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || ((uintptr_t)A.T.addr & 15) || A.T.k > 32 ||
         (uint32_t)ctx->cu_count < A.T.E)   // >= E blocks: a block's share spans at most two experts
         return NERVE_HIP_UNSUPPORTED;

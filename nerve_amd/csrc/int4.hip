@@ -266,19 +266,26 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_fixed_kernel(Int4Args A) {
 }
 
 // Decode-sized GPTQ linear (M <= GEMV_MAX_M tokens) on the vector ALU.  With
-// one or two tokens an MFMA tile would waste most of its rows, so each lane
-// owns one column and contracts packed words directly: a word's 8 codes become
-// four bf16 (128 + q) pairs (one and-or each) and v_dot2_f32_bf16 multiplies
-// each pair with the matching activation pair, so that
+// one or two tokens an MFMA tile would waste most of its rows, so the packed
+// words are contracted directly: a word's 8 codes become four bf16 (128 + q)
+// pairs (one and-or each) and v_dot2_f32_bf16 multiplies each pair with the
+// matching activation pair, so that
 //   sum_k x (q - z) = sum_k x (128 + q) - (128 + z) sum_k x
-// per group as in the MFMA kernels.  16 waves split the groups.
+// per group as in the MFMA kernels.  A block owns 64 columns and its 16 waves
+// split the packed rows in batches of 32.
 //
-// Every load of a 32-row batch is issued up front and unconditionally, oldest
-// first in the order they are needed (the wave's activation slice, group
-// scales and zero codes, then the 32 packed words), so the wave waits for the
-// slice alone and then contracts each row as its word lands.  The slice is
-// permuted into pair order and parked in the wave's own LDS region (read back
-// as broadcasts); sum_k x per group is a reduction over the slice's lanes.
+// Weights are read 16 bytes per lane: lane (q = l / 16, c = l % 16) loads
+// columns 4c..4c+3 of packed rows 4i + q (i = 0..7) of the batch, so one load
+// instruction covers four whole 256-byte row segments (a dword per lane would
+// take four times the instructions and memory requests for the same bytes).
+// Every load of a batch is issued up front and unconditionally, oldest first
+// in the order they are needed (the wave's activation slice, group scales and
+// zero codes, then the packed words), so the wave waits for the slice alone
+// and then contracts each load as it lands.  The slice is permuted into pair
+// order and parked in the wave's own LDS region (read back as 4-address
+// broadcasts); sum_k x over each lane's rows of a group comes from shuffles
+// over the slice.  The four q lanes of a column are summed by shuffles, the
+// 16 waves through LDS.
 constexpr uint32_t GEMV_MAX_M = 2;
 constexpr uint32_t GEMV_ROWS = 32;       // packed rows per wave batch (256 k)
 
@@ -300,23 +307,27 @@ template <int KS, int G, bool ZP>
 __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
     constexpr uint32_t GR = G / 8;                 // packed rows per group
     constexpr uint32_t GPB = GEMV_ROWS / GR;       // groups per batch
-    static_assert(GR <= GEMV_ROWS && GEMV_ROWS % GR == 0, "group length must divide the batch");
+    constexpr uint32_t LR = GEMV_ROWS / 4;         // packed rows per lane per batch
+    static_assert(GR % 4 == 0 && GR <= GEMV_ROWS && GEMV_ROWS % GR == 0, "group length must divide the batch");
     __shared__ v4i xw[KS][GEMV_MAX_M][GEMV_ROWS];
-    __shared__ float part[KS][GEMV_MAX_M][64];
+    __shared__ v4f part[KS][GEMV_MAX_M][16];
     const uint32_t K = A.K, N = A.N, M = A.B, prow = K / 8;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63, lr = lane & (GEMV_ROWS - 1);
+    const uint32_t q = lane >> 4, c = lane & 15;
     const uint32_t per_xcd = gridDim.x / 8;
     const uint32_t tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     const uint32_t n0 = tile * 64;
     if (n0 >= N) return;
-    const uint32_t col = n0 + lane;
+    const uint32_t col = n0 + 4 * c;               // first of the lane's 4 columns
     const uint32_t ngroups = K / G;
     const uint32_t nbatch = (ngroups + GPB - 1) / GPB;
     const uint32_t per = (nbatch + KS - 1) / KS;
     const uint32_t b0 = min(nbatch, wave * per), b1 = min(nbatch, b0 + per);
-    const uint32_t* wq = A.qw + col;
-    float acc[GEMV_MAX_M] = {0.f, 0.f};
+    const uint32_t zshift = 4 * (col % 8);
+    v4f acc[GEMV_MAX_M];
+#pragma unroll
+    for (uint32_t t = 0; t < GEMV_MAX_M; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = b0; b < b1; b++) {
         const uint32_t grp0 = b * GPB, row0 = grp0 * GR;
         // Loads, oldest first.
@@ -324,79 +335,92 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
 #pragma unroll
         for (uint32_t t = 0; t < GEMV_MAX_M; t++)
             xl[t] = *reinterpret_cast<const v4i*>(A.x + (uint64_t)min(t, M - 1) * K + 8 * min(row0 + lr, prow - 1));
+        v2i sb[GPB];
         uint32_t zb[GPB];
-        uint16_t sb[GPB];
 #pragma unroll
         for (uint32_t gb = 0; gb < GPB; gb++) {
             const uint32_t gi = min(grp0 + gb, ngroups - 1);
-            sb[gb] = A.scales[(uint64_t)gi * N + col];
-            zb[gb] = ZP ? A.qzeros[(uint64_t)gi * (N / 8) + col / 8] : 0x88888888u;
+            sb[gb] = *reinterpret_cast<const v2i*>(A.scales + (uint64_t)gi * N + col);
+            zb[gb] = ZP ? A.qzeros[(uint64_t)gi * (N / 8) + col / 8] >> zshift : 0x8888u;
         }
         // Scheduling fences keep the issue order (the compiler would otherwise
         // hoist the packed-word loads ahead and then drain them all for the
         // slice).
         __builtin_amdgcn_sched_barrier(0);
-        uint32_t w[GEMV_ROWS];
+        v4i w[LR];
 #pragma unroll
-        for (uint32_t r = 0; r < GEMV_ROWS; r++) w[r] = wq[(uint64_t)min(row0 + r, prow - 1) * N];
+        for (uint32_t i = 0; i < LR; i++)
+            w[i] = *reinterpret_cast<const v4i*>(A.qw + (uint64_t)min(row0 + 4 * i + q, prow - 1) * N + col);
         __builtin_amdgcn_sched_barrier(0);
-        // Activation slice: pair order into LDS, and per-group sums (lane lr
-        // holds row row0 + lr; lanes 32..63 mirror lanes 0..31).
+        // Activation slice: pair order into LDS (lane lr holds row row0 + lr;
+        // lanes 32..63 mirror lanes 0..31), and per (group, q) sums of the
+        // rows 4 i + q that lane q contracts.
         float gsum[GEMV_MAX_M][GPB];
 #pragma unroll
         for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
             if (lane < GEMV_ROWS) xw[wave][t][lr] = permute_act(xl[t]);
             float v = sum8_bf16(xl[t]);
 #pragma unroll
-            for (uint32_t d = 1; d < GR; d <<= 1) v += __shfl_xor(v, d);
+            for (uint32_t d = 4; d < GR; d <<= 1) v += __shfl_xor(v, d);
 #pragma unroll
-            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = __shfl(v, gb * GR);
+            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = __shfl(v, gb * GR + q);
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (uint32_t gb = 0; gb < GPB; gb++) {
-            const uint32_t gi = grp0 + gb;
-            if (gi >= ngroups) continue;
-            const float sc = decode_scale(sb[gb], A.scale_bf16);
-            const float off = 128.0f + (float)((zb[gb] >> (4 * (col % 8))) & 15u);
-            float ag[GEMV_MAX_M] = {0.f, 0.f};
-            // Activation rows are read from LDS four at a time ahead of use.
-            constexpr uint32_t XR = GR < 4 ? GR : 4;
+            if (grp0 + gb >= ngroups) continue;
+            v4f ag[GEMV_MAX_M];
 #pragma unroll
-            for (uint32_t r0 = 0; r0 < GR; r0 += XR) {
-                v4i xv[GEMV_MAX_M][XR];
+            for (uint32_t t = 0; t < GEMV_MAX_M; t++) ag[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (uint32_t t = 0; t < GEMV_MAX_M; t++)
+            for (uint32_t i = gb * (GR / 4); i < (gb + 1) * (GR / 4); i++) {
+                v4i xv[GEMV_MAX_M];
 #pragma unroll
-                    for (uint32_t u = 0; u < XR; u++) xv[t][u] = xw[wave][t][gb * GR + r0 + u];
+                for (uint32_t t = 0; t < GEMV_MAX_M; t++) xv[t] = xw[wave][t][4 * i + q];
 #pragma unroll
-                for (uint32_t u = 0; u < XR; u++) {
-                    const v4i d = dequant_word(w[gb * GR + r0 + u]);
+                for (uint32_t j = 0; j < 4; j++) {
+                    const v4i d = dequant_word((uint32_t)w[i][j]);
 #pragma unroll
                     for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
                         if (t < M) {
-                            ag[t] = dot2_bf16((uint32_t)xv[t][u].x, (uint32_t)d.x, ag[t]);
-                            ag[t] = dot2_bf16((uint32_t)xv[t][u].y, (uint32_t)d.y, ag[t]);
-                            ag[t] = dot2_bf16((uint32_t)xv[t][u].z, (uint32_t)d.z, ag[t]);
-                            ag[t] = dot2_bf16((uint32_t)xv[t][u].w, (uint32_t)d.w, ag[t]);
+                            float a = ag[t][j];
+                            a = dot2_bf16((uint32_t)xv[t].x, (uint32_t)d.x, a);
+                            a = dot2_bf16((uint32_t)xv[t].y, (uint32_t)d.y, a);
+                            a = dot2_bf16((uint32_t)xv[t].z, (uint32_t)d.z, a);
+                            a = dot2_bf16((uint32_t)xv[t].w, (uint32_t)d.w, a);
+                            ag[t][j] = a;
                         }
                     }
                 }
             }
 #pragma unroll
-            for (uint32_t t = 0; t < GEMV_MAX_M; t++) acc[t] = fmaf(sc, ag[t] - off * gsum[t][gb], acc[t]);
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t sbits = (uint32_t)sb[gb][j / 2] >> (16 * (j % 2));
+                const float sc = decode_scale((uint16_t)(sbits & 0xFFFFu), A.scale_bf16);
+                const float off = 128.0f + (float)((zb[gb] >> (4 * j)) & 15u);
+#pragma unroll
+                for (uint32_t t = 0; t < GEMV_MAX_M; t++) acc[t][j] = fmaf(sc, ag[t][j] - off * gsum[t][gb], acc[t][j]);
+            }
         }
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
-    for (uint32_t t = 0; t < GEMV_MAX_M; t++) part[wave][t][lane] = acc[t];
+    for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            acc[t][j] += __shfl_xor(acc[t][j], 16);
+            acc[t][j] += __shfl_xor(acc[t][j], 32);
+        }
+        if (lane < 16) part[wave][t][lane] = acc[t];
+    }
     __syncthreads();
     if (wave != 0) return;
+    const float* pf = reinterpret_cast<const float*>(&part[0][0][0]);
     for (uint32_t t = 0; t < M; t++) {
-        float v = part[0][t][lane];
+        float v = pf[t * 64 + lane];
 #pragma unroll
-        for (int w2 = 1; w2 < KS; w2++) v += part[w2][t][lane];
-        finalize_store(A, t, col, v);
+        for (int w2 = 1; w2 < KS; w2++) v += pf[(w2 * GEMV_MAX_M + t) * 64 + lane];
+        finalize_store(A, t, n0 + lane, v);
     }
 }
 
@@ -644,7 +668,8 @@ extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char
         dim3 grid((tiles + 7) / 8 * 8, row_tiles);
         const uint32_t steps = A.G / 32;
         // Decode-sized batches go to the vector-ALU kernel.
-        if (wide && batch_width <= GEMV_MAX_M && (A.G == 32 || A.G == 64 || A.G == 128 || A.G == 256)) {
+        if (wide && batch_width <= GEMV_MAX_M && (A.G == 32 || A.G == 64 || A.G == 128 || A.G == 256) &&
+            ((uintptr_t)scales & 7) == 0) {
             dim3 g1((tiles + 7) / 8 * 8);
             const bool zp = zeros != nullptr;
 #define NERVE_INT4_GEMV(GG)                                                                  \

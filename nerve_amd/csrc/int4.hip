@@ -265,28 +265,30 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_fixed_kernel(Int4Args A) {
     }
 }
 
-// Decode-sized GPTQ linear (M <= GEMV_MAX_M tokens) on the vector ALU.  With
-// one or two tokens an MFMA tile would waste most of its rows, so the packed
-// words are contracted directly: a word's 8 codes become four bf16 (128 + q)
-// pairs (one and-or each) and v_dot2_f32_bf16 multiplies each pair with the
-// matching activation pair, so that
-//   sum_k x (q - z) = sum_k x (128 + q) - (128 + z) sum_k x
-// per group as in the MFMA kernels.  A block owns 64 columns and its 16 waves
-// split the packed rows in batches of 32.
+// Decode-sized GPTQ linear (M <= GEMV_MAX_M tokens).  The kernel is shaped
+// for the weight stream: a block owns 64 columns and its 16 waves split the
+// packed rows in batches of 32, each wave issuing every load of its batch up
+// front.  Weights are read 16 bytes per lane: lane (q = l / 16, c = l % 16)
+// loads columns 4c..4c+3 of packed rows 4i + q (i = 0..7) of the batch, so one
+// load instruction covers four whole 256-byte row segments (a dword per lane
+// would take four times the instructions and memory requests for the bytes).
 //
-// Weights are read 16 bytes per lane: lane (q = l / 16, c = l % 16) loads
-// columns 4c..4c+3 of packed rows 4i + q (i = 0..7) of the batch, so one load
-// instruction covers four whole 256-byte row segments (a dword per lane would
-// take four times the instructions and memory requests for the same bytes).
-// Every load of a batch is issued up front and unconditionally, oldest first
-// in the order they are needed (the wave's activation slice, group scales and
-// zero codes, then the packed words), so the wave waits for the slice alone
-// and then contracts each load as it lands.  The slice is permuted into pair
-// order and parked in the wave's own LDS region (read back as 4-address
-// broadcasts); sum_k x over each lane's rows of a group comes from shuffles
-// over the slice.  The four q lanes of a column are summed by shuffles, the
-// 16 waves through LDS.
-constexpr uint32_t GEMV_MAX_M = 2;
+// The loaded words are exactly the B operand of v_mfma_f32_16x16x32_bf16
+// (lane (q, c) = k-slice q of column c) once each 4-bit code is turned into
+// the bf16 value 128 + q (one and-or per two codes), so MFMA j of step i
+// contracts columns 4c + j; A row c is token min(c, M - 1), and only result
+// rows t < M are read.  The matrix core does the multiply-adds that would
+// otherwise cost four v_dot2 per word per token; the vector ALU is left with
+// the code expansion.  As in the other kernels
+//   sum_k x (q - z) = sum_k x (128 + q) - (128 + z) sum_k x
+// per group, with sum_k x from shuffles over the activation slice.
+//
+// Loads go oldest first in the order they are needed (the wave's activation
+// slice, group scales and zero codes, then the packed words), so the wave
+// waits for the slice alone and then contracts each load as it lands.  The
+// slice is permuted into pair order and parked in the wave's own LDS region;
+// the 16 waves' partial sums meet in LDS.
+constexpr uint32_t GEMV_MAX_M = 4;
 constexpr uint32_t GEMV_ROWS = 32;       // packed rows per wave batch (256 k)
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
@@ -303,14 +305,14 @@ __device__ __forceinline__ float sum8_bf16(v4i v) {
     return s;
 }
 
-template <int KS, int G, bool ZP>
+template <int KS, int G, bool ZP, uint32_t MT>
 __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
     constexpr uint32_t GR = G / 8;                 // packed rows per group
     constexpr uint32_t GPB = GEMV_ROWS / GR;       // groups per batch
     constexpr uint32_t LR = GEMV_ROWS / 4;         // packed rows per lane per batch
     static_assert(GR % 4 == 0 && GR <= GEMV_ROWS && GEMV_ROWS % GR == 0, "group length must divide the batch");
-    __shared__ v4i xw[KS][GEMV_MAX_M][GEMV_ROWS];
-    __shared__ v4f part[KS][GEMV_MAX_M][16];
+    __shared__ v4i xw[KS][MT][GEMV_ROWS];
+    __shared__ v4f part[KS][MT][16];
     const uint32_t K = A.K, N = A.N, M = A.B, prow = K / 8;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63, lr = lane & (GEMV_ROWS - 1);
@@ -325,15 +327,15 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
     const uint32_t per = (nbatch + KS - 1) / KS;
     const uint32_t b0 = min(nbatch, wave * per), b1 = min(nbatch, b0 + per);
     const uint32_t zshift = 4 * (col % 8);
-    v4f acc[GEMV_MAX_M];
+    v4f acc[MT];
 #pragma unroll
-    for (uint32_t t = 0; t < GEMV_MAX_M; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t t = 0; t < MT; t++) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = b0; b < b1; b++) {
         const uint32_t grp0 = b * GPB, row0 = grp0 * GR;
         // Loads, oldest first.
-        v4i xl[GEMV_MAX_M];
+        v4i xl[MT];
 #pragma unroll
-        for (uint32_t t = 0; t < GEMV_MAX_M; t++)
+        for (uint32_t t = 0; t < MT; t++)
             xl[t] = *reinterpret_cast<const v4i*>(A.x + (uint64_t)min(t, M - 1) * K + 8 * min(row0 + lr, prow - 1));
         v2i sb[GPB];
         uint32_t zb[GPB];
@@ -353,45 +355,34 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
             w[i] = *reinterpret_cast<const v4i*>(A.qw + (uint64_t)min(row0 + 4 * i + q, prow - 1) * N + col);
         __builtin_amdgcn_sched_barrier(0);
         // Activation slice: pair order into LDS (lane lr holds row row0 + lr;
-        // lanes 32..63 mirror lanes 0..31), and per (group, q) sums of the
-        // rows 4 i + q that lane q contracts.
-        float gsum[GEMV_MAX_M][GPB];
+        // lanes 32..63 mirror lanes 0..31), and per-group sums of the slice.
+        float gsum[MT][GPB];
 #pragma unroll
-        for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
+        for (uint32_t t = 0; t < MT; t++) {
             if (lane < GEMV_ROWS) xw[wave][t][lr] = permute_act(xl[t]);
             float v = sum8_bf16(xl[t]);
 #pragma unroll
-            for (uint32_t d = 4; d < GR; d <<= 1) v += __shfl_xor(v, d);
+            for (uint32_t d = 1; d < GR; d <<= 1) v += __shfl_xor(v, d);
 #pragma unroll
-            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = __shfl(v, gb * GR + q);
+            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = __shfl(v, gb * GR);
         }
         __builtin_amdgcn_wave_barrier();
+        // MFMA j of step i contracts packed rows 4 i .. 4 i + 3 (k-slice q)
+        // of columns 4 c + j against the activations: A row c is token
+        // min(c, M - 1), so result rows t < M are the tokens and the rest are
+        // never read.  Result lane (0, c) holds D[t][4 c + j] in element t.
+        const uint32_t tsel = min(c, M - 1);
 #pragma unroll
         for (uint32_t gb = 0; gb < GPB; gb++) {
             if (grp0 + gb >= ngroups) continue;
-            v4f ag[GEMV_MAX_M];
+            v4f ag[4];
 #pragma unroll
-            for (uint32_t t = 0; t < GEMV_MAX_M; t++) ag[t] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (uint32_t j = 0; j < 4; j++) ag[j] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (uint32_t i = gb * (GR / 4); i < (gb + 1) * (GR / 4); i++) {
-                v4i xv[GEMV_MAX_M];
+                const v4i xv = xw[wave][tsel][4 * i + q];
 #pragma unroll
-                for (uint32_t t = 0; t < GEMV_MAX_M; t++) xv[t] = xw[wave][t][4 * i + q];
-#pragma unroll
-                for (uint32_t j = 0; j < 4; j++) {
-                    const v4i d = dequant_word((uint32_t)w[i][j]);
-#pragma unroll
-                    for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
-                        if (t < M) {
-                            float a = ag[t][j];
-                            a = dot2_bf16((uint32_t)xv[t].x, (uint32_t)d.x, a);
-                            a = dot2_bf16((uint32_t)xv[t].y, (uint32_t)d.y, a);
-                            a = dot2_bf16((uint32_t)xv[t].z, (uint32_t)d.z, a);
-                            a = dot2_bf16((uint32_t)xv[t].w, (uint32_t)d.w, a);
-                            ag[t][j] = a;
-                        }
-                    }
-                }
+                for (uint32_t j = 0; j < 4; j++) ag[j] = mfma_bf16(xv, dequant_word((uint32_t)w[i][j]), ag[j]);
             }
 #pragma unroll
             for (uint32_t j = 0; j < 4; j++) {
@@ -399,27 +390,21 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
                 const float sc = decode_scale((uint16_t)(sbits & 0xFFFFu), A.scale_bf16);
                 const float off = 128.0f + (float)((zb[gb] >> (4 * j)) & 15u);
 #pragma unroll
-                for (uint32_t t = 0; t < GEMV_MAX_M; t++) acc[t][j] = fmaf(sc, ag[t][j] - off * gsum[t][gb], acc[t][j]);
+                for (uint32_t t = 0; t < MT; t++) acc[t][j] = fmaf(sc, ag[j][t] - off * gsum[t][gb], acc[t][j]);
             }
         }
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
-    for (uint32_t t = 0; t < GEMV_MAX_M; t++) {
-#pragma unroll
-        for (uint32_t j = 0; j < 4; j++) {
-            acc[t][j] += __shfl_xor(acc[t][j], 16);
-            acc[t][j] += __shfl_xor(acc[t][j], 32);
-        }
+    for (uint32_t t = 0; t < MT; t++)
         if (lane < 16) part[wave][t][lane] = acc[t];
-    }
     __syncthreads();
     if (wave != 0) return;
     const float* pf = reinterpret_cast<const float*>(&part[0][0][0]);
     for (uint32_t t = 0; t < M; t++) {
         float v = pf[t * 64 + lane];
 #pragma unroll
-        for (int w2 = 1; w2 < KS; w2++) v += pf[(w2 * GEMV_MAX_M + t) * 64 + lane];
+        for (int w2 = 1; w2 < KS; w2++) v += pf[(w2 * MT + t) * 64 + lane];
         finalize_store(A, t, n0 + lane, v);
     }
 }
@@ -672,9 +657,11 @@ extern "C" nerve_hip_status nerve_hip_int4_linear(nerve_hip_ctx* ctx, const char
             ((uintptr_t)scales & 7) == 0) {
             dim3 g1((tiles + 7) / 8 * 8);
             const bool zp = zeros != nullptr;
-#define NERVE_INT4_GEMV(GG)                                                                  \
-    (zp ? int4_gptq_gemv_kernel<16, GG, true><<<g1, 1024, 0, strm>>>(A)                     \
-        : int4_gptq_gemv_kernel<16, GG, false><<<g1, 1024, 0, strm>>>(A))
+#define NERVE_INT4_GEMV(GG)                                                                   \
+    (batch_width == 1 ? (zp ? int4_gptq_gemv_kernel<16, GG, true, 1><<<g1, 1024, 0, strm>>>(A)   \
+                            : int4_gptq_gemv_kernel<16, GG, false, 1><<<g1, 1024, 0, strm>>>(A)) \
+                      : (zp ? int4_gptq_gemv_kernel<16, GG, true, 4><<<g1, 1024, 0, strm>>>(A)   \
+                            : int4_gptq_gemv_kernel<16, GG, false, 4><<<g1, 1024, 0, strm>>>(A)))
             if (A.G == 128) NERVE_INT4_GEMV(128);
             else if (A.G == 64) NERVE_INT4_GEMV(64);
             else if (A.G == 32) NERVE_INT4_GEMV(32);

@@ -58,7 +58,7 @@ def test_int4_gptq_parity(ctx, dev, M, symmetric, K, N):
 # M = 2 takes the vector-ALU decode kernel where N % 64 == 0, M = 5 the MFMA one.
 @pytest.mark.parametrize("G", [32, 64, 96, 256])
 @pytest.mark.parametrize("N", [512, 48])
-@pytest.mark.parametrize("M", [2, 5])
+@pytest.mark.parametrize("M", [2, 3, 5])
 def test_int4_gptq_group_lengths(ctx, dev, G, N, M):
     K = 768
     rng = np.random.default_rng(G * 7 + N + M)

@@ -330,7 +330,8 @@ def int4_gemv(args, ctx, dev):
     gbs = alg / (kms * 1e-3) / 1e9
     out = base_line(args, gbs, "GB/s", ms, "bf16xint4->f32",
                     {"workload": f"int4_gptq_g128_asym_m{M}_k4096_n14336", "weight_copies_rotated": copies})
-    kname = "int4_gptq_gemv_kernel<16, 128, true>" if M <= 2 else "int4_gptq_fixed_kernel<16, 4, 4>"
+    kname = ("int4_gptq_gemv_kernel<16, 128, true, 1u>" if M == 1 else "int4_gptq_gemv_kernel<16, 128, true, 4u>"
+             if M <= 4 else "int4_gptq_fixed_kernel<16, 4, 4>")
     out["roofline"] = {"bound": "hbm", "kernel": kname, "achieved": gbs, "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": traffic_for(kname),
                        "algorithmic_bytes_per_launch": alg, "launch_ms": kms}

@@ -44,6 +44,7 @@ struct QuantArgs {
     uint8_t* q;              // e4m3 [rows, cols]
     float* s;                // f32 [rows, ceil(cols/128)]
     uint32_t* zero_word;     // set to 0 by the standalone quantizer (a counter of the next kernel), or null
+    uint32_t vec8 = 0;       // x rows, frames and q rows 16-byte aligned: quant_unit8 may be used
 };
 
 // One 32-lane cluster quantizes one (row, 128-column block) unit.  All 32
@@ -71,6 +72,54 @@ __device__ __forceinline__ void quant_unit(const QuantArgs& Q, uint32_t unit, ui
     const uint32_t packed = f32_to_e4m3(v[0] / sc) | (f32_to_e4m3(v[1] / sc) << 8) |
                             (f32_to_e4m3(v[2] / sc) << 16) | (f32_to_e4m3(v[3] / sc) << 24);
     *reinterpret_cast<uint32_t*>(Q.q + (uint64_t)row * Q.cols + col) = packed;
+}
+
+// The same quantization with 16 lanes per unit and 8 columns (one 16-byte
+// load, one 8-byte store) per lane, for the preparation launch where many
+// rows are quantized and the per-lane load size sets the pace.  The load is
+// unconditional (clamped to the unit's first column when out of range) so
+// that nothing waits on a branch.  With a power-of-two scale the division is
+// a multiplication by its exact reciprocal (the same correctly rounded
+// quotient).  Requires Q.vec8.
+template <bool POW2>
+__device__ __forceinline__ void quant_unit8(const QuantArgs& Q, uint32_t unit, uint32_t cl) {
+    const uint32_t nblk = (Q.cols + 127) / 128;
+    const uint32_t row = min(unit / nblk, Q.rows - 1), blk = unit % nblk;
+    const bool unit_ok = unit / nblk < Q.rows;
+    const uint32_t col = blk * 128 + cl * 8;
+    const bool valid = unit_ok && col < Q.cols;
+    const uint16_t* xr = Q.x + (uint64_t)(row / Q.k) * Q.frame_elems + (uint64_t)(row % Q.k) * Q.seg_elems;
+    const v4i w = *reinterpret_cast<const v4i*>(xr + (valid ? col : blk * 128));
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = valid ? bf16_to_f32((uint32_t)w[i]) : 0.f;
+        v[2 * i + 1] = valid ? bf16_to_f32((uint32_t)w[i] >> 16) : 0.f;
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 8));
+    m = fmaxf(m, __shfl_xor(m, 4));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    if (!valid) return;
+    const float sc = POW2 ? pow2_fp8_scale(m) : amax_fp8_scale(m);
+    if (cl == 0) Q.s[(uint64_t)row * nblk + blk] = sc;
+    uint32_t p[2];
+    if (POW2) {
+        const float inv = 1.0f / sc;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            p[h] = f32_to_e4m3(v[4 * h] * inv) | (f32_to_e4m3(v[4 * h + 1] * inv) << 8) |
+                   (f32_to_e4m3(v[4 * h + 2] * inv) << 16) | (f32_to_e4m3(v[4 * h + 3] * inv) << 24);
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            p[h] = f32_to_e4m3(v[4 * h] / sc) | (f32_to_e4m3(v[4 * h + 1] / sc) << 8) |
+                   (f32_to_e4m3(v[4 * h + 2] / sc) << 16) | (f32_to_e4m3(v[4 * h + 3] / sc) << 24);
+    }
+    *reinterpret_cast<v2i*>(Q.q + (uint64_t)row * Q.cols + col) = v2i{(int)p[0], (int)p[1]};
 }
 
 // a2 standalone: blockwise e4m3 quantization of bf16 rows (quantize_hidden,
@@ -660,8 +709,14 @@ __global__ __launch_bounds__(1024) void moe_prep_kernel(TileArgs T, QuantArgs Q)
         build_tiles<MAXE>(T);
         return;
     }
-    // Quantization blocks stride over the (row, 128-column) units, 32 per pass.
+    // Quantization blocks stride over the (row, 128-column) units, 64 per
+    // pass with 16-byte loads (32 per pass otherwise).
     const uint64_t nblk = (Q.cols + 127) / 128, units = (uint64_t)Q.rows * nblk;
+    if (Q.vec8) {
+        for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 64; u < units; u += (uint64_t)(gridDim.x - 1) * 64)
+            quant_unit8<true>(Q, (uint32_t)u + (threadIdx.x >> 4), threadIdx.x & 15);
+        return;
+    }
     for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 32; u < units; u += (uint64_t)(gridDim.x - 1) * 32)
         quant_unit<true>(Q, (uint32_t)u + (threadIdx.x >> 5), threadIdx.x & 31);
 }
@@ -3524,7 +3579,11 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     {
         // Block 0 builds the tiles; the others stride over the quantization
         // units (a few per CU keep the loads in flight).
-        const uint32_t qblocks = (uint32_t)std::min<uint64_t>((units + 31) / 32, (uint64_t)4 * ctx->cu_count);
+        Q.vec8 = ((((uintptr_t)Q.x | (uintptr_t)Q.q) & 15) == 0 && Q.cols % 8 == 0 && Q.frame_elems % 8 == 0 &&
+                  Q.seg_elems % 8 == 0 && Q.rows > 0) ? 1u : 0u;
+        const uint32_t per_pass = Q.vec8 ? 64 : 32;
+        const uint32_t qblocks =
+            (uint32_t)std::min<uint64_t>((units + per_pass - 1) / per_pass, (uint64_t)4 * ctx->cu_count);
         if (E <= 1024) moe_prep_kernel<1024><<<1 + qblocks, 1024, 0, stream>>>(ta, Q);
         else moe_prep_kernel<MAX_EXPERTS><<<1 + qblocks, 1024, 0, stream>>>(ta, Q);
     }

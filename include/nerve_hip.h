@@ -34,7 +34,9 @@
  *   BatchControl       u32[7] {batch_width, expert_start, expert_count,
  *                      owned_route_count, dispatch_x, dispatch_y, dispatch_z}
  *   address record     u32[8] {addr_lo, addr_hi, bytes_lo, bytes_hi, gen_lo,
- *                      gen_hi, resident(==1), representation}
+ *                      gen_hi, resident(==1), representation}; the record
+ *                      table passed to the MXFP4 projections must be 16-byte
+ *                      aligned (NERVE_HIP_INVALID_ARGUMENT otherwise)
  *
  * Shape extension: the reference compiler requires hidden/intermediate/K to
  * be multiples of 128 (nerve/model_package_shader_templates.py:4805-4807,
@@ -183,7 +185,9 @@ nerve_hip_status nerve_hip_moe_router_topk(nerve_hip_ctx* ctx, const char* spec,
  * those logits.  logits_bf16 may be NULL.  hidden comes from moe_spec; the
  * top-k experts and k (plus always-selected experts) must match moe_spec.
  * Returns NERVE_HIP_UNSUPPORTED (nothing launched) above 64 tokens, 256
- * experts or 1024 routes: use the three entry points then. */
+ * experts or 1024 routes: use the three entry points then.  Calls on one
+ * context must not overlap (other streams, parallel graph branches): they
+ * share the context's partial-sum buffer and arrival counter. */
 nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_spec,
                                            const char* moe_spec, const void* x_bf16,
                                            const void* router_weight_bf16, void* logits_bf16,
@@ -302,7 +306,8 @@ nerve_hip_status nerve_hip_moe_reduce(nerve_hip_ctx* ctx, const void* expert_out
  * either NULL (every expert) or a BatchControl whose words 1 and 2 give the
  * owned expert range (DispatchControl {expert_start, expert_count}).
  * Slots that are unbound, beyond the table, or whose record has a null or
- * misaligned address or fewer bytes than the expert's tensor skip the route
+ * misaligned address (weights: 16-byte aligned, scales: 2-byte aligned) or
+ * fewer bytes than the expert's tensor skip the route
  * (the reference skips unbound slots only).  Needs K % 32 == 0 and
  * K <= 16384. */
 nerve_hip_status nerve_hip_int4_moe_gate_up(nerve_hip_ctx* ctx, const char* spec, const void* hidden_bf16,

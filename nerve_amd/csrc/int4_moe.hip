@@ -143,7 +143,7 @@ __global__ __launch_bounds__(64 * SM_WAVES) void sparse_int4_kernel(SmArgs A) {
     const uint32_t rw = A.routes[c];
     const uint32_t e = rw & 0xffffu;
     if (e >= A.E || (count != 0u && (e < start || e - start >= count))) return;
-    const uint32_t* W = static_cast<const uint32_t*>(sm_param(A, 2 * e, A.w_bytes, 4));
+    const uint32_t* W = static_cast<const uint32_t*>(sm_param(A, 2 * e, A.w_bytes, 16));
     const uint16_t* S = static_cast<const uint16_t*>(sm_param(A, 2 * e + 1, A.s_bytes, 2));
     if (!W || !S) return;
     const uint32_t b = c / A.k, r = c % A.k;

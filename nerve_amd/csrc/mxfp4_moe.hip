@@ -24,6 +24,13 @@
 #include "common.h"
 #include "async_copy.h"
 
+#ifdef NERVE_PREP_PROBE
+__device__ unsigned long long g_probe[64];
+#define PROBE(i) do { if (threadIdx.x == 0) g_probe[(i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define PROBE(i) do { } while (0)
+#endif
+
 namespace {
 
 constexpr uint32_t UNBOUND_SLOT = 0xffffffffu;
@@ -420,6 +427,7 @@ __device__ void build_tiles(const TileArgs& A) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
     const uint32_t cap = A.batch_width * A.k;
     const uint32_t P = A.P;   // 4 (gate, gate scales, up, up scales) or 2 (down, down scales)
+    PROBE(0);
 
     // ---- round 1: slot words of expert tid, route map entry tid, control
     // Every load of the two rounds is issued unconditionally (from a clamped
@@ -524,6 +532,7 @@ __device__ void build_tiles(const TileArgs& A) {
         cnt[e] = 0;
     }
     __syncthreads();
+    PROBE(1);
     // Expert of every compacted slot c < n (NO_EXPERT when invalid).
     auto slot_expert = [&](uint32_t c, uint32_t rw, uint32_t rt) -> uint32_t {
         if (c >= n || rw >= cap) return NO_EXPERT;
@@ -547,6 +556,7 @@ __device__ void build_tiles(const TileArgs& A) {
         wave_add_one(cnt, e, false);
     }
     __syncthreads();
+    PROBE(2);
     // Exclusive scans of route counts and tile counts over experts.
     const uint32_t per = (A.E + nt - 1) / nt;
     const uint32_t e0 = min(A.E, tid * per), e1 = min(A.E, e0 + per);
@@ -566,6 +576,7 @@ __device__ void build_tiles(const TileArgs& A) {
         ot += (cnt[e] + A.TM - 1) / A.TM;
     }
     __syncthreads();
+    PROBE(3);
     for (uint32_t e = tid; e < A.E; e += nt) {
         const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM;
         for (uint32_t t = 0; t < nte; t++) {
@@ -593,6 +604,7 @@ __device__ void build_tiles(const TileArgs& A) {
         }
     }
     __syncthreads();
+    PROBE(4);
     // Route slots in expert order.  For the persistent grouped GEMM the slot
     // also goes into its tile's route list (position rank % TM of tile
     // tst[e] + rank / TM), with its activation row and route weight.
@@ -628,6 +640,7 @@ __device__ void build_tiles(const TileArgs& A) {
         place(e, r, rt);
     }
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
+    PROBE(5);
     if (A.items) {
         // Work items (expert, row block, tile) with tiles fastest, grouped by
         // the expert's route count: experts with more than 64 routes, 33-64,
@@ -667,6 +680,7 @@ __device__ void build_tiles(const TileArgs& A) {
             A.n_tiles[2] = nt1;
         }
         __syncthreads();
+        PROBE(6);
         // One thread per (expert, row block): its tiles' items.
         const uint32_t nrb = A.item_nrb;
         for (uint32_t pr = tid; pr < A.E * nrb; pr += nt) {
@@ -697,6 +711,10 @@ __device__ void build_tiles(const TileArgs& A) {
                 A.items[base + kk] = o;
             }
         }
+#ifdef NERVE_PREP_PROBE
+        __syncthreads();
+        PROBE(7);
+#endif
     }
 }
 
@@ -712,9 +730,16 @@ __global__ __launch_bounds__(1024) void moe_prep_kernel(TileArgs T, QuantArgs Q)
     // Quantization blocks stride over the (row, 128-column) units, 64 per
     // pass with 16-byte loads (32 per pass otherwise).
     const uint64_t nblk = (Q.cols + 127) / 128, units = (uint64_t)Q.rows * nblk;
+#ifdef NERVE_PREP_PROBE
+    if (threadIdx.x == 0) atomicMin(&g_probe[8], __builtin_amdgcn_s_memrealtime());
+#endif
     if (Q.vec8) {
         for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 64; u < units; u += (uint64_t)(gridDim.x - 1) * 64)
             quant_unit8<true>(Q, (uint32_t)u + (threadIdx.x >> 4), threadIdx.x & 15);
+#ifdef NERVE_PREP_PROBE
+        __syncthreads();
+        if (threadIdx.x == 0) atomicMax(&g_probe[9], __builtin_amdgcn_s_memrealtime());
+#endif
         return;
     }
     for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 32; u < units; u += (uint64_t)(gridDim.x - 1) * 32)
@@ -3363,6 +3388,16 @@ nerve_hip_status quantize_rows(const uint16_t* x, uint32_t cols, uint32_t rows, 
 // C ABI
 // ---------------------------------------------------------------------------
 extern "C" {
+#ifdef NERVE_PREP_PROBE
+int nerve_probe_read(unsigned long long* out) {
+    hipDeviceSynchronize();
+    int r = (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_probe), sizeof(g_probe));
+    unsigned long long init[64] = {0};
+    init[8] = ~0ull;
+    hipMemcpyToSymbol(HIP_SYMBOL(g_probe), init, sizeof(init));
+    return r;
+}
+#endif
 
 nerve_hip_status nerve_hip_quantize_fp8_e4m3(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16, uint32_t rows,
                                              void* q_e4m3, void* scales_f32, void* stream) {
@@ -3434,6 +3469,9 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         count_control_kernel<<<1, 64, 0, stream>>>(count_control, k, (H + 63) / 64);
         return nh::check_launch("moe_route_count");
     }
+    // Address records are read as two 16-byte loads each.
+    if ((uintptr_t)addresses & 15)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "the address record table must be 16-byte aligned");
     const uint32_t K = gate_up ? H : I;       // contraction
     const uint32_t N = gate_up ? I : H;       // output rows per matrix
     const uint32_t nblk = (K + 127) / 128;

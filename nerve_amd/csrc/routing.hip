@@ -233,13 +233,14 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
             __syncthreads();
         }
     }
-    // ---- arrival: wave 0's stores are complete before thread 0 counts in
+    // ---- arrival: the block's partial sums are released before thread 0
+    // counts in, and the last block acquires every other block's.  The
+    // counter wraps to 0 in the same atomic that counts the last block, so
+    // no separate reset store can interleave with another arrival.
     if (threadIdx.x == 0) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         const uint32_t nb = gridDim.x * gridDim.y;
-        const uint32_t old = __hip_atomic_fetch_add(F.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __builtin_amdgcn_atomic_inc32(F.arrive, nb - 1, __ATOMIC_ACQ_REL, "agent");
         is_last = old == nb - 1 ? 1u : 0u;
-        if (old == nb - 1) __hip_atomic_store(F.arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ctl2 = F.C.control[2];
         ctl0 = F.C.control[0];
     }

@@ -143,13 +143,15 @@ def _argmax_ok(ids, ref_logits, tol):
 # GEMM (token tiles of 64 / 128 / 256 rows;
 # partial token and vocabulary tiles, N % 4 != 0, the 64-column K tail,
 # K = 4096) or, with fewer K chunks than its ring has stages, the register
-# form.
+# form; K > 4096 takes the tiled fallback (fp8_head_kernel).
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (7, 4096, 2880), (64, 2048, 512), (130, 600, 384),
                                    (16, 2000, 4096), (2, 777, 64), (5, 1001, 384), (3, 30010, 2880),
                                    (20, 1000, 2880), (64, 4099, 640), (100, 777, 1024), (128, 3000, 2880),
                                    (300, 1300, 640), (257, 2051, 4096), (512, 5000, 2880),
                                    # stream form with 2 token tiles (partial last tile); M = 33: the GEMM
-                                   (17, 2002, 384), (32, 3000, 2880), (33, 1500, 1024)])
+                                   (17, 2002, 384), (32, 3000, 2880), (33, 1500, 1024),
+                                   # K > 4096: the tiled fallback kernel
+                                   (5, 1000, 5120), (70, 1500, 5120)])
 def test_fp8_head_parity(ctx, dev, M, N, K):
     rng = np.random.default_rng(M * N + K)
     d = wl.fp8_head(rng, N, K, M)

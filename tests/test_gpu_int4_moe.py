@@ -180,8 +180,9 @@ def test_unbatched_form(ctx, dev, use_range):
 
 
 def test_invalid_slots_skip_the_route(ctx, dev):
-    """Unbound slot, slot beyond the table, short byte count and null address:
-    that expert's routes are skipped; the others are unaffected."""
+    """Unbound slot, slot beyond the table, short byte count, null address and
+    a weight address that is not 16-byte aligned: that expert's routes are
+    skipped; the others are unaffected."""
     E, k, B, H, I, G = 8, 2, 4, 256, 128, 32
     rig = Rig(dev, H, I, E, k, G, True, nb=E, seed=99)
     experts = np.array([[0, 1], [2, 3], [4, 5], [6, 7]])
@@ -197,6 +198,8 @@ def test_invalid_slots_skip_the_route(ctx, dev):
     g2 = gslots.copy(); g2[2 * 3 + 1] = 10_000; cases.append((3, recs, g2))
     r3 = recs.copy(); r3[gslots[2 * 5 + 0], 2] -= 1; cases.append((5, r3, gslots))
     r4 = recs.copy(); r4[gslots[2 * 6 + 1], 0:2] = 0; cases.append((6, r4, gslots))
+    # a weight record 4-byte but not 16-byte aligned (rows are read in 16-byte pieces)
+    r5 = recs.copy(); r5[gslots[2 * 7 + 0], 0] += 4; cases.append((7, r5, gslots))
     for bad, rec, gs in cases:
         bank = rig.bank
         saved = (bank.addresses, bank.gate_slots)

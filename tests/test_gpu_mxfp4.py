@@ -6,7 +6,7 @@ import pytest
 
 import oracle
 from nerve_amd import workloads as wl
-from nerve_amd.hip import check_specialization
+from nerve_amd.hip import NerveHipError, check_specialization
 from nerve_amd.moe import ExpertBank, address_record, down_spec, gate_up_spec, u32_tensor
 
 from helpers import bf16_close, rel_err_normwise, to_dev, to_np
@@ -264,6 +264,13 @@ def test_fail_closed_invalid_metadata(ctx, dev, H, I):
         assert np.all(h[1, 0] == sentinel), name           # invalidated expert record
         assert not np.any(h[0, 0] == sentinel), name       # valid routes still computed
         assert not np.any(h[1, 1] == sentinel), name
+    # A record table that is 4-byte but not 16-byte aligned is refused before
+    # any launch (records are read as 16-byte pieces).
+    flat = np.concatenate([np.zeros(1, np.uint32), bad.reshape(-1).astype(np.uint32)])
+    shifted = u32_tensor(flat, dev)[1:]
+    assert shifted.data_ptr() % 16 == 4
+    with pytest.raises(NerveHipError):
+        rig.run(ctx, hidden, addresses=shifted)
 
 
 # E <= 64: the token-form gate_up kernel; E = 80: the streaming kernel's tiles.

@@ -41,7 +41,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--workload", default="moe_decode",
                    choices=["moe_decode", "moe_prefill", "mxfp4_gemv", "int4_gemv", "int4_moe", "fp8_head",
-                            "hbm_copy"])
+                            "hbm_copy", "hbm_read"])
     p.add_argument("--summarize-traffic", nargs=4, metavar="DIR",
                    help="FETCH_SIZE and WRITE_SIZE rocprofv3 CSV dirs of a run, then of the hbm_copy run")
     p.add_argument("--m", type=int, default=1, help="batch rows for int4_gemv / int4_moe / fp8_head")
@@ -471,6 +471,48 @@ def hbm_copy(args, ctx, dev):
     return out
 
 
+HBM_READ_MODES = {0: "register loads, nontemporal (1 KB per wave load)", 1: "register loads, temporal",
+                  2: "global_load_lds copies, contiguous 1 KB", 3: "global_load_lds copies, 16 rows x 64 B (prefill weights)"}
+
+
+def hbm_read(args, ctx, dev):
+    """Read-only calibration: the kernels of libnerve_calib.so stream a 1 GiB
+    buffer once per launch (larger than the 256 MB Infinity Cache), one line
+    per read mode; the headline is the fastest mode."""
+    import ctypes
+
+    import torch
+
+    from nerve_amd import build as nb
+
+    lib = ctypes.CDLL(nb.CALIB_LIB)
+    lib.nerve_calib_read.restype = ctypes.c_int
+    lib.nerve_calib_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_void_p]
+    n = 2 ** 30
+    buf = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream()
+    modes = {}
+    for mode, what in HBM_READ_MODES.items():
+        # the row pattern reads 22 of every 22.5 64-byte columns: count what it reads
+        nbytes = n if mode != 3 else (n // (cus * 16384)) * cus * 16384
+        fn = lambda i, m=mode: lib.nerve_calib_read(ctypes.c_void_p(buf.data_ptr()), n, m,
+                                                    ctypes.c_void_p(sink.data_ptr()), cus,
+                                                    ctypes.c_void_p(stream.cuda_stream))
+        assert fn(0) == 0, f"nerve_calib_read mode {mode} failed"
+        kms = batch_event_ms(fn, max(20, args.steps), stream)
+        modes[mode] = {"mode": what, "ms": kms, "gbs": nbytes / (kms * 1e-3) / 1e9}
+    best = max(modes.values(), key=lambda v: v["gbs"])
+    out = base_line(args, best["gbs"], "GB/s", best["ms"], "u8", {"workload": "hbm_read_1GiB"})
+    out["modes"] = list(modes.values())
+    out["roofline"] = {"bound": "hbm", "kernel": "nerve_calib_read (" + best["mode"] + ")", "achieved": best["gbs"],
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": best["gbs"] / HBM_PEAK_GBS, "traffic": None,
+                       "launch_ms": best["ms"]}
+    return out
+
+
 def _pmc_per_dispatch(csv_dirs, counter):
     """{kernel name: mean counter value per dispatch} from rocprofv3 CSVs
     under the comma-separated directories `csv_dirs`."""
@@ -583,6 +625,8 @@ def main():
         out = int4_moe(args, ctx, dev)
     elif args.workload == "hbm_copy":
         out = hbm_copy(args, ctx, dev)
+    elif args.workload == "hbm_read":
+        out = hbm_read(args, ctx, dev)
     else:
         out = fp8_head(args, ctx, dev)
     print(json.dumps(out))

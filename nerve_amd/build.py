@@ -44,15 +44,26 @@ def _compile(src: str) -> str:
     return out
 
 
-def build() -> str:
-    os.makedirs(OBJ, exist_ok=True)
-    srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB, *objs]
+# Read-only HBM calibration kernels for bench.py's hbm_read workload: a
+# library of their own, so the hot-path library carries no measurement code.
+CALIB_SOURCES = ["hbm_calib.hip"]
+CALIB_LIB = os.path.join(HERE, "libnerve_calib.so")
+
+
+def _link(objs, out):
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+
+
+def build() -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    srcs = [s for s in SOURCES + CALIB_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = dict(zip(srcs, ex.map(_compile, srcs)))
+    _link([objs[s] for s in SOURCES if s in objs], LIB)
+    _link([objs[s] for s in CALIB_SOURCES if s in objs], CALIB_LIB)
     return LIB
 
 

@@ -1,0 +1,135 @@
+// Read-only HBM calibration kernels (measurement only; not part of the hot
+// path).  They stream a device buffer once and fold it into one word per
+// block, so the timed work is the read itself.  bench.py's hbm_read
+// workload times them on a buffer larger than the 256 MB Infinity Cache to
+// ground the "streaming ceiling" figures the hot-path kernels are compared
+// with:
+//   mode 0: 16-byte register loads, nontemporal, 4 loads in flight per lane,
+//           grid-stride over 1 KB wave pieces (what the decode streams use);
+//   mode 1: the same with ordinary (temporal) loads;
+//   mode 2: global_load_lds 16-byte copies into an LDS ring, one 768-thread
+//           block per CU, four waves issuing (the prefill producer waves'
+//           copy engine), contiguous 1 KB per copy;
+//   mode 3: as mode 2, but each copy takes 64 bytes of 16 rows 1440 bytes
+//           apart (the prefill weight-copy pattern: a 128-k chunk of a
+//           16-row MXFP4 subtile), rows walked in order.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const v4i global_v4i;
+
+template <bool NT>
+__global__ __launch_bounds__(256) void read_regs_kernel(const v4i* __restrict__ buf, uint64_t n16,
+                                                        uint32_t* __restrict__ sink) {
+    constexpr uint32_t U = 4;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    v4i acc = v4i{0, 0, 0, 0};
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        v4i v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++) {
+            const global_v4i* p = reinterpret_cast<const global_v4i*>(reinterpret_cast<uintptr_t>(buf + i + u * stride));
+            v[u] = NT ? __builtin_nontemporal_load(p) : *p;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++) acc ^= v[u];
+    }
+    for (; i < n16; i += stride) acc ^= buf[i];
+    const uint32_t x = (uint32_t)(acc.x ^ acc.y ^ acc.z ^ acc.w);
+    if (x == 0x9e3779b9u) sink[blockIdx.x] = x;   // practically never taken: keeps the loads
+}
+
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm_imm() {
+    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | 0x0F70u);
+}
+
+// One block per CU; waves 0-3 copy, waves 4-11 only take part in the
+// barriers (as the prefill consumers do).  Ring of 4 stages x 16 KB; each
+// issuing wave copies 4 KB per stage and keeps three stages in flight.
+template <bool ROWS>
+__global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                       uint32_t* __restrict__ sink) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    constexpr uint32_t STAGE = 16384, PER_WAVE = 4096;
+    const uint64_t per_step = (uint64_t)gridDim.x * STAGE;
+    const uint64_t steps = bytes / per_step;
+    // ROWS: stage s of block b covers a 16 KB piece of the row pattern: 16
+    // subtiles of 16 rows x 64 B, subtile x at rows 16 x.., the 64-byte
+    // column (s % 22) of a 1440-byte row; blocks and 22-step groups walk
+    // the buffer in 16 x 16-row = 368 KB blocks.
+    auto src = [&](uint64_t step, uint32_t u) -> const uint8_t* {
+        if (!ROWS) return buf + (step * gridDim.x + blockIdx.x) * STAGE + wave * PER_WAVE + u * 1024 + lane * 16;
+        const uint64_t blk = (step / 22) * gridDim.x + blockIdx.x;   // 256-row block
+        const uint32_t col = (uint32_t)(step % 22);
+        const uint32_t x = wave * 4 + u, r = lane & 15, piece = lane >> 4;
+        const uint64_t off = (blk * 256 + x * 16 + r) * 1440 + col * 64 + piece * 16;
+        return buf + (off + 16 <= bytes ? off : 0);
+    };
+    if (wave < 4) {
+        auto issue = [&](uint64_t step) {
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++)
+                __builtin_amdgcn_global_load_lds(src(step, u), ring + (step % 4) * STAGE + wave * PER_WAVE + u * 1024,
+                                                 16, 0, 0);
+        };
+        for (uint64_t s = 0; s < 3 && s < steps; s++) issue(s);
+        for (uint64_t s = 0; s < steps; s++) {
+            if (s + 3 < steps) {
+                issue(s + 3);
+                wait_vm_imm<8>();
+            } else {
+                wait_vm_imm<0>();
+            }
+            __builtin_amdgcn_s_barrier();
+        }
+    } else {
+        for (uint64_t s = 0; s < steps; s++) __builtin_amdgcn_s_barrier();
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && ring[lane] == 0xA5 && ring[STAGE] == 0x5A) sink[blockIdx.x] = 1u;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Streams `bytes` of `buf` (16-byte aligned) once with read mode `mode`
+// (0-3, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
+// Returns 0, or 1 for an unknown mode or a launch error.
+int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int cu_count, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t* out = static_cast<uint32_t*>(sink);
+    if (mode == 0 || mode == 1) {
+        const uint32_t grid = 4 * (uint32_t)cu_count;
+        if (mode == 0)
+            read_regs_kernel<true><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out);
+        else
+            read_regs_kernel<false><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out);
+    } else if (mode == 2 || mode == 3) {
+        static bool attr = false;
+        if (!attr) {
+            if (hipFuncSetAttribute((const void*)read_lds_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    65536) != hipSuccess ||
+                hipFuncSetAttribute((const void*)read_lds_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    65536) != hipSuccess)
+                return 1;
+            attr = true;
+        }
+        // 64 KB of LDS per block, 768 threads: one block per CU.
+        if (mode == 2)
+            read_lds_kernel<false><<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
+        else
+            read_lds_kernel<true><<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
+    } else {
+        return 1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+}  // extern "C"

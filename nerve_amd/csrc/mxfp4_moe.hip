@@ -51,7 +51,7 @@ struct QuantArgs {
     uint8_t* q;              // e4m3 [rows, cols]
     float* s;                // f32 [rows, ceil(cols/128)]
     uint32_t* zero_word;     // set to 0 by the standalone quantizer (a counter of the next kernel), or null
-    uint32_t vec8 = 0;       // x rows, frames and q rows 16-byte aligned: quant_unit8 may be used
+    uint32_t vec8 = 0;       // x rows, frames and q rows 16-byte aligned: quant_units8_pow2 may be used
 };
 
 // One 32-lane cluster quantizes one (row, 128-column block) unit.  All 32
@@ -81,52 +81,71 @@ __device__ __forceinline__ void quant_unit(const QuantArgs& Q, uint32_t unit, ui
     *reinterpret_cast<uint32_t*>(Q.q + (uint64_t)row * Q.cols + col) = packed;
 }
 
-// The same quantization with 16 lanes per unit and 8 columns (one 16-byte
-// load, one 8-byte store) per lane, for the preparation launch where many
-// rows are quantized and the per-lane load size sets the pace.  The load is
-// unconditional (clamped to the unit's first column when out of range) so
-// that nothing waits on a branch.  With a power-of-two scale the division is
-// a multiplication by its exact reciprocal (the same correctly rounded
-// quotient).  Requires Q.vec8.
-template <bool POW2>
-__device__ __forceinline__ void quant_unit8(const QuantArgs& Q, uint32_t unit, uint32_t cl) {
+// Power-of-two block quantization of QU units per 16-lane cluster with all
+// QU loads issued before any arithmetic, and the hardware e4m3 conversion:
+// x * (1 / s) is exact for a power-of-two s, every quotient of a finite
+// block lies in [-448, 448] where v_cvt_pk_fp8_f32 rounds exactly like
+// f32_to_e4m3, and a block with a NaN code or an infinite max takes the
+// software conversion.  Unit i of the call is unit u0 + i * ustride.
+// Requires Q.vec8.
+template <uint32_t QU>
+__device__ __forceinline__ void quant_units8_pow2(const QuantArgs& Q, uint64_t u0, uint32_t ustride, uint32_t cl) {
     const uint32_t nblk = (Q.cols + 127) / 128;
-    const uint32_t row = min(unit / nblk, Q.rows - 1), blk = unit % nblk;
-    const bool unit_ok = unit / nblk < Q.rows;
-    const uint32_t col = blk * 128 + cl * 8;
-    const bool valid = unit_ok && col < Q.cols;
-    const uint16_t* xr = Q.x + (uint64_t)(row / Q.k) * Q.frame_elems + (uint64_t)(row % Q.k) * Q.seg_elems;
-    const v4i w = *reinterpret_cast<const v4i*>(xr + (valid ? col : blk * 128));
-    float v[8];
+    const uint64_t units = (uint64_t)Q.rows * nblk;
+    v4i w[QU];
+    uint32_t row[QU], blk[QU];
+    bool valid[QU];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[2 * i] = valid ? bf16_to_f32((uint32_t)w[i]) : 0.f;
-        v[2 * i + 1] = valid ? bf16_to_f32((uint32_t)w[i] >> 16) : 0.f;
+    for (uint32_t i = 0; i < QU; i++) {
+        const uint64_t u = u0 + (uint64_t)i * ustride;
+        const uint32_t uu = (uint32_t)(u < units ? u : 0u);
+        row[i] = uu / nblk;
+        blk[i] = uu % nblk;
+        const uint32_t col = blk[i] * 128 + cl * 8;
+        valid[i] = u < units && col < Q.cols;
+        const uint16_t* xr = Q.x + (uint64_t)(row[i] / Q.k) * Q.frame_elems + (uint64_t)(row[i] % Q.k) * Q.seg_elems;
+        w[i] = *reinterpret_cast<const v4i*>(xr + (valid[i] ? col : blk[i] * 128));
     }
-    float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
-    m = fmaxf(m, __shfl_xor(m, 8));
-    m = fmaxf(m, __shfl_xor(m, 4));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    m = fmaxf(m, __shfl_xor(m, 1));
-    if (!valid) return;
-    const float sc = POW2 ? pow2_fp8_scale(m) : amax_fp8_scale(m);
-    if (cl == 0) Q.s[(uint64_t)row * nblk + blk] = sc;
-    uint32_t p[2];
-    if (POW2) {
-        const float inv = 1.0f / sc;
+    for (uint32_t i = 0; i < QU; i++) {
+        float v[8];
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-            p[h] = f32_to_e4m3(v[4 * h] * inv) | (f32_to_e4m3(v[4 * h + 1] * inv) << 8) |
-                   (f32_to_e4m3(v[4 * h + 2] * inv) << 16) | (f32_to_e4m3(v[4 * h + 3] * inv) << 24);
-    } else {
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = valid[i] ? bf16_to_f32((uint32_t)w[i][j]) : 0.f;
+            v[2 * j + 1] = valid[i] ? bf16_to_f32((uint32_t)w[i][j] >> 16) : 0.f;
+        }
+        float m = 0.f;
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-            p[h] = f32_to_e4m3(v[4 * h] / sc) | (f32_to_e4m3(v[4 * h + 1] / sc) << 8) |
-                   (f32_to_e4m3(v[4 * h + 2] / sc) << 16) | (f32_to_e4m3(v[4 * h + 3] / sc) << 24);
+        for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(v[j]));
+        m = fmaxf(m, __shfl_xor(m, 8));
+        m = fmaxf(m, __shfl_xor(m, 4));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        m = fmaxf(m, __shfl_xor(m, 1));
+        if (!valid[i]) continue;
+        const float sc = pow2_fp8_scale(m);
+        uint32_t p[2];
+        bool soft = !(m <= 3.4028235e38f);
+        if (!soft) {
+            const float inv = __uint_as_float((254u << 23) - __float_as_uint(sc));
+            uint32_t nan_bytes = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                int t = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h] * inv, v[4 * h + 1] * inv, 0, false);
+                t = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h + 2] * inv, v[4 * h + 3] * inv, t, true);
+                p[h] = (uint32_t)t;
+                nan_bytes |= ((p[h] & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+            }
+            soft = nan_bytes != 0;
+        }
+        if (soft) {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                p[h] = f32_to_e4m3(v[4 * h] / sc) | (f32_to_e4m3(v[4 * h + 1] / sc) << 8) |
+                       (f32_to_e4m3(v[4 * h + 2] / sc) << 16) | (f32_to_e4m3(v[4 * h + 3] / sc) << 24);
+        }
+        if (cl == 0) Q.s[(uint64_t)row[i] * nblk + blk[i]] = sc;
+        *reinterpret_cast<v2i*>(Q.q + (uint64_t)row[i] * Q.cols + blk[i] * 128 + cl * 8) = v2i{(int)p[0], (int)p[1]};
     }
-    *reinterpret_cast<v2i*>(Q.q + (uint64_t)row * Q.cols + col) = v2i{(int)p[0], (int)p[1]};
 }
 
 // a2 standalone: blockwise e4m3 quantization of bf16 rows (quantize_hidden,
@@ -325,9 +344,10 @@ struct ItemRec {
 };
 
 // Route list of one 128-route tile of the persistent grouped GEMM, in the
-// order the tile's rows are laid out (entries past the count repeat the
-// first route): route id, activation row and route weight.  2 KB, so a tile
-// is copied into LDS by two 1 KB wave copies.
+// order the tile's rows are laid out: route id, activation row and route
+// weight.  Entries past the tile's count are never written (they hold
+// whatever the workspace held), so readers clamp positions >= count to
+// entry 0.  2 KB, so a tile is copied into LDS by two 1 KB wave copies.
 constexpr uint32_t PG_TILE = 128;
 struct PgList {
     uint32_t route[PG_TILE];
@@ -378,6 +398,7 @@ __device__ __forceinline__ bool record_valid(uint32_t slot, uint32_t n_records, 
 
 constexpr uint32_t PREP_R = 8;                 // slots per thread whose route ids stay in registers
 constexpr uint16_t NO_EXPERT = 0xffffu;
+constexpr uint32_t PREP_QU = 4;                // quantization units per 16-lane cluster per pass
 
 // atomicAdd(&cnt[e], 1) for every lane of the wave with e != NO_EXPERT,
 // one LDS atomic per distinct expert of the wave (routes come in expert
@@ -456,6 +477,14 @@ __device__ void build_tiles(const TileArgs& A) {
     }
     const uint32_t rword = rw_r[0];
     const uint32_t c2 = A.control[2], c3 = A.control[3];
+#ifdef NERVE_PREP_PROBE
+    {
+        uint32_t acc = c2 + slot[0] + slot[1] + slot[2] + slot[3];
+        for (uint32_t i = 0; i < PREP_R; i++) acc += rw_r[i];
+        if (acc == 0x12345678u) g_probe[20] = 1;
+        PROBE(10);
+    }
+#endif
     // ---- round 2: address records, route word
     uint32_t rec[4][8] = {};
     if (A.n_records != 0) {
@@ -479,6 +508,14 @@ __device__ void build_tiles(const TileArgs& A) {
         rt_r[i] = (c < cap && rw_r[i] < cap) ? rv[i] : 0u;
     }
     const uint32_t route = rt_r[0];
+#ifdef NERVE_PREP_PROBE
+    {
+        uint32_t acc = rec[0][0] + rec[1][0] + rec[2][0] + rec[3][0];
+        for (uint32_t i = 0; i < PREP_R; i++) acc += rt_r[i];
+        if (acc == 0x12345678u) g_probe[20] = 1;
+        PROBE(11);
+    }
+#endif
 
     uint32_t n = c2 != 0u ? c3 : cap;
     if (n > cap) n = cap;
@@ -734,8 +771,8 @@ __global__ __launch_bounds__(1024) void moe_prep_kernel(TileArgs T, QuantArgs Q)
     if (threadIdx.x == 0) atomicMin(&g_probe[8], __builtin_amdgcn_s_memrealtime());
 #endif
     if (Q.vec8) {
-        for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 64; u < units; u += (uint64_t)(gridDim.x - 1) * 64)
-            quant_unit8<true>(Q, (uint32_t)u + (threadIdx.x >> 4), threadIdx.x & 15);
+        for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 64 * PREP_QU; u < units; u += (uint64_t)(gridDim.x - 1) * 64 * PREP_QU)
+            quant_units8_pow2<PREP_QU>(Q, u + (threadIdx.x >> 4), 64, threadIdx.x & 15);
 #ifdef NERVE_PREP_PROBE
         __syncthreads();
         if (threadIdx.x == 0) atomicMax(&g_probe[9], __builtin_amdgcn_s_memrealtime());
@@ -1594,7 +1631,7 @@ __device__ __forceinline__ void sload_rec(const TileRec* rec, uint32_t& begin, u
     u4s h;
     u8s p;
     asm volatile("s_load_dwordx4 %0, %2, 0x0\n\ts_load_dwordx8 %1, %2, 0x10\n\ts_waitcnt lgkmcnt(0)"
-                 : "=s"(h), "=s"(p)
+                 : "=&s"(h), "=&s"(p)
                  : "s"(rec));
     begin = h.y;
     count = h.z;
@@ -2902,6 +2939,8 @@ struct PgArgs {
     uint16_t* out;              // gate_up: frames as u16; down: expert_outputs
     uint64_t frame_elems;
     float limit;
+    uint32_t a_rows;            // activation rows (aq / as); list rows are clamped below it
+    uint32_t routes;            // route slots (batch_width * k); larger route ids are skipped
 };
 
 template <uint32_t OFF>
@@ -3335,6 +3374,435 @@ __global__ __launch_bounds__(512) void moe_pgemm_kernel(PgArgs A) {
     pg_range<NMAT, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
 }
 
+// ---------------------------------------------------------------------------
+// Prefill grouped GEMM, producer / consumer form (moe_pg2_kernel).
+//
+// One 768-thread block per CU walks the same work items as the form above
+// (a tile of <= 128 routes of one expert x a 256-row weight block; gate_up:
+// 128 gate + the same 128 up channels).  The waves have fixed roles:
+//  - waves 8-11 (producers) only copy: each 128-k chunk of the item's weights
+//    (256 rows x 64 B) and of its routes' e4m3 activations (<= 128 x 128 B)
+//    goes global -> LDS with global_load_lds into a 4-stage ring, three
+//    chunks ahead.  A producer that stalls at issue (the CU's miss queue
+//    full) delays no MFMA;
+//  - waves 0-7 (consumers) only read LDS and run the scaled MFMAs; each owns
+//    a 64-route x 64-row (or 64 x 32, 32 x 32) block of the item, so every
+//    16-byte operand read from LDS feeds two to four MFMAs.  They load their
+//    rows' e8m0 bytes and their routes' block scales themselves, one chunk
+//    ahead.
+// One barrier per chunk joins both roles: the producers have waited for the
+// next chunk's copies, the consumers are done with the stage the producers
+// refill next.  The LDS layout is piece-major inside every 16-row (or
+// 16-route) subtile, [piece][row] x 16 B, so lane (g, r) of an operand read
+// takes the 16 bytes at lane * 16: every read is one contiguous 1 KB.
+// ---------------------------------------------------------------------------
+constexpr uint32_t P2_KC = 128;            // k per chunk (one MFMA)
+constexpr uint32_t P2_W_BYTES = 16384;     // weights of a stage: 16 subtiles of 16 rows x 64 B
+constexpr uint32_t P2_MAX_SB = 92;         // e8m0 bytes per weight row (K <= 2944)
+constexpr uint32_t P2_SPAN_SLOT = PG_ROWS * P2_MAX_SB;   // an item's scale rows
+constexpr uint32_t P2_LDS = 160 * 1024;
+constexpr uint32_t P2_LIST_OFF = P2_LDS - 2 * sizeof(PgList);       // [2][2 KB] route lists by item parity
+constexpr uint32_t P2_SPAN_OFF = P2_LIST_OFF - 2 * P2_SPAN_SLOT;    // [2] scale-row slots by item parity
+constexpr uint32_t P2_RING = P2_SPAN_OFF;  // ring stages of (weights, activations, block scales)
+// The next item's list is copied when chunk NS - 1 of an item is issued and
+// read when its last chunk is issued, NS - 1 chunks before its end.
+constexpr uint32_t P2_MIN_CHUNKS = 12;
+// Ring stages of a route-count group (nat 16-route subtiles per tile): as
+// many as fit.
+__host__ __device__ constexpr uint32_t p2_stages(uint32_t nat) {
+    return P2_RING / (P2_W_BYTES + nat * (16u * 128u + 16u * 4u));
+}
+static_assert(p2_stages(8) >= 3 && p2_stages(2) <= 6, "ring depth");
+
+struct PgItem {
+    uint32_t rb, count, tile;
+    const uint8_t* w[2];
+    const uint8_t* s[2];
+};
+
+// An item record through the scalar cache (reads only).
+__device__ __forceinline__ PgItem p2_item(const ItemRec* rec) {
+    u4s h;
+    u8s p;
+    asm volatile("s_load_dwordx4 %0, %2, 0x0\n\ts_load_dwordx8 %1, %2, 0x10\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&s"(h), "=&s"(p)
+                 : "s"(rec));
+    PgItem it;
+    it.rb = h.x;
+    it.count = h.y;
+    it.tile = h.z;
+    it.w[0] = reinterpret_cast<const uint8_t*>((uint64_t)p[0] | ((uint64_t)p[1] << 32));
+    it.w[1] = reinterpret_cast<const uint8_t*>((uint64_t)p[2] | ((uint64_t)p[3] << 32));
+    it.s[0] = reinterpret_cast<const uint8_t*>((uint64_t)p[4] | ((uint64_t)p[5] << 32));
+    it.s[1] = reinterpret_cast<const uint8_t*>((uint64_t)p[6] | ((uint64_t)p[7] << 32));
+    return it;
+}
+
+// LDS dword read that waits for itself.
+__device__ __forceinline__ uint32_t p2_lds32(uint32_t a) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a));
+    return r;
+}
+
+// Item row of row subtile j of consumer wave w.  NJ = 4 (tiles of up to 128
+// routes): waves (route half w / 4, row quarter w % 4), 64 rows each;
+// NJ = 2: every wave takes all routes and 32 rows.  gate_up: the first NJ / 2
+// subtiles are gate rows, the others the same up channels (item rows
+// 128 + ...).
+template <int NMAT, int NJ>
+__device__ __forceinline__ uint32_t p2_irow(uint32_t w, uint32_t j) {
+    if constexpr (NJ == 4) {
+        const uint32_t q = w % 4;
+        return NMAT == 2 ? (j < 2 ? 32 * q + 16 * j : 128 + 32 * q + 16 * (j - 2)) : 64 * q + 16 * j;
+    } else {
+        return NMAT == 2 ? j * 128 + 16 * w : 32 * w + 16 * j;
+    }
+}
+
+// Items [i0, n_items) of one route-count group.  NAT: route subtiles the
+// tile holds (8, 4, 2); NAW route subtiles and NJ row subtiles per consumer
+// wave.
+template <int NMAT, int NAT, int NAW, int NJ>
+__device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t n_items) {
+    constexpr uint32_t NR = NAT * 16;                       // routes per tile
+    constexpr uint32_t SBY = P2_W_BYTES + NR * 128 + NR * 4;  // stage: weights, activations, block scales
+    constexpr uint32_t NS = p2_stages(NAT);                 // ring stages
+    constexpr uint32_t NAI = 2 * NAT / 4;                   // activation copies per producer per chunk
+    constexpr uint32_t NAS = (NR + 63) / 64;                // block-scale copies per chunk
+    extern __shared__ __attribute__((aligned(16))) uint8_t p2_ring[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + P2_KC - 1) / P2_KC;
+    const uint32_t nsa = (K + 127) / 128;
+    constexpr uint32_t RPM = PG_ROWS / NMAT;
+    const uint32_t G = gridDim.x;
+    const uint32_t ring = lds_addr(p2_ring);
+
+    // This block's items: s * G + slot (slot XCD-aware, as in pg_range).
+    const uint32_t slot = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    const uint32_t first = i0 + (slot + G - i0 % G) % G;
+    if (first >= n_items) return;   // uniform over the block: no barrier below is reached
+    const uint32_t n_mine = (n_items - first + G - 1) / G;
+    const uint32_t T = n_mine * nch;   // steps (chunks) of this group for the block
+
+    if (wave >= 8) {
+        // ================= producers =================
+        const uint32_t p = wave - 8;
+        uint32_t pitem = first, pord = 0, pc = 0;      // item being issued, its ordinal, next chunk
+        PgItem it = p2_item(A.items + pitem);
+        // per-lane source offsets of the current issue item
+        uint32_t woff[4], aoff[NAI], soff = 0;
+        const uint8_t* wb = nullptr;
+        auto setup = [&]() __attribute__((always_inline)) {
+            // weights: subtiles x = 4 p .. 4 p + 3 (16 rows each), lane (piece i / 16, row i % 16)
+            // (selects, not a run-time index: an indexed record would live in
+            // scratch memory, whose loads count in vmcnt)
+            wb = (NMAT == 2 && p >= 2) ? it.w[1] : it.w[0];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                const uint32_t irow = 16 * (4 * p + u) + rr;             // item row
+                const uint32_t n = it.rb * RPM + irow % RPM;             // matrix row
+                woff[u] = (n < N ? n : 0u) * RB + g * 16;
+            }
+            // activations: copy u = p * NAI + v covers route subtile y = u / 2,
+            // pieces 4 (u % 2) + i / 16; block scales: copy p < NAS covers
+            // routes 64 p + i.  List entries past the tile's count are not
+            // written: their positions read entry 0.
+            const uint32_t list = ring + P2_LIST_OFF + (pord & 1u) * (uint32_t)sizeof(PgList);
+#pragma unroll
+            for (uint32_t v = 0; v < NAI; v++) {
+                const uint32_t u = p * NAI + v, y = u / 2, q = u % 2;
+                const uint32_t pos = 16 * y + rr < it.count ? 16 * y + rr : 0u;
+                const uint32_t arow = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1);
+                aoff[v] = arow * K + (4 * q + g) * 16;
+            }
+            if (p < NAS) {
+                const uint32_t pos = 64 * p + lane < it.count ? 64 * p + lane : 0u;
+                soff = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1) * nsa;
+            }
+        };
+        // The scale rows of item `nx` (one contiguous span per matrix part,
+        // rows * K / 32 bytes) into span slot `slot`: 256-byte pieces dealt
+        // round-robin over the producers, the last piece of a part aligned
+        // to its end.  Returns the copies issued.
+        auto copy_span = [&](const PgItem& nx, uint32_t sslot) __attribute__((always_inline)) -> uint32_t {
+            uint32_t cnt = 0;
+            uint8_t* const base = p2_ring + P2_SPAN_OFF + sslot * P2_SPAN_SLOT;
+#pragma unroll
+            for (uint32_t m = 0; m < (uint32_t)NMAT; m++) {
+                const uint32_t rows = min(RPM, N - nx.rb * RPM), slen = rows * SB;
+                const uint8_t* src = (m == 0 ? nx.s[0] : nx.s[1]) + (uint64_t)nx.rb * RPM * SB;
+                const uint32_t np = (slen + 255) / 256;
+                for (uint32_t q = p; q < np; q += 4) {
+                    const uint32_t o = min(q * 256, slen - 256);
+                    __builtin_amdgcn_global_load_lds(src + o + lane * 4, base + m * RPM * SB + o, 4, 0, 0);
+                    cnt++;
+                }
+            }
+            return cnt;
+        };
+        bool issuing = true;
+        // Issue the next chunk into its stage; returns the ops issued.
+        auto issue = [&](uint32_t stage) __attribute__((always_inline)) -> uint32_t {
+            if (!issuing) return 0u;
+            uint32_t n = 0;
+            const bool last = pc + 1 == nch;
+            uint8_t* const st = p2_ring + stage * SBY;
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                const uint32_t bo = (!last || pc * 64 + g * 16 < RB) ? pc * 64 : 0u;
+                __builtin_amdgcn_global_load_lds(wb + woff[u] + bo, st + (4 * p + u) * 1024, 16, 0, 0);
+            }
+            n += 4;
+#pragma unroll
+            for (uint32_t v = 0; v < NAI; v++) {
+                const uint32_t q = (p * NAI + v) % 2;
+                const bool ok = !last || pc * P2_KC + (4 * q + g) * 16 < K;
+                __builtin_amdgcn_global_load_lds(ok ? A.aq + pc * P2_KC + aoff[v] : kZeroPage,
+                                                 st + P2_W_BYTES + (p * NAI + v) * 1024, 16, 0, 0);
+            }
+            n += NAI;
+            if (p < NAS) {
+                // routes 64 p + lane (a tile of 32 routes: lanes < 32)
+                if (NR >= 64 || lane < NR)
+                    __builtin_amdgcn_global_load_lds(A.as + soff + pc, st + P2_W_BYTES + NR * 128 + p * 256, 4, 0, 0);
+                n += 1;
+            }
+            // The next item's route list and scale rows, once the consumers
+            // are done with the slots they go to (the item before this one).
+            if (pc == NS - 1 && pord + 1 < n_mine) {
+                const PgItem nx = p2_item(A.items + pitem + G);
+                if (p < 2) {
+                    const PgList* src = A.lists + nx.tile;
+                    uint8_t* dst = p2_ring + P2_LIST_OFF + ((pord + 1) & 1u) * (uint32_t)sizeof(PgList) + p * 1024;
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(src) + p * 1024 + lane * 16, dst,
+                                                     16, 0, 0);
+                    n += 1;
+                }
+                n += copy_span(nx, (pord + 1) & 1u);
+            }
+            if (++pc == nch) {
+                pc = 0;
+                pord++;
+                pitem += G;
+                issuing = pord < n_mine;
+                if (issuing) {
+                    it = p2_item(A.items + pitem);
+                    setup();
+                }
+            }
+            return n;
+        };
+        // prologue: the first item's list and scale rows (synchronously),
+        // then chunks 0 .. NS - 2
+        if (p < 2) {
+            const PgList* src = A.lists + it.tile;
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(src) + p * 1024 + lane * 16,
+                                             p2_ring + P2_LIST_OFF + p * 1024, 16, 0, 0);
+        }
+        copy_span(it, 0);
+        wait_vm_imm<0>();
+        __syncthreads();   // (1) the first list and scale rows are in LDS
+        setup();
+        // n[s]: ops this wave issued with the chunk of stage s (indexed by
+        // compile-time constants only, so it stays in registers)
+        uint32_t n[NS];
+        static_for<NS>([&](auto s_) __attribute__((always_inline)) { n[decltype(s_)::value] = 0; });
+        static_for<NS - 1>([&](auto s_) __attribute__((always_inline)) {
+            constexpr uint32_t st = decltype(s_)::value;
+            n[st] = issue(st);
+        });
+        {
+            uint32_t x = 0;
+            static_for<NS - 2>([&](auto q_) __attribute__((always_inline)) { x += n[decltype(q_)::value + 1]; });
+            wait_vm(x);
+        }
+        __syncthreads();   // (2) chunk 0 landed
+        // Step t issues chunk t + NS - 1 into stage (t + NS - 1) % NS and
+        // waits for chunk t + 1: what was issued after it is the last NS - 2
+        // batches.  A bare barrier: __syncthreads() would also wait for
+        // every copy in flight (its release fence drains vmcnt).
+        for (uint32_t t = 0; t < T; t += NS) {
+            bool done = false;
+            static_for<NS>([&](auto s_) __attribute__((always_inline)) {
+                constexpr uint32_t sp = decltype(s_)::value;
+                if (done || t + sp >= T) {
+                    done = true;
+                    return;
+                }
+                constexpr uint32_t sn = (sp + NS - 1) % NS;
+                n[sn] = issue(sn);
+                uint32_t x = 0;
+                static_for<NS - 2>([&](auto q_) __attribute__((always_inline)) {
+                    x += n[(sp + 2 + decltype(q_)::value) % NS];
+                });
+                wait_vm(x);
+                __builtin_amdgcn_s_barrier();
+            });
+        }
+        return;
+    }
+
+    // ================= consumers =================
+    // Only LDS reads, MFMAs and the epilogue's stores: every operand and
+    // scale of a chunk is in its ring stage or the item's scale-row slot.
+    const uint32_t a0 = NJ == 4 ? 4 * (wave / 4) : 0u;   // first route subtile of this wave
+    const uint32_t LW = ring + lane * 16;                  // + stage + subtile * 1 KB
+    const uint32_t LA = LW + P2_W_BYTES;                   // + stage + subtile * 2 KB (+ 1 KB: pieces 4-7)
+    const uint32_t LS = ring + P2_W_BYTES + NR * 128 + rr * 4;   // + stage + route subtile * 64
+    uint32_t item = first, ord = 0;
+    PgItem it = p2_item(A.items + item);
+    uint32_t srow[NJ];   // LDS address of this lane's scale row of subtile j in the item's slot (+ 4 c + g)
+    auto start_item = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t j = 0; j < (uint32_t)NJ; j++)
+            srow[j] = ring + P2_SPAN_OFF + (ord & 1u) * P2_SPAN_SLOT + (p2_irow<NMAT, NJ>(wave, j) + rr) * SB + g;
+    };
+    v4f acc[NAW][NJ];
+#pragma unroll
+    for (int a = 0; a < NAW; a++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();   // (1)
+    start_item();
+    __syncthreads();   // (2)
+    uint32_t c = 0;
+    for (uint32_t t = 0; t < T; t++) {
+        const uint32_t so = (t % NS) * SBY;
+        const bool item_end = c + 1 == nch;
+        // operands and scales of chunk c
+        v4i bw[NJ];
+        v8i av[NAW];
+        uint32_t sw[NJ], sa[NAW];
+#pragma unroll
+        for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+            const uint32_t x = p2_irow<NMAT, NJ>(wave, j) / 16;
+            asm volatile("ds_read_b128 %0, %1" : "=v"(bw[j]) : "v"(LW + so + x * 1024));
+            asm volatile("ds_read_u8 %0, %1" : "=v"(sw[j]) : "v"(srow[j] + 4 * c));
+        }
+#pragma unroll
+        for (uint32_t a = 0; a < (uint32_t)NAW; a++) {
+            v4i lo, hi;
+            const uint32_t ad = LA + so + (a0 + a) * 2048;
+            // early-clobber outputs: the second read must not find its address
+            // register overwritten by the first read's data
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024" : "=&v"(lo), "=&v"(hi) : "v"(ad));
+            av[a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            asm volatile("ds_read_b32 %0, %1" : "=v"(sa[a]) : "v"(LS + so + (a0 + a) * 64));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (uint32_t j = 0; j < (uint32_t)NJ; j++) asm volatile("" : "+v"(bw[j]), "+v"(sw[j]));
+#pragma unroll
+        for (uint32_t a = 0; a < (uint32_t)NAW; a++) asm volatile("" : "+v"(av[a]), "+v"(sa[a]));
+        uint32_t ew[NJ], ea[NAW];
+        {
+            const bool blk_ok = 4 * c + g < SB;   // scale blocks past K (last chunk): 2^0
+#pragma unroll
+            for (uint32_t j = 0; j < (uint32_t)NJ; j++) ew[j] = blk_ok ? sw[j] : 127u;
+#pragma unroll
+            for (uint32_t a = 0; a < (uint32_t)NAW; a++) ea[a] = (sa[a] >> 23) & 0xffu;
+        }
+#pragma unroll
+        for (uint32_t a = 0; a < (uint32_t)NAW; a++)
+#pragma unroll
+            for (uint32_t j = 0; j < (uint32_t)NJ; j++) acc[a][j] = mfma_fp8_fp4(av[a], bw[j], ea[a], ew[j], acc[a][j]);
+        if (item_end) {
+            // ---- epilogue of the item ----
+            const uint32_t list = ring + P2_LIST_OFF + (ord & 1u) * (uint32_t)sizeof(PgList);
+            const uint32_t count = it.count;
+#pragma unroll
+            for (uint32_t a = 0; a < (uint32_t)NAW; a++) {
+                const uint32_t tb = 16 * (a0 + a);
+                if (tb >= count) continue;
+                v4i rt, wv;
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024\n\ts_waitcnt lgkmcnt(0)"
+                             : "=&v"(rt), "=&v"(wv)
+                             : "v"(list + (tb + 4 * g) * 4));
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    const uint32_t r = (uint32_t)rt[i];
+                    if (tb + 4 * g + i >= count || r >= A.routes) continue;
+                    if constexpr (NMAT == 2) {
+                        const uint64_t ob = (uint64_t)(r / A.k) * A.frame_elems + (uint64_t)(r % A.k) * N;
+#pragma unroll
+                        for (uint32_t j = 0; j < (uint32_t)NJ / 2; j++) {
+                            const uint32_t ch = it.rb * RPM + p2_irow<NMAT, NJ>(wave, j) + rr;
+                            if (ch >= N) continue;
+                            float gv = round_bf16(acc[a][j][i]);
+                            float uv = round_bf16(acc[a][j + NJ / 2][i]);
+                            if (A.limit > 0.0f) {
+                                gv = fminf(gv, A.limit);
+                                uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                            }
+                            A.out[ob + ch] = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
+                        }
+                    } else {
+                        const float wr = __int_as_float(wv[i]);
+#pragma unroll
+                        for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
+                            const uint32_t row = it.rb * RPM + p2_irow<NMAT, NJ>(wave, j) + rr;
+                            if (row < N) A.out[(uint64_t)r * N + row] = (uint16_t)f32_to_bf16(acc[a][j][i] * wr);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < NAW; a++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) acc[a][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            c = 0;
+            ord++;
+            item += G;
+            if (ord < n_mine) {
+                it = p2_item(A.items + item);
+                start_item();
+            }
+        } else {
+            c++;
+        }
+        __builtin_amdgcn_s_barrier();
+    }
+}
+
+template <int NMAT>
+__global__ __launch_bounds__(768) void moe_pg2_kernel(PgArgs A) {
+    constexpr uint32_t RPM = PG_ROWS / NMAT;
+    const uint32_t nrb = (A.N + RPM - 1) / RPM;
+    const uint32_t nt = __builtin_amdgcn_readfirstlane(A.n_tiles[0]);
+    const uint32_t nt0 = __builtin_amdgcn_readfirstlane(A.n_tiles[1]);
+    const uint32_t nt1 = __builtin_amdgcn_readfirstlane(A.n_tiles[2]);
+#ifdef NERVE_PREP_PROBE
+#define P2P(i) do { __syncthreads(); if (threadIdx.x == 0) atomicMax(&g_probe[32 + 4 * NMAT + (i)], __builtin_amdgcn_s_memrealtime()); } while (0)
+    if (threadIdx.x == 0) atomicMin(&g_probe[8], __builtin_amdgcn_s_memrealtime());
+#else
+#define P2P(i) __syncthreads()
+#endif
+    p2_range<NMAT, 8, 4, 4>(A, 0, nt0 * nrb);
+    P2P(0);
+    p2_range<NMAT, 4, 4, 2>(A, nt0 * nrb, (nt0 + nt1) * nrb);
+    P2P(1);
+    p2_range<NMAT, 2, 2, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
+#ifdef NERVE_PREP_PROBE
+    P2P(2);
+#endif
+}
+
+template <int NMAT>
+nerve_hip_status launch_pg2(const PgArgs& A, const nerve_hip_ctx* ctx, hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)moe_pg2_kernel<NMAT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                P2_LDS) != hipSuccess)
+            return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for moe_pg2_kernel");
+        attr_set = true;
+    }
+    moe_pg2_kernel<NMAT><<<ctx->cu_count, 768, P2_LDS, st>>>(A);
+    return nh::check_launch("moe_pg2_kernel");
+}
+
 template <int NMAT>
 nerve_hip_status launch_pgemm(const PgArgs& A, const nerve_hip_ctx* ctx, hipStream_t st) {
     static bool attr_set = false;
@@ -3619,7 +4087,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         // units (a few per CU keep the loads in flight).
         Q.vec8 = ((((uintptr_t)Q.x | (uintptr_t)Q.q) & 15) == 0 && Q.cols % 8 == 0 && Q.frame_elems % 8 == 0 &&
                   Q.seg_elems % 8 == 0 && Q.rows > 0) ? 1u : 0u;
-        const uint32_t per_pass = Q.vec8 ? 64 : 32;
+        const uint32_t per_pass = Q.vec8 ? 64 * PREP_QU : 32;
         const uint32_t qblocks =
             (uint32_t)std::min<uint64_t>((units + per_pass - 1) / per_pass, (uint64_t)4 * ctx->cu_count);
         if (E <= 1024) moe_prep_kernel<1024><<<1 + qblocks, 1024, 0, stream>>>(ta, Q);
@@ -3669,9 +4137,18 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         return nh::check_launch("mx_wfmt_kernel");
     }
     if (persistent) {
+        // Producer / consumer form: the item's scale rows fit their LDS
+        // slot and an item has enough chunks for the descriptor prefetch.
+#ifdef NERVE_PG1
+        const bool p2_ok = false;
+#else
+        const bool p2_ok = K % 32 == 0 && K / 32 <= P2_MAX_SB && (K + P2_KC - 1) / P2_KC >= P2_MIN_CHUNKS;
+#endif
         PgArgs pa;
         pa.aq = aq;
         pa.as = as;
+        pa.a_rows = arows;
+        pa.routes = cap;
         pa.K = K;
         pa.N = N;
         pa.k = k;
@@ -3682,9 +4159,11 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         pa.limit = ms.limit;
         if (gate_up) {
             pa.out = static_cast<uint16_t*>(intermediates);
+            if (p2_ok) return launch_pg2<2>(pa, ctx, stream);
             return launch_pgemm<2>(pa, ctx, stream);
         }
         pa.out = static_cast<uint16_t*>(expert_outputs);
+        if (p2_ok) return launch_pg2<1>(pa, ctx, stream);
         return launch_pgemm<1>(pa, ctx, stream);
     }
     if (grouped) {

@@ -16,7 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace {
+namespace nerve_calib {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const v4i global_v4i;
@@ -51,9 +51,9 @@ __device__ __forceinline__ void wait_vm_imm() {
 // One block per CU; waves 0-3 copy, waves 4-11 only take part in the
 // barriers (as the prefill consumers do).  Ring of 4 stages x 16 KB; each
 // issuing wave copies 4 KB per stage and keeps three stages in flight.
-template <bool ROWS>
 __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
-                                                       uint32_t* __restrict__ sink) {
+                                                       uint32_t* __restrict__ sink, uint32_t rows) {
+    const bool ROWS = rows != 0;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     constexpr uint32_t STAGE = 16384, PER_WAVE = 4096;
@@ -95,7 +95,9 @@ __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict
     if (threadIdx.x == 0 && ring[lane] == 0xA5 && ring[STAGE] == 0x5A) sink[blockIdx.x] = 1u;
 }
 
-}  // namespace
+}  // namespace nerve_calib
+
+using namespace nerve_calib;
 
 extern "C" {
 
@@ -114,18 +116,13 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
     } else if (mode == 2 || mode == 3) {
         static bool attr = false;
         if (!attr) {
-            if (hipFuncSetAttribute((const void*)read_lds_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    65536) != hipSuccess ||
-                hipFuncSetAttribute((const void*)read_lds_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    65536) != hipSuccess)
+            if (hipFuncSetAttribute((const void*)read_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 65536) !=
+                hipSuccess)
                 return 1;
             attr = true;
         }
         // 64 KB of LDS per block, 768 threads: one block per CU.
-        if (mode == 2)
-            read_lds_kernel<false><<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
-        else
-            read_lds_kernel<true><<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
+        read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out, mode == 3 ? 1u : 0u);
     } else {
         return 1;
     }

@@ -472,7 +472,9 @@ def hbm_copy(args, ctx, dev):
 
 
 HBM_READ_MODES = {0: "register loads, nontemporal (1 KB per wave load)", 1: "register loads, temporal",
-                  2: "global_load_lds copies, contiguous 1 KB", 3: "global_load_lds copies, 16 rows x 64 B (prefill weights)"}
+                  2: "global_load_lds copies, contiguous 1 KB", 3: "global_load_lds copies, 16 rows x 64 B (prefill weights)",
+                  4: "register loads, nontemporal, 48 KB items, 2 in flight per CU (decode streams)",
+                  5: "global_load_lds copies, 48 KB items, 2 ahead in a 3-slot ring"}
 
 
 def hbm_read(args, ctx, dev):
@@ -497,7 +499,7 @@ def hbm_read(args, ctx, dev):
     modes = {}
     for mode, what in HBM_READ_MODES.items():
         # the row pattern reads 22 of every 22.5 64-byte columns: count what it reads
-        nbytes = n if mode != 3 else (n // (cus * 16384)) * cus * 16384
+        nbytes = {3: (n // (cus * 16384)) * cus * 16384, 4: (n // 49152) * 49152, 5: (n // 49152) * 49152}.get(mode, n)
         fn = lambda i, m=mode: lib.nerve_calib_read(ctypes.c_void_p(buf.data_ptr()), n, m,
                                                     ctypes.c_void_p(sink.data_ptr()), cus,
                                                     ctypes.c_void_p(stream.cuda_stream))

@@ -12,7 +12,12 @@
 //           copy engine), contiguous 1 KB per copy;
 //   mode 3: as mode 2, but each copy takes 64 bytes of 16 rows 1440 bytes
 //           apart (the prefill weight-copy pattern: a 128-k chunk of a
-//           16-row MXFP4 subtile), rows walked in order.
+//           16-row MXFP4 subtile), rows walked in order;
+//   mode 4: one 512-thread block per CU, nontemporal register loads of
+//           contiguous 48 KB items, two items (96 KB) in flight per CU (the
+//           decode streams' item pattern);
+//   mode 5: one 512-thread block per CU, global_load_lds copies of the same
+//           48 KB items into a 3-slot LDS ring, two items ahead.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -95,6 +100,70 @@ __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict
     if (threadIdx.x == 0 && ring[lane] == 0xA5 && ring[STAGE] == 0x5A) sink[blockIdx.x] = 1u;
 }
 
+// Modes 4 and 5: 8 waves, items of 48 KB (6 KB per wave = 6 x 1 KB pieces);
+// block b streams items b, b + G, ...
+constexpr uint32_t ITEM = 49152, IPW = 6;
+
+__global__ __launch_bounds__(512) void read_items_regs_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                              uint32_t* __restrict__ sink) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint64_t items = bytes / ITEM;
+    v4i acc = v4i{0, 0, 0, 0};
+    auto ld = [&](uint64_t it, v4i (&r)[IPW]) {
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++) {
+            const global_v4i* p = reinterpret_cast<const global_v4i*>(
+                reinterpret_cast<uintptr_t>(buf + it * ITEM + (wave * IPW + q) * 1024 + lane * 16));
+            r[q] = __builtin_nontemporal_load(p);
+        }
+    };
+    v4i r0[IPW], r1[IPW];
+    uint64_t it = blockIdx.x;
+    if (it < items) ld(it, r0);
+    if (it + gridDim.x < items) ld(it + gridDim.x, r1);
+    for (; it < items; it += 2 * gridDim.x) {
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++) acc ^= r0[q];
+        if (it + 2 * gridDim.x < items) ld(it + 2 * gridDim.x, r0);
+        if (it + gridDim.x >= items) break;
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++) acc ^= r1[q];
+        if (it + 3 * gridDim.x < items) ld(it + 3 * gridDim.x, r1);
+    }
+    const uint32_t x = (uint32_t)(acc.x ^ acc.y ^ acc.z ^ acc.w);
+    if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
+}
+
+__global__ __launch_bounds__(512) void read_items_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                             uint32_t* __restrict__ sink) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint64_t items = bytes / ITEM;
+    const uint64_t mine = items > blockIdx.x ? (items - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    auto issue = [&](uint64_t k) {
+        const uint64_t it = blockIdx.x + k * gridDim.x;
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++)
+            __builtin_amdgcn_global_load_lds(buf + it * ITEM + (wave * IPW + q) * 1024 + lane * 16,
+                                             ring + (k % 3) * ITEM + (wave * IPW + q) * 1024, 16, 0, 0);
+    };
+    if (mine > 0) issue(0);
+    if (mine > 1) issue(1);
+    for (uint64_t k = 0; k < mine; k++) {
+        if (k + 2 < mine) {
+            issue(k + 2);
+            wait_vm_imm<2 * IPW>();
+        } else if (k + 1 < mine) {
+            wait_vm_imm<IPW>();
+        } else {
+            wait_vm_imm<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && ring[lane] == 0xA5 && ring[ITEM] == 0x5A) sink[blockIdx.x] = 1u;
+}
+
 }  // namespace nerve_calib
 
 using namespace nerve_calib;
@@ -102,7 +171,7 @@ using namespace nerve_calib;
 extern "C" {
 
 // Streams `bytes` of `buf` (16-byte aligned) once with read mode `mode`
-// (0-3, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
+// (0-5, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
 // Returns 0, or 1 for an unknown mode or a launch error.
 int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int cu_count, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -123,6 +192,17 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
         }
         // 64 KB of LDS per block, 768 threads: one block per CU.
         read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out, mode == 3 ? 1u : 0u);
+    } else if (mode == 4) {
+        read_items_regs_kernel<<<cu_count, 512, 0, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
+    } else if (mode == 5) {
+        static bool attr5 = false;
+        if (!attr5) {
+            if (hipFuncSetAttribute((const void*)read_items_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    3 * ITEM) != hipSuccess)
+                return 1;
+            attr5 = true;
+        }
+        read_items_lds_kernel<<<cu_count, 512, 3 * ITEM, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
     } else {
         return 1;
     }

@@ -1240,10 +1240,6 @@ nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid,
 
 }  // namespace
 
-extern "C" {
-
-}  // extern "C"
-
 namespace {
 // The projection with its scratch either from the context workspace
 // (fixed == nullptr; may grow it with hipMalloc) or from `fixed`, a buffer of

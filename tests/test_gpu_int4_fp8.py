@@ -6,6 +6,7 @@ import pytest
 import oracle
 from nerve_amd import workloads as wl
 
+from bounds import fp8_head_dequant, gptq_dequant, linear_atol
 from helpers import bf16_close, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
@@ -49,7 +50,7 @@ def test_int4_gptq_parity(ctx, dev, M, symmetric, K, N):
     y = _run_int4(ctx, dev, spec, x, d["qweight"], d["scales"], None if symmetric else d["qzeros"], None, M, N)
     ref = oracle.int4_linear("gptq", x, d["qweight"], d["scales"].view(np.uint16), G,
                              zeros=None if symmetric else d["qzeros"])
-    ok, worst, exact = bf16_close(y, ref)
+    ok, worst, exact = bf16_close(y, ref, atol=linear_atol(x, gptq_dequant(d)), name="int4 gptq")
     assert ok and exact > 0.9, (worst, exact)
 
 
@@ -67,7 +68,7 @@ def test_int4_gptq_group_lengths(ctx, dev, G, N, M):
     spec = f"linear_batch16_int4_gptq_sf16_g{G}_{K}x{N}.comp"
     y = _run_int4(ctx, dev, spec, x, d["qweight"], d["scales"], d["qzeros"], None, M, N)
     ref = oracle.int4_linear("gptq", x, d["qweight"], d["scales"].view(np.uint16), G, zeros=d["qzeros"])
-    ok, worst, exact = bf16_close(y, ref)
+    ok, worst, exact = bf16_close(y, ref, atol=linear_atol(x, gptq_dequant(d)), name="int4 group lengths")
     assert ok and exact > 0.9, (worst, exact)
 
 
@@ -78,7 +79,7 @@ def test_int4_config1_full_size(ctx, dev, M):
     spec = f"linear_batch16_int4_gptq_sf16_g{G}_{K}x{N}.comp"
     y = _run_int4(ctx, dev, spec, d["x"], d["qweight"], d["scales"], d["qzeros"], None, M, N)
     ref = oracle.int4_linear("gptq", d["x"], d["qweight"], d["scales"].view(np.uint16), G, zeros=d["qzeros"])
-    ok, worst, exact = bf16_close(y, ref)
+    ok, worst, exact = bf16_close(y, ref, atol=linear_atol(d["x"], gptq_dequant(d)), name="int4 config1")
     assert ok and exact > 0.9, (worst, exact)
 
 
@@ -103,13 +104,14 @@ def test_int4_ct_and_finalize(ctx, dev, finalize, bf16_scales):
     sc_bits = sc.view(np.uint16)
     y = _run_int4(ctx, dev, spec, x, qw, sc_bits, None, aux, M, N)
     ref = oracle.int4_linear("ct", x, qw, sc_bits, G, scale_bf16=bf16_scales, finalize=finalize, aux=aux)
-    ok, worst, exact = bf16_close(y, ref)
+    atol = linear_atol(x, gptq_dequant(d), finalize)
+    ok, worst, exact = bf16_close(y, ref, atol=atol, name="int4 ct finalize")
     assert ok and exact > 0.9, (worst, exact)
     # the same codes in the GPTQ layout give the same result
     gspec = f"{op}_batch16_int4_gptq_s{sdt}_g{G}_{K}x{N}.comp"
     g_sc = np.ascontiguousarray(sc_bits.T)
     y2 = _run_int4(ctx, dev, gspec, x, d["qweight"], g_sc, None, aux, M, N)
-    ok, worst, _ = bf16_close(y2, ref)
+    ok, worst, _ = bf16_close(y2, ref, atol=atol)
     assert ok, worst
 
 
@@ -160,7 +162,8 @@ def test_fp8_head_parity(ctx, dev, M, N, K):
     ref = oracle.fp8_output_projection(d["x"], d["W"], d["scale_inv"], 1, 1.0)
     err = np.max(np.abs(lf.astype(np.float64) - ref)) / np.max(np.abs(ref))
     assert err <= 1e-3, err
-    ok, worst, _ = bf16_close(lb, wl.f32_to_bf16_bits(ref))
+    ok, worst, _ = bf16_close(lb, wl.f32_to_bf16_bits(ref), atol=linear_atol(d["x"], fp8_head_dequant(d["W"], d["scale_inv"])),
+                              name="fp8 head")
     assert ok, worst
     assert np.array_equal(lb, wl.f32_to_bf16_bits(lf))
     assert np.array_equal(am, oracle.argmax(lf))       # fused argmax == argmax of its own logits
@@ -243,5 +246,5 @@ def test_int4_cooperative_batch64(ctx, dev, B, layout, G, finalize):
     spec = f"{op}_batch64_cooperative_int4_{layout}_sf16_g{G}_{K}x{N}.comp"
     y = _run_int4(ctx, dev, spec, x, qw, sc.view(np.uint16), None, aux, B, N)
     ref = oracle.int4_linear(layout, x, qw, sc.view(np.uint16), G, finalize=finalize, aux=aux)
-    ok, worst, exact = bf16_close(y, ref)
+    ok, worst, exact = bf16_close(y, ref, atol=linear_atol(x, gptq_dequant(d), finalize), name="int4 cooperative")
     assert ok and exact > 0.9, (worst, exact)

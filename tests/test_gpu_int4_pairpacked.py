@@ -9,6 +9,7 @@ import pytest
 import oracle
 from nerve_amd import workloads as wl
 
+from bounds import gptq_dequant, linear_atol
 from helpers import bf16_close, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
@@ -61,7 +62,8 @@ def test_int4_linear_pairpacked(ctx, dev, M, K, N, G, finalize, bf16_scales):
     qr, sr, sumr = oracle.quantize_i8_pairpacked(x)
     ref = oracle.int4_linear_pairpacked(qr, sr, sumr, d["qweight"], sc, G, scale_bf16=bf16_scales,
                                         finalize=finalize, aux=aux)
-    ok, worst, exact = bf16_close(to_np(y, np.uint16), ref)
+    ok, worst, exact = bf16_close(to_np(y, np.uint16), ref, atol=linear_atol(x, gptq_dequant(d), finalize),
+                                  name="pairpacked")
     assert ok and exact > 0.9, (worst, exact)
 
 
@@ -170,5 +172,6 @@ def test_int4_linear_prequant_unpaired(ctx, dev, M, K, N, G, layout, finalize):
     qr, sr = oracle.quantize_i8(x)
     ref = oracle.int4_linear_prequant(layout, qr, sr, qw, sc_bits, G, scale_bf16=bf16_scales, finalize=finalize,
                                       aux=aux)
-    ok, worst, exact = bf16_close(to_np(y, np.uint16), ref)
+    ok, worst, exact = bf16_close(to_np(y, np.uint16), ref, atol=linear_atol(x, gptq_dequant(d), finalize),
+                                  name="prequant unpaired")
     assert ok and exact > 0.9, (worst, exact)

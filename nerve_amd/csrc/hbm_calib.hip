@@ -13,6 +13,15 @@
 //   mode 3: as mode 2, but each copy takes 64 bytes of 16 rows 1440 bytes
 //           apart (the prefill weight-copy pattern: a 128-k chunk of a
 //           16-row MXFP4 subtile), rows walked in order;
+//   mode 6: as mode 3, but each copy takes 128 bytes (a whole line) of 8
+//           rows: a stage holds 128 rows x 128 B;
+//   mode 7: as mode 2, and mode 8: as mode 0, over the first 2 MB of the
+//           buffer again and again (an L2-resident window: the on-chip
+//           rates the gathered activation rows of the prefill see);
+//   mode 9: as mode 4, but each 46080-byte item is 32 rows x 1440 B (two
+//           16-row subtiles of a K = 2880 MXFP4 matrix) and every load is
+//           an MFMA operand: lane (g, r) takes 16 B of row r at 64 c + 16 g,
+//           wave w the 64-byte chunks c = 3 w .. 3 w + 2 of both subtiles;
 //   mode 4: one 512-thread block per CU, nontemporal register loads of
 //           contiguous 48 KB items, two items (96 KB) in flight per CU (the
 //           decode streams' item pattern);
@@ -28,7 +37,7 @@ typedef __attribute__((address_space(1))) const v4i global_v4i;
 
 template <bool NT>
 __global__ __launch_bounds__(256) void read_regs_kernel(const v4i* __restrict__ buf, uint64_t n16,
-                                                        uint32_t* __restrict__ sink) {
+                                                        uint32_t* __restrict__ sink, uint64_t wmask16) {
     constexpr uint32_t U = 4;
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -37,13 +46,14 @@ __global__ __launch_bounds__(256) void read_regs_kernel(const v4i* __restrict__ 
         v4i v[U];
 #pragma unroll
         for (uint32_t u = 0; u < U; u++) {
-            const global_v4i* p = reinterpret_cast<const global_v4i*>(reinterpret_cast<uintptr_t>(buf + i + u * stride));
+            const global_v4i* p =
+                reinterpret_cast<const global_v4i*>(reinterpret_cast<uintptr_t>(buf + ((i + u * stride) & wmask16)));
             v[u] = NT ? __builtin_nontemporal_load(p) : *p;
         }
 #pragma unroll
         for (uint32_t u = 0; u < U; u++) acc ^= v[u];
     }
-    for (; i < n16; i += stride) acc ^= buf[i];
+    for (; i < n16; i += stride) acc ^= buf[i & wmask16];
     const uint32_t x = (uint32_t)(acc.x ^ acc.y ^ acc.z ^ acc.w);
     if (x == 0x9e3779b9u) sink[blockIdx.x] = x;   // practically never taken: keeps the loads
 }
@@ -57,7 +67,7 @@ __device__ __forceinline__ void wait_vm_imm() {
 // barriers (as the prefill consumers do).  Ring of 4 stages x 16 KB; each
 // issuing wave copies 4 KB per stage and keeps three stages in flight.
 __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
-                                                       uint32_t* __restrict__ sink, uint32_t rows) {
+                                                       uint32_t* __restrict__ sink, uint32_t rows, uint64_t wmask) {
     const bool ROWS = rows != 0;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -67,9 +77,18 @@ __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict
     // ROWS: stage s of block b covers a 16 KB piece of the row pattern: 16
     // subtiles of 16 rows x 64 B, subtile x at rows 16 x.., the 64-byte
     // column (s % 22) of a 1440-byte row; blocks and 22-step groups walk
-    // the buffer in 16 x 16-row = 368 KB blocks.
+    // the buffer in 16 x 16-row = 368 KB blocks.  rows == 2: 16 subtiles of
+    // 8 rows x 128 B, the 128-byte column (s % 11), 128-row blocks.
     auto src = [&](uint64_t step, uint32_t u) -> const uint8_t* {
-        if (!ROWS) return buf + (step * gridDim.x + blockIdx.x) * STAGE + wave * PER_WAVE + u * 1024 + lane * 16;
+        if (!ROWS)
+            return buf + (((step * gridDim.x + blockIdx.x) * STAGE + wave * PER_WAVE + u * 1024 + lane * 16) & wmask);
+        if (rows == 2) {
+            const uint64_t blk = (step / 11) * gridDim.x + blockIdx.x;   // 128-row block
+            const uint32_t col = (uint32_t)(step % 11);
+            const uint32_t x = wave * 4 + u, r = lane & 7, piece = lane >> 3;
+            const uint64_t off = (blk * 128 + x * 8 + r) * 1440 + col * 128 + piece * 16;
+            return buf + (off + 16 <= bytes ? off : 0);
+        }
         const uint64_t blk = (step / 22) * gridDim.x + blockIdx.x;   // 256-row block
         const uint32_t col = (uint32_t)(step % 22);
         const uint32_t x = wave * 4 + u, r = lane & 15, piece = lane >> 4;
@@ -134,6 +153,47 @@ __global__ __launch_bounds__(512) void read_items_regs_kernel(const uint8_t* __r
     if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
 }
 
+// Mode 9: MFMA-operand register loads of 32-row x 1440-byte items.
+constexpr uint32_t OITEM = 46080;
+__global__ __launch_bounds__(512) void read_items_operand_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                                 uint32_t* __restrict__ sink) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
+    const uint64_t items = bytes / OITEM;
+    v4i acc = v4i{0, 0, 0, 0};
+    // chunk 22 holds 32 bytes per row (lanes g < 2); wave 7's third chunk
+    // (23) does not exist: it re-reads chunk 21
+    uint32_t off[IPW];
+#pragma unroll
+    for (uint32_t q = 0; q < IPW; q++) {
+        uint32_t c = 3 * wave + q % 3;
+        if (c == 23 || (c == 22 && g >= 2)) c = 21;
+        off[q] = ((q / 3) * 16 + r) * 1440 + c * 64 + g * 16;
+    }
+    auto ld = [&](uint64_t it, v4i (&v)[IPW]) {
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++) {
+            const global_v4i* p =
+                reinterpret_cast<const global_v4i*>(reinterpret_cast<uintptr_t>(buf + it * OITEM + off[q]));
+            v[q] = __builtin_nontemporal_load(p);
+        }
+    };
+    v4i r0[IPW], r1[IPW];
+    uint64_t it = blockIdx.x;
+    if (it < items) ld(it, r0);
+    if (it + gridDim.x < items) ld(it + gridDim.x, r1);
+    for (; it < items; it += 2 * gridDim.x) {
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++) acc ^= r0[q];
+        if (it + 2 * gridDim.x < items) ld(it + 2 * gridDim.x, r0);
+        if (it + gridDim.x >= items) break;
+#pragma unroll
+        for (uint32_t q = 0; q < IPW; q++) acc ^= r1[q];
+        if (it + 3 * gridDim.x < items) ld(it + 3 * gridDim.x, r1);
+    }
+    const uint32_t x = (uint32_t)(acc.x ^ acc.y ^ acc.z ^ acc.w);
+    if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
+}
+
 __global__ __launch_bounds__(512) void read_items_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
                                                              uint32_t* __restrict__ sink) {
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
@@ -171,18 +231,20 @@ using namespace nerve_calib;
 extern "C" {
 
 // Streams `bytes` of `buf` (16-byte aligned) once with read mode `mode`
-// (0-5, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
+// (0-9, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
 // Returns 0, or 1 for an unknown mode or a launch error.
 int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int cu_count, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     uint32_t* out = static_cast<uint32_t*>(sink);
-    if (mode == 0 || mode == 1) {
+    constexpr uint64_t WIN = 2u << 20;   // modes 7 and 8
+    if (mode == 0 || mode == 1 || mode == 8) {
         const uint32_t grid = 4 * (uint32_t)cu_count;
-        if (mode == 0)
-            read_regs_kernel<true><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out);
+        const uint64_t m16 = mode == 8 ? WIN / 16 - 1 : ~0ull;
+        if (mode != 1)
+            read_regs_kernel<true><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out, m16);
         else
-            read_regs_kernel<false><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out);
-    } else if (mode == 2 || mode == 3) {
+            read_regs_kernel<false><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out, m16);
+    } else if (mode == 2 || mode == 3 || mode == 6 || mode == 7) {
         static bool attr = false;
         if (!attr) {
             if (hipFuncSetAttribute((const void*)read_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 65536) !=
@@ -191,7 +253,11 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
             attr = true;
         }
         // 64 KB of LDS per block, 768 threads: one block per CU.
-        read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out, mode == 3 ? 1u : 0u);
+        read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out,
+                                                                   mode == 3 ? 1u : mode == 6 ? 2u : 0u,
+                                                                   mode == 7 ? WIN - 1 : ~0ull);
+    } else if (mode == 9) {
+        read_items_operand_kernel<<<cu_count, 512, 0, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
     } else if (mode == 4) {
         read_items_regs_kernel<<<cu_count, 512, 0, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
     } else if (mode == 5) {

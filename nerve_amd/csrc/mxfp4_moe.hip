@@ -25,7 +25,7 @@
 #include "async_copy.h"
 
 #ifdef NERVE_PREP_PROBE
-__device__ unsigned long long g_probe[64];
+__device__ unsigned long long g_probe[128];
 #define PROBE(i) do { if (threadIdx.x == 0) g_probe[(i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define PROBE(i) do { } while (0)
@@ -3624,6 +3624,10 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
         // waits for chunk t + 1: what was issued after it is the last NS - 2
         // batches.  A bare barrier: __syncthreads() would also wait for
         // every copy in flight (its release fence drains vmcnt).
+#ifdef NERVE_P2_TIMING
+        uint64_t tw = 0, tb = 0, ti = 0;
+        const uint64_t tstart = __builtin_amdgcn_s_memtime();
+#endif
         for (uint32_t t = 0; t < T; t += NS) {
             bool done = false;
             static_for<NS>([&](auto s_) __attribute__((always_inline)) {
@@ -3633,15 +3637,39 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
                     return;
                 }
                 constexpr uint32_t sn = (sp + NS - 1) % NS;
+#ifdef NERVE_P2_TIMING
+                const uint64_t q0 = __builtin_amdgcn_s_memtime();
+#endif
                 n[sn] = issue(sn);
                 uint32_t x = 0;
                 static_for<NS - 2>([&](auto q_) __attribute__((always_inline)) {
                     x += n[(sp + 2 + decltype(q_)::value) % NS];
                 });
+#ifdef NERVE_P2_TIMING
+                const uint64_t q1 = __builtin_amdgcn_s_memtime();
+                wait_vm(x);
+                const uint64_t q2 = __builtin_amdgcn_s_memtime();
+                __builtin_amdgcn_s_barrier();
+                const uint64_t q3 = __builtin_amdgcn_s_memtime();
+                ti += q1 - q0;
+                tw += q2 - q1;
+                tb += q3 - q2;
+#else
                 wait_vm(x);
                 __builtin_amdgcn_s_barrier();
+#endif
             });
         }
+#ifdef NERVE_P2_TIMING
+        if (p == 0 && lane == 0) {
+            constexpr uint32_t gi = NAT == 8 ? 0 : NAT == 4 ? 1 : 2;
+            atomicAdd(&g_probe[64 + gi * 16 + 0], (unsigned long long)ti);
+            atomicAdd(&g_probe[64 + gi * 16 + 1], (unsigned long long)tw);
+            atomicAdd(&g_probe[64 + gi * 16 + 2], (unsigned long long)tb);
+            atomicAdd(&g_probe[64 + gi * 16 + 3], (unsigned long long)(__builtin_amdgcn_s_memtime() - tstart));
+            atomicAdd(&g_probe[64 + gi * 16 + 4], (unsigned long long)T);
+        }
+#endif
         return;
     }
 
@@ -3669,6 +3697,10 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
     start_item();
     __syncthreads();   // (2)
     uint32_t c = 0;
+#ifdef NERVE_P2_TIMING
+    uint64_t cl = 0, cb = 0, ce = 0;
+    const uint64_t cstart = __builtin_amdgcn_s_memtime();
+#endif
     for (uint32_t t = 0; t < T; t++) {
         const uint32_t so = (t % NS) * SBY;
         const bool item_end = c + 1 == nch;
@@ -3692,7 +3724,13 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
             av[a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             asm volatile("ds_read_b32 %0, %1" : "=v"(sa[a]) : "v"(LS + so + (a0 + a) * 64));
         }
+#ifdef NERVE_P2_TIMING
+        const uint64_t r0 = __builtin_amdgcn_s_memtime();
+#endif
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#ifdef NERVE_P2_TIMING
+        cl += __builtin_amdgcn_s_memtime() - r0;
+#endif
 #pragma unroll
         for (uint32_t j = 0; j < (uint32_t)NJ; j++) asm volatile("" : "+v"(bw[j]), "+v"(sw[j]));
 #pragma unroll
@@ -3763,6 +3801,348 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
         } else {
             c++;
         }
+#ifdef NERVE_P2_TIMING
+        const uint64_t b0 = __builtin_amdgcn_s_memtime();
+        __builtin_amdgcn_s_barrier();
+        cb += __builtin_amdgcn_s_memtime() - b0;
+#else
+        __builtin_amdgcn_s_barrier();
+#endif
+    }
+#ifdef NERVE_P2_TIMING
+    if (lane == 0) {
+        constexpr uint32_t gi = NAT == 8 ? 0 : NAT == 4 ? 1 : 2;
+        atomicAdd(&g_probe[64 + gi * 16 + 5 + (wave == 0 ? 0 : 3)], (unsigned long long)cl);
+        atomicAdd(&g_probe[64 + gi * 16 + 6 + (wave == 0 ? 0 : 3)], (unsigned long long)cb);
+        atomicAdd(&g_probe[64 + gi * 16 + 7 + (wave == 0 ? 0 : 3)], (unsigned long long)(__builtin_amdgcn_s_memtime() - cstart));
+    }
+    (void)ce;
+#endif
+}
+
+// ---------------------------------------------------------------------------
+// Whole-line form of the producer / consumer loop, for tiles of <= 64 routes
+// (the route-count groups where the weights are most of the copied bytes).
+// A ring stage holds one half of the item's 256 rows (gate_up: the 128 gate
+// or the 128 up rows; down: rows 0-127 or 128-255) over a k pair (256 k), so
+// every weight copy takes whole 128-byte lines: 8 rows x 128 B per
+// instruction.  Copying 64 bytes of 16 rows per instruction and the other
+// half of each line a chunk later streams at ~5.0 TB/s over the chip; whole
+// lines stream at ~6.0.  Row r's eight 16-byte pieces sit in its 128 LDS
+// bytes XOR-swizzled by (r / 2) % 8 (r within its 16-row subtile), so the
+// 16 lanes that read one piece column of a subtile hit distinct bank groups.
+// The activations go by k pair as well: 4 routes x 256 B per instruction
+// into an activation slot that both stages of the pair read, pieces
+// swizzled by route % 16, with the pair's two block scales per route.
+// Consumer wave w owns rows 16 w .. 16 w + 15 of each half (subtile j =
+// half) for every route of the tile.
+// ---------------------------------------------------------------------------
+constexpr uint32_t WL_W_BYTES = 16384;   // weight stage: 128 rows x 128 B
+
+template <int NMAT, int NAT>
+__device__ __forceinline__ void p2_range_wl(const PgArgs& A, uint32_t i0, uint32_t n_items) {
+    constexpr uint32_t NR = NAT * 16;                       // routes per tile
+    constexpr uint32_t NSW = NAT <= 2 ? 4 : 3;              // weight stages
+    constexpr uint32_t NSA = (NSW + 2) / 2;                 // activation slots: 2 NSA >= NSW + 1
+    constexpr uint32_t ABY = NR * 256 + NR * 8;             // activation slot: pieces, then block scales
+    constexpr uint32_t AOFF = NSW * WL_W_BYTES;
+    static_assert(AOFF + NSA * ABY <= P2_RING, "whole-line ring");
+    constexpr uint32_t NAI = NR / 16;                       // activation copies per producer per pair
+    constexpr uint32_t NAS = NR / 32;                       // block-scale copies per pair (producers p < NAS)
+    extern __shared__ __attribute__((aligned(16))) uint8_t p2_ring[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t g = lane >> 4, rr = lane & 15;
+    const uint32_t K = A.K, N = A.N, RB = K / 2, SB = K / 32, nch = (K + P2_KC - 1) / P2_KC;
+    const uint32_t NP2 = (nch + 1) / 2, SPI = 2 * NP2;      // k pairs and steps per item
+    const uint32_t nsa = (K + 127) / 128;
+    constexpr uint32_t RPM = PG_ROWS / NMAT;
+    const uint32_t G = gridDim.x;
+    const uint32_t ring = lds_addr(p2_ring);
+
+    const uint32_t slot = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    const uint32_t first = i0 + (slot + G - i0 % G) % G;
+    if (first >= n_items) return;   // uniform over the block: no barrier below is reached
+    const uint32_t n_mine = (n_items - first + G - 1) / G;
+    const uint32_t T = n_mine * SPI;   // steps of this group for the block (even)
+
+    if (wave >= 8) {
+        // ================= producers =================
+        const uint32_t p = wave - 8;
+        uint32_t pitem = first, pord = 0, ps = 0;      // item being issued, its ordinal, next step in it
+        PgItem it = p2_item(A.items + pitem);
+        // row offsets of copy u in half 0 / half 1 (two arrays and a select:
+        // an array indexed by the run-time half would live in scratch)
+        uint32_t wo0[4], wo1[4], aoff[NAI], soff = 0;
+        auto setup = [&]() __attribute__((always_inline)) {
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                const uint32_t hr = 32 * p + 8 * u + (lane >> 3);   // row within the half
+                const uint32_t n0 = it.rb * RPM + hr;
+                const uint32_t n1 = it.rb * RPM + (NMAT == 2 ? hr : 128 + hr);
+                wo0[u] = (n0 < N ? n0 : 0u) * RB;
+                wo1[u] = (n1 < N ? n1 : 0u) * RB;
+            }
+            // activation copy v: routes 4 (p NAI + v) + lane / 16; block
+            // scales: routes 32 p + lane / 2.  List entries past the tile's
+            // count are not written: their positions read entry 0.
+            const uint32_t list = ring + P2_LIST_OFF + (pord & 1u) * (uint32_t)sizeof(PgList);
+#pragma unroll
+            for (uint32_t v = 0; v < NAI; v++) {
+                const uint32_t route = 4 * (p * NAI + v) + (lane >> 4);
+                const uint32_t pos = route < it.count ? route : 0u;
+                aoff[v] = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1) * K;
+            }
+            if (p < NAS) {
+                const uint32_t route = 32 * p + (lane >> 1);
+                const uint32_t pos = route < it.count ? route : 0u;
+                soff = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1) * nsa;
+            }
+        };
+        // The scale rows of item `nx` into span slot `sslot` (as p2_range).
+        auto copy_span = [&](const PgItem& nx, uint32_t sslot) __attribute__((always_inline)) -> uint32_t {
+            uint32_t cnt = 0;
+            uint8_t* const base = p2_ring + P2_SPAN_OFF + sslot * P2_SPAN_SLOT;
+#pragma unroll
+            for (uint32_t m = 0; m < (uint32_t)NMAT; m++) {
+                const uint32_t rows = min(RPM, N - nx.rb * RPM), slen = rows * SB;
+                const uint8_t* src = (m == 0 ? nx.s[0] : nx.s[1]) + (uint64_t)nx.rb * RPM * SB;
+                const uint32_t np = (slen + 255) / 256;
+                for (uint32_t q = p; q < np; q += 4) {
+                    const uint32_t o = min(q * 256, slen - 256);
+                    __builtin_amdgcn_global_load_lds(src + o + lane * 4, base + m * RPM * SB + o, 4, 0, 0);
+                    cnt++;
+                }
+            }
+            return cnt;
+        };
+        bool issuing = true;
+        // Issue the next step into weight stage `wst`; returns the ops issued.
+        auto issue = [&](uint32_t wst) __attribute__((always_inline)) -> uint32_t {
+            if (!issuing) return 0u;
+            uint32_t n = 0;
+            const uint32_t h = ps & 1u, cp = ps >> 1;
+            const uint8_t* wb = (NMAT == 2 && h) ? it.w[1] : it.w[0];
+            uint8_t* const st = p2_ring + wst * WL_W_BYTES;
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                // LDS piece slot lane % 8 of row 8 (u % 2) + lane / 8 of its subtile
+                const uint32_t gp = (lane & 7u) ^ ((u & 1u) * 4u + (lane >> 4));
+                const uint32_t bo = cp * 128 + gp * 16;
+                const uint32_t wo = h ? wo1[u] : wo0[u];
+                __builtin_amdgcn_global_load_lds(wb + wo + (bo < RB ? bo : 0u), st + (4 * p + u) * 1024, 16, 0, 0);
+            }
+            n += 4;
+            if (h == 0) {
+                // the pair's activations and block scales
+                uint8_t* const as_ = p2_ring + AOFF + ((pord * NP2 + cp) % NSA) * ABY;
+#pragma unroll
+                for (uint32_t v = 0; v < NAI; v++) {
+                    const uint32_t y = p * NAI + v;
+                    const uint32_t gp = (lane & 15u) ^ ((4 * y + (lane >> 4)) & 15u);
+                    const uint32_t kb = cp * 256 + gp * 16;
+                    __builtin_amdgcn_global_load_lds(kb < K ? A.aq + aoff[v] + kb : kZeroPage, as_ + y * 1024, 16, 0, 0);
+                }
+                n += NAI;
+                if (p < NAS) {
+                    const uint32_t c = min(2 * cp + (lane & 1u), nsa - 1);
+                    __builtin_amdgcn_global_load_lds(A.as + soff + c, as_ + NR * 256 + p * 256, 4, 0, 0);
+                    n += 1;
+                }
+            }
+            // The next item's route list and scale rows, once the consumers
+            // are done with the slots they go to (the item before this one).
+            if (ps == NSW - 1 && pord + 1 < n_mine) {
+                const PgItem nx = p2_item(A.items + pitem + G);
+                if (p < 2) {
+                    const PgList* src = A.lists + nx.tile;
+                    uint8_t* dst = p2_ring + P2_LIST_OFF + ((pord + 1) & 1u) * (uint32_t)sizeof(PgList) + p * 1024;
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(src) + p * 1024 + lane * 16, dst,
+                                                     16, 0, 0);
+                    n += 1;
+                }
+                n += copy_span(nx, (pord + 1) & 1u);
+            }
+            if (++ps == SPI) {
+                ps = 0;
+                pord++;
+                pitem += G;
+                issuing = pord < n_mine;
+                if (issuing) {
+                    it = p2_item(A.items + pitem);
+                    setup();
+                }
+            }
+            return n;
+        };
+        if (p < 2) {
+            const PgList* src = A.lists + it.tile;
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(src) + p * 1024 + lane * 16,
+                                             p2_ring + P2_LIST_OFF + p * 1024, 16, 0, 0);
+        }
+        copy_span(it, 0);
+        wait_vm_imm<0>();
+        __syncthreads();   // (1) the first list and scale rows are in LDS
+        setup();
+        uint32_t n[NSW];
+        static_for<NSW>([&](auto s_) __attribute__((always_inline)) { n[decltype(s_)::value] = 0; });
+        static_for<NSW - 1>([&](auto s_) __attribute__((always_inline)) {
+            constexpr uint32_t st = decltype(s_)::value;
+            n[st] = issue(st);
+        });
+        {
+            uint32_t x = 0;
+            static_for<NSW - 2>([&](auto q_) __attribute__((always_inline)) { x += n[decltype(q_)::value + 1]; });
+            wait_vm(x);
+        }
+        __syncthreads();   // (2) step 0 landed
+        // Step t issues step t + NSW - 1 and waits for step t + 1 (what was
+        // issued after it is the last NSW - 2 batches); a bare barrier.
+        for (uint32_t t = 0; t < T; t += NSW) {
+            bool done = false;
+            static_for<NSW>([&](auto s_) __attribute__((always_inline)) {
+                constexpr uint32_t sp = decltype(s_)::value;
+                if (done || t + sp >= T) {
+                    done = true;
+                    return;
+                }
+                constexpr uint32_t sn = (sp + NSW - 1) % NSW;
+                n[sn] = issue(sn);
+                uint32_t x = 0;
+                static_for<NSW - 2>([&](auto q_) __attribute__((always_inline)) {
+                    x += n[(sp + 2 + decltype(q_)::value) % NSW];
+                });
+                wait_vm(x);
+                __builtin_amdgcn_s_barrier();
+            });
+        }
+        return;
+    }
+
+    // ================= consumers =================
+    const uint32_t wsw = (rr >> 1) & 7u;                    // this lane's row swizzle
+    const uint32_t LWr = ring + (16 * wave + rr) * 128;     // + stage + piece slot * 16
+    const uint32_t LAr = ring + AOFF + rr * 256;            // + slot + subtile * 4 KB + piece slot * 16
+    const uint32_t LSr = ring + AOFF + NR * 256 + rr * 8;   // + slot + subtile * 128 + 4 ch
+    uint32_t item = first, ord = 0;
+    PgItem it = p2_item(A.items + item);
+    uint32_t srow0, srow1;   // this lane's scale row of subtile 0 / 1 in the item's slot (+ 4 c + g)
+    auto start_item = [&]() __attribute__((always_inline)) {
+        const uint32_t b = ring + P2_SPAN_OFF + (ord & 1u) * P2_SPAN_SLOT + g;
+        srow0 = b + (16 * wave + rr) * SB;
+        srow1 = b + (128 + 16 * wave + rr) * SB;
+    };
+    v4f acc0[NAT], acc1[NAT];
+#pragma unroll
+    for (int a = 0; a < NAT; a++) {
+        acc0[a] = v4f{0.f, 0.f, 0.f, 0.f};
+        acc1[a] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();   // (1)
+    start_item();
+    __syncthreads();   // (2)
+    uint32_t cp = 0;
+    // One step: half H of k pair cp from weight stage t % NSW.
+    auto step = [&](uint32_t t, auto h_) __attribute__((always_inline)) {
+        constexpr uint32_t H = decltype(h_)::value;
+        const uint32_t wst = (t % NSW) * WL_W_BYTES;
+        const uint32_t ab = ((ord * NP2 + cp) % NSA) * ABY;
+        const bool ch1 = 2 * cp + 1 < nch;   // the pair's second chunk exists
+        v4i bw[2], alo[NAT][2], ahi[NAT][2];
+        uint32_t sw[2], sa[NAT][2];
+#pragma unroll
+        for (uint32_t ch = 0; ch < 2; ch++) {
+            asm volatile("ds_read_b128 %0, %1" : "=v"(bw[ch]) : "v"(LWr + wst + (((4 * ch + g) ^ wsw) * 16)));
+            asm volatile("ds_read_u8 %0, %1" : "=v"(sw[ch]) : "v"((H ? srow1 : srow0) + 4 * (2 * cp + ch)));
+#pragma unroll
+            for (uint32_t a = 0; a < (uint32_t)NAT; a++) {
+                const uint32_t base = LAr + ab + a * 4096;
+                asm volatile("ds_read_b128 %0, %1" : "=v"(alo[a][ch]) : "v"(base + (((8 * ch + g) ^ rr) * 16)));
+                asm volatile("ds_read_b128 %0, %1" : "=v"(ahi[a][ch]) : "v"(base + (((8 * ch + 4 + g) ^ rr) * 16)));
+                asm volatile("ds_read_b32 %0, %1" : "=v"(sa[a][ch]) : "v"(LSr + ab + a * 128 + 4 * ch));
+            }
+        }
+        // every result is used (even copied) only after the wait and the
+        // laundering asm
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        v8i av[NAT][2];
+#pragma unroll
+        for (uint32_t ch = 0; ch < 2; ch++) {
+            asm volatile("" : "+v"(bw[ch]), "+v"(sw[ch]));
+#pragma unroll
+            for (uint32_t a = 0; a < (uint32_t)NAT; a++) {
+                asm volatile("" : "+v"(alo[a][ch]), "+v"(ahi[a][ch]), "+v"(sa[a][ch]));
+                const v4i lo = alo[a][ch], hi = ahi[a][ch];
+                av[a][ch] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+        }
+#pragma unroll
+        for (uint32_t ch = 0; ch < 2; ch++) {
+            if (ch == 1 && !ch1) continue;
+            const uint32_t c = 2 * cp + ch;
+            const uint32_t ew = 4 * c + g < SB ? sw[ch] : 127u;   // scale blocks past K (last chunk): 2^0
+#pragma unroll
+            for (uint32_t a = 0; a < (uint32_t)NAT; a++) {
+                const uint32_t ea = (sa[a][ch] >> 23) & 0xffu;
+                if constexpr (H == 0) acc0[a] = mfma_fp8_fp4(av[a][ch], bw[ch], ea, ew, acc0[a]);
+                else acc1[a] = mfma_fp8_fp4(av[a][ch], bw[ch], ea, ew, acc1[a]);
+            }
+        }
+    };
+    for (uint32_t t = 0; t < T; t += 2) {
+        step(t, std::integral_constant<uint32_t, 0>{});
+        __builtin_amdgcn_s_barrier();
+        step(t + 1, std::integral_constant<uint32_t, 1>{});
+        if (cp + 1 == NP2) {
+            // ---- epilogue of the item ----
+            const uint32_t list = ring + P2_LIST_OFF + (ord & 1u) * (uint32_t)sizeof(PgList);
+            const uint32_t count = it.count;
+#pragma unroll
+            for (uint32_t a = 0; a < (uint32_t)NAT; a++) {
+                const uint32_t tb = 16 * a;
+                if (tb >= count) continue;
+                v4i rt, wv;
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024\n\ts_waitcnt lgkmcnt(0)"
+                             : "=&v"(rt), "=&v"(wv)
+                             : "v"(list + (tb + 4 * g) * 4));
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    const uint32_t r = (uint32_t)rt[i];
+                    if (tb + 4 * g + i >= count || r >= A.routes) continue;
+                    if constexpr (NMAT == 2) {
+                        const uint64_t ob = (uint64_t)(r / A.k) * A.frame_elems + (uint64_t)(r % A.k) * N;
+                        const uint32_t ch = it.rb * RPM + 16 * wave + rr;
+                        if (ch >= N) continue;
+                        float gv = round_bf16(acc0[a][i]);
+                        float uv = round_bf16(acc1[a][i]);
+                        if (A.limit > 0.0f) {
+                            gv = fminf(gv, A.limit);
+                            uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                        }
+                        A.out[ob + ch] = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
+                    } else {
+                        const float wr = __int_as_float(wv[i]);
+                        const uint32_t row0 = it.rb * RPM + 16 * wave + rr, row1 = row0 + 128;
+                        if (row0 < N) A.out[(uint64_t)r * N + row0] = (uint16_t)f32_to_bf16(acc0[a][i] * wr);
+                        if (row1 < N) A.out[(uint64_t)r * N + row1] = (uint16_t)f32_to_bf16(acc1[a][i] * wr);
+                    }
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < NAT; a++) {
+                acc0[a] = v4f{0.f, 0.f, 0.f, 0.f};
+                acc1[a] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+            cp = 0;
+            ord++;
+            item += G;
+            if (ord < n_mine) {
+                it = p2_item(A.items + item);
+                start_item();
+            }
+        } else {
+            cp++;
+        }
         __builtin_amdgcn_s_barrier();
     }
 }
@@ -3782,9 +4162,17 @@ __global__ __launch_bounds__(768) void moe_pg2_kernel(PgArgs A) {
 #endif
     p2_range<NMAT, 8, 4, 4>(A, 0, nt0 * nrb);
     P2P(0);
+    // Tiles of 33-64 and of 1-32 routes: the whole-line form (the 128-route
+    // tiles' activation slots would not fit its LDS ring).
+#ifdef NERVE_P2_NOWL
     p2_range<NMAT, 4, 4, 2>(A, nt0 * nrb, (nt0 + nt1) * nrb);
     P2P(1);
     p2_range<NMAT, 2, 2, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
+#else
+    p2_range_wl<NMAT, 4>(A, nt0 * nrb, (nt0 + nt1) * nrb);
+    P2P(1);
+    p2_range_wl<NMAT, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
+#endif
 #ifdef NERVE_PREP_PROBE
     P2P(2);
 #endif
@@ -3860,7 +4248,7 @@ extern "C" {
 int nerve_probe_read(unsigned long long* out) {
     hipDeviceSynchronize();
     int r = (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_probe), sizeof(g_probe));
-    unsigned long long init[64] = {0};
+    unsigned long long init[128] = {0};
     init[8] = ~0ull;
     hipMemcpyToSymbol(HIP_SYMBOL(g_probe), init, sizeof(init));
     return r;

@@ -478,7 +478,9 @@ HBM_READ_MODES = {0: "register loads, nontemporal (1 KB per wave load)", 1: "reg
                   6: "global_load_lds copies, 8 rows x 128 B (whole lines of the prefill weight rows)",
                   7: "global_load_lds copies, contiguous 1 KB, 2 MB L2-resident window (on-chip rate)",
                   8: "register loads, nontemporal, 2 MB L2-resident window (on-chip rate)",
-                  9: "register loads in the MFMA operand layout (16 rows x 64 B of 1440-byte rows), 2 items in flight"}
+                  9: "register loads in the MFMA operand layout (16 rows x 64 B of 1440-byte rows), 2 items in flight",
+                  10: "global_load_lds copies, 16 rows x 64 B, 2 MB L2-resident window (on-chip rate)",
+                  11: "global_load_lds copies, 8 rows x 128 B, 2 MB L2-resident window (on-chip rate)"}
 
 
 def hbm_read(args, ctx, dev):
@@ -504,7 +506,7 @@ def hbm_read(args, ctx, dev):
     for mode, what in HBM_READ_MODES.items():
         # the row pattern reads 22 of every 22.5 64-byte columns: count what it reads
         rows_bytes = (n // (cus * 16384)) * cus * 16384
-        nbytes = {3: rows_bytes, 6: rows_bytes, 7: rows_bytes, 4: (n // 49152) * 49152, 5: (n // 49152) * 49152,
+        nbytes = {3: rows_bytes, 6: rows_bytes, 7: rows_bytes, 10: rows_bytes, 11: rows_bytes, 4: (n // 49152) * 49152, 5: (n // 49152) * 49152,
                   9: (n // 46080) * 46080}.get(mode, n)
         fn = lambda i, m=mode: lib.nerve_calib_read(ctypes.c_void_p(buf.data_ptr()), n, m,
                                                     ctypes.c_void_p(sink.data_ptr()), cus,
@@ -512,8 +514,8 @@ def hbm_read(args, ctx, dev):
         assert fn(0) == 0, f"nerve_calib_read mode {mode} failed"
         kms = batch_event_ms(fn, max(20, args.steps), stream)
         modes[mode] = {"mode": what, "ms": kms, "gbs": nbytes / (kms * 1e-3) / 1e9}
-    # the headline is an HBM rate: the L2-resident modes (7, 8) are reported only
-    best = max((v for m, v in modes.items() if m not in (7, 8)), key=lambda v: v["gbs"])
+    # the headline is an HBM rate: the L2-resident modes (7, 8, 10, 11) are reported only
+    best = max((v for m, v in modes.items() if m not in (7, 8, 10, 11)), key=lambda v: v["gbs"])
     out = base_line(args, best["gbs"], "GB/s", best["ms"], "u8", {"workload": "hbm_read_1GiB"})
     out["modes"] = list(modes.values())
     out["roofline"] = {"bound": "hbm", "kernel": "nerve_calib_read (" + best["mode"] + ")", "achieved": best["gbs"],

@@ -22,6 +22,8 @@
 //           16-row subtiles of a K = 2880 MXFP4 matrix) and every load is
 //           an MFMA operand: lane (g, r) takes 16 B of row r at 64 c + 16 g,
 //           wave w the 64-byte chunks c = 3 w .. 3 w + 2 of both subtiles;
+//   modes 10 and 11: modes 3 and 6 over the 2 MB window (the L2-hit weight
+//           rows of tiles that share an expert);
 //   mode 4: one 512-thread block per CU, nontemporal register loads of
 //           contiguous 48 KB items, two items (96 KB) in flight per CU (the
 //           decode streams' item pattern);
@@ -86,13 +88,13 @@ __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict
             const uint64_t blk = (step / 11) * gridDim.x + blockIdx.x;   // 128-row block
             const uint32_t col = (uint32_t)(step % 11);
             const uint32_t x = wave * 4 + u, r = lane & 7, piece = lane >> 3;
-            const uint64_t off = (blk * 128 + x * 8 + r) * 1440 + col * 128 + piece * 16;
+            const uint64_t off = ((blk * 128 + x * 8 + r) * 1440 + col * 128 + piece * 16) & wmask;
             return buf + (off + 16 <= bytes ? off : 0);
         }
         const uint64_t blk = (step / 22) * gridDim.x + blockIdx.x;   // 256-row block
         const uint32_t col = (uint32_t)(step % 22);
         const uint32_t x = wave * 4 + u, r = lane & 15, piece = lane >> 4;
-        const uint64_t off = (blk * 256 + x * 16 + r) * 1440 + col * 64 + piece * 16;
+        const uint64_t off = ((blk * 256 + x * 16 + r) * 1440 + col * 64 + piece * 16) & wmask;
         return buf + (off + 16 <= bytes ? off : 0);
     };
     if (wave < 4) {
@@ -231,7 +233,7 @@ using namespace nerve_calib;
 extern "C" {
 
 // Streams `bytes` of `buf` (16-byte aligned) once with read mode `mode`
-// (0-9, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
+// (0-11, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
 // Returns 0, or 1 for an unknown mode or a launch error.
 int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int cu_count, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -244,7 +246,7 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
             read_regs_kernel<true><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out, m16);
         else
             read_regs_kernel<false><<<grid, 256, 0, st>>>(static_cast<const v4i*>(buf), bytes / 16, out, m16);
-    } else if (mode == 2 || mode == 3 || mode == 6 || mode == 7) {
+    } else if (mode == 2 || mode == 3 || mode == 6 || mode == 7 || mode == 10 || mode == 11) {
         static bool attr = false;
         if (!attr) {
             if (hipFuncSetAttribute((const void*)read_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 65536) !=
@@ -254,8 +256,8 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
         }
         // 64 KB of LDS per block, 768 threads: one block per CU.
         read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out,
-                                                                   mode == 3 ? 1u : mode == 6 ? 2u : 0u,
-                                                                   mode == 7 ? WIN - 1 : ~0ull);
+                                                                   (mode == 3 || mode == 10) ? 1u : (mode == 6 || mode == 11) ? 2u : 0u,
+                                                                   (mode == 7 || mode >= 10) ? WIN - 1 : ~0ull);
     } else if (mode == 9) {
         read_items_operand_kernel<<<cu_count, 512, 0, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
     } else if (mode == 4) {

@@ -300,29 +300,43 @@ __device__ __forceinline__ const uint8_t* param_ptr(const uint32_t* __restrict__
     return reinterpret_cast<const uint8_t*>((uint64_t)rec[0] | ((uint64_t)rec[1] << 32));
 }
 
-__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tot, uint32_t* total) {
+// Exclusive prefix sums of four per-thread values over the block in thread
+// order, with one barrier: each wave scans its lanes, then every thread adds
+// the totals of the waves before its own.  `tot` receives the block totals.
+// wave_tot must not be rewritten until every thread has returned (the
+// caller's next barrier).
+__device__ uint4 block_exclusive_scan4(uint4 v, uint4* wave_tot, uint4& tot) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    uint32_t inc = v;
+    uint4 inc = v;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        uint32_t t = __shfl_up(inc, d);
-        if (lane >= (uint32_t)d) inc += t;
+        const uint32_t a = __shfl_up(inc.x, d), b = __shfl_up(inc.y, d), c = __shfl_up(inc.z, d),
+                       e = __shfl_up(inc.w, d);
+        if (lane >= (uint32_t)d) {
+            inc.x += a;
+            inc.y += b;
+            inc.z += c;
+            inc.w += e;
+        }
     }
     if (lane == 63) wave_tot[wave] = inc;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (uint32_t w = 0; w < nwave; w++) {
-            uint32_t t = wave_tot[w];
-            wave_tot[w] = run;
-            run += t;
+    uint4 pre = make_uint4(0, 0, 0, 0), all = make_uint4(0, 0, 0, 0);
+    for (uint32_t w = 0; w < nwave; w++) {
+        const uint4 t = wave_tot[w];
+        if (w < wave) {
+            pre.x += t.x;
+            pre.y += t.y;
+            pre.z += t.z;
+            pre.w += t.w;
         }
-        *total = run;
+        all.x += t.x;
+        all.y += t.y;
+        all.z += t.z;
+        all.w += t.w;
     }
-    __syncthreads();
-    uint32_t r = wave_tot[wave] + inc - v;
-    __syncthreads();
-    return r;
+    tot = all;
+    return make_uint4(pre.x + inc.x - v.x, pre.y + inc.y - v.y, pre.z + inc.z - v.z, pre.w + inc.w - v.w);
 }
 
 // One unit of expert work: up to TM routes of one expert, with the expert's
@@ -439,8 +453,8 @@ __device__ void build_tiles(const TileArgs& A) {
     __shared__ uint32_t tst[MAXE];
     __shared__ uint32_t est[MAXE];
     __shared__ uint8_t valid[MAXE];
-    __shared__ uint32_t wave_tot[16];
-    __shared__ uint32_t total;
+    __shared__ uint32_t gst[MAXE];
+    __shared__ uint4 wave_tot4[16];
     // Expert pointers (w0, s0, w1, s1) for the work-item expansion, when
     // every expert has its own thread.
     constexpr bool EPTR = MAXE <= 1024;
@@ -594,26 +608,44 @@ __device__ void build_tiles(const TileArgs& A) {
     }
     __syncthreads();
     PROBE(2);
-    // Exclusive scans of route counts and tile counts over experts.
+    // Exclusive scans over experts, in one pass: route counts, tile counts,
+    // and the tiles of the route-count groups of the persistent grouped GEMM
+    // (experts with more than 64 routes, 33-64, then 1-32: it contracts 128,
+    // 64 or 32 routes per tile for them) -- the first two packed as 16-bit
+    // halves.
+    auto group_of = [](uint32_t c) -> uint32_t { return c > 64 ? 0u : c > 32 ? 1u : 2u; };
     const uint32_t per = (A.E + nt - 1) / nt;
     const uint32_t e0 = min(A.E, tid * per), e1 = min(A.E, e0 + per);
-    uint32_t lc = 0, lt = 0;
+    uint4 lv = make_uint4(0, 0, 0, 0);
     for (uint32_t e = e0; e < e1; e++) {
-        lc += cnt[e];
-        lt += (cnt[e] + A.TM - 1) / A.TM;
+        const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM, gr = group_of(cnt[e]);
+        lv.x += cnt[e];
+        lv.y += nte;
+        if (gr == 0) lv.z += nte;
+        else if (gr == 1) lv.z += nte << 16;
+        else lv.w += nte;
     }
-    uint32_t oc = block_exclusive_scan(lc, wave_tot, &total);
-    uint32_t ot = block_exclusive_scan(lt, wave_tot, &total);
-    const uint32_t tiles_total = total;
+    uint4 tot;
+    uint4 o = block_exclusive_scan4(lv, wave_tot4, tot);
+    const uint32_t tiles_total = tot.y;
+    const uint32_t nt0 = tot.z & 0xffffu, nt1 = tot.z >> 16;
     for (uint32_t e = e0; e < e1; e++) {
-        cur[e] = oc;
-        est[e] = oc;
-        tst[e] = ot;
-        oc += cnt[e];
-        ot += (cnt[e] + A.TM - 1) / A.TM;
+        const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM, gr = group_of(cnt[e]);
+        cur[e] = o.x;
+        est[e] = o.x;
+        tst[e] = o.y;
+        // first tile of expert e among its group's tiles
+        gst[e] = gr == 0 ? (o.z & 0xffffu) : gr == 1 ? (o.z >> 16) : o.w;
+        o.x += cnt[e];
+        o.y += nte;
+        if (gr == 0) o.z += nte;
+        else if (gr == 1) o.z += nte << 16;
+        else o.w += nte;
     }
     __syncthreads();
     PROBE(3);
+    // From here on every phase only writes global memory (and the route
+    // counters in cur[]), so the phases run without barriers between them.
     for (uint32_t e = tid; e < A.E; e += nt) {
         const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM;
         for (uint32_t t = 0; t < nte; t++) {
@@ -623,7 +655,7 @@ __device__ void build_tiles(const TileArgs& A) {
                 // Bits 16-17: the expert's weight format (known to its own
                 // thread; experts past the block size are compact).
                 rec_out.expert = e | ((e == tid ? my_fmt : 0u) << 16);
-                rec_out.begin = cur[e] + t * A.TM;
+                rec_out.begin = est[e] + t * A.TM;
                 rec_out.count = min(A.TM, cnt[e] - t * A.TM);
                 rec_out.pad = (t << 16) | nte;   // tile index within the expert, expert's tile count
                 for (uint32_t m = 0; m < 2; m++) {
@@ -640,7 +672,6 @@ __device__ void build_tiles(const TileArgs& A) {
             }
         }
     }
-    __syncthreads();
     PROBE(4);
     // Route slots in expert order.  For the persistent grouped GEMM the slot
     // also goes into its tile's route list (position rank % TM of tile
@@ -680,43 +711,16 @@ __device__ void build_tiles(const TileArgs& A) {
     PROBE(5);
     if (A.items) {
         // Work items (expert, row block, tile) with tiles fastest, grouped by
-        // the expert's route count: experts with more than 64 routes, 33-64,
-        // then 1-32 (the grouped GEMM contracts 128, 64 or 32 routes per tile
-        // for them).  est[] (free now) takes each expert's first tile among
-        // its group's tiles; n_tiles[1], n_tiles[2] the first two groups' tile
-        // counts.  The tile records written above are visible after the
-        // barrier.
-        __syncthreads();
-        auto group_of = [](uint32_t c) -> uint32_t { return c > 64 ? 0u : c > 32 ? 1u : 2u; };
-        uint32_t l01 = 0, l2 = 0;
-        for (uint32_t e = e0; e < e1; e++) {
-            const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM, gr = group_of(cnt[e]);
-            if (gr == 0) l01 += nte;
-            else if (gr == 1) l01 += nte << 16;
-            else l2 += nte;
-        }
-        uint32_t o01 = block_exclusive_scan(l01, wave_tot, &total);
-        const uint32_t t01 = total;
-        uint32_t o2 = block_exclusive_scan(l2, wave_tot, &total);
-        for (uint32_t e = e0; e < e1; e++) {
-            const uint32_t nte = (cnt[e] + A.TM - 1) / A.TM, gr = group_of(cnt[e]);
-            if (gr == 0) {
-                est[e] = o01 & 0xffffu;
-                o01 += nte;
-            } else if (gr == 1) {
-                est[e] = o01 >> 16;
-                o01 += nte << 16;
-            } else {
-                est[e] = o2;
-                o2 += nte;
-            }
-        }
-        const uint32_t nt0 = t01 & 0xffffu, nt1 = t01 >> 16;
+        // the expert's route count (gst[]: the expert's first tile among its
+        // group's tiles); n_tiles[1], n_tiles[2] the first two groups' tile
+        // counts.
         if (tid == 0) {
             A.n_tiles[1] = nt0;
             A.n_tiles[2] = nt1;
         }
-        __syncthreads();
+        // Without per-expert pointers in LDS the items copy them from the
+        // tile records: wait until every record is written.
+        if constexpr (!EPTR) __syncthreads();
         PROBE(6);
         // One thread per (expert, row block): its tiles' items.
         const uint32_t nrb = A.item_nrb;
@@ -726,7 +730,7 @@ __device__ void build_tiles(const TileArgs& A) {
             if (nte == 0) continue;
             const uint32_t gr = group_of(cnt[e]);
             const uint32_t gbase = gr == 0 ? 0u : gr == 1 ? nt0 * nrb : (nt0 + nt1) * nrb;
-            const uint32_t base = gbase + est[e] * nrb + rb * nte;
+            const uint32_t base = gbase + gst[e] * nrb + rb * nte;
             for (uint32_t kk = 0; kk < nte; kk++) {
                 const uint32_t t = tst[e] + kk;
                 ItemRec o;

@@ -608,10 +608,19 @@ struct HgLayout {
 // the 16 rows a read touches land on 16 distinct 16-byte bank groups.
 __host__ __device__ __forceinline__ uint32_t hg_swz(uint32_t r) { return (r & 7u) ^ ((r >> 3) & 1u); }
 
-template <int WM, int WN, int TT, int NJ, int NS>
+// NPW = 0: every wave copies its share of each chunk and contracts; NPW > 0:
+// NPW extra waves (NW .. NW + NPW - 1) only copy, three chunks ahead, and
+// the NW waves only contract, so a copy that stalls at issue (the CU's miss
+// queue full) holds up no MFMA.  The copy waves take part in every barrier
+// of the contracting waves (their item starts and epilogues included).
+template <int WM, int WN, int TT, int NJ, int NS, int NPW>
 __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
     using L = HgLayout<WM, WN, TT, NJ, NS>;
     constexpr uint32_t TM = L::TM, TN = L::TN, NW = L::NW;
+    // copy issuers and each one's share of a chunk
+    constexpr uint32_t NI = NPW > 0 ? NPW : NW;
+    constexpr uint32_t ACI = TM / 8 / NI, BCI = TN / 8 / NI, CBI = ACI + BCI;
+    static_assert(ACI * 8 * NI == TM && BCI * 8 * NI == TN && ACI >= 1 && BCI >= 2 && BCI % 2 == 0, "copy split");
     extern __shared__ __attribute__((aligned(16))) uint8_t hg_lds[];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -626,8 +635,18 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
     const uint32_t n_my = (A.n_items - slot + G - 1) / G;     // >= 1: G <= n_items
     const uint32_t tail_cols = K - (nblk - 1) * 128;          // columns of the last chunk (32..128)
 
+    const bool producer = NPW > 0 && wave >= NW;
+    const uint32_t wi = NPW > 0 ? (producer ? wave - NW : 0u) : wave;   // issuer index
+    // item-start copies q < XW (q < TN / 64: 64 row scales; q = TN / 64: the
+    // row flags) go to issuers q % NI
+    auto xw_count = [&]() -> uint32_t {
+        uint32_t n = 0;
+        for (uint32_t q = wi; q < L::XW; q += NI) n++;
+        return n;
+    };
+    const uint32_t n_xw = xw_count();
     // ---- issue side --------------------------------------------------------
-    // Weight copy j of a wave fills 8 rows (group wave BC + j) with 8 pieces
+    // Weight copy j of an issuer fills 8 rows (group wi BCI + j) with 8 pieces
     // each: lane l copies piece (l & 7) ^ f(row) of row l >> 3, where
     // f(row) = (l >> 3) ^ (group parity), so the lane part of every weight
     // copy address is one of two values; rows past N (last tile) are
@@ -642,35 +661,37 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
         i_n0 = (i_item / A.ntt) * TN;
     };
     auto issue_chunk = [&](uint32_t ST) __attribute__((always_inline)) {
-        uint8_t* const dA = hg_lds + ST * L::STAGE + wave * L::AC * 1024;
-        uint8_t* const dB = hg_lds + ST * L::STAGE + L::A_BYTES + wave * L::BC * 1024;
+        uint8_t* const dA = hg_lds + ST * L::STAGE + wi * ACI * 1024;
+        uint8_t* const dB = hg_lds + ST * L::STAGE + L::A_BYTES + wi * BCI * 1024;
         uint8_t* const dS = hg_lds + ST * L::STAGE + L::A_BYTES + L::B_BYTES;
         const bool last = ic + 1 == nblk;
-        const uint8_t* a = A.xq + ((uint64_t)ic * Mpad + i_t0) * 128 + wave * L::AC * 1024 + lane * 16;
-        const uint8_t* w = A.W + (uint64_t)(i_n0 + wave * L::BC * 8) * K + ic * 128;
+        const uint8_t* a = A.xq + ((uint64_t)ic * Mpad + i_t0) * 128 + wi * ACI * 1024 + lane * 16;
+        const uint8_t* w = A.W + (uint64_t)(i_n0 + wi * BCI * 8) * K + ic * 128;
         const bool wpart = i_n0 + TN > N;                        // last vocabulary tile
-        static_for<L::AC>([&](auto ji) __attribute__((always_inline)) {
+        static_for<ACI>([&](auto ji) __attribute__((always_inline)) {
             constexpr uint32_t j = decltype(ji)::value;
             __builtin_amdgcn_global_load_lds(a + j * 1024, dA + j * 1024, 16, 0, 0);
         });
-        static_for<L::BC>([&](auto ji) __attribute__((always_inline)) {
+        static_for<BCI>([&](auto ji) __attribute__((always_inline)) {
             constexpr uint32_t j = decltype(ji)::value;
             const uint8_t* src = w + j * 8 * K + lane_off[j & 1];
-            if (wpart && i_n0 + (wave * L::BC + j) * 8 + lr >= N) src = A.W + (uint64_t)i_n0 * K + ic * 128;
+            if (wpart && i_n0 + (wi * BCI + j) * 8 + lr >= N) src = A.W + (uint64_t)i_n0 * K + ic * 128;
             __builtin_amdgcn_global_load_lds((!last || tail_ok[j & 1]) ? src : kHeadZero, dB + j * 1024, 16, 0, 0);
         });
-        if (wave == 0 && lane < TM / 4)   // the chunk's TM block scales: one 16-byte piece per lane
+        if (wi == 0 && lane < TM / 4)   // the chunk's TM block scales: one 16-byte piece per lane
             __builtin_amdgcn_global_load_lds(A.xs + (uint64_t)ic * Mpad + i_t0 + lane * 4, dS, 16, 0, 0);
-        if (ic == 0 && wave < L::XW) {
-            // Item start: the tile's row scales (waves 0 .. TN/64 - 1) or its
-            // row flags (wave TN/64), into the slot of the item's parity.
+        if (ic == 0) {
+            // Item start: the tile's row scales (copies q < TN/64) and its
+            // row flags (copy TN/64), into the slot of the item's parity.
             const uint32_t par = i_ord & 1u;
-            if (wave < TN / 64) {
-                const uint32_t row = i_n0 + 64 * wave + lane;
-                __builtin_amdgcn_global_load_lds(A.sw_row + (row < N ? row : N - 1),
-                                                 hg_lds + L::SWROW + par * TN * 4 + 64 * wave * 4, 4, 0, 0);
-            } else if (lane < TN / 4) {
-                __builtin_amdgcn_global_load_lds(A.nonuni + i_n0 + 4 * lane, hg_lds + L::FLAGS + par * TN, 4, 0, 0);
+            for (uint32_t q = wi; q < L::XW; q += NI) {
+                if (q < TN / 64) {
+                    const uint32_t row = i_n0 + 64 * q + lane;
+                    __builtin_amdgcn_global_load_lds(A.sw_row + (row < N ? row : N - 1),
+                                                     hg_lds + L::SWROW + par * TN * 4 + 64 * q * 4, 4, 0, 0);
+                } else if (lane < TN / 4) {
+                    __builtin_amdgcn_global_load_lds(A.nonuni + i_n0 + 4 * lane, hg_lds + L::FLAGS + par * TN, 4, 0, 0);
+                }
             }
         }
     };
@@ -756,7 +777,6 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
         // MFMAs earlier (past its latency), so the vector ALU works while the
         // matrix core is busy.  (Compiler scheduling placed each accumulate
         // right behind its own MFMA and waited for it.)
-        v4f pr[2][NJ];             // general form: results of tiles t, t - 1
         v4f pring[NJ + 1];         // fast form: ring of MFMA results
         float sxp[2];
         const uint32_t unit = 127u;                 // e8m0 1.0: unscaled e4m3 x e4m3
@@ -807,24 +827,18 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
                                      : "=&v"(pring[wslot])
                                      : "v"(bw), "v"(bt), "v"(unit));
                     } else {
-                        pr[cur][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bw, bt, v4f{0.f, 0.f, 0.f, 0.f}, 0,
-                                                                                      0, 0, 127, 0, 127);
+                        // general form (tiles with rows whose scale varies along
+                        // K): accumulate each result right away, which keeps
+                        // one result live instead of two rows of them
+                        const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bw, bt, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                                       0, 0, 0, 127, 0, 127);
+                        const float sx = sxp[cur];
+                        const uint32_t w0 = (uint32_t)swp[j].x, w1 = (uint32_t)swp[j].y;
+                        acc[t][j][0] = fmaf(p[0], sx * __uint_as_float(w0 << 16), acc[t][j][0]);
+                        acc[t][j][1] = fmaf(p[1], sx * __uint_as_float(w0 & 0xffff0000u), acc[t][j][1]);
+                        acc[t][j][2] = fmaf(p[2], sx * __uint_as_float(w1 << 16), acc[t][j][2]);
+                        acc[t][j][3] = fmaf(p[3], sx * __uint_as_float(w1 & 0xffff0000u), acc[t][j][3]);
                     }
-                }
-            }
-            if constexpr (general && t >= 1) {
-                constexpr uint32_t tp = t - 1, pp = tp & 1u;
-                const float sx = sxp[pp];
-#pragma unroll
-                for (uint32_t j = 0; j < (uint32_t)NJ; j++) {
-                    const v4f p = pr[pp][j];
-                    const uint32_t w0 = (uint32_t)swp[j].x, w1 = (uint32_t)swp[j].y;
-                    const float s0 = sx * __uint_as_float(w0 << 16), s1 = sx * __uint_as_float(w0 & 0xffff0000u);
-                    const float s2 = sx * __uint_as_float(w1 << 16), s3 = sx * __uint_as_float(w1 & 0xffff0000u);
-                    acc[tp][j][0] = fmaf(p[0], s0, acc[tp][j][0]);
-                    acc[tp][j][1] = fmaf(p[1], s1, acc[tp][j][1]);
-                    acc[tp][j][2] = fmaf(p[2], s2, acc[tp][j][2]);
-                    acc[tp][j][3] = fmaf(p[3], s3, acc[tp][j][3]);
                 }
             }
             if constexpr (!general && t == (uint32_t)TT) {
@@ -1045,27 +1059,71 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
     // be in flight: CB copies each, plus one at an item's first chunk for
     // waves below XW.
     const uint32_t total = n_my * nblk;
-    setup_issue();
-    for (uint32_t k = 0; k + 1 < (uint32_t)NS; k++) issue_next(k);
+    // copies an issuer puts in flight with chunk s2 of the sequence
+    auto copies_of = [&](uint32_t s2) -> uint32_t {
+        return CBI + (wi == 0 ? 1u : 0u) + (s2 % nblk == 0 ? n_xw : 0u);
+    };
+    if (producer) {
+        // Copy waves: wait for chunk sidx, join its barrier, issue chunk
+        // sidx + NS - 1 into the stage chunk sidx - 1 left, and join the
+        // contracting waves' barriers of this step (item start of the
+        // general form, epilogue).
+        setup_issue();
+        for (uint32_t k = 0; k + 1 < (uint32_t)NS; k++) issue_next(k);
+        uint32_t st = 0, pc = 0, pord = 0;
+        for (uint32_t sidx = 0;; sidx++) {
+            uint32_t x = 0;
+            for (uint32_t k = 1; k + 1 < (uint32_t)NS; k++) {
+                const uint32_t s2 = sidx + k;
+                if (s2 < total) x += copies_of(s2);
+            }
+            wait_vm(x);
+            __builtin_amdgcn_s_barrier();
+            issue_next(st == 0 ? NS - 1 : st - 1);
+            if (pc == 0) {
+                // the item's row flags landed with its chunk 0: the same
+                // decision as the contracting waves' start_item
+                uint32_t f = 0;
+                if (lane < TN / 4) f = lds_read_b32(hg_lds + L::FLAGS + (pord & 1u) * TN + 4 * lane);
+                lds_drain();
+                asm volatile("" : "+v"(f));
+                if (__ballot(f != 0u) != 0ull) __builtin_amdgcn_s_barrier();
+            }
+            if (++pc == nblk) {
+                __builtin_amdgcn_s_barrier();                   // epilogue: the stage is free
+                if (A.part_val) __builtin_amdgcn_s_barrier();   // epilogue: the argmax exchange
+                if (++pord == n_my) break;
+                pc = 0;
+            }
+            st = st + 1 == (uint32_t)NS ? 0 : st + 1;
+        }
+        return;
+    }
+    if constexpr (NPW == 0) {
+        setup_issue();
+        for (uint32_t k = 0; k + 1 < (uint32_t)NS; k++) issue_next(k);
+    }
     uint32_t st = 0;
     for (uint32_t sidx = 0;; sidx++) {
-        uint32_t x = 0;
-        for (uint32_t k = 1; k + 1 < (uint32_t)NS; k++) {
-            const uint32_t s2 = sidx + k;
-            if (s2 < total) x += L::CB + (wave == 0 ? 1u : 0u) + ((s2 % nblk == 0 && wave < L::XW) ? 1u : 0u);
+        if constexpr (NPW == 0) {
+            uint32_t x = 0;
+            for (uint32_t k = 1; k + 1 < (uint32_t)NS; k++) {
+                const uint32_t s2 = sidx + k;
+                if (s2 < total) x += copies_of(s2);
+            }
+            wait_vm(x);
         }
-        wait_vm(x);
         __builtin_amdgcn_s_barrier();
         // Half the waves issue their copies before contracting, half after:
         // the copies queue at the texture unit, and a wave waiting to issue
         // them leaves its SIMD to the other wave, which is contracting.
         const bool early = wave < NW / 2;
-        if (early) issue_next(st == 0 ? NS - 1 : st - 1);
+        if (NPW == 0 && early) issue_next(st == 0 ? NS - 1 : st - 1);
         if (c == 0) start_item();
         const uint32_t stb = __builtin_amdgcn_readfirstlane(st * L::STAGE);
         if (general) compute(stb, std::true_type{});
         else compute(stb, std::false_type{});
-        if (!early) issue_next(st == 0 ? NS - 1 : st - 1);
+        if (NPW == 0 && !early) issue_next(st == 0 ? NS - 1 : st - 1);
         if (++c == nblk) {
             epilogue(st);
             if (++c_ord == n_my) break;
@@ -1076,9 +1134,9 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
     }
 }
 
-template <int WM, int WN, int TT, int NJ, int NS>
-__global__ __launch_bounds__(64 * WM * WN, 1) void fp8_head_gemm_kernel(HeadGemmArgs A) {
-    fp8_head_gemm_body<WM, WN, TT, NJ, NS>(A);
+template <int WM, int WN, int TT, int NJ, int NS, int NPW>
+__global__ __launch_bounds__(64 * (WM * WN + NPW), 1) void fp8_head_gemm_kernel(HeadGemmArgs A) {
+    fp8_head_gemm_body<WM, WN, TT, NJ, NS, NPW>(A);
 }
 
 // Activation quantization for the tiled form (tied_output_projection_batch_
@@ -1210,18 +1268,18 @@ __global__ __launch_bounds__(1024) void argmax_f32_kernel(const float* __restric
     if (lane == 0) out[row] = si[0];
 }
 
-template <int WM, int WN, int TT, int NJ, int NS>
+template <int WM, int WN, int TT, int NJ, int NS, int NPW>
 nerve_hip_status launch_head_gemm_t(const HeadGemmArgs& G, uint32_t grid, hipStream_t st) {
     constexpr uint32_t lds = HgLayout<WM, WN, TT, NJ, NS>::BYTES;
     static_assert(lds <= 160 * 1024, "LDS");
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)fp8_head_gemm_kernel<WM, WN, TT, NJ, NS>,
+        if (hipFuncSetAttribute((const void*)fp8_head_gemm_kernel<WM, WN, TT, NJ, NS, NPW>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
             return nh::fail(NERVE_HIP_DEVICE_ERROR, "hipFuncSetAttribute failed for fp8_head_gemm_kernel");
         attr_set = true;
     }
-    fp8_head_gemm_kernel<WM, WN, TT, NJ, NS><<<grid, 64 * WM * WN, lds, st>>>(G);
+    fp8_head_gemm_kernel<WM, WN, TT, NJ, NS, NPW><<<grid, 64 * (WM * WN + NPW), lds, st>>>(G);
     return nh::check_launch("fp8_head_gemm_kernel");
 }
 
@@ -1233,9 +1291,18 @@ struct HgConfig {
 constexpr HgConfig kHgConfigs[3] = {{64, 256, 3}, {128, 128, 4}, {256, 128, 3}};
 
 nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid, hipStream_t st) {
-    if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 4, 3>(G, grid, st);
-    if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4>(G, grid, st);
-    return launch_head_gemm_t<4, 2, 4, 4, 3>(G, grid, st);
+    // 64- and 128-token tiles: four copy waves beside the 8 contracting
+    // ones (measured 159 against 164 us at M = 64, 194 against 211 at
+    // M = 128).  The 256-token tile keeps the copies in its contracting
+    // waves: its ~250 registers per wave do not fit 12 waves per CU.
+#ifdef NERVE_HG_NOPC
+    constexpr int NPW = 0;
+#else
+    constexpr int NPW = 4;
+#endif
+    if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 4, 3, NPW>(G, grid, st);
+    if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4, NPW>(G, grid, st);
+    return launch_head_gemm_t<4, 2, 4, 4, 3, 0>(G, grid, st);
 }
 
 }  // namespace

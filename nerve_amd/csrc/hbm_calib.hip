@@ -24,6 +24,13 @@
 //           wave w the 64-byte chunks c = 3 w .. 3 w + 2 of both subtiles;
 //   modes 10 and 11: modes 3 and 6 over the 2 MB window (the L2-hit weight
 //           rows of tiles that share an expert);
+//   modes 12 and 13: one GEMM chunk per step as the FP8 head's tiled GEMM
+//           streams it: 16 KB of weights (128 rows x 128 B of 2880-byte rows,
+//           from HBM, global_load_lds) plus 32 KB of token rows (contiguous
+//           1 KB pieces from the 2 MB window), two steps ahead, one barrier
+//           per step; mode 12 reads the tokens with register loads and
+//           writes them to LDS when their step comes up, mode 13 copies
+//           them with global_load_lds like the weights;
 //   mode 4: one 512-thread block per CU, nontemporal register loads of
 //           contiguous 48 KB items, two items (96 KB) in flight per CU (the
 //           decode streams' item pattern);
@@ -196,6 +203,85 @@ __global__ __launch_bounds__(512) void read_items_operand_kernel(const uint8_t* 
     if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
 }
 
+// Modes 12 and 13.  512 threads; LDS: 3 weight stages of 16 KB, then (mode
+// 13) 3 token stages of 32 KB or (mode 12) one 32 KB token slot.
+// (A device-function body: the host pass instantiates kernel template
+// bodies, where the gfx950 copy builtin does not exist.)
+template <bool REG>
+__device__ __forceinline__ void gemm_chunks_body(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                 uint32_t* __restrict__ sink) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    constexpr uint32_t WST = 16384, TST = 32768, ROW = 2880, COLS = 22;
+    constexpr uint64_t WINDOW = 2u << 20;
+    // weight steps: 128-row blocks x 22 columns of 128 B
+    const uint64_t nblk_rows = bytes / ((uint64_t)128 * ROW);
+    const uint64_t steps = (nblk_rows / gridDim.x) * COLS;
+    auto wsrc = [&](uint64_t st, uint32_t j) -> const uint8_t* {
+        const uint64_t blk = (st / COLS) * gridDim.x + blockIdx.x;
+        const uint32_t col = (uint32_t)(st % COLS), row = (wave * 2 + j) * 8 + (lane >> 3), piece = lane & 7u;
+        return buf + (blk * 128 + row) * ROW + col * 128 + piece * 16;
+    };
+    auto tsrc = [&](uint64_t st, uint32_t j) -> const uint8_t* {
+        return buf + (((st * gridDim.x + blockIdx.x) * TST + (wave * 4 + j) * 1024 + lane * 16) & (WINDOW - 1));
+    };
+    auto issue = [&](uint64_t st, v4i (&r)[4]) {
+#pragma unroll
+        for (uint32_t j = 0; j < 2; j++)
+            __builtin_amdgcn_global_load_lds(wsrc(st, j), ring + (st % 3) * WST + (wave * 2 + j) * 1024, 16, 0, 0);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            if constexpr (REG) {
+                asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r[j]) : "v"(tsrc(st, j)) : "memory");
+            } else {
+                __builtin_amdgcn_global_load_lds(tsrc(st, j), ring + 3 * WST + (st % 3) * TST + (wave * 4 + j) * 1024,
+                                                 16, 0, 0);
+            }
+        }
+    };
+    v4i r0[4], r1[4], r2[4];
+    if (steps > 0) issue(0, r0);
+    if (steps > 1) issue(1, r1);
+    uint32_t acc = 0;
+    // rn: the register set of step s + 2 (free: its step s - 1 is done)
+    auto step = [&](uint64_t s, v4i (&r)[4], v4i (&rn)[4]) {
+        if (s + 2 < steps) {
+            issue(s + 2, rn);
+            wait_vm_imm<12>();
+        } else if (s + 1 < steps) {
+            wait_vm_imm<6>();
+        } else {
+            wait_vm_imm<0>();
+        }
+        if constexpr (REG) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                asm volatile("" : "+v"(r[j]));
+                *reinterpret_cast<v4i*>(ring + 3 * WST + (wave * 4 + j) * 1024 + lane * 16) = r[j];
+            }
+        }
+        __builtin_amdgcn_s_barrier();
+        acc ^= ring[(s % 3) * WST + lane];
+        __builtin_amdgcn_s_barrier();
+    };
+    for (uint64_t s = 0; s < steps; s += 3) {
+        step(s, r0, r2);
+        if (s + 1 < steps) step(s + 1, r1, r0);
+        if (s + 2 < steps) step(s + 2, r2, r1);
+    }
+    if (acc == 0x12345u) sink[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(512) void gemm_chunks_reg_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                              uint32_t* __restrict__ sink) {
+    gemm_chunks_body<true>(buf, bytes, sink);
+}
+
+__global__ __launch_bounds__(512) void gemm_chunks_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                              uint32_t* __restrict__ sink) {
+    gemm_chunks_body<false>(buf, bytes, sink);
+}
+
 __global__ __launch_bounds__(512) void read_items_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
                                                              uint32_t* __restrict__ sink) {
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
@@ -233,7 +319,7 @@ using namespace nerve_calib;
 extern "C" {
 
 // Streams `bytes` of `buf` (16-byte aligned) once with read mode `mode`
-// (0-11, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
+// (0-13, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
 // Returns 0, or 1 for an unknown mode or a launch error.
 int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int cu_count, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -258,6 +344,21 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
         read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out,
                                                                    (mode == 3 || mode == 10) ? 1u : (mode == 6 || mode == 11) ? 2u : 0u,
                                                                    (mode == 7 || mode >= 10) ? WIN - 1 : ~0ull);
+    } else if (mode == 12 || mode == 13) {
+        static bool attr12 = false;
+        if (!attr12) {
+            if (hipFuncSetAttribute((const void*)gemm_chunks_reg_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    3 * 16384 + 3 * 32768) != hipSuccess ||
+                hipFuncSetAttribute((const void*)gemm_chunks_lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    3 * 16384 + 3 * 32768) != hipSuccess)
+                return 1;
+            attr12 = true;
+        }
+        if (mode == 12)
+            gemm_chunks_reg_kernel<<<cu_count, 512, 3 * 16384 + 32768, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
+        else
+            gemm_chunks_lds_kernel<<<cu_count, 512, 3 * 16384 + 3 * 32768, st>>>(static_cast<const uint8_t*>(buf), bytes,
+                                                                                   out);
     } else if (mode == 9) {
         read_items_operand_kernel<<<cu_count, 512, 0, st>>>(static_cast<const uint8_t*>(buf), bytes, out);
     } else if (mode == 4) {

@@ -230,7 +230,14 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
  * :299-355) take e4m3 weights [I, H] with the per-32 scales (pre-expanded)
  * or a [ceil(I/128), ceil(H/128)] e8m0 grid (experts >= N); adaptive banks
  * pick compact or expanded per expert by address-record word 7.  Both
- * projection entry points accept them for E <= 1024. */
+ * projection entry points accept them for E <= 1024.
+ * Tensor-parallel slices (…gate_up_batch1[_tensor_parallel][_prequant]_…,
+ * template :487-641): one rank's share; the expert's four records cover its
+ * rows [0, L) of the intermediate, L = gate weight record bytes / (H / 2),
+ * and intermediates receives bf16 route-major local rows [B, k, L]; routes
+ * are read per token in order (no route map) and control is not read (any
+ * non-null buffer).  A token's routes after its first out-of-range or
+ * invalid expert are left untouched.  Compact MXFP4 only, H <= 4096. */
 nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spec,
                                              const void* hidden, const void* hidden_scales,
                                              const void* routes_u32, void* intermediates,
@@ -249,7 +256,16 @@ nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spe
  * parameters are W [I/128, H, 64] and S [I/128, H, 4] bytes
  * (…down_batch1_mxfp4.comp.template:229-233, :260-263); decode-sized
  * batches stream that layout, larger ones read it through the preparation
- * launch and a register-fed kernel (E <= 1024). */
+ * launch and a register-fed kernel (E <= 1024).
+ * Tensor-parallel slice (…down_batch1_tensor_parallel_input_block_major_b128_
+ * …, template :421-505): control points to the device push constants
+ * {input_start, input_count}; intermediates holds the local slice bf16
+ * [B, k, input_count] (input_count a multiple of 32, at most I, else nothing
+ * is written), the records the slice's blocks [I-blocks, H, 64] / [.., H, 4];
+ * expert_outputs receives f32 [B, k, H] partial sums, not scaled by the route
+ * weight (the ranks' partials are summed, then scaled, by the caller).
+ * A token's routes after its first invalid expert are left untouched.
+ * Compact MXFP4 only, I <= 4096; the counted form refuses it. */
 nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec,
                                           const void* intermediates, const void* routes_u32,
                                           void* expert_outputs,

@@ -138,11 +138,10 @@ static nerve_hip_status parse_moe_spec_uncached(const char* spec, MoeSpec* out) 
     if (s.hidden == 0 || s.hidden % 32 || s.inter == 0 || s.inter % 32 || !(0 < s.k && s.k <= s.experts) ||
         s.gate_up != s.has_limit || s.experts > 65536)
         return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid demand-addressed MXFP4 expert kernel ") + spec);
-    if (s.tensor_parallel) return fail(NERVE_HIP_UNSUPPORTED, "tensor-parallel expert partials are a multi-GPU path; this backend is single-GPU");
     // Native FP8 banks: 0 < start < E, not with tensor-parallel partials or
     // the block-major layout (nerve/model_package_shader_templates.py:4809-4817).
     if (s.native_fp8_start >= 0 && (s.native_fp8_start == 0 || (uint32_t)s.native_fp8_start >= s.experts ||
-                                    s.input_block_major))
+                                    s.input_block_major || s.tensor_parallel))
         return fail(NERVE_HIP_INVALID_SPEC, std::string("invalid native FP8 expert range in ") + spec);
     // input_block_major_b128 is a down-weight layout
     // (nerve/model_package_independent_experts.py:164-170) and needs whole
@@ -150,6 +149,10 @@ static nerve_hip_status parse_moe_spec_uncached(const char* spec, MoeSpec* out) 
     if (s.input_block_major && (s.gate_up || s.inter % 128))
         return fail(NERVE_HIP_INVALID_SPEC, std::string("input_block_major_b128 needs a down kernel with I % 128 == 0: ") + spec);
     if (s.prequant && !s.gate_up) return fail(NERVE_HIP_INVALID_SPEC, "prequant applies to gate_up only");
+    // A tensor-parallel down slice reads block-major weights, and only it
+    // (nerve/model_package_shader_templates.py:4818-4821).
+    if (s.tensor_parallel && s.gate_up == s.input_block_major)
+        return fail(NERVE_HIP_INVALID_SPEC, std::string("tensor-parallel slices: down needs input_block_major_b128, gate_up must not have it: ") + spec);
     *out = s;
     return NERVE_HIP_OK;
 }

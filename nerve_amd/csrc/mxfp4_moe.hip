@@ -4245,6 +4245,230 @@ nerve_hip_status quantize_rows(const uint16_t* x, uint32_t cols, uint32_t rows, 
 }  // namespace nh
 
 // ---------------------------------------------------------------------------
+// Tensor-parallel expert slices (…gate_up_batch1_mxfp4.comp.template:487-641,
+// …down_batch1_mxfp4.comp.template:421-505): one rank's share of an expert
+// projection.  On one GPU the ranks' shares are separate calls.
+//  - gate_up: the expert's gate/up records cover the rank's rows [0, L) of
+//    the intermediate, L = gate weight bytes / (H / 2); the output is bf16
+//    route-major local rows [B][k][L].
+//  - down: the local intermediate slice [B][k][count] (count = range[1])
+//    against input-block-major down weights whose records start at the
+//    slice's first 128-column block; the output is f32 [B][k][H], not scaled
+//    by the route weight (the ranks' partials are summed, then scaled).
+// Block = (tile of 32 gate_up / 64 down rows, token b), 4 waves of 16 rows
+// (gate_up: waves 0-1 gate, 2-3 up).  The token's routes run in order; the
+// first route whose expert is out of range or has an invalid record ends the
+// block, as the reference's `return` does, so that token's later routes keep
+// whatever their outputs held.  The activation row is quantized into LDS
+// (pow2 block scales, zero past K); every lane of a wave feeds the same
+// token to the MFMA's 16 activation rows.
+// ---------------------------------------------------------------------------
+constexpr uint32_t TP_MAX_K = 4096;   // contraction length staged in LDS
+
+struct TpArgs {
+    const uint16_t* x;        // gate_up: hidden bf16 [B, H]; down: local intermediates bf16 [B, k, count]
+    const uint8_t* xq;        // gate_up with prequantized input: e4m3 [B, H]
+    const float* xs;          //   and its pow2 block scales [B, ceil(H / 128)]
+    const uint32_t* routes;   // [B, k]
+    const uint32_t* addr;
+    uint32_t n_records;
+    const uint32_t* slots;
+    uint32_t n_slot_words;
+    const uint32_t* range;    // down: {input_start, input_count}
+    uint16_t* out16;          // gate_up
+    float* out32;             // down
+    uint32_t H, I, E, k;
+    float limit;
+};
+
+template <bool GU>
+__device__ __forceinline__ void mx_tp_body(const TpArgs& A) {
+    constexpr uint32_t TR = GU ? 32 : 64, P = GU ? 4 : 2;
+    __shared__ __attribute__((aligned(16))) uint8_t q[TP_MAX_K];
+    __shared__ float qs[TP_MAX_K / 128];
+    __shared__ float gu[2][32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, rr = lane & 15;
+    const uint32_t b = blockIdx.y, first = blockIdx.x * TR;
+    const uint32_t H = A.H;
+    // contraction length: H, or the slice's column count (a multiple of 32,
+    // at most I, else the launch writes nothing); it is also the row stride
+    // of the local frames
+    const uint32_t cnt = GU ? 0u : A.range[1];
+    if (!GU && (cnt % 32 != 0 || cnt > A.I)) return;
+    const uint32_t K = GU ? H : cnt;
+    const uint32_t nch = (K + 127) / 128;
+    const bool preq = GU && A.xq != nullptr;
+    // Quantize bf16 row xr (K columns) into q / qs: one 32-lane cluster per
+    // 128-column block, the same arithmetic as quant_unit.
+    auto quantize = [&](const uint16_t* xr) {
+        for (uint32_t blk = tid >> 5; blk < nch; blk += 8) {
+            const uint32_t cl = tid & 31, col = blk * 128 + cl * 4;
+            const bool valid = col < K;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (valid) {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(xr + col);
+                const uint32_t w0 = p[0], w1 = p[1];
+                v[0] = bf16_to_f32(w0); v[1] = bf16_to_f32(w0 >> 16);
+                v[2] = bf16_to_f32(w1); v[3] = bf16_to_f32(w1 >> 16);
+            }
+            float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            m = wave_max32(m);
+            const float sc = pow2_fp8_scale(m);
+            if (cl == 0) qs[blk] = sc;
+            const uint32_t packed = valid ? (f32_to_e4m3(v[0] / sc) | (f32_to_e4m3(v[1] / sc) << 8) |
+                                             (f32_to_e4m3(v[2] / sc) << 16) | (f32_to_e4m3(v[3] / sc) << 24))
+                                          : 0u;
+            *reinterpret_cast<uint32_t*>(q + col) = packed;
+        }
+    };
+    if (GU && !preq) {
+        quantize(A.x + (uint64_t)b * H);
+        __syncthreads();
+    }
+    for (uint32_t r = 0; r < A.k; r++) {
+        const uint32_t e = A.routes[(uint64_t)b * A.k + r] & 0xffffu;
+        // Validity of the expert's records (uniform over the block).  The
+        // reference asks for one row (gate_up) or one 128-column block
+        // (down); here every record must also cover what is read: the L
+        // local rows of all four gate_up records (L from the gate weight
+        // record), every block of the down slice.
+        bool ok = e < A.E;
+        uint32_t rec[P][8];
+        uint32_t slot[P];
+#pragma unroll
+        for (uint32_t p = 0; p < P; p++) {
+            const uint32_t idx = e * P + p;
+            slot[p] = (ok && idx < A.n_slot_words) ? A.slots[idx] : UNBOUND_SLOT;
+            const bool has = slot[p] != UNBOUND_SLOT && slot[p] < A.n_records;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) rec[p][j] = has ? A.addr[(uint64_t)slot[p] * 8 + j] : 0u;
+        }
+        const uint64_t gbytes = (uint64_t)rec[0][2] | ((uint64_t)rec[0][3] << 32);
+        const uint64_t L64 = GU ? gbytes / (H / 2) : H;
+        const uint32_t L = L64 > 0xffffffffull ? 0xffffffffu : (uint32_t)L64;
+        const uint64_t nb = nch > 0 ? nch : 1u;
+#pragma unroll
+        for (uint32_t p = 0; p < P; p++) {
+            const bool is_w = (p % 2) == 0;
+            const uint64_t need = GU ? (is_w ? (uint64_t)(H / 2) : (uint64_t)((H + 31) / 32)) * (L64 > 0 ? L64 : 1u)
+                                     : (is_w ? nb * H * 64 : nb * H * 4);
+            ok = record_valid(slot[p], A.n_records, rec[p], need, is_w ? 16u : 4u) && ok;
+        }
+        if (!ok) return;
+        auto ptr = [&](uint32_t p) {
+            return reinterpret_cast<const uint8_t*>((uint64_t)rec[p][0] | ((uint64_t)rec[p][1] << 32));
+        };
+        if constexpr (!GU) {
+            quantize(A.x + ((uint64_t)b * A.k + r) * cnt);
+            __syncthreads();
+        }
+        const uint32_t m = GU ? (wave >> 1) : 0u;
+        const uint32_t row = first + (GU ? 16 * (wave & 1u) : 16 * wave) + rr;
+        const uint32_t lrow = row < L ? row : 0u;   // rows past the slice read row 0 and are not written
+        const uint8_t* W = ptr(GU ? 2 * m : 0);
+        const uint8_t* S = ptr(GU ? 2 * m + 1 : 1);
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+        if (first < L) {
+            for (uint32_t c = 0; c < nch; c++) {
+                v8i av;
+                uint32_t sa;
+                if (preq) {
+                    load_a(A.xq + (uint64_t)b * H, A.xs + (uint64_t)b * nch, K, c, g, av, sa);
+                } else {
+                    const uint32_t k0 = c * 128 + g * 16;
+                    const v4i lo = *reinterpret_cast<const v4i*>(q + k0);
+                    const v4i hi = *reinterpret_cast<const v4i*>(q + k0 + 64);
+                    av = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                    sa = pow2_to_e8m0(qs[c]);
+                }
+                v4i w;
+                uint32_t sw;
+                if constexpr (GU) {
+                    load_w(W + (uint64_t)lrow * (H / 2), S + (uint64_t)lrow * ((H + 31) / 32), K, c, g, w, sw);
+                } else {
+                    // input-block-major: W [blocks][H][64 B], S [blocks][H][4 B]
+                    if (c * 128 + g * 32 < K) {
+                        w = *reinterpret_cast<const v4i*>(W + ((uint64_t)c * H + lrow) * 64 + g * 16);
+                        sw = S[((uint64_t)c * H + lrow) * 4 + g];
+                    } else {
+                        w = v4i{0, 0, 0, 0};
+                        sw = 127;
+                    }
+                }
+                acc = mfma_fp8_fp4(av, w, sa, sw, acc);
+            }
+        }
+        // every activation row is the token: D[0][rr] is row `row`'s sum
+        if constexpr (GU) {
+            if (g == 0) gu[m][16 * (wave & 1u) + rr] = acc[0];
+            __syncthreads();
+            if (tid < TR) {
+                const uint32_t orow = first + tid;
+                if (orow < L) {
+                    float gv = round_bf16(gu[0][tid]);
+                    float uv = round_bf16(gu[1][tid]);
+                    if (A.limit > 0.0f) {
+                        gv = fminf(gv, A.limit);
+                        uv = fminf(fmaxf(uv, -A.limit), A.limit);
+                    }
+                    A.out16[((uint64_t)b * A.k + r) * L + orow] = (uint16_t)f32_to_bf16(silu_fast(gv) * uv);
+                }
+            }
+        } else {
+            if (g == 0 && row < H) A.out32[((uint64_t)b * A.k + r) * H + row] = acc[0];
+        }
+        __syncthreads();   // LDS (activations, exchange) reused by the next route
+    }
+}
+
+__global__ __launch_bounds__(256) void mx_tp_gate_up_kernel(TpArgs A) { mx_tp_body<true>(A); }
+__global__ __launch_bounds__(256) void mx_tp_down_kernel(TpArgs A) { mx_tp_body<false>(A); }
+
+static nerve_hip_status moe_tensor_parallel(const nh::MoeSpec& ms, bool gate_up, const void* act, const void* pre_s,
+                                            const void* routes, void* out, const void* addresses,
+                                            uint32_t address_records, const void* slots, uint32_t slot_words,
+                                            const void* range, uint32_t batch_width, hipStream_t stream) {
+    if (ms.weight_repr != 0)
+        return nh::fail(NERVE_HIP_UNSUPPORTED, "tensor-parallel slices are supported for compact MXFP4 experts");
+    if ((gate_up ? ms.hidden : ms.inter) > TP_MAX_K)
+        return nh::fail(NERVE_HIP_UNSUPPORTED, "tensor-parallel slices contract at most 4096 columns");
+    if ((uintptr_t)addresses & 15)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "the address record table must be 16-byte aligned");
+    if (batch_width == 0) return nh::ok();
+    if (batch_width > 65535) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "batch too large");
+    TpArgs A{};
+    A.routes = static_cast<const uint32_t*>(routes);
+    A.addr = static_cast<const uint32_t*>(addresses);
+    A.n_records = address_records;
+    A.slots = static_cast<const uint32_t*>(slots);
+    A.n_slot_words = slot_words;
+    A.H = ms.hidden;
+    A.I = ms.inter;
+    A.E = ms.experts;
+    A.k = ms.k;
+    A.limit = ms.limit;
+    if (gate_up) {
+        if (ms.prequant) {
+            A.xq = static_cast<const uint8_t*>(act);
+            A.xs = static_cast<const float*>(pre_s);
+        } else {
+            if (((uintptr_t)act & 3) || ms.hidden % 2)
+                return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "hidden rows must be 4-byte aligned");
+            A.x = static_cast<const uint16_t*>(act);
+        }
+        A.out16 = static_cast<uint16_t*>(out);
+        mx_tp_gate_up_kernel<<<dim3((ms.inter + 31) / 32, batch_width), 256, 0, stream>>>(A);
+    } else {
+        if ((uintptr_t)act & 3) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "intermediates must be 4-byte aligned");
+        A.x = static_cast<const uint16_t*>(act);
+        A.range = static_cast<const uint32_t*>(range);
+        A.out32 = static_cast<float*>(out);
+        mx_tp_down_kernel<<<dim3((ms.hidden + 63) / 64, batch_width), 256, 0, stream>>>(A);
+    }
+    return nh::check_launch(gate_up ? "mx_tp_gate_up_kernel" : "mx_tp_down_kernel");
+}
+
+// ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
 extern "C" {
@@ -4636,6 +4860,10 @@ nerve_hip_status nerve_hip_mxfp4_moe_gate_up(nerve_hip_ctx* ctx, const char* spe
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (ms.prequant && ((uintptr_t)hidden & 15)) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "prequantized hidden must be 16-byte aligned");
     if (ms.prequant && ((uintptr_t)hidden_scales & 3)) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "hidden scales must be 4-byte aligned");
+    if (ms.tensor_parallel)
+        return moe_tensor_parallel(ms, true, hidden, hidden_scales, routes_u32, intermediates, addresses_u32,
+                                   address_records, param_slots_u32, param_slot_words, nullptr, batch_width,
+                                   (hipStream_t)stream);
     return moe_common(ctx, ms, true, hidden, hidden, hidden_scales, routes_u32, intermediates, nullptr, addresses_u32,
                       address_records, param_slots_u32, param_slot_words, control_u32, batch_width,
                       (hipStream_t)stream);
@@ -4654,6 +4882,10 @@ nerve_hip_status nerve_hip_mxfp4_moe_down(nerve_hip_ctx* ctx, const char* spec, 
     if (ms.gate_up) return nh::fail(NERVE_HIP_INVALID_SPEC, "down entry given a gate_up specialization");
     if (!intermediates || !routes_u32 || !expert_outputs || !addresses_u32 || !param_slots_u32 || !control_u32)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (ms.tensor_parallel)
+        return moe_tensor_parallel(ms, false, intermediates, nullptr, routes_u32, expert_outputs, addresses_u32,
+                                   address_records, param_slots_u32, param_slot_words, control_u32, batch_width,
+                                   (hipStream_t)stream);
     return moe_common(ctx, ms, false, nullptr, nullptr, nullptr, routes_u32, const_cast<void*>(intermediates),
                       expert_outputs, addresses_u32, address_records, param_slots_u32, param_slot_words, control_u32,
                       batch_width, (hipStream_t)stream);
@@ -4672,6 +4904,8 @@ nerve_hip_status nerve_hip_mxfp4_moe_down_counted(nerve_hip_ctx* ctx, const char
     if (ms.gate_up) return nh::fail(NERVE_HIP_INVALID_SPEC, "down entry given a gate_up specialization");
     if (!intermediates || !routes_u32 || !expert_outputs || !addresses_u32 || !param_slots_u32 || !control_u32)
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
+    if (ms.tensor_parallel)
+        return nh::fail(NERVE_HIP_INVALID_SPEC, "a tensor-parallel down slice takes no count stage (its push constants are the input range)");
     return moe_common(ctx, ms, false, nullptr, nullptr, nullptr, routes_u32, const_cast<void*>(intermediates),
                       expert_outputs, addresses_u32, address_records, param_slots_u32, param_slot_words, control_u32,
                       batch_width, (hipStream_t)stream, static_cast<uint32_t*>(control_u32));

@@ -28,13 +28,24 @@ def float_token(v: float) -> str:
     return format(v, ".9g")
 
 
-def gate_up_spec(H: int, I: int, E: int, k: int, limit: float, batch1: bool = True, prequant: bool = False) -> str:
-    return (f"independent_sparse_moe_gate_up{'_batch1' if batch1 else ''}{'_prequant' if prequant else ''}"
+def gate_up_spec(H: int, I: int, E: int, k: int, limit: float, batch1: bool = True, prequant: bool = False,
+                 tensor_parallel: bool = False) -> str:
+    """independent_sparse_moe_gate_up specialization; tensor_parallel names
+    one rank's slice (nerve/model_package_physical_experts.py:228-260)."""
+    return (f"independent_sparse_moe_gate_up{'_batch1' if batch1 else ''}"
+            f"{'_tensor_parallel' if tensor_parallel else ''}{'_prequant' if prequant else ''}"
             f"_mxfp4_e2m1_g32_h{H}_i{I}_e{E}_k{k}_limit{float_token(limit)}.comp")
 
 
-def down_spec(H: int, I: int, E: int, k: int, batch1: bool = True) -> str:
-    return f"independent_sparse_moe_down{'_batch1' if batch1 else ''}_mxfp4_e2m1_g32_h{H}_i{I}_e{E}_k{k}.comp"
+def down_spec(H: int, I: int, E: int, k: int, batch1: bool = True, block_major: bool = False,
+              tensor_parallel: bool = False) -> str:
+    """independent_sparse_moe_down specialization; a tensor-parallel slice
+    reads input-block-major weights (nerve/model_package_physical_experts.py:
+    262-330)."""
+    return (f"independent_sparse_moe_down{'_batch1' if batch1 else ''}"
+            f"{'_tensor_parallel' if tensor_parallel else ''}"
+            f"{'_input_block_major_b128' if (block_major or tensor_parallel) else ''}"
+            f"_mxfp4_e2m1_g32_h{H}_i{I}_e{E}_k{k}.comp")
 
 
 def int4_ct_spec(stage: str, H: int, I: int, E: int, k: int, group: int, *, scale_bf16: bool = True,

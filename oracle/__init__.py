@@ -62,6 +62,7 @@ def _declare(l) -> None:
         "o_route_compact": (None, [P, I, ctypes.c_uint32, P, P]),
         "o_moe_gate_up": (None, [P, P, P, I, I, I, I, I, I, F, P, P, P, P, P]),
         "o_moe_down": (None, [P, P, P, I, I, I, I, I, I, P, P, P]),
+        "o_moe_down_tp": (None, [P, P, I, I, I, I, I, I, I, P, P, P]),
         "o_moe_reduce": (None, [P, I, I, I, F, P]),
         "o_int4_linear": (None, [I, P, P, P, I, P, I, I, I, I, I, P, P]),
         "o_quantize_i8_pairpacked": (None, [P, I, I, P, P, P]),
@@ -253,6 +254,21 @@ def moe_down(inter, routes, cmap, n_routes, dw, ds, out=None):
     o = np.zeros((B, k, H), np.uint16) if out is None else _c(out, np.uint16).copy()
     lib().o_moe_down(_p(it), _p(_c(routes, np.uint32)), _p(_c(cmap, np.uint32)), n_routes,
                      B, k, E, H, I, _p(_c(dw, np.uint8)), _p(_c(ds, np.uint8)), _p(o))
+    return o
+
+
+def moe_down_tp(inter_slice, routes, start, dw, ds, out=None):
+    """Tensor-parallel down slice: inter_slice bf16 [B, k, count] = columns
+    [start, start + count) of the intermediates; dw [E, H, I/2], ds [E, H,
+    I/32] (row layout).  Returns f32 [B, k, H], not scaled by the route
+    weight; routes of a token after its first out-of-range expert keep
+    ``out``'s values."""
+    it = _c(inter_slice, np.uint16)
+    B, k, count = it.shape
+    E, H, I2 = dw.shape
+    o = np.zeros((B, k, H), np.float32) if out is None else _c(out, np.float32).copy()
+    lib().o_moe_down_tp(_p(it), _p(_c(routes, np.uint32)), B, k, E, H, 2 * I2, int(start), count,
+                        _p(_c(dw, np.uint8)), _p(_c(ds, np.uint8)), _p(o))
     return o
 
 

@@ -539,6 +539,39 @@ void o_moe_down(const uint16_t* inter, const uint32_t* routes, const uint32_t* m
     free(q); free(s); free(qf);
 }
 
+/* Tensor-parallel down slice (…down_batch1_mxfp4.comp.template:421-505,
+ * with INPUT_BLOCK_MAJOR addressing :229-233, :260-263): the local slice
+ * h [B, k, count] holds intermediate columns [start, start + count); each
+ * route's slice is quantized per 128-column block (pow2 scales) and
+ * contracted against the same columns of the down weights; out f32
+ * [B, k, H] = y, not scaled by the route weight.  A token's routes run in
+ * order and the first one with an out-of-range expert ends the token (the
+ * shader's `return`; later outputs untouched).  dw / ds are given in the
+ * package row layout [E, H, I/2], [E, H, I/32]; block-major storage only
+ * changes where a byte lives. */
+void o_moe_down_tp(const uint16_t* inter, const uint32_t* routes, int B, int k, int E, int H, int I,
+                   int start, int count, const uint8_t* dw, const uint8_t* ds, float* out) {
+    int nblk = (count + 127) / 128;
+    uint8_t* q = (uint8_t*)malloc((size_t)(count > 0 ? count : 1));
+    float* s = (float*)malloc(sizeof(float) * (size_t)(nblk > 0 ? nblk : 1));
+    float* qf = (float*)malloc(sizeof(float) * (size_t)(count > 0 ? count : 1));
+    for (int b = 0; b < B; b++) {
+        for (int route = 0; route < k; route++) {
+            uint32_t e = routes[(size_t)b * k + route] & 0xffffu;
+            if (e >= (uint32_t)E) break;
+            o_quantize_blocks(inter + ((size_t)b * k + route) * count, count, 1, count, 1, q, s);
+            decode_q(q, count, qf);
+            const uint8_t* dwe = dw + (size_t)e * H * (I / 2);
+            const uint8_t* dse = ds + (size_t)e * H * (I / 32);
+            #pragma omp parallel for schedule(static)
+            for (int j = 0; j < H; j++)
+                out[((size_t)b * k + route) * H + j] =
+                    mxfp4_row_dot(qf, s, count, dwe + (size_t)j * (I / 2) + start / 2, dse + (size_t)j * (I / 32) + start / 32);
+        }
+    }
+    free(q); free(s); free(qf);
+}
+
 /* a8: moe_reduce_batch1_bf16.comp.template:29-54 */
 void o_moe_reduce(const uint16_t* expert_out, int B, int k, int H, float routed_scale, uint16_t* out) {
     for (int b = 0; b < B; b++)

@@ -72,8 +72,13 @@ def test_null_context_is_rejected():
     ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_g32_h2880_i2880_e4_k5_limit7.comp", 2),
     ("independent_sparse_moe_down_batch1_mxfp4_e2m1_g32_h2880_i2880_e32_k4_limit7.comp", 2),
     ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_g32_h2880_i2880_e32_k4.comp", 2),
-    # families outside this build
-    ("independent_sparse_moe_down_batch1_tensor_parallel_input_block_major_b128_mxfp4_e2m1_g32_h128_i128_e2_k1.comp", 3),
+    # tensor-parallel slices: down needs the block-major layout, gate_up must
+    # not have it, no native FP8 banks
+    ("independent_sparse_moe_down_batch1_tensor_parallel_input_block_major_b128_mxfp4_e2m1_g32_h128_i128_e2_k1.comp", 0),
+    ("independent_sparse_moe_gate_up_batch1_tensor_parallel_mxfp4_e2m1_g32_h128_i128_e2_k1_limit7.comp", 0),
+    ("independent_sparse_moe_gate_up_batch1_tensor_parallel_prequant_mxfp4_e2m1_g32_h128_i128_e2_k1_limit7.comp", 0),
+    ("independent_sparse_moe_down_batch1_tensor_parallel_mxfp4_e2m1_g32_h128_i128_e2_k1.comp", 2),
+    ("independent_sparse_moe_down_batch1_tensor_parallel_input_block_major_b128_mxfp4_e2m1_g32_native_fp8_e4m3_se8m0_b128_nf1_h128_i128_e2_k1.comp", 2),
     # e4m3 expert banks (resident / adaptive pre-expanded, native FP8 experts)
     ("independent_sparse_moe_gate_up_batch1_mxfp4_e2m1_resident_fp8_e4m3_g32_h128_i128_e2_k1_limit7.comp", 0),
     ("independent_sparse_moe_down_batch1_mxfp4_e2m1_adaptive_fp8_e4m3_g32_h128_i128_e2_k1.comp", 0),

@@ -1295,11 +1295,7 @@ nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid,
     // ones (measured 159 against 164 us at M = 64, 194 against 211 at
     // M = 128).  The 256-token tile keeps the copies in its contracting
     // waves: its ~250 registers per wave do not fit 12 waves per CU.
-#ifdef NERVE_HG_NOPC
-    constexpr int NPW = 0;
-#else
     constexpr int NPW = 4;
-#endif
     if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 4, 3, NPW>(G, grid, st);
     if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4, NPW>(G, grid, st);
     return launch_head_gemm_t<4, 2, 4, 4, 3, 0>(G, grid, st);

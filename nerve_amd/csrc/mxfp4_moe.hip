@@ -24,13 +24,6 @@
 #include "common.h"
 #include "async_copy.h"
 
-#ifdef NERVE_PREP_PROBE
-__device__ unsigned long long g_probe[128];
-#define PROBE(i) do { if (threadIdx.x == 0) g_probe[(i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define PROBE(i) do { } while (0)
-#endif
-
 namespace {
 
 constexpr uint32_t UNBOUND_SLOT = 0xffffffffu;
@@ -462,7 +455,6 @@ __device__ void build_tiles(const TileArgs& A) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
     const uint32_t cap = A.batch_width * A.k;
     const uint32_t P = A.P;   // 4 (gate, gate scales, up, up scales) or 2 (down, down scales)
-    PROBE(0);
 
     // ---- round 1: slot words of expert tid, route map entry tid, control
     // Every load of the two rounds is issued unconditionally (from a clamped
@@ -491,14 +483,6 @@ __device__ void build_tiles(const TileArgs& A) {
     }
     const uint32_t rword = rw_r[0];
     const uint32_t c2 = A.control[2], c3 = A.control[3];
-#ifdef NERVE_PREP_PROBE
-    {
-        uint32_t acc = c2 + slot[0] + slot[1] + slot[2] + slot[3];
-        for (uint32_t i = 0; i < PREP_R; i++) acc += rw_r[i];
-        if (acc == 0x12345678u) g_probe[20] = 1;
-        PROBE(10);
-    }
-#endif
     // ---- round 2: address records, route word
     uint32_t rec[4][8] = {};
     if (A.n_records != 0) {
@@ -522,14 +506,6 @@ __device__ void build_tiles(const TileArgs& A) {
         rt_r[i] = (c < cap && rw_r[i] < cap) ? rv[i] : 0u;
     }
     const uint32_t route = rt_r[0];
-#ifdef NERVE_PREP_PROBE
-    {
-        uint32_t acc = rec[0][0] + rec[1][0] + rec[2][0] + rec[3][0];
-        for (uint32_t i = 0; i < PREP_R; i++) acc += rt_r[i];
-        if (acc == 0x12345678u) g_probe[20] = 1;
-        PROBE(11);
-    }
-#endif
 
     uint32_t n = c2 != 0u ? c3 : cap;
     if (n > cap) n = cap;
@@ -583,7 +559,6 @@ __device__ void build_tiles(const TileArgs& A) {
         cnt[e] = 0;
     }
     __syncthreads();
-    PROBE(1);
     // Expert of every compacted slot c < n (NO_EXPERT when invalid).
     auto slot_expert = [&](uint32_t c, uint32_t rw, uint32_t rt) -> uint32_t {
         if (c >= n || rw >= cap) return NO_EXPERT;
@@ -607,7 +582,6 @@ __device__ void build_tiles(const TileArgs& A) {
         wave_add_one(cnt, e, false);
     }
     __syncthreads();
-    PROBE(2);
     // Exclusive scans over experts, in one pass: route counts, tile counts,
     // and the tiles of the route-count groups of the persistent grouped GEMM
     // (experts with more than 64 routes, 33-64, then 1-32: it contracts 128,
@@ -643,7 +617,6 @@ __device__ void build_tiles(const TileArgs& A) {
         else o.w += nte;
     }
     __syncthreads();
-    PROBE(3);
     // From here on every phase only writes global memory (and the route
     // counters in cur[]), so the phases run without barriers between them.
     for (uint32_t e = tid; e < A.E; e += nt) {
@@ -672,7 +645,6 @@ __device__ void build_tiles(const TileArgs& A) {
             }
         }
     }
-    PROBE(4);
     // Route slots in expert order.  For the persistent grouped GEMM the slot
     // also goes into its tile's route list (position rank % TM of tile
     // tst[e] + rank / TM), with its activation row and route weight.
@@ -708,7 +680,6 @@ __device__ void build_tiles(const TileArgs& A) {
         place(e, r, rt);
     }
     if (tid == 0) *A.n_tiles = min(tiles_total, A.max_tiles);
-    PROBE(5);
     if (A.items) {
         // Work items (expert, row block, tile) with tiles fastest, grouped by
         // the expert's route count (gst[]: the expert's first tile among its
@@ -721,7 +692,6 @@ __device__ void build_tiles(const TileArgs& A) {
         // Without per-expert pointers in LDS the items copy them from the
         // tile records: wait until every record is written.
         if constexpr (!EPTR) __syncthreads();
-        PROBE(6);
         // One thread per (expert, row block): its tiles' items.
         const uint32_t nrb = A.item_nrb;
         for (uint32_t pr = tid; pr < A.E * nrb; pr += nt) {
@@ -752,10 +722,6 @@ __device__ void build_tiles(const TileArgs& A) {
                 A.items[base + kk] = o;
             }
         }
-#ifdef NERVE_PREP_PROBE
-        __syncthreads();
-        PROBE(7);
-#endif
     }
 }
 
@@ -771,16 +737,9 @@ __global__ __launch_bounds__(1024) void moe_prep_kernel(TileArgs T, QuantArgs Q)
     // Quantization blocks stride over the (row, 128-column) units, 64 per
     // pass with 16-byte loads (32 per pass otherwise).
     const uint64_t nblk = (Q.cols + 127) / 128, units = (uint64_t)Q.rows * nblk;
-#ifdef NERVE_PREP_PROBE
-    if (threadIdx.x == 0) atomicMin(&g_probe[8], __builtin_amdgcn_s_memrealtime());
-#endif
     if (Q.vec8) {
         for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 64 * PREP_QU; u < units; u += (uint64_t)(gridDim.x - 1) * 64 * PREP_QU)
             quant_units8_pow2<PREP_QU>(Q, u + (threadIdx.x >> 4), 64, threadIdx.x & 15);
-#ifdef NERVE_PREP_PROBE
-        __syncthreads();
-        if (threadIdx.x == 0) atomicMax(&g_probe[9], __builtin_amdgcn_s_memrealtime());
-#endif
         return;
     }
     for (uint64_t u = (uint64_t)(blockIdx.x - 1) * 32; u < units; u += (uint64_t)(gridDim.x - 1) * 32)
@@ -3628,10 +3587,6 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
         // waits for chunk t + 1: what was issued after it is the last NS - 2
         // batches.  A bare barrier: __syncthreads() would also wait for
         // every copy in flight (its release fence drains vmcnt).
-#ifdef NERVE_P2_TIMING
-        uint64_t tw = 0, tb = 0, ti = 0;
-        const uint64_t tstart = __builtin_amdgcn_s_memtime();
-#endif
         for (uint32_t t = 0; t < T; t += NS) {
             bool done = false;
             static_for<NS>([&](auto s_) __attribute__((always_inline)) {
@@ -3641,39 +3596,15 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
                     return;
                 }
                 constexpr uint32_t sn = (sp + NS - 1) % NS;
-#ifdef NERVE_P2_TIMING
-                const uint64_t q0 = __builtin_amdgcn_s_memtime();
-#endif
                 n[sn] = issue(sn);
                 uint32_t x = 0;
                 static_for<NS - 2>([&](auto q_) __attribute__((always_inline)) {
                     x += n[(sp + 2 + decltype(q_)::value) % NS];
                 });
-#ifdef NERVE_P2_TIMING
-                const uint64_t q1 = __builtin_amdgcn_s_memtime();
-                wait_vm(x);
-                const uint64_t q2 = __builtin_amdgcn_s_memtime();
-                __builtin_amdgcn_s_barrier();
-                const uint64_t q3 = __builtin_amdgcn_s_memtime();
-                ti += q1 - q0;
-                tw += q2 - q1;
-                tb += q3 - q2;
-#else
                 wait_vm(x);
                 __builtin_amdgcn_s_barrier();
-#endif
             });
         }
-#ifdef NERVE_P2_TIMING
-        if (p == 0 && lane == 0) {
-            constexpr uint32_t gi = NAT == 8 ? 0 : NAT == 4 ? 1 : 2;
-            atomicAdd(&g_probe[64 + gi * 16 + 0], (unsigned long long)ti);
-            atomicAdd(&g_probe[64 + gi * 16 + 1], (unsigned long long)tw);
-            atomicAdd(&g_probe[64 + gi * 16 + 2], (unsigned long long)tb);
-            atomicAdd(&g_probe[64 + gi * 16 + 3], (unsigned long long)(__builtin_amdgcn_s_memtime() - tstart));
-            atomicAdd(&g_probe[64 + gi * 16 + 4], (unsigned long long)T);
-        }
-#endif
         return;
     }
 
@@ -3701,10 +3632,6 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
     start_item();
     __syncthreads();   // (2)
     uint32_t c = 0;
-#ifdef NERVE_P2_TIMING
-    uint64_t cl = 0, cb = 0, ce = 0;
-    const uint64_t cstart = __builtin_amdgcn_s_memtime();
-#endif
     for (uint32_t t = 0; t < T; t++) {
         const uint32_t so = (t % NS) * SBY;
         const bool item_end = c + 1 == nch;
@@ -3728,13 +3655,7 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
             av[a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             asm volatile("ds_read_b32 %0, %1" : "=v"(sa[a]) : "v"(LS + so + (a0 + a) * 64));
         }
-#ifdef NERVE_P2_TIMING
-        const uint64_t r0 = __builtin_amdgcn_s_memtime();
-#endif
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#ifdef NERVE_P2_TIMING
-        cl += __builtin_amdgcn_s_memtime() - r0;
-#endif
 #pragma unroll
         for (uint32_t j = 0; j < (uint32_t)NJ; j++) asm volatile("" : "+v"(bw[j]), "+v"(sw[j]));
 #pragma unroll
@@ -3805,23 +3726,8 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
         } else {
             c++;
         }
-#ifdef NERVE_P2_TIMING
-        const uint64_t b0 = __builtin_amdgcn_s_memtime();
         __builtin_amdgcn_s_barrier();
-        cb += __builtin_amdgcn_s_memtime() - b0;
-#else
-        __builtin_amdgcn_s_barrier();
-#endif
     }
-#ifdef NERVE_P2_TIMING
-    if (lane == 0) {
-        constexpr uint32_t gi = NAT == 8 ? 0 : NAT == 4 ? 1 : 2;
-        atomicAdd(&g_probe[64 + gi * 16 + 5 + (wave == 0 ? 0 : 3)], (unsigned long long)cl);
-        atomicAdd(&g_probe[64 + gi * 16 + 6 + (wave == 0 ? 0 : 3)], (unsigned long long)cb);
-        atomicAdd(&g_probe[64 + gi * 16 + 7 + (wave == 0 ? 0 : 3)], (unsigned long long)(__builtin_amdgcn_s_memtime() - cstart));
-    }
-    (void)ce;
-#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -4158,28 +4064,13 @@ __global__ __launch_bounds__(768) void moe_pg2_kernel(PgArgs A) {
     const uint32_t nt = __builtin_amdgcn_readfirstlane(A.n_tiles[0]);
     const uint32_t nt0 = __builtin_amdgcn_readfirstlane(A.n_tiles[1]);
     const uint32_t nt1 = __builtin_amdgcn_readfirstlane(A.n_tiles[2]);
-#ifdef NERVE_PREP_PROBE
-#define P2P(i) do { __syncthreads(); if (threadIdx.x == 0) atomicMax(&g_probe[32 + 4 * NMAT + (i)], __builtin_amdgcn_s_memrealtime()); } while (0)
-    if (threadIdx.x == 0) atomicMin(&g_probe[8], __builtin_amdgcn_s_memrealtime());
-#else
-#define P2P(i) __syncthreads()
-#endif
     p2_range<NMAT, 8, 4, 4>(A, 0, nt0 * nrb);
-    P2P(0);
+    __syncthreads();
     // Tiles of 33-64 and of 1-32 routes: the whole-line form (the 128-route
     // tiles' activation slots would not fit its LDS ring).
-#ifdef NERVE_P2_NOWL
-    p2_range<NMAT, 4, 4, 2>(A, nt0 * nrb, (nt0 + nt1) * nrb);
-    P2P(1);
-    p2_range<NMAT, 2, 2, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
-#else
     p2_range_wl<NMAT, 4>(A, nt0 * nrb, (nt0 + nt1) * nrb);
-    P2P(1);
+    __syncthreads();
     p2_range_wl<NMAT, 2>(A, (nt0 + nt1) * nrb, nt * nrb);
-#endif
-#ifdef NERVE_PREP_PROBE
-    P2P(2);
-#endif
 }
 
 template <int NMAT>
@@ -4472,16 +4363,6 @@ static nerve_hip_status moe_tensor_parallel(const nh::MoeSpec& ms, bool gate_up,
 // C ABI
 // ---------------------------------------------------------------------------
 extern "C" {
-#ifdef NERVE_PREP_PROBE
-int nerve_probe_read(unsigned long long* out) {
-    hipDeviceSynchronize();
-    int r = (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_probe), sizeof(g_probe));
-    unsigned long long init[128] = {0};
-    init[8] = ~0ull;
-    hipMemcpyToSymbol(HIP_SYMBOL(g_probe), init, sizeof(init));
-    return r;
-}
-#endif
 
 nerve_hip_status nerve_hip_quantize_fp8_e4m3(nerve_hip_ctx* ctx, const char* spec, const void* x_bf16, uint32_t rows,
                                              void* q_e4m3, void* scales_f32, void* stream) {
@@ -4755,11 +4636,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     if (persistent) {
         // Producer / consumer form: the item's scale rows fit their LDS
         // slot and an item has enough chunks for the descriptor prefetch.
-#ifdef NERVE_PG1
-        const bool p2_ok = false;
-#else
         const bool p2_ok = K % 32 == 0 && K / 32 <= P2_MAX_SB && (K + P2_KC - 1) / P2_KC >= P2_MIN_CHUNKS;
-#endif
         PgArgs pa;
         pa.aq = aq;
         pa.as = as;

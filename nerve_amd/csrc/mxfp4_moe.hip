@@ -41,10 +41,11 @@ struct QuantArgs {
     uint64_t frame_elems;    // elements per frame
     uint64_t seg_elems;      // elements between rows of one frame
     uint32_t cols, rows;
-    uint8_t* q;              // e4m3 [rows, cols]
+    uint8_t* q;              // e4m3 [rows, ldq]: row r's cols bytes at r * ldq
     float* s;                // f32 [rows, ceil(cols/128)]
     uint32_t* zero_word;     // set to 0 by the standalone quantizer (a counter of the next kernel), or null
     uint32_t vec8 = 0;       // x rows, frames and q rows 16-byte aligned: quant_units8_pow2 may be used
+    uint32_t ldq = 0;        // q row stride in bytes, >= cols and a multiple of 4
 };
 
 // One 32-lane cluster quantizes one (row, 128-column block) unit.  All 32
@@ -71,7 +72,7 @@ __device__ __forceinline__ void quant_unit(const QuantArgs& Q, uint32_t unit, ui
     if (cl == 0) Q.s[(uint64_t)row * nblk + blk] = sc;
     const uint32_t packed = f32_to_e4m3(v[0] / sc) | (f32_to_e4m3(v[1] / sc) << 8) |
                             (f32_to_e4m3(v[2] / sc) << 16) | (f32_to_e4m3(v[3] / sc) << 24);
-    *reinterpret_cast<uint32_t*>(Q.q + (uint64_t)row * Q.cols + col) = packed;
+    *reinterpret_cast<uint32_t*>(Q.q + (uint64_t)row * Q.ldq + col) = packed;
 }
 
 // Power-of-two block quantization of QU units per 16-lane cluster with all
@@ -137,7 +138,7 @@ __device__ __forceinline__ void quant_units8_pow2(const QuantArgs& Q, uint64_t u
                        (f32_to_e4m3(v[4 * h + 2] / sc) << 16) | (f32_to_e4m3(v[4 * h + 3] / sc) << 24);
         }
         if (cl == 0) Q.s[(uint64_t)row[i] * nblk + blk[i]] = sc;
-        *reinterpret_cast<v2i*>(Q.q + (uint64_t)row[i] * Q.cols + blk[i] * 128 + cl * 8) = v2i{(int)p[0], (int)p[1]};
+        *reinterpret_cast<v2i*>(Q.q + (uint64_t)row[i] * Q.ldq + blk[i] * 128 + cl * 8) = v2i{(int)p[0], (int)p[1]};
     }
 }
 
@@ -2893,7 +2894,8 @@ constexpr uint32_t PG_MIN_CHUNKS = 7;
 __device__ __attribute__((aligned(16))) const uint8_t kZeroPage[1024] = {0};
 
 struct PgArgs {
-    const uint8_t* aq;          // e4m3 activations, row stride K
+    const uint8_t* aq;          // e4m3 activations, row stride lda
+    uint32_t lda;               // K, or K rounded up to 128 so every 128-k chunk of a row is one cache line
     const float* as;            // pow2 scales, row stride ceil(K / 128)
     uint32_t K, N, k;
     const ItemRec* items;
@@ -3015,7 +3017,7 @@ __device__ __forceinline__ void pg_range(const PgArgs& A, uint32_t i0, uint32_t 
             const uint32_t t = 32 * i + 4 * wave + (lane >> 4);
             const uint32_t p = (lane & 15) ^ (t & 15);
             const uint32_t row = lds_rd32_sync<512>(list + 4 * (t < count ? t : 0));
-            S.off[i] = row * K + p * 16;
+            S.off[i] = row * A.lda + p * 16;
             tail |= (last * PG_KC + p * 16 < K ? 1u : 0u) << i;
             on |= (32 * i + 4 * wave < count ? 1u : 0u) << i;
         }
@@ -3456,7 +3458,7 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
         uint32_t pitem = first, pord = 0, pc = 0;      // item being issued, its ordinal, next chunk
         PgItem it = p2_item(A.items + pitem);
         // per-lane source offsets of the current issue item
-        uint32_t woff[4], aoff[NAI], soff = 0;
+        uint32_t woff[4], aoff[NAI], apc[NAI], soff = 0;
         const uint8_t* wb = nullptr;
         auto setup = [&]() __attribute__((always_inline)) {
             // weights: subtiles x = 4 p .. 4 p + 3 (16 rows each), lane (piece i / 16, row i % 16)
@@ -3469,17 +3471,20 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
                 const uint32_t n = it.rb * RPM + irow % RPM;             // matrix row
                 woff[u] = (n < N ? n : 0u) * RB + g * 16;
             }
-            // activations: copy u = p * NAI + v covers route subtile y = u / 2,
-            // pieces 4 (u % 2) + i / 16; block scales: copy p < NAS covers
+            // activations: copy u = p * NAI + v covers the whole 128-byte
+            // chunk of routes 8 (u % 2) .. + 7 of route subtile y = u / 2,
+            // lane i route 8 (u % 2) + i / 8, slot i % 8 holding piece
+            // (i % 8) ^ (route / 2); block scales: copy p < NAS covers
             // routes 64 p + i.  List entries past the tile's count are not
             // written: their positions read entry 0.
             const uint32_t list = ring + P2_LIST_OFF + (pord & 1u) * (uint32_t)sizeof(PgList);
 #pragma unroll
             for (uint32_t v = 0; v < NAI; v++) {
-                const uint32_t u = p * NAI + v, y = u / 2, q = u % 2;
-                const uint32_t pos = 16 * y + rr < it.count ? 16 * y + rr : 0u;
+                const uint32_t u = p * NAI + v, y = u / 2, rt = 8 * (u % 2) + lane / 8;
+                const uint32_t pos = 16 * y + rt < it.count ? 16 * y + rt : 0u;
                 const uint32_t arow = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1);
-                aoff[v] = arow * K + (4 * q + g) * 16;
+                apc[v] = ((lane % 8) ^ (rt / 2)) * 16;
+                aoff[v] = arow * A.lda + apc[v];
             }
             if (p < NAS) {
                 const uint32_t pos = 64 * p + lane < it.count ? 64 * p + lane : 0u;
@@ -3521,8 +3526,7 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
             n += 4;
 #pragma unroll
             for (uint32_t v = 0; v < NAI; v++) {
-                const uint32_t q = (p * NAI + v) % 2;
-                const bool ok = !last || pc * P2_KC + (4 * q + g) * 16 < K;
+                const bool ok = !last || pc * P2_KC + apc[v] < K;
                 __builtin_amdgcn_global_load_lds(ok ? A.aq + pc * P2_KC + aoff[v] : kZeroPage,
                                                  st + P2_W_BYTES + (p * NAI + v) * 1024, 16, 0, 0);
             }
@@ -3613,7 +3617,10 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
     // scale of a chunk is in its ring stage or the item's scale-row slot.
     const uint32_t a0 = NJ == 4 ? 4 * (wave / 4) : 0u;   // first route subtile of this wave
     const uint32_t LW = ring + lane * 16;                  // + stage + subtile * 1 KB
-    const uint32_t LA = LW + P2_W_BYTES;                   // + stage + subtile * 2 KB (+ 1 KB: pieces 4-7)
+    // + stage + subtile * 2 KB: route rr's chunk at (rr / 8) KB + (rr % 8) * 128,
+    // piece x in slot x ^ (rr / 2); this lane reads pieces g and g + 4
+    const uint32_t LA = ring + P2_W_BYTES + (rr / 8) * 1024 + (rr % 8) * 128;
+    const uint32_t LAlo = LA + ((g ^ (rr / 2)) & 7) * 16, LAhi = LA + ((g ^ (rr / 2) ^ 4) & 7) * 16;
     const uint32_t LS = ring + P2_W_BYTES + NR * 128 + rr * 4;   // + stage + route subtile * 64
     uint32_t item = first, ord = 0;
     PgItem it = p2_item(A.items + item);
@@ -3648,10 +3655,10 @@ __device__ __forceinline__ void p2_range(const PgArgs& A, uint32_t i0, uint32_t 
 #pragma unroll
         for (uint32_t a = 0; a < (uint32_t)NAW; a++) {
             v4i lo, hi;
-            const uint32_t ad = LA + so + (a0 + a) * 2048;
+            const uint32_t ad = so + (a0 + a) * 2048;
             // early-clobber outputs: the second read must not find its address
             // register overwritten by the first read's data
-            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:1024" : "=&v"(lo), "=&v"(hi) : "v"(ad));
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3" : "=&v"(lo), "=&v"(hi) : "v"(LAlo + ad), "v"(LAhi + ad));
             av[a] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
             asm volatile("ds_read_b32 %0, %1" : "=v"(sa[a]) : "v"(LS + so + (a0 + a) * 64));
         }
@@ -3801,7 +3808,7 @@ __device__ __forceinline__ void p2_range_wl(const PgArgs& A, uint32_t i0, uint32
             for (uint32_t v = 0; v < NAI; v++) {
                 const uint32_t route = 4 * (p * NAI + v) + (lane >> 4);
                 const uint32_t pos = route < it.count ? route : 0u;
-                aoff[v] = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1) * K;
+                aoff[v] = min(p2_lds32(list + 512 + 4 * pos), A.a_rows - 1) * A.lda;
             }
             if (p < NAS) {
                 const uint32_t route = 32 * p + (lane >> 1);
@@ -4121,6 +4128,7 @@ QuantArgs plain_rows(const uint16_t* x, uint32_t cols, uint32_t rows, uint8_t* q
     Q.q = q;
     Q.s = s;
     Q.zero_word = nullptr;
+    Q.ldq = cols;
     return Q;
 }
 
@@ -4462,8 +4470,13 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
                             (pg_tail * (K / 32)) % 4 == 0 && (pg_tail == 0 || pg_tail * (K / 32) >= 256);
     const uint32_t TM = persistent ? PG_TM : grouped ? 64 : 16;
     const uint32_t max_tiles = (cap + TM - 1) / TM + (E < cap ? E : cap);
+    // The persistent GEMM copies activations in 128-byte row pieces: rows it
+    // quantizes itself start on 128-byte boundaries (prequantized rows keep
+    // the caller's stride K).
+    const bool own_q = !(gate_up && ms.prequant);
+    const uint32_t lda = persistent && own_q ? (K + 127) / 128 * 128 : K;
     nh::Carver cv;
-    size_t o_aq = cv.take<uint8_t>((size_t)arows * K);
+    size_t o_aq = cv.take<uint8_t>((size_t)arows * lda);
     size_t o_as = cv.take<float>((size_t)arows * nblk);
     size_t o_seg = cv.take<uint32_t>(cap + 16);   // +16: the streaming kernel reads 16 entries at once
     size_t o_rec = cv.take<TileRec>(max_tiles);
@@ -4488,6 +4501,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     Q.zero_word = nullptr;
     if (gate_up) {
         Q = plain_rows(static_cast<const uint16_t*>(act_bf16), H, batch_width, aq, as);
+        Q.ldq = lda;
         if (ms.prequant) {
             aq = const_cast<uint8_t*>(static_cast<const uint8_t*>(pre_q));
             as = const_cast<float*>(static_cast<const float*>(pre_s));
@@ -4502,6 +4516,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         Q.rows = cap;
         Q.q = aq;
         Q.s = as;
+        Q.ldq = lda;
     }
     TileArgs ta;
     ta.frames = static_cast<const uint32_t*>(intermediates);
@@ -4582,7 +4597,8 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
     {
         // Block 0 builds the tiles; the others stride over the quantization
         // units (a few per CU keep the loads in flight).
-        Q.vec8 = ((((uintptr_t)Q.x | (uintptr_t)Q.q) & 15) == 0 && Q.cols % 8 == 0 && Q.frame_elems % 8 == 0 &&
+        Q.vec8 = ((((uintptr_t)Q.x | (uintptr_t)Q.q) & 15) == 0 && Q.cols % 8 == 0 && Q.ldq % 8 == 0 &&
+                  Q.frame_elems % 8 == 0 &&
                   Q.seg_elems % 8 == 0 && Q.rows > 0) ? 1u : 0u;
         const uint32_t per_pass = Q.vec8 ? 64 * PREP_QU : 32;
         const uint32_t qblocks =
@@ -4639,6 +4655,7 @@ static nerve_hip_status moe_common(nerve_hip_ctx* ctx, const nh::MoeSpec& ms, bo
         const bool p2_ok = K % 32 == 0 && K / 32 <= P2_MAX_SB && (K + P2_KC - 1) / P2_KC >= P2_MIN_CHUNKS;
         PgArgs pa;
         pa.aq = aq;
+        pa.lda = lda;
         pa.as = as;
         pa.a_rows = arows;
         pa.routes = cap;

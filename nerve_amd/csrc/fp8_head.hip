@@ -571,6 +571,9 @@ struct HeadGemmArgs {
     const uint8_t* nonuni;        // u8 [nvt * TN]: 1 = the row's scale varies along K
     uint32_t M, Mpad, K, N, BR, nblk;
     uint32_t ntt, n_items, nvt;
+    // Item i covers vocabulary rows row0 + (i / ntt) TN ..; its argmax
+    // partial is column part0 + i / ntt of the nvt per token.
+    uint32_t row0, part0;
     float out_scale;
     float* logits_f32;            // [M, N] or null
     uint16_t* logits_bf16;        // [M, N] or null
@@ -658,7 +661,7 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
     bool issuing = true;
     auto setup_issue = [&]() __attribute__((always_inline)) {
         i_t0 = (i_item % A.ntt) * TM;
-        i_n0 = (i_item / A.ntt) * TN;
+        i_n0 = A.row0 + (i_item / A.ntt) * TN;
     };
     auto issue_chunk = [&](uint32_t ST) __attribute__((always_inline)) {
         uint8_t* const dA = hg_lds + ST * L::STAGE + wi * ACI * 1024;
@@ -735,7 +738,7 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
             // The tile's scale block, transposed to [chunk][row] bf16.  Plain
             // loads: the compiler drains the copies in flight before their use
             // (a pipeline bubble on this form only).
-            const uint32_t n0 = (c_item / A.ntt) * TN;
+            const uint32_t n0 = A.row0 + (c_item / A.ntt) * TN;
             for (uint32_t e = tid; e < nblk * TN; e += 64 * NW) {
                 const uint32_t ch = e / TN, R = e % TN, n = n0 + R < N ? n0 + R : N - 1;
                 const uint32_t v = A.scale_inv[(uint64_t)(n / A.BR) * nblk + ch];
@@ -809,7 +812,7 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
                     // MFMA number m = t NJ + j writes ring slot m % (NJ + 1); the
                     // accumulate reads the slot of MFMA m - NJ.
                     const uint32_t m = t * NJ + j, wslot = m % (NJ + 1), rslot = (m + 1) % (NJ + 1);
-                    if constexpr (!general && t >= 1) {
+                    if constexpr (!general && NJ >= 2 && t >= 1) {
                         v4f& a4 = acc[t - 1][j];
                         const v4f po = pring[rslot];
                         asm volatile(
@@ -822,10 +825,17 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
                             : "v"(bw), "v"(bt), "v"(unit), "v"(po[0]), "v"(po[1]), "v"(po[2]), "v"(po[3]),
                               "v"(sxp[cur ^ 1u])
                             : );
-                    } else if constexpr (!general) {
+                    } else if constexpr (!general && NJ >= 2) {
                         asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0]"
                                      : "=&v"(pring[wslot])
                                      : "v"(bw), "v"(bt), "v"(unit));
+                    } else if constexpr (!general) {
+                        // NJ = 1: no second MFMA to cover the first one's
+                        // latency; the compiler places the wait states.
+                        const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bw, bt, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                                       0, 0, 0, 127, 0, 127);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[t][j][i] = fmaf(p[i], sxp[cur], acc[t][j][i]);
                     } else {
                         // general form (tiles with rows whose scale varies along
                         // K): accumulate each result right away, which keeps
@@ -841,7 +851,7 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
                     }
                 }
             }
-            if constexpr (!general && t == (uint32_t)TT) {
+            if constexpr (!general && NJ >= 2 && t == (uint32_t)TT) {
                 // The last tile's accumulate: its MFMAs were the last issued, so
                 // wait out their latency first (inline-asm results get no
                 // compiler-inserted wait states).
@@ -870,7 +880,7 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
     // row segments, 16 bytes per lane, and the scale-block region carries
     // the argmax exchange between the WN waves of a token range.
     auto epilogue = [&](uint32_t ST) __attribute__((always_inline)) {
-        const uint32_t vt = c_item / A.ntt, t0 = (c_item % A.ntt) * TM, n0 = vt * TN;
+        const uint32_t vt = A.part0 + c_item / A.ntt, t0 = (c_item % A.ntt) * TM, n0 = A.row0 + (c_item / A.ntt) * TN;
         const uint32_t nw0 = n0 + wn * 16 * NJ;                  // first vocabulary row of this wave
         if (!general) {
             v4i r[NJ];
@@ -950,8 +960,10 @@ __device__ __forceinline__ void fp8_head_gemm_body(const HeadGemmArgs& A) {
         const bool full = nw0 + 16 * NJ <= N;
         const uint32_t sbase = ring + ST * L::STAGE + wave * 16 * L::F32_STRIDE;
         if (A.logits_bf16) {
-            if (full && (N & 7u) == 0) {
-                constexpr uint32_t LPR = 2 * NJ, RPR = 64 / LPR;     // lanes per row, rows per read
+            // (NJ = 1: two lanes per row would need 32 rows per read; the
+            // register path stores those slices)
+            if (full && (N & 7u) == 0 && NJ >= 2) {
+                constexpr uint32_t LPR = 2 * NJ, RPR = NJ >= 2 ? 64 / LPR : 16;   // lanes per row, rows per read
 #pragma unroll
                 for (uint32_t t = 0; t < (uint32_t)TT; t++) {
 #pragma unroll
@@ -1145,10 +1157,10 @@ __global__ __launch_bounds__(64 * (WM * WN + NPW), 1) void fp8_head_gemm_kernel(
 // contiguous copies: q[chunk][row][128 B] with 16-byte piece p of row r at
 // piece p ^ f(r), s[chunk][row]; rows M .. Mpad are zeros.  One 32-lane
 // cluster per (row, chunk), 4 columns per lane.
-__global__ __launch_bounds__(256) void head_quant_kernel(const uint16_t* __restrict__ x, uint32_t M, uint32_t Mpad,
-                                                         uint32_t K, uint8_t* __restrict__ q, float* __restrict__ s) {
+__device__ __forceinline__ void head_quant_body(uint32_t bid, const uint16_t* __restrict__ x, uint32_t M, uint32_t Mpad,
+                                                uint32_t K, uint8_t* __restrict__ q, float* __restrict__ s) {
     const uint32_t nblk = (K + 127) / 128;
-    const uint32_t unit = blockIdx.x * 8 + (threadIdx.x >> 5), cl = threadIdx.x & 31;
+    const uint32_t unit = bid * 8 + (threadIdx.x >> 5), cl = threadIdx.x & 31;
     const uint32_t row = unit / nblk, blk = unit % nblk;
     if (row >= Mpad) return;                     // uniform per cluster
     const uint32_t col = blk * 128 + cl * 4;
@@ -1176,11 +1188,11 @@ __global__ __launch_bounds__(256) void head_quant_kernel(const uint16_t* __restr
 // varies across the K blocks (rows of the last tile past N: flag 0).  A block
 // covers 256 rows; their scale rows are one contiguous span, read coalesced
 // into LDS and checked there (nblk <= 32).
-__global__ __launch_bounds__(256) void head_scale_scan_kernel(const uint16_t* __restrict__ scale_inv, uint32_t N,
-                                                              uint32_t rows_pad, uint32_t BR, uint32_t nblk,
-                                                              float* __restrict__ sw_row, uint8_t* __restrict__ nonuni) {
+__device__ __forceinline__ void head_scale_scan_body(uint32_t bid, const uint16_t* __restrict__ scale_inv, uint32_t N,
+                                                     uint32_t rows_pad, uint32_t BR, uint32_t nblk,
+                                                     float* __restrict__ sw_row, uint8_t* __restrict__ nonuni) {
     __shared__ __attribute__((aligned(16))) uint16_t sh[256 * 32];
-    const uint32_t n0 = blockIdx.x * 256, tid = threadIdx.x;
+    const uint32_t n0 = bid * 256, tid = threadIdx.x;
     if (n0 >= N) {
         if (n0 + tid < rows_pad) nonuni[n0 + tid] = 0;
         return;
@@ -1212,6 +1224,18 @@ __global__ __launch_bounds__(256) void head_scale_scan_kernel(const uint16_t* __
     for (uint32_t c = 1; c < nblk; c++) diff |= row[c] ^ s0;
     sw_row[n] = bf16_to_f32(s0);
     nonuni[n] = diff ? 1 : 0;
+}
+
+// The GEMM form's two preparation passes in one launch: blocks < qblocks
+// quantize the token rows (head_quant_body), the others scan the vocabulary
+// rows' scales (head_scale_scan_body).
+__global__ __launch_bounds__(256) void head_prep_kernel(const uint16_t* __restrict__ x, uint32_t M, uint32_t Mpad,
+                                                        uint32_t K, uint8_t* __restrict__ q, float* __restrict__ s,
+                                                        uint32_t qblocks, const uint16_t* __restrict__ scale_inv,
+                                                        uint32_t N, uint32_t rows_pad, uint32_t BR,
+                                                        float* __restrict__ sw_row, uint8_t* __restrict__ nonuni) {
+    if (blockIdx.x < qblocks) head_quant_body(blockIdx.x, x, M, Mpad, K, q, s);
+    else head_scale_scan_body(blockIdx.x - qblocks, scale_inv, N, rows_pad, BR, (K + 127) / 128, sw_row, nonuni);
 }
 
 // Second pass: one block per row over the partials (argmax_candidate_reduce.
@@ -1298,6 +1322,7 @@ nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid,
     constexpr int NPW = 4;
     if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 4, 3, NPW>(G, grid, st);
     if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4, NPW>(G, grid, st);
+    if (cfg == 3) return launch_head_gemm_t<2, 4, 2, 1, 3, NPW>(G, grid, st);   // cfg 0's tail: 64-row tiles
     return launch_head_gemm_t<4, 2, 4, 4, 3, 0>(G, grid, st);
 }
 
@@ -1355,7 +1380,14 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
     const uint32_t hg_nvt = (N + hg_tn - 1) / hg_tn, hg_ntt = (M + hg_tm - 1) / hg_tm;
     const uint32_t hg_items = hg_nvt * hg_ntt;
     const uint32_t hg_grid = std::min<uint32_t>(hg_items, (uint32_t)ctx->cu_count);
-    const uint32_t nparts = stream_form ? hs_grid : skinny ? sk_grid : gemm_form ? hg_nvt : nblocks;
+    // 64-token tiles: when the 256-row tiles leave a last round for a few
+    // blocks, those rows go to 64-row tiles instead (a second launch).
+    const uint32_t cu = (uint32_t)ctx->cu_count;
+    const uint32_t hg_main = hg_nvt / cu * cu;
+    const bool hg_tail = gemm_form && hg_cfg == 0 && hg_ntt == 1 && hg_main > 0 && hg_main < hg_nvt &&
+                         (hg_nvt - hg_main) * 4 <= cu;
+    const uint32_t hg_nparts = hg_tail ? hg_main + (N - hg_main * hg_tn + 63) / 64 : hg_nvt;
+    const uint32_t nparts = stream_form ? hs_grid : skinny ? sk_grid : gemm_form ? hg_nparts : nblocks;
     nh::Carver cv;
     // The GEMM form reads whole token tiles: rows up to the padded count.
     const size_t m_rows = gemm_form ? (size_t)hg_ntt * hg_tm : M;
@@ -1380,11 +1412,16 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
     A.xq = base + o_q;
     A.xs = reinterpret_cast<float*>(base + o_s);
     if (gemm_form) {
-        // chunk-major, swizzled token rows padded to whole tiles
+        // chunk-major, swizzled token rows padded to whole tiles, and the
+        // vocabulary rows' scale scan, in one launch
         const uint32_t mpad = hg_ntt * hg_tm;
-        head_quant_kernel<<<(uint32_t)(((uint64_t)mpad * nblk + 7) / 8), 256, 0, strm>>>(
-            static_cast<const uint16_t*>(x_bf16), M, mpad, K, const_cast<uint8_t*>(A.xq), const_cast<float*>(A.xs));
-        if ((st = nh::check_launch("head_quant"))) return st;
+        const uint32_t qblocks = (uint32_t)(((uint64_t)mpad * nblk + 7) / 8);
+        const uint32_t rows_pad = hg_nvt * hg_tn;
+        head_prep_kernel<<<qblocks + (rows_pad + 255) / 256, 256, 0, strm>>>(
+            static_cast<const uint16_t*>(x_bf16), M, mpad, K, const_cast<uint8_t*>(A.xq), const_cast<float*>(A.xs),
+            qblocks, static_cast<const uint16_t*>(scale_inv_bf16), N, rows_pad, s.block_rows,
+            reinterpret_cast<float*>(base + o_swr), base + o_nu);
+        if ((st = nh::check_launch("head_prep"))) return st;
     } else if ((st = nh::quantize_rows(static_cast<const uint16_t*>(x_bf16), K, M, false, const_cast<uint8_t*>(A.xq),
                                        const_cast<float*>(A.xs), strm))) {
         return st;
@@ -1441,17 +1478,29 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
         G.ntt = hg_ntt;
         G.n_items = hg_items;
         G.nvt = hg_nvt;
+        G.row0 = 0;
+        G.part0 = 0;
         G.out_scale = s.output_scale;
         G.logits_f32 = A.logits_f32;
         G.logits_bf16 = A.logits_bf16;
         G.part_val = A.part_val;
         G.part_idx = A.part_idx;
         A.nblocks = hg_nvt;
-        const uint32_t rows_pad = hg_nvt * hg_tn;
-        head_scale_scan_kernel<<<(rows_pad + 255) / 256, 256, 0, strm>>>(
-            A.scale_inv, N, rows_pad, s.block_rows, nblk, reinterpret_cast<float*>(base + o_swr), base + o_nu);
-        if ((st = nh::check_launch("head_scale_scan"))) return st;
-        if ((st = launch_head_gemm(hg_cfg, G, hg_grid, strm))) return st;
+        if (hg_tail) {
+            // Whole rounds of 256-row tiles, then the rest of the vocabulary
+            // in 64-row tiles over as many blocks (a last round of a few
+            // 256-row tiles would hold up the launch for a whole tile).
+            G.n_items = hg_main * hg_ntt;
+            G.nvt = hg_nparts;
+            if ((st = launch_head_gemm(0, G, std::min<uint32_t>(G.n_items, (uint32_t)ctx->cu_count), strm))) return st;
+            G.row0 = hg_main * hg_tn;
+            G.part0 = hg_main;
+            G.n_items = (hg_nparts - hg_main) * hg_ntt;
+            if ((st = launch_head_gemm(3, G, std::min<uint32_t>(G.n_items, (uint32_t)ctx->cu_count), strm))) return st;
+            A.nblocks = hg_nparts;
+        } else if ((st = launch_head_gemm(hg_cfg, G, hg_grid, strm))) {
+            return st;
+        }
     } else {
         dim3 grid(nblocks, (M + 16 * HEAD_MT - 1) / (16 * HEAD_MT));
         fp8_head_kernel<<<grid, 64 * HEAD_WAVES, 0, strm>>>(A);

@@ -264,13 +264,14 @@ __device__ void topk_token_fast(const uint16_t* lg, const void* bias, uint32_t* 
     if (!valid) return;
     if (chosen || (lane == 0 && nsel < k)) {
         // Position in ascending expert order (the reference's insertion
-        // sort); missing selections are expert 0 and sort first.
-        const uint32_t pos0 = chosen ? (uint32_t)__popcll(chosen_mask & ((1ull << lane) - 1ull)) + (k - nsel) : 0u;
-        const uint32_t copies = chosen ? 1u : k - nsel;
+        // sort); missing selections are expert 0 and sort first, before
+        // expert 0's own selection.
         float w = sig ? sigmoidf_(raw) : expf(raw - maximum);
         if (P.normalize || !sig) w /= den;
         const uint32_t word = (f32_to_bf16(w) << 16) | lane;
-        for (uint32_t c = 0; c < copies; c++) routes[(uint64_t)b * k + pos0 + c] = word;
+        if (lane == 0)
+            for (uint32_t c = 0; c < k - nsel; c++) routes[(uint64_t)b * k + c] = word;
+        if (chosen) routes[(uint64_t)b * k + (uint32_t)__popcll(chosen_mask & ((1ull << lane) - 1ull)) + (k - nsel)] = word;
     }
     if (!telemetry) return;
     auto count = [&](uint32_t i) {
@@ -365,12 +366,13 @@ __device__ void topk_pair32(const uint16_t* lg, uint32_t stride, const void* bia
     const uint32_t nsel = (uint32_t)__popc(hm);
     if (!valid) return;
     if (chosen || (e == 0 && nsel < k)) {
-        const uint32_t pos0 = chosen ? (uint32_t)__popc(hm & ((1u << e) - 1u)) + (k - nsel) : 0u;
-        const uint32_t copies = chosen ? 1u : k - nsel;
+        // missing selections (expert 0) first, then the selected experts
         float w = sig ? sigmoidf_(raw) : expf(raw - maximum);
         if (P.normalize || !sig) w /= den;
         const uint32_t word = (f32_to_bf16(w) << 16) | e;
-        for (uint32_t c = 0; c < copies; c++) routes[(uint64_t)b * k + pos0 + c] = word;
+        if (e == 0)
+            for (uint32_t c = 0; c < k - nsel; c++) routes[(uint64_t)b * k + c] = word;
+        if (chosen) routes[(uint64_t)b * k + (uint32_t)__popc(hm & ((1u << e) - 1u)) + (k - nsel)] = word;
     }
     if (!telemetry) return;
     auto count = [&](uint32_t i) {

@@ -249,3 +249,46 @@ def test_route_fused_declines_large_batches(ctx, dev):
     w = torch.zeros(E, H, dtype=torch.int16, device=dev)
     assert not ctx.moe_route_fused(topk_spec(E, k), gate_up_spec(H, 64, E, k, 7.0), x, w, None, None, routes, None,
                                    None, control, B)
+
+
+@pytest.mark.parametrize("E", [32, 100])
+def test_topk_fewer_selectable_than_k(ctx, dev, E):
+    """A row with only two non-NaN logits (experts 0 and 5) and k = 4: the
+    rounds that find nothing select expert 0, which sorts first, so the
+    route list is 0, 0, 0, 5 with expert 0's weight three times; expert 0 is
+    counted three times and the pair (0, 5) three times.  E = 32 takes the
+    lane-parallel form, E = 100 the round-by-round one: both must agree."""
+    torch = _torch()
+    k = 4
+    lg = np.full((1, E), 0x7FC0, np.uint16)            # bf16 NaN
+    lg[0, 0] = wl.f32_to_bf16_bits(np.float32(1.0))
+    lg[0, 5] = wl.f32_to_bf16_bits(np.float32(2.0))
+    T = E + E * (E - 1) // 2
+    routes = torch.full((1, k), -1, dtype=torch.int32, device=dev)
+    tel = torch.zeros(T, dtype=torch.int32, device=dev)
+    ctx.moe_router_topk(topk_spec(E, k), to_dev(lg, dev), None, routes, tel, 1)
+    got = to_np(routes, np.uint32)[0]
+    assert list(got & 0xFFFF) == [0, 0, 0, 5]
+    e1 = np.exp(np.float32(-1.0))
+    den = np.float32(1.0) + e1 + e1 + e1
+    w = wl.bf16_bits_to_f32((got >> 16).astype(np.uint16))
+    assert np.allclose(w, [e1 / den, e1 / den, e1 / den, 1.0 / den], rtol=1e-2)
+    assert len(set(got[:3].tolist())) == 1
+    t = to_np(tel, np.uint32)
+    assert t[0] == 3 and t[5] == 1 and t[E + 5 - 1] == 3 and t.sum() == 7
+    if E == 32:
+        # the same row through the fused decode routing (two tokens per wave)
+        H, I = 64, 64
+        x = np.zeros((1, H), np.uint16)
+        w = np.zeros((E, H), np.uint16)
+        x[0, 0] = wl.f32_to_bf16_bits(np.float32(1.0))
+        w[:, 0] = lg[0]                                   # logit e = 1 * w[e, 0]
+        frame_words = k * I // 2 + k
+        r2 = torch.full((1, k), -1, dtype=torch.int32, device=dev)
+        t2 = torch.zeros(T, dtype=torch.int32, device=dev)
+        inter = torch.zeros(frame_words, dtype=torch.int32, device=dev)
+        control = to_dev(np.array([1, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev)
+        assert ctx.moe_route_fused(topk_spec(E, k), gate_up_spec(H, I, E, k, 7.0), to_dev(x, dev), to_dev(w, dev),
+                                   None, None, r2, t2, inter, control, 1)
+        assert np.array_equal(to_np(r2, np.uint32)[0], got)
+        assert np.array_equal(to_np(t2, np.uint32), t)

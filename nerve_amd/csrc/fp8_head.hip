@@ -1307,12 +1307,16 @@ nerve_hip_status launch_head_gemm_t(const HeadGemmArgs& G, uint32_t grid, hipStr
     return nh::check_launch("fp8_head_gemm_kernel");
 }
 
-// Tiled-form configurations: token tiles of 64 / 128 / 256 rows, 128
-// vocabulary rows per tile, 8 waves.
+// Tiled-form configurations: token tiles of 64 / 128 / 256 rows with 256 /
+// 128 / 128 vocabulary rows per tile, 8 contracting waves; and the tail
+// configurations that take the rows past the last whole round of each
+// (64 x 64, 128 x 64, 128 x 128 tiles: configurations 3, 4 and 1).
 struct HgConfig {
     uint32_t tm, tn, ns;
 };
 constexpr HgConfig kHgConfigs[3] = {{64, 256, 3}, {128, 128, 4}, {256, 128, 3}};
+constexpr HgConfig kHgTail[3] = {{64, 64, 3}, {128, 64, 4}, {128, 128, 4}};
+constexpr int kHgTailCfg[3] = {3, 4, 1};
 
 nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid, hipStream_t st) {
     // 64- and 128-token tiles: four copy waves beside the 8 contracting
@@ -1322,7 +1326,8 @@ nerve_hip_status launch_head_gemm(int cfg, const HeadGemmArgs& G, uint32_t grid,
     constexpr int NPW = 4;
     if (cfg == 0) return launch_head_gemm_t<2, 4, 2, 4, 3, NPW>(G, grid, st);
     if (cfg == 1) return launch_head_gemm_t<2, 4, 4, 2, 4, NPW>(G, grid, st);
-    if (cfg == 3) return launch_head_gemm_t<2, 4, 2, 1, 3, NPW>(G, grid, st);   // cfg 0's tail: 64-row tiles
+    if (cfg == 3) return launch_head_gemm_t<2, 4, 2, 1, 3, NPW>(G, grid, st);   // cfg 0's tail: 64 x 64
+    if (cfg == 4) return launch_head_gemm_t<2, 4, 4, 1, 4, NPW>(G, grid, st);   // cfg 1's tail: 128 x 64
     return launch_head_gemm_t<4, 2, 4, 4, 3, 0>(G, grid, st);
 }
 
@@ -1380,13 +1385,18 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
     const uint32_t hg_nvt = (N + hg_tn - 1) / hg_tn, hg_ntt = (M + hg_tm - 1) / hg_tm;
     const uint32_t hg_items = hg_nvt * hg_ntt;
     const uint32_t hg_grid = std::min<uint32_t>(hg_items, (uint32_t)ctx->cu_count);
-    // 64-token tiles: when the 256-row tiles leave a last round for a few
-    // blocks, those rows go to 64-row tiles instead (a second launch).
+    // When the items leave a last round for a few blocks, the main launch
+    // takes the vocabulary tiles of the whole rounds and a second launch the
+    // remaining rows in smaller tiles, one round over more blocks.
     const uint32_t cu = (uint32_t)ctx->cu_count;
-    const uint32_t hg_main = hg_nvt / cu * cu;
-    const bool hg_tail = gemm_form && hg_cfg == 0 && hg_ntt == 1 && hg_main > 0 && hg_main < hg_nvt &&
-                         (hg_nvt - hg_main) * 4 <= cu;
-    const uint32_t hg_nparts = hg_tail ? hg_main + (N - hg_main * hg_tn + 63) / 64 : hg_nvt;
+    const HgConfig hg_tc = kHgTail[hg_cfg];
+    const uint32_t hg_mpad = hg_ntt * hg_tm;
+    const uint32_t hg_main = hg_items / cu * cu / hg_ntt;        // vocabulary tiles of the whole rounds
+    const uint32_t hg_tail_rows = N > hg_main * hg_tn ? N - hg_main * hg_tn : 0u;
+    const uint32_t hg_tail_vt = (hg_tail_rows + hg_tc.tn - 1) / hg_tc.tn, hg_tail_ntt = hg_mpad / hg_tc.tm;
+    const bool hg_tail = gemm_form && hg_main > 0 && hg_tail_vt > 0 && hg_mpad % hg_tc.tm == 0 &&
+                         hg_tail_vt * hg_tail_ntt <= cu && nblk >= hg_tc.ns;
+    const uint32_t hg_nparts = hg_tail ? hg_main + hg_tail_vt : hg_nvt;
     const uint32_t nparts = stream_form ? hs_grid : skinny ? sk_grid : gemm_form ? hg_nparts : nblocks;
     nh::Carver cv;
     // The GEMM form reads whole token tiles: rows up to the padded count.
@@ -1487,16 +1497,17 @@ nerve_hip_status fp8_projection(nerve_hip_ctx* ctx, const char* spec, const void
         G.part_idx = A.part_idx;
         A.nblocks = hg_nvt;
         if (hg_tail) {
-            // Whole rounds of 256-row tiles, then the rest of the vocabulary
-            // in 64-row tiles over as many blocks (a last round of a few
-            // 256-row tiles would hold up the launch for a whole tile).
+            // Whole rounds of tiles, then the rest of the vocabulary in
+            // smaller tiles over more blocks (a last round of a few whole
+            // tiles would hold up the launch for a whole tile).
             G.n_items = hg_main * hg_ntt;
             G.nvt = hg_nparts;
-            if ((st = launch_head_gemm(0, G, std::min<uint32_t>(G.n_items, (uint32_t)ctx->cu_count), strm))) return st;
+            if ((st = launch_head_gemm(hg_cfg, G, std::min<uint32_t>(G.n_items, cu), strm))) return st;
             G.row0 = hg_main * hg_tn;
             G.part0 = hg_main;
-            G.n_items = (hg_nparts - hg_main) * hg_ntt;
-            if ((st = launch_head_gemm(3, G, std::min<uint32_t>(G.n_items, (uint32_t)ctx->cu_count), strm))) return st;
+            G.ntt = hg_tail_ntt;
+            G.n_items = hg_tail_vt * hg_tail_ntt;
+            if ((st = launch_head_gemm(kHgTailCfg[hg_cfg], G, std::min<uint32_t>(G.n_items, cu), strm))) return st;
             A.nblocks = hg_nparts;
         } else if ((st = launch_head_gemm(hg_cfg, G, hg_grid, strm))) {
             return st;

@@ -145,9 +145,9 @@ def _argmax_ok(ids, ref_logits, tol):
 # GEMM (token tiles of 64 / 128 / 256 rows;
 # partial token and vocabulary tiles, N % 4 != 0, the 64-column K tail,
 # K = 4096) or, with fewer K chunks than its ring has stages, the register
-# form; K > 4096 takes the tiled fallback (fp8_head_kernel).  With 64-token
-# tiles and more 256-row vocabulary tiles than whole rounds over the CUs,
-# the rows past the last whole round take 64-row tiles in a second launch.
+# form; K > 4096 takes the tiled fallback (fp8_head_kernel).  When the
+# GEMM's items leave a part of a round, the rows past the last whole round
+# take smaller tiles in a second launch.
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 256), (7, 4096, 2880), (64, 2048, 512), (130, 600, 384),
                                    (16, 2000, 4096), (2, 777, 64), (5, 1001, 384), (3, 30010, 2880),
                                    (20, 1000, 2880), (64, 4099, 640), (100, 777, 1024), (128, 3000, 2880),
@@ -158,7 +158,10 @@ def _argmax_ok(ids, ref_logits, tol):
                                    (5, 1000, 5120), (70, 1500, 5120),
                                    # 64-token tiles past one round of 256-row tiles per CU: the
                                    # rest in 64-row tiles (a partial last one; exactly one)
-                                   (40, 66000, 384), (64, 65600, 256)])
+                                   (40, 66000, 384), (64, 65600, 256),
+                                   # the same for 128-token tiles (tail in 128 x 64 tiles) and
+                                   # 256-token tiles (tail in 128 x 128 tiles, 4 token tiles)
+                                   (100, 33000, 384), (300, 16500, 640)])
 def test_fp8_head_parity(ctx, dev, M, N, K):
     rng = np.random.default_rng(M * N + K)
     d = wl.fp8_head(rng, N, K, M)

@@ -64,6 +64,51 @@ __device__ __forceinline__ float amax_fp8_scale(float block_max) {
 // e8m0 byte of a power-of-two f32 scale (its biased exponent field).
 __device__ __forceinline__ uint32_t pow2_to_e8m0(float s) { return (__float_as_uint(s) >> 23) & 0xffu; }
 
+// Lane sums over aligned groups of lanes without the LDS-routed shuffles:
+// DPP row operations within 16-lane rows and the gfx950 row swaps across
+// rows.  At every step the partner lane holds the value the __shfl_xor
+// butterfly would pair (an xor partner, or one holding the same value once
+// the previous steps made the smaller groups uniform), and each lane adds
+// own + partner, so the results are those of that butterfly bit for bit.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum_xor16(float v) {   // v + v of lane ^ 16
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {   // v + v of lane ^ 32
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The butterfly with partners lane ^ 1, ^ 2, ..., ^ (L / 2) (L = 2 .. 32).
+template <uint32_t L>
+__device__ __forceinline__ float lanes_sum_up(float v) {
+    if constexpr (L >= 2) v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (L >= 4) v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (L >= 8) v += dpp_f32<0x141>(v);   // row_half_mirror: the other quad of the 8
+    if constexpr (L >= 16) v += dpp_f32<0x140>(v);  // row_mirror: the other 8 of the row
+    if constexpr (L >= 32) v = sum_xor16(v);
+    return v;
+}
+// The butterfly with partners lane ^ (L / 2), ..., ^ 2, ^ 1 (L = 16, 32, 64).
+template <uint32_t L>
+__device__ __forceinline__ float lanes_sum_down(float v) {
+    static_assert(L == 16 || L == 32 || L == 64, "lane group");
+    if constexpr (L >= 64) v = sum_xor32(v);
+    if constexpr (L >= 32) v = sum_xor16(v);
+    v += dpp_f32<0x128>(v);   // row_ror:8 = lane ^ 8
+    v += dpp_f32<0x124>(v);   // row_ror:4 (pairs {i, i ^ 8} uniform)
+    v += dpp_f32<0x122>(v);   // row_ror:2
+    v += dpp_f32<0x121>(v);   // row_ror:1
+    return v;
+}
+// Lane `src` (a compile-time or uniform index) to every lane.
+__device__ __forceinline__ float lane_bcast(float v, uint32_t src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
 __device__ __forceinline__ float wave_max32(float v) {
     // Reduction inside each 32-lane half of the wave (subgroupClusteredMax(v, 32)).
     v = fmaxf(v, __shfl_xor(v, 16));

@@ -361,10 +361,9 @@ __global__ __launch_bounds__(64 * KS) void int4_gptq_gemv_kernel(Int4Args A) {
         for (uint32_t t = 0; t < MT; t++) {
             if (lane < GEMV_ROWS) xw[wave][t][lr] = permute_act(xl[t]);
             float v = sum8_bf16(xl[t]);
+            v = lanes_sum_up<GR>(v);   // the __shfl_xor butterfly 1, 2, ..., GR / 2
 #pragma unroll
-            for (uint32_t d = 1; d < GR; d <<= 1) v += __shfl_xor(v, d);
-#pragma unroll
-            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = __shfl(v, gb * GR);
+            for (uint32_t gb = 0; gb < GPB; gb++) gsum[t][gb] = lane_bcast(v, gb * GR);
         }
         __builtin_amdgcn_wave_barrier();
         // MFMA j of step i contracts packed rows 4 i .. 4 i + 3 (k-slice q)

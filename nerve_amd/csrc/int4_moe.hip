@@ -232,8 +232,7 @@ __global__ __launch_bounds__(64 * SM_WAVES) void sparse_int4_kernel(SmArgs A) {
     // Row sums across the LU lanes of each row.
 #pragma unroll
     for (uint32_t j = 0; j < RPL; j++) {
-#pragma unroll
-        for (uint32_t off = LU / 2; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off);
+        acc[j] = lanes_sum_down<LU>(acc[j]);   // the __shfl_xor butterfly LU / 2, ..., 1
     }
 
     if constexpr (GATE_UP) {
@@ -243,7 +242,7 @@ __global__ __launch_bounds__(64 * SM_WAVES) void sparse_int4_kernel(SmArgs A) {
 #pragma unroll
         for (uint32_t li = 0; li < SM_WROWS; li++) {
             // lanes of row group li / RPL hold row li in acc[li % RPL]
-            const float v = __shfl(acc[li % RPL], (li / RPL) * LU);
+            const float v = lane_bcast(acc[li % RPL], (li / RPL) * LU);
             if (li < OR && lane == li) gate = v;
             if (li >= OR && lane == li - OR) up = v;
         }
@@ -258,7 +257,7 @@ __global__ __launch_bounds__(64 * SM_WAVES) void sparse_int4_kernel(SmArgs A) {
         float y = 0.0f;
 #pragma unroll
         for (uint32_t li = 0; li < SM_WROWS; li++) {
-            const float v = __shfl(acc[li % RPL], (li / RPL) * LU);
+            const float v = lane_bcast(acc[li % RPL], (li / RPL) * LU);
             if (lane == li) y = v;
         }
         const uint32_t row = orow0 + lane;

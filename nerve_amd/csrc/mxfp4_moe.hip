@@ -419,14 +419,14 @@ __device__ __forceinline__ uint32_t wave_add_one(uint32_t* cnt, uint32_t e, bool
     uint32_t mine = 0;
     while (todo) {
         const uint32_t leader = (uint32_t)__ffsll((unsigned long long)todo) - 1u;
-        const uint32_t el = __shfl(e, leader);
+        const uint32_t el = (uint32_t)__builtin_amdgcn_readlane((int)e, (int)leader);   // leader: wave-uniform
         const uint64_t m = __ballot(e == el);
         uint32_t base = 0;
         if (lane == leader) {
             if (want_old) base = atomicAdd(&cnt[el], (uint32_t)__popcll(m));
             else atomicAdd(&cnt[el], (uint32_t)__popcll(m));
         }
-        if (want_old) base = __shfl(base, leader);
+        if (want_old) base = (uint32_t)__builtin_amdgcn_readlane((int)base, (int)leader);
         if (e == el) mine = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
         todo &= ~m;
     }

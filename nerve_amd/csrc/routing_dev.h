@@ -348,7 +348,14 @@ __device__ void topk_pair32(const uint16_t* lg, uint32_t stride, const void* bia
         const uint32_t m = (uint32_t)(__ballot(chosen && rank == r) >> base);
         return m ? (uint32_t)__builtin_ctz(m) : 0u;
     };
-    auto from = [&](float v, uint32_t x) -> float { return __shfl(v, (int)(base + x)); };
+    // Value of expert x of this lane's token: x is uniform within each half
+    // of the wave, so two lane reads and a select instead of a shuffle.
+    auto from = [&](float v, uint32_t x) -> float {
+        const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), x1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
+        const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)x0));
+        const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)(32 + x1)));
+        return h ? hi : lo;
+    };
     const bool sig = P.activation != 0;
     float maximum = from(raw, top_of(0));
     float den = 0.0f;

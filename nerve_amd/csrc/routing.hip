@@ -269,17 +269,22 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     // wave; otherwise one token per wave.
     uint32_t* telp = F.telemetry ? (tel_in_lds ? tel : F.telemetry) : nullptr;
     if (F.P.mode == 0 && E <= 32) {
+        // Waves without a token skip the call (it synchronizes nothing but
+        // the wave): at B <= 16 the other half of the block would only add
+        // to each SIMD's vector-ALU queue.
         for (uint32_t b0 = 0; b0 < B; b0 += 32)
-            topk_pair32(lg, E, F.bias, rl, telp, b0 + 2 * wave, B, F.P, t_raw[wave], tel_in_lds);
+            if (b0 + 2 * wave < B)
+                topk_pair32(lg, E, F.bias, rl, telp, b0 + 2 * wave, B, F.P, t_raw[wave], tel_in_lds);
     } else {
         TopkScratch S{t_raw[wave], t_sel[wave], t_top[wave], t_wts[wave], &t_f[wave][0], &t_f[wave][1],
                       &t_u[wave][0], &t_u[wave][1]};
         const bool fast = F.P.mode == 0 && E <= 64;
         for (uint32_t b0 = 0; b0 < B; b0 += 16) {
             const uint32_t b = b0 + wave;
-            if (fast)
-                topk_token_fast(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, tel_in_lds ? tel : nullptr,
-                                t_raw[wave]);
+            if (fast) {
+                if (b < B)   // wave-level only, like topk_pair32
+                    topk_token_fast(lg + b * E, F.bias, rl, telp, b, true, F.P, tel_in_lds ? tel : nullptr, t_raw[wave]);
+            }
             else topk_token(lg + (b < B ? b : 0) * E, F.bias, rl, telp, b, b < B, F.P, S, tel_in_lds ? tel : nullptr);
         }
     }

@@ -9,6 +9,18 @@
 
 namespace {
 
+// An LDS count.  The telemetry pointer of the forms below may address LDS
+// or global memory, so the compiler would emit a flat atomic (the slow path
+// through the vector memory unit); the explicit LDS address space makes it
+// a ds_add.
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+__device__ __forceinline__ void lds_count(uint32_t* p) { __atomic_fetch_add((lds_u32_t*)p, 1u, __ATOMIC_RELAXED); }
+// A device-memory count (agent scope), as a global atomic rather than a flat one.
+typedef __attribute__((address_space(1))) uint32_t global_u32_t;
+__device__ __forceinline__ void global_count(uint32_t* p) {
+    __hip_atomic_fetch_add((global_u32_t*)p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------
 // a6: top-k.  One wave per token.
 // ---------------------------------------------------------------------------
@@ -31,8 +43,8 @@ __device__ __forceinline__ void topk_publish(uint32_t b, uint32_t lane, const ui
                                              uint32_t total_sel, uint32_t total_res, uint32_t* routes,
                                              uint32_t* telemetry, uint32_t* tel_lds) {
     auto count = [&](uint32_t i) {
-        if (tel_lds) atomicAdd(&tel_lds[i], 1u);
-        else __hip_atomic_fetch_add(&telemetry[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tel_lds) lds_count(&tel_lds[i]);
+        else global_count(&telemetry[i]);
     };
     if (lane < total_sel) {
         routes[(uint64_t)b * total_sel + lane] = (f32_to_bf16(wts[lane]) << 16) | top[lane];
@@ -275,8 +287,8 @@ __device__ void topk_token_fast(const uint16_t* lg, const void* bias, uint32_t* 
     }
     if (!telemetry) return;
     auto count = [&](uint32_t i) {
-        if (tel_lds) atomicAdd(&tel_lds[i], 1u);
-        else __hip_atomic_fetch_add(&telemetry[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tel_lds) lds_count(&tel_lds[i]);
+        else global_count(&telemetry[i]);
     };
     // counts[expert] per selection, and every pair of selections (left < right
     // in the sorted list; equal experts are not counted as a pair).
@@ -383,8 +395,8 @@ __device__ void topk_pair32(const uint16_t* lg, uint32_t stride, const void* bia
     }
     if (!telemetry) return;
     auto count = [&](uint32_t i) {
-        if (tel_is_lds) atomicAdd(&telemetry[i], 1u);
-        else __hip_atomic_fetch_add(&telemetry[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tel_is_lds) lds_count(&telemetry[i]);
+        else global_count(&telemetry[i]);
     };
     if (chosen) count(e);
     if (e == 0 && nsel < k)

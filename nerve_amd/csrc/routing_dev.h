@@ -429,6 +429,7 @@ __device__ void topk_pair32(const uint16_t* lg, uint32_t stride, const void* bia
 // routes in source order.  The control words are written either way.
 // ---------------------------------------------------------------------------
 constexpr uint32_t COMPACT_LDS_ROUTES = 8192;
+constexpr uint32_t COMPACT_RPL = 8;            // 64-route chunks per wave held in registers
 constexpr uint32_t COUNT_MAX_EXPERTS = 512;
 
 struct CompactArgs {
@@ -475,10 +476,41 @@ __device__ bool compact_counting(const CompactArgs& A, uint32_t* cnt, uint32_t* 
     __syncthreads();
     const uint32_t seg = (n + nw - 1) / nw;
     const uint32_t s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
-    for (uint32_t i = s0 + lane; i < s1; i += 64) {
-        const uint32_t e = A.routes[i] & 0xffffu;
-        if (e < E) atomicAdd(&cnt[wave * E + e], 1u);
-        else *flag = 1;
+    // Segments of up to COMPACT_RPL * 64 routes: every route word loaded at
+    // once into registers, each 64-route chunk's lanes grouped by expert with
+    // one ballot per key bit (E <= 512), one LDS add per group.  The same
+    // groups give each route's rank within its chunk for the placement.
+    const bool regs = seg <= COMPACT_RPL * 64;
+    uint32_t er[COMPACT_RPL], before_r[COMPACT_RPL], after_r[COMPACT_RPL];
+    if (regs) {
+#pragma unroll
+        for (uint32_t c = 0; c < COMPACT_RPL; c++) {
+            const uint32_t i = s0 + 64 * c + lane;
+            er[c] = i < s1 ? (A.routes[i] & 0xffffu) : 0xffffffffu;
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < COMPACT_RPL; c++) {
+            if (s0 + 64 * c >= s1) break;   // wave-uniform
+            const uint32_t e = er[c];
+            const bool valid = e != 0xffffffffu;
+            if (valid && e >= E) *flag = 1;
+            uint64_t eq = __ballot(valid && e < E);
+#pragma unroll
+            for (int bit = 0; bit < 9; bit++) {
+                const bool one = (e >> bit) & 1u;
+                const uint64_t m = __ballot(one);
+                eq &= one ? m : ~m;
+            }
+            before_r[c] = (uint32_t)__popcll(eq & ((1ull << lane) - 1ull));
+            after_r[c] = (uint32_t)__popcll(eq >> lane) - 1u;
+            if (valid && e < E && before_r[c] == 0) __atomic_fetch_add((lds_u32_t*)&cnt[wave * E + e], (uint32_t)__popcll(eq), __ATOMIC_RELAXED);
+        }
+    } else {
+        for (uint32_t i = s0 + lane; i < s1; i += 64) {
+            const uint32_t e = A.routes[i] & 0xffffu;
+            if (e < E) atomicAdd(&cnt[wave * E + e], 1u);
+            else *flag = 1;
+        }
     }
     __syncthreads();
     if (*flag) return false;
@@ -510,6 +542,22 @@ __device__ bool compact_counting(const CompactArgs& A, uint32_t* cnt, uint32_t* 
         }
     }
     __syncthreads();
+    if (regs) {
+        // Chunks in order: a chunk's group reads its expert's running
+        // position, its last lane advances it (a wave's LDS accesses
+        // complete in order).
+#pragma unroll
+        for (uint32_t c = 0; c < COMPACT_RPL; c++) {
+            if (s0 + 64 * c >= s1) break;   // wave-uniform
+            const uint32_t e = er[c], i = s0 + 64 * c + lane;
+            if (e != 0xffffffffu) {
+                const uint32_t pos = cnt[wave * E + e] + before_r[c];
+                put_map(A, pos, i);
+                if (after_r[c] == 0) cnt[wave * E + e] = pos + 1;
+            }
+        }
+        return true;
+    }
     for (uint32_t base = s0; base < s1; base += 64) {
         const uint32_t i = base + lane;
         const bool valid = i < s1;

@@ -315,8 +315,6 @@ __global__ __launch_bounds__(256) void reduce_kernel(const uint16_t* __restrict_
     out[idx] = (uint16_t)f32_to_bf16(acc * routed_scale);
 }
 
-constexpr uint32_t REDUCE_BATCH = 8;
-
 // The same combine, 8 columns per thread with 16-byte loads and stores
 // (H % 8 == 0, 16-byte aligned buffers).
 __global__ __launch_bounds__(256) void reduce8_kernel(const uint16_t* __restrict__ eo, uint16_t* __restrict__ out,
@@ -326,26 +324,14 @@ __global__ __launch_bounds__(256) void reduce8_kernel(const uint16_t* __restrict
     if (idx >= (uint64_t)B * H8) return;
     const uint32_t b = (uint32_t)(idx / H8), j = (uint32_t)(idx % H8) * 8;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const uint16_t* src = eo + (uint64_t)b * k * H + j;
-    auto add = [&](const v4i& v) {
+    for (uint32_t r = 0; r < k; r++) {
+        const v4i v = *reinterpret_cast<const v4i*>(eo + ((uint64_t)b * k + r) * H + j);
         const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             acc[2 * q] = round_bf16(acc[2 * q] + bf16_to_f32(w[q] & 0xffffu));
             acc[2 * q + 1] = round_bf16(acc[2 * q + 1] + bf16_to_f32(w[q] >> 16));
         }
-    };
-    if (k <= REDUCE_BATCH) {
-        // All k rows in flight at once (the sum order is unchanged).
-        v4i v[REDUCE_BATCH];
-#pragma unroll
-        for (uint32_t r = 0; r < REDUCE_BATCH; r++)
-            if (r < k) v[r] = *reinterpret_cast<const v4i*>(src + (uint64_t)r * H);
-#pragma unroll
-        for (uint32_t r = 0; r < REDUCE_BATCH; r++)
-            if (r < k) add(v[r]);
-    } else {
-        for (uint32_t r = 0; r < k; r++) add(*reinterpret_cast<const v4i*>(src + (uint64_t)r * H));
     }
     uint32_t o[4];
 #pragma unroll

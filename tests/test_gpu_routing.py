@@ -120,7 +120,11 @@ def test_score_router(ctx, dev, act):
     assert np.array_equal(to_np(tel, np.uint32), ref_tel)
 
 
-@pytest.mark.parametrize("B,k,E", [(16, 4, 32), (2048, 4, 128), (1, 1, 8), (300, 6, 64)])
+# n = B k routes: one wave's ballot ranks (n <= 64), the counting sort with
+# each wave's segment in registers (1024 < n <= 8192; 8192 fills them), its
+# looped form (n > 8192), and the rank loop (64 < n <= 1024).
+@pytest.mark.parametrize("B,k,E", [(16, 4, 32), (2048, 4, 128), (1, 1, 8), (300, 6, 64), (2100, 4, 128),
+                                   (100, 4, 32)])
 @pytest.mark.parametrize("partition", [None, (8, 20)])
 def test_route_compact(ctx, dev, B, k, E, partition):
     torch = _torch()

@@ -488,7 +488,11 @@ HBM_READ_MODES = {0: "register loads, nontemporal (1 KB per wave load)", 1: "reg
                   10: "global_load_lds copies, 16 rows x 64 B, 2 MB L2-resident window (on-chip rate)",
                   11: "global_load_lds copies, 8 rows x 128 B, 2 MB L2-resident window (on-chip rate)",
                   12: "FP8-head GEMM chunks: weight rows by global_load_lds + L2 token rows by register loads (both counted)",
-                  13: "FP8-head GEMM chunks: weight rows + L2 token rows, both by global_load_lds (both counted)"}
+                  13: "FP8-head GEMM chunks: weight rows + L2 token rows, both by global_load_lds (both counted)",
+                  14: "register loads written to the LDS ring, 8 rows x 128 B, 2 MB L2-resident window (mode 11's depth)",
+                  15: "register loads written to the LDS ring, 16 rows x 64 B, 2 MB L2-resident window (mode 10's depth)",
+                  16: "register loads written to the LDS ring, 8 rows x 128 B (mode 6's depth)",
+                  17: "register loads written to the LDS ring, contiguous 1 KB, 2 MB L2-resident window (mode 7's depth)"}
 
 
 def hbm_read(args, ctx, dev):
@@ -515,7 +519,8 @@ def hbm_read(args, ctx, dev):
         # the row pattern reads 22 of every 22.5 64-byte columns: count what it reads
         rows_bytes = (n // (cus * 16384)) * cus * 16384
         gemm_steps = (n // (128 * 2880) // cus) * 22
-        nbytes = {3: rows_bytes, 6: rows_bytes, 7: rows_bytes, 10: rows_bytes, 11: rows_bytes,
+        nbytes = {3: rows_bytes, 6: rows_bytes, 7: rows_bytes, 10: rows_bytes, 11: rows_bytes, 14: rows_bytes,
+                  15: rows_bytes, 16: rows_bytes, 17: rows_bytes,
                   12: gemm_steps * cus * 49152, 13: gemm_steps * cus * 49152, 4: (n // 49152) * 49152, 5: (n // 49152) * 49152,
                   9: (n // 46080) * 46080}.get(mode, n)
         fn = lambda i, m=mode: lib.nerve_calib_read(ctypes.c_void_p(buf.data_ptr()), n, m,
@@ -525,8 +530,8 @@ def hbm_read(args, ctx, dev):
         kms = batch_event_ms(fn, max(20, args.steps), stream)
         modes[mode] = {"mode": what, "ms": kms, "gbs": nbytes / (kms * 1e-3) / 1e9}
     # the headline is an HBM rate: the modes reading an L2-resident window (7,
-    # 8, 10-13) are reported only
-    best = max((v for m, v in modes.items() if m not in (7, 8, 10, 11, 12, 13)), key=lambda v: v["gbs"])
+    # 8, 10-15, 17) are reported only
+    best = max((v for m, v in modes.items() if m not in (7, 8, 10, 11, 12, 13, 14, 15, 17)), key=lambda v: v["gbs"])
     out = base_line(args, best["gbs"], "GB/s", best["ms"], "u8", {"workload": "hbm_read_1GiB"})
     out["modes"] = list(modes.values())
     out["roofline"] = {"bound": "hbm", "kernel": "nerve_calib_read (" + best["mode"] + ")", "achieved": best["gbs"],

@@ -31,6 +31,10 @@
 //           per step; mode 12 reads the tokens with register loads and
 //           writes them to LDS when their step comes up, mode 13 copies
 //           them with global_load_lds like the weights;
+//   modes 14-17: the stages, sources and depth of modes 11, 10, 6 and 7
+//           (8 rows x 128 B and 16 rows x 64 B over the 2 MB window, 8 rows
+//           x 128 B from HBM, contiguous 1 KB over the window) with register
+//           loads written to the LDS stage instead of copies;
 //   mode 4: one 512-thread block per CU, nontemporal register loads of
 //           contiguous 48 KB items, two items (96 KB) in flight per CU (the
 //           decode streams' item pattern);
@@ -72,38 +76,45 @@ __device__ __forceinline__ void wait_vm_imm() {
     __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | 0x0F70u);
 }
 
+constexpr uint32_t RING_STAGE = 16384, RING_PER_WAVE = 4096;
+
+// Source of 16-byte piece `lane` of copy u of issuing wave `wave` at step
+// `step` (modes 2, 3, 6, 7, 10, 11 and 14-17).  rows == 0: contiguous; rows
+// == 1: stage s of block b covers 16 subtiles of 16 rows x 64 B, subtile x
+// at rows 16 x.., the 64-byte column (s % 22) of a 1440-byte row; blocks
+// and 22-step groups walk the buffer in 16 x 16-row = 368 KB blocks.  rows
+// == 2: 16 subtiles of 8 rows x 128 B, the 128-byte column (s % 11),
+// 128-row blocks.
+__device__ __forceinline__ const uint8_t* ring_src(const uint8_t* buf, uint64_t bytes, uint32_t rows, uint64_t wmask,
+                                                   uint64_t step, uint32_t wave, uint32_t u) {
+    const uint32_t lane = threadIdx.x & 63;
+    if (rows == 0)
+        return buf + (((step * gridDim.x + blockIdx.x) * RING_STAGE + wave * RING_PER_WAVE + u * 1024 + lane * 16) & wmask);
+    if (rows == 2) {
+        const uint64_t blk = (step / 11) * gridDim.x + blockIdx.x;   // 128-row block
+        const uint32_t col = (uint32_t)(step % 11);
+        const uint32_t x = wave * 4 + u, r = lane & 7, piece = lane >> 3;
+        const uint64_t off = ((blk * 128 + x * 8 + r) * 1440 + col * 128 + piece * 16) & wmask;
+        return buf + (off + 16 <= bytes ? off : 0);
+    }
+    const uint64_t blk = (step / 22) * gridDim.x + blockIdx.x;   // 256-row block
+    const uint32_t col = (uint32_t)(step % 22);
+    const uint32_t x = wave * 4 + u, r = lane & 15, piece = lane >> 4;
+    const uint64_t off = ((blk * 256 + x * 16 + r) * 1440 + col * 64 + piece * 16) & wmask;
+    return buf + (off + 16 <= bytes ? off : 0);
+}
+
 // One block per CU; waves 0-3 copy, waves 4-11 only take part in the
 // barriers (as the prefill consumers do).  Ring of 4 stages x 16 KB; each
 // issuing wave copies 4 KB per stage and keeps three stages in flight.
 __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
                                                        uint32_t* __restrict__ sink, uint32_t rows, uint64_t wmask) {
-    const bool ROWS = rows != 0;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    constexpr uint32_t STAGE = 16384, PER_WAVE = 4096;
+    constexpr uint32_t STAGE = RING_STAGE, PER_WAVE = RING_PER_WAVE;
     const uint64_t per_step = (uint64_t)gridDim.x * STAGE;
     const uint64_t steps = bytes / per_step;
-    // ROWS: stage s of block b covers a 16 KB piece of the row pattern: 16
-    // subtiles of 16 rows x 64 B, subtile x at rows 16 x.., the 64-byte
-    // column (s % 22) of a 1440-byte row; blocks and 22-step groups walk
-    // the buffer in 16 x 16-row = 368 KB blocks.  rows == 2: 16 subtiles of
-    // 8 rows x 128 B, the 128-byte column (s % 11), 128-row blocks.
-    auto src = [&](uint64_t step, uint32_t u) -> const uint8_t* {
-        if (!ROWS)
-            return buf + (((step * gridDim.x + blockIdx.x) * STAGE + wave * PER_WAVE + u * 1024 + lane * 16) & wmask);
-        if (rows == 2) {
-            const uint64_t blk = (step / 11) * gridDim.x + blockIdx.x;   // 128-row block
-            const uint32_t col = (uint32_t)(step % 11);
-            const uint32_t x = wave * 4 + u, r = lane & 7, piece = lane >> 3;
-            const uint64_t off = ((blk * 128 + x * 8 + r) * 1440 + col * 128 + piece * 16) & wmask;
-            return buf + (off + 16 <= bytes ? off : 0);
-        }
-        const uint64_t blk = (step / 22) * gridDim.x + blockIdx.x;   // 256-row block
-        const uint32_t col = (uint32_t)(step % 22);
-        const uint32_t x = wave * 4 + u, r = lane & 15, piece = lane >> 4;
-        const uint64_t off = ((blk * 256 + x * 16 + r) * 1440 + col * 64 + piece * 16) & wmask;
-        return buf + (off + 16 <= bytes ? off : 0);
-    };
+    auto src = [&](uint64_t step, uint32_t u) { return ring_src(buf, bytes, rows, wmask, step, wave, u); };
     if (wave < 4) {
         auto issue = [&](uint64_t step) {
 #pragma unroll
@@ -126,6 +137,57 @@ __global__ __launch_bounds__(768) void read_lds_kernel(const uint8_t* __restrict
     }
     __syncthreads();
     if (threadIdx.x == 0 && ring[lane] == 0xA5 && ring[STAGE] == 0x5A) sink[blockIdx.x] = 1u;
+}
+
+// Modes 14-17: read_lds_kernel's stages, sources and depth (waves 0-3
+// issue, three stages ahead, one barrier per stage), with register loads
+// into four register sets instead of copies; the oldest set is written to
+// its LDS stage before the barrier.
+__global__ __launch_bounds__(768) void read_regs_ring_kernel(const uint8_t* __restrict__ buf, uint64_t bytes,
+                                                             uint32_t* __restrict__ sink, uint32_t rows, uint64_t wmask) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint64_t steps = bytes / ((uint64_t)gridDim.x * RING_STAGE);
+    if (wave < 4) {
+        v4i r0[4], r1[4], r2[4], r3[4];
+        auto issue = [&](uint64_t st, v4i (&r)[4]) {
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++)
+                asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r[u]) : "v"(ring_src(buf, bytes, rows, wmask, st, wave, u)) : "memory");
+        };
+        // cur: the set of step s; fr: the set step s - 1 wrote to LDS (free)
+        auto step = [&](uint64_t s, v4i (&cur)[4], v4i (&fr)[4]) {
+            if (s + 3 < steps) {
+                issue(s + 3, fr);
+                wait_vm_imm<12>();
+            } else if (s + 2 < steps) {
+                wait_vm_imm<8>();
+            } else if (s + 1 < steps) {
+                wait_vm_imm<4>();
+            } else {
+                wait_vm_imm<0>();
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                asm volatile("" : "+v"(cur[u]));
+                *reinterpret_cast<v4i*>(ring + (s % 4) * RING_STAGE + wave * RING_PER_WAVE + u * 1024 + lane * 16) = cur[u];
+            }
+            __builtin_amdgcn_s_barrier();
+        };
+        if (steps > 0) issue(0, r0);
+        if (steps > 1) issue(1, r1);
+        if (steps > 2) issue(2, r2);
+        for (uint64_t s = 0; s < steps; s += 4) {
+            step(s, r0, r3);
+            if (s + 1 < steps) step(s + 1, r1, r0);
+            if (s + 2 < steps) step(s + 2, r2, r1);
+            if (s + 3 < steps) step(s + 3, r3, r2);
+        }
+    } else {
+        for (uint64_t s = 0; s < steps; s++) __builtin_amdgcn_s_barrier();
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && ring[lane] == 0xA5 && ring[RING_STAGE] == 0x5A) sink[blockIdx.x] = 1u;
 }
 
 // Modes 4 and 5: 8 waves, items of 48 KB (6 KB per wave = 6 x 1 KB pieces);
@@ -319,7 +381,7 @@ using namespace nerve_calib;
 extern "C" {
 
 // Streams `bytes` of `buf` (16-byte aligned) once with read mode `mode`
-// (0-13, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
+// (0-17, above) on `stream`; `sink` takes one u32 per block (grid <= 4096).
 // Returns 0, or 1 for an unknown mode or a launch error.
 int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int cu_count, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -344,6 +406,20 @@ int nerve_calib_read(const void* buf, uint64_t bytes, int mode, void* sink, int 
         read_lds_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out,
                                                                    (mode == 3 || mode == 10) ? 1u : (mode == 6 || mode == 11) ? 2u : 0u,
                                                                    (mode == 7 || mode >= 10) ? WIN - 1 : ~0ull);
+    } else if (mode >= 14 && mode <= 17) {
+        static bool attr14 = false;
+        if (!attr14) {
+            if (hipFuncSetAttribute((const void*)read_regs_ring_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    65536) != hipSuccess)
+                return 1;
+            attr14 = true;
+        }
+        // 14: 8 rows x 128 B over the 2 MB window; 15: 16 rows x 64 B over
+        // the window; 16: 8 rows x 128 B from HBM; 17: contiguous 1 KB over
+        // the window.
+        const uint32_t rows = mode == 15 ? 1u : mode == 17 ? 0u : 2u;
+        read_regs_ring_kernel<<<cu_count, 768, 65536, st>>>(static_cast<const uint8_t*>(buf), bytes, out, rows,
+                                                            mode == 16 ? ~0ull : WIN - 1);
     } else if (mode == 12 || mode == 13) {
         static bool attr12 = false;
         if (!attr12) {

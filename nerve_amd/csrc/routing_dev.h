@@ -466,7 +466,7 @@ __device__ void compact_rank_loop(const CompactArgs& A, uint16_t* ex) {
 // Stable counting sort for large n: wave w owns a contiguous segment; per-
 // wave expert histograms give each (expert, wave) its output offset, then
 // each wave places its routes in order, ranking equal experts inside a
-// 64-lane group with shuffles.  Returns false (nothing written) if an
+// 64-route chunk with ballots.  Returns false (nothing written) if an
 // expert id is outside [0, E).
 __device__ bool compact_counting(const CompactArgs& A, uint32_t* cnt, uint32_t* wave_tot, uint32_t* flag) {
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;

@@ -179,17 +179,23 @@ def moe_decode(args, ctx, dev):
         r = layers[L].buffers(B)["routes"].cpu().numpy().view(np.uint32)
         U.append(len(np.unique(r & 0xFFFF)))
     mat = I * H // 2 + I * H // 32                 # one MXFP4 matrix + scales
-    gate_up_bytes = [u * 2 * mat + B * H * 2 + B * k * I * 2 for u in U]
+    # gate_up reads the hidden rows as the routing launch quantized them
+    # (e4m3 bytes + f32 block scales)
+    gate_up_bytes = [u * 2 * mat + B * H + B * ((H + 127) // 128) * 4 + B * k * I * 2 for u in U]
     down_bytes = [u * mat + B * k * I * 2 + B * k * H * 2 for u in U]
-    step_bytes = float(np.mean([g + dn + E * H * 2 + 2 * B * H * 2 + B * k * H * 2
-                                for g, dn in zip(gate_up_bytes, down_bytes)]))
+    # + router weights, hidden in and block output out, the quantized rows the
+    # routing launch writes, the expert outputs the combine reads
+    step_bytes = float(np.mean([g + dn + E * H * 2 + 2 * B * H * 2 + B * H + B * ((H + 127) // 128) * 4
+                                + B * k * H * 2 for g, dn in zip(gate_up_bytes, down_bytes)]))
 
     ms = wall_ms(lambda i: layers[i % 2].forward(hidden[i % 2]), args.steps, args.warmup)
 
     def gate_up(i):
+        # the launch MoEBlock.forward makes: the prequantized form on the
+        # routing launch's e4m3 rows
         L = layers[i % 2]
         b = L.buffers(B)
-        ctx.mxfp4_moe_gate_up(L.gate_up, hidden[i % 2], None, b["routes"], b["inter"], L.bank.addresses,
+        ctx.mxfp4_moe_gate_up(L.gate_up_pq, b["hidden_q"], b["hidden_s"], b["routes"], b["inter"], L.bank.addresses,
                               L.bank.gate_slots, b["control"], B, stream)
 
     # routes / maps of both layers are in their own buffers already

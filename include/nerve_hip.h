@@ -184,6 +184,11 @@ nerve_hip_status nerve_hip_moe_router_topk(nerve_hip_ctx* ctx, const char* spec,
  * nerve_hip_moe_router_topk + nerve_hip_moe_route_compact produce from
  * those logits.  logits_bf16 may be NULL.  hidden comes from moe_spec; the
  * top-k experts and k (plus always-selected experts) must match moe_spec.
+ * hidden_e4m3 / hidden_scales_f32 (both or neither; u8 [B, H], f32
+ * [B, ceil(H/128)]): the hidden rows quantized as the gate/up projection
+ * quantizes them (quantize_hidden, …gate_up_batch1_mxfp4.comp.template:
+ * 366-382: pow2 block scales), bit for bit, for its `_prequant` form; the
+ * blocks that finish their partial sums before the last one write them.
  * Returns NERVE_HIP_UNSUPPORTED (nothing launched) above 64 tokens, 256
  * experts or 1024 routes: use the three entry points then.  Calls on one
  * context must not overlap (other streams, parallel graph branches): they
@@ -193,7 +198,8 @@ nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_
                                            const void* router_weight_bf16, void* logits_bf16,
                                            const void* bias, void* routes_u32,
                                            void* telemetry_u32, void* intermediates,
-                                           void* control_u32, uint32_t batch_width,
+                                           void* control_u32, void* hidden_e4m3,
+                                           void* hidden_scales_f32, uint32_t batch_width,
                                            void* stream);
 
 /* ---- a7: expert-sorted route permutation -------------------------------- */

@@ -4,6 +4,7 @@
 #include <cmath>
 
 #include "common.h"
+#include "quant_dev.h"
 #include "routing_dev.h"
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -164,7 +165,23 @@ struct FusedRouteArgs {
     uint32_t* telemetry;
     TopkParams P;
     CompactArgs C;
+    QuantArgs Q;           // the hidden rows' e4m3 blocks, when quant is set
+    uint32_t quant;
 };
+
+// The hidden rows' e4m3 blocks (pow2 scales, the gate/up projection's own
+// quantization): worker w of `workers` takes units w U, w U + workers U, ...
+// (U units per block pass).
+__device__ __forceinline__ void route_quant_rows(const QuantArgs& Q, uint32_t w, uint32_t workers) {
+    const uint64_t units = (uint64_t)Q.rows * ((Q.cols + 127) / 128);
+    if (Q.vec8) {
+        for (uint64_t u0 = (uint64_t)w * 64; u0 < units; u0 += (uint64_t)workers * 64)   // block-uniform bound
+            quant_units8_pow2<1>(Q, u0 + (threadIdx.x >> 4), 0, threadIdx.x & 15);
+    } else {
+        for (uint64_t u0 = (uint64_t)w * 32; u0 < units; u0 += (uint64_t)workers * 32)
+            quant_unit<true>(Q, (uint32_t)(u0 + (threadIdx.x >> 5)), threadIdx.x & 31);
+    }
+}
 
 constexpr uint32_t FR_LDS_TELEMETRY = 4096;   // telemetry arrays up to this size are counted in LDS
 
@@ -187,7 +204,7 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     __shared__ uint32_t tel[FR_LDS_TELEMETRY];
     __shared__ uint32_t wave_tot[16];
     __shared__ uint32_t misc[2];
-    __shared__ uint32_t ctl2, ctl0, is_last;
+    __shared__ uint32_t ctl2, ctl0, is_last, arrival;
     __shared__ v4f red[16][64];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, E = F.P.E, B = F.B;
     // ---- partial sums of expert tile blockIdx.x over K slice blockIdx.y
@@ -241,11 +258,19 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
         const uint32_t nb = gridDim.x * gridDim.y;
         const uint32_t old = __builtin_amdgcn_atomic_inc32(F.arrive, nb - 1, __ATOMIC_ACQ_REL, "agent");
         is_last = old == nb - 1 ? 1u : 0u;
+        arrival = old;
         ctl2 = F.C.control[2];
         ctl0 = F.C.control[0];
     }
     __syncthreads();
-    if (!is_last) return;
+    // The blocks done before the last one quantize the hidden rows for the
+    // gate/up projection, off the routing's critical path (a one-block grid
+    // does it at its end).
+    const uint32_t nb = gridDim.x * gridDim.y;
+    if (!is_last) {
+        if (F.quant) route_quant_rows(F.Q, arrival, nb - 1);
+        return;
+    }
     const uint32_t total_sel = F.P.k + F.P.always_count, total_res = E + F.P.always_count;
     const uint32_t T = total_res + total_res * (total_res - 1) / 2;
     const bool tel_in_lds = F.telemetry && T <= FR_LDS_TELEMETRY;
@@ -300,6 +325,7 @@ __global__ __launch_bounds__(1024) void route_fused_kernel(FusedRouteArgs F) {
     if (tel_in_lds)
         for (uint32_t i = threadIdx.x; i < T; i += blockDim.x)
             if (tel[i]) __hip_atomic_fetch_add(&F.telemetry[i], tel[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (F.quant && nb == 1) route_quant_rows(F.Q, 0, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -423,8 +449,8 @@ nerve_hip_status nerve_hip_moe_route_compact(nerve_hip_ctx* ctx, const char* spe
 nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_spec, const char* moe_spec,
                                            const void* x_bf16, const void* router_weight_bf16, void* logits_bf16,
                                            const void* bias, void* routes_u32, void* telemetry_u32,
-                                           void* intermediates, void* control_u32, uint32_t batch_width,
-                                           void* stream) {
+                                           void* intermediates, void* control_u32, void* hidden_e4m3,
+                                           void* hidden_scales_f32, uint32_t batch_width, void* stream) {
     nerve_hip_status st = nh::enter(ctx);
     if (st) return st;
     nh::TopkSpec ts;
@@ -435,6 +461,12 @@ nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_
         return nh::fail(NERVE_HIP_INVALID_SPEC, "the unbatched INT4 expert form reads no route map");
     if (!x_bf16 || !router_weight_bf16 || !routes_u32 || !control_u32) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "null buffer");
     if (ts.bias != 0 && !bias) return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "specialization requires a selection bias");
+    if (!hidden_e4m3 != !hidden_scales_f32)
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "the quantized hidden rows need both the e4m3 and the scale buffer");
+    if (hidden_scales_f32 && ((uintptr_t)hidden_scales_f32 & 3))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "hidden scales must be 4-byte aligned");
+    if (hidden_e4m3 && (ms.hidden % 4 || ((uintptr_t)hidden_e4m3 & 3)))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "quantized hidden rows need hidden % 4 == 0 and a 4-byte aligned buffer");
     if (ts.experts != ms.experts || ts.k + ts.always_count != ms.k)
         return nh::fail(NERVE_HIP_INVALID_SPEC, "top-k and projection specializations disagree on experts or k");
     if (batch_width == 0) return nh::ok();
@@ -464,6 +496,19 @@ nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_
     F.bias = bias;
     F.routes = static_cast<uint32_t*>(routes_u32);
     F.telemetry = static_cast<uint32_t*>(telemetry_u32);
+    F.quant = hidden_e4m3 ? 1u : 0u;
+    F.Q = QuantArgs{};
+    F.Q.x = F.x;
+    F.Q.k = 1;
+    F.Q.frame_elems = H;
+    F.Q.seg_elems = 0;
+    F.Q.cols = H;
+    F.Q.rows = batch_width;
+    F.Q.q = static_cast<uint8_t*>(hidden_e4m3);
+    F.Q.s = static_cast<float*>(hidden_scales_f32);
+    F.Q.zero_word = nullptr;
+    F.Q.ldq = H;
+    F.Q.vec8 = ((((uintptr_t)F.Q.x | (uintptr_t)F.Q.q) & 15) == 0 && H % 8 == 0) ? 1u : 0u;
     F.P.E = ts.experts;
     F.P.k = ts.k;
     F.P.always_count = ts.always_count;

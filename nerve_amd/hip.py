@@ -89,7 +89,7 @@ def _declare(lib) -> None:
         "nerve_hip_router_linear_bf16": (ctypes.c_int, [P, P, P, P, U32, U32, U32, P]),
         "nerve_hip_moe_router_topk": (ctypes.c_int, [P, S, P, P, P, P, U32, P]),
         "nerve_hip_moe_route_compact": (ctypes.c_int, [P, S, P, P, P, U32, P]),
-        "nerve_hip_moe_route_fused": (ctypes.c_int, [P, S, S, P, P, P, P, P, P, P, P, U32, P]),
+        "nerve_hip_moe_route_fused": (ctypes.c_int, [P, S, S, P, P, P, P, P, P, P, P, P, P, U32, P]),
         "nerve_hip_mxfp4_moe_gate_up": (ctypes.c_int, [P, S, P, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_mxfp4_moe_down": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
         "nerve_hip_mxfp4_moe_down_counted": (ctypes.c_int, [P, S, P, P, P, P, U32, P, U32, P, U32, P]),
@@ -218,13 +218,15 @@ class Context:
 
     # ---- a5 + a6 + a7
     def moe_route_fused(self, topk_spec, moe_spec, x, router_weight, logits, bias, routes, telemetry, intermediates,
-                        control, batch_width, stream=None) -> bool:
-        """One launch for router linear + top-k + compaction.  Returns False
-        (nothing launched) when the batch is too large for the fused form."""
+                        control, batch_width, stream=None, hidden_q=None, hidden_scales=None) -> bool:
+        """One launch for router linear + top-k + compaction (and, with
+        hidden_q / hidden_scales, the hidden rows quantized for the gate/up
+        projection's prequantized form).  Returns False (nothing launched)
+        when the batch is too large for the fused form."""
         st = self.lib.nerve_hip_moe_route_fused(self.handle, _spec(topk_spec), _spec(moe_spec), ptr(x),
                                                 ptr(router_weight), ptr(logits), ptr(bias), ptr(routes),
-                                                ptr(telemetry), ptr(intermediates), ptr(control), batch_width,
-                                                _stream(stream))
+                                                ptr(telemetry), ptr(intermediates), ptr(control), ptr(hidden_q),
+                                                ptr(hidden_scales), batch_width, _stream(stream))
         if st == UNSUPPORTED:
             return False
         _check(st)

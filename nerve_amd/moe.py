@@ -167,6 +167,9 @@ class MoEBlock:
         self.limit = limit
         self.routed_scale = routed_scale
         self.gate_up = gate_up_spec(self.H, self.I, self.E, k, limit)
+        # The same projection on hidden rows the fused routing launch has
+        # already quantized (bit-identical to its own quantization).
+        self.gate_up_pq = gate_up_spec(self.H, self.I, self.E, k, limit, prequant=True)
         self.down = down_spec(self.H, self.I, self.E, k)
         self.topk = topk_spec(self.E, k, sigmoid=sigmoid, normalize=normalize)
         self.fuse_routing = True
@@ -187,6 +190,9 @@ class MoEBlock:
                 control=torch.tensor([B, 0, 0, 0, 0, 0, 0, 0], dtype=torch.int32, device=dev),
                 expert_out=torch.empty(B, k, H, dtype=torch.int16, device=dev),
                 out=torch.empty(B, H, dtype=torch.int16, device=dev),
+                # the hidden rows' e4m3 blocks and pow2 scales (fused routing)
+                hidden_q=torch.empty(B, H, dtype=torch.uint8, device=dev),
+                hidden_s=torch.empty(B, (H + 127) // 128, dtype=torch.float32, device=dev),
             )
         return self._bufs[B]
 
@@ -196,15 +202,20 @@ class MoEBlock:
         c = self.ctx
         b = self.buffers(B)
         bank = self.bank
-        # Decode-sized batches: router linear + top-k + compaction in one launch.
-        if not (self.fuse_routing and c.moe_route_fused(self.topk, self.gate_up, hidden, self.router_w, b["logits"],
-                                                        None, b["routes"], b["telemetry"], b["inter"], b["control"],
-                                                        B, stream)):
+        # Decode-sized batches: router linear + top-k + compaction in one
+        # launch, which also quantizes the hidden rows for gate_up.
+        fused = self.fuse_routing and c.moe_route_fused(
+            self.topk, self.gate_up, hidden, self.router_w, b["logits"], None, b["routes"], b["telemetry"],
+            b["inter"], b["control"], B, stream, hidden_q=b["hidden_q"], hidden_scales=b["hidden_s"])
+        if fused:
+            c.mxfp4_moe_gate_up(self.gate_up_pq, b["hidden_q"], b["hidden_s"], b["routes"], b["inter"], bank.addresses,
+                                bank.gate_slots, b["control"], B, stream)
+        else:
             c.router_linear_bf16(hidden, self.router_w, b["logits"], B, self.H, self.E, stream)
             c.moe_router_topk(self.topk, b["logits"], None, b["routes"], b["telemetry"], B, stream)
             c.moe_route_compact(self.gate_up, b["routes"], b["inter"], b["control"], B, stream)
-        c.mxfp4_moe_gate_up(self.gate_up, hidden, None, b["routes"], b["inter"], bank.addresses, bank.gate_slots,
-                            b["control"], B, stream)
+            c.mxfp4_moe_gate_up(self.gate_up, hidden, None, b["routes"], b["inter"], bank.addresses,
+                                bank.gate_slots, b["control"], B, stream)
         if self.fuse_routing:
             # Count stage folded into the down launch (same control words).
             c.mxfp4_moe_down_counted(self.down, b["inter"], b["routes"], b["expert_out"], bank.addresses,

@@ -136,6 +136,14 @@ def test_moe_block_forward_config2(ctx, dev):
     eo_chain = oracle.moe_down(h_ref, routes, cmap, B * k, d["down_w"], d["down_s"])
     out_chain = wl.bf16_bits_to_f32(oracle.moe_reduce(eo_chain, 1.0))
     assert rel_err_normwise(wl.bf16_bits_to_f32(out), out_chain) <= 2e-2
+    # gate_up ran in its prequantized form on the routing launch's quantized
+    # hidden rows: the bf16-input form on the same routes writes the same h
+    torch = _torch()
+    inter2 = b["inter"].clone()
+    ctx.mxfp4_moe_gate_up(block.gate_up, _dv(d["hidden"], dev), None, b["routes"], inter2, bank.addresses,
+                          bank.gate_slots, b["control"], B)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(inter2, np.uint32), frames.reshape(-1))
 
 
 # --------------------------------------------------------------------------

@@ -190,11 +190,14 @@ def test_route_compact_expert_ids_beyond_spec(ctx, dev):
     (1, 2880, 32, 4, "softmax"),
     (64, 512, 128, 8, "sigmoid_biasbf16"),
     (5, 160, 48, 3, "score_softmax"),      # E not a multiple of 32, always-selected experts
+    (3, 96, 16, 2, "softmax"),             # one block (it quantizes at its end); q 4 bytes off 16: 32-lane units
 ])
 def test_route_fused_matches_separate(ctx, dev, B, H, E, k, kind):
     """nerve_hip_moe_route_fused: logits within one bf16 ulp of the router linear's
     (and of the oracle's); routes, telemetry, route map and control words
-    bit-identical to top-k + compaction run on its own logits."""
+    bit-identical to top-k + compaction run on its own logits; the quantized
+    hidden rows bit-identical to the standalone pow2 quantizer's and the
+    oracle's."""
     torch = _torch()
     rng = np.random.default_rng(B * E + k)
     x = wl.bf16_normal(rng, (B, H))
@@ -224,8 +227,19 @@ def test_route_fused_matches_separate(ctx, dev, B, H, E, k, kind):
 
     xd, wd = to_dev(x, dev), to_dev(w, dev)
     f = bufs()
+    nblk = (H + 127) // 128
+    off = 4 if H == 96 else 0
+    hq = torch.full((B * H + off,), 0x55, dtype=torch.uint8, device=dev)[off:].view(B, H)
+    hs = torch.full((B, nblk), -1.0, dtype=torch.float32, device=dev)
     assert ctx.moe_route_fused(tspec, mspec, xd, wd, f["logits"], bias, f["routes"], f["tel"], f["inter"],
-                               f["control"], B)
+                               f["control"], B, hidden_q=hq, hidden_scales=hs)
+    sq = torch.zeros(B, H, dtype=torch.uint8, device=dev)
+    ss = torch.zeros(B, nblk, dtype=torch.float32, device=dev)
+    ctx.quantize_fp8_e4m3(f"quantize_fp8_e4m3_spow2_b128_h{H}.comp", xd, B, sq, ss)
+    oq, os_ = oracle.quantize_blocks(x, True)
+    assert np.array_equal(to_np(hq, np.uint8), to_np(sq, np.uint8))
+    assert np.array_equal(to_np(hs, np.float32), to_np(ss, np.float32))
+    assert np.array_equal(to_np(hq, np.uint8), oq) and np.array_equal(to_np(hs, np.float32), os_)
     lin = torch.zeros(B, E, dtype=torch.int16, device=dev)
     ctx.router_linear_bf16(xd, wd, lin, B, H, E)
     got = wl.bf16_bits_to_f32(to_np(f["logits"], np.uint16)).astype(np.float64)

@@ -465,8 +465,9 @@ nerve_hip_status nerve_hip_moe_route_fused(nerve_hip_ctx* ctx, const char* topk_
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "the quantized hidden rows need both the e4m3 and the scale buffer");
     if (hidden_scales_f32 && ((uintptr_t)hidden_scales_f32 & 3))
         return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "hidden scales must be 4-byte aligned");
-    if (hidden_e4m3 && (ms.hidden % 4 || ((uintptr_t)hidden_e4m3 & 3)))
-        return nh::fail(NERVE_HIP_INVALID_ARGUMENT, "quantized hidden rows need hidden % 4 == 0 and a 4-byte aligned buffer");
+    if (hidden_e4m3 && (ms.hidden % 4 || (((uintptr_t)hidden_e4m3 | (uintptr_t)x_bf16) & 3)))
+        return nh::fail(NERVE_HIP_INVALID_ARGUMENT,
+                        "quantized hidden rows need hidden % 4 == 0 and 4-byte aligned hidden and e4m3 buffers");
     if (ts.experts != ms.experts || ts.k + ts.always_count != ms.k)
         return nh::fail(NERVE_HIP_INVALID_SPEC, "top-k and projection specializations disagree on experts or k");
     if (batch_width == 0) return nh::ok();

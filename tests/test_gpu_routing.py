@@ -258,6 +258,22 @@ def test_route_fused_matches_separate(ctx, dev, B, H, E, k, kind):
         assert np.array_equal(to_np(f["routes"], np.uint32) & 0xFFFF, ref & 0xFFFF)
 
 
+def test_route_fused_quantized_rows_need_both_buffers(ctx, dev):
+    from nerve_amd.hip import NerveHipError
+
+    torch = _torch()
+    B, H, E, k = 4, 256, 8, 2
+    routes = torch.zeros(B, k, dtype=torch.int32, device=dev)
+    control = to_dev(np.array([B, 0, 0, 0, 0, 0, 0, 0], np.uint32), dev)
+    x = torch.zeros(B, H, dtype=torch.int16, device=dev)
+    w = torch.zeros(E, H, dtype=torch.int16, device=dev)
+    inter = torch.zeros(B * (k * 64 // 2 + k), dtype=torch.int32, device=dev)
+    hq = torch.zeros(B, H, dtype=torch.uint8, device=dev)
+    with pytest.raises(NerveHipError, match="INVALID_ARGUMENT"):
+        ctx.moe_route_fused(topk_spec(E, k), gate_up_spec(H, 64, E, k, 7.0), x, w, None, None, routes, None, inter,
+                            control, B, hidden_q=hq)
+
+
 def test_route_fused_declines_large_batches(ctx, dev):
     torch = _torch()
     B, H, E, k = 65, 64, 8, 2

@@ -2040,8 +2040,10 @@ __device__ __forceinline__ void block_share(uint32_t G, uint32_t b, uint32_t n_t
 // index and expert are in range and every parameter record of its expert is
 // valid; 16 routes per tile in expert order), while the other waves wait at
 // one barrier.  Routes of a tile are taken in slot order.  The address table
-// is staged in LDS by all waves first.
-__device__ __forceinline__ void fused_small_plan(const TileArgs& A, SmallPlan& S, uint32_t* addr_lds, uint32_t nrb) {
+// is staged in LDS by all waves first (a table the LDS does not hold is read
+// from memory, its experts' records only, after the slot words).
+__device__ __forceinline__ void fused_small_plan(const TileArgs& A, SmallPlan& S, uint32_t* addr_lds, uint32_t nrb,
+                                                 bool big_table) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t cap = A.batch_width * A.k, P = A.P, E = A.E;
     uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
@@ -2057,7 +2059,9 @@ __device__ __forceinline__ void fused_small_plan(const TileArgs& A, SmallPlan& S
         c2 = A.control[2];
         c3 = A.control[3];
     }
-    {
+    // A table the LDS does not hold (a package-wide one) is not staged: wave
+    // 0 reads its experts' records from memory after the slot words.
+    if (!big_table) {
         const v4i* src = reinterpret_cast<const v4i*>(A.addr);
         v4i* dst = reinterpret_cast<v4i*>(addr_lds);
         for (uint32_t i = tid; i < 2 * A.n_records; i += nt) dst[i] = src[i];
@@ -2066,12 +2070,22 @@ __device__ __forceinline__ void fused_small_plan(const TileArgs& A, SmallPlan& S
     if (wave == 0) {
         // Records of expert `lane`: all eight 16-byte reads first.
         v4i lo[4], hi[4];
+        if (big_table) {
 #pragma unroll
-        for (uint32_t p = 0; p < 4; p++) {
-            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
-            const v4i* r = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
-            lo[p] = r[0];
-            hi[p] = r[1];
+            for (uint32_t p = 0; p < 4; p++) {
+                const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
+                const v4i* r = reinterpret_cast<const v4i*>(A.addr + (uint64_t)(has ? sl[p] : 0u) * 8);
+                lo[p] = r[0];
+                hi[p] = r[1];
+            }
+        } else {
+#pragma unroll
+            for (uint32_t p = 0; p < 4; p++) {
+                const bool has = sl[p] != UNBOUND_SLOT && sl[p] < A.n_records;
+                const v4i* r = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
+                lo[p] = r[0];
+                hi[p] = r[1];
+            }
         }
         bool valid = lane < E;
         uint64_t ptr[4];
@@ -2165,7 +2179,7 @@ __global__ __launch_bounds__(64 * NW) void mx_stream_kernel(StreamArgs A) {
     uint32_t* addr_lds = reinterpret_cast<uint32_t*>(ring + (sizeof(FusedTables) + 15) / 16 * 16);
     if (FUSED && A.small_plan) {
         SmallPlan& S = F.plan;
-        fused_small_plan(A.T, S, addr_lds, nrb);
+        fused_small_plan(A.T, S, addr_lds, nrb, A.T.n_records > A.addr_lds_records);
         const uint32_t lo_rb = S.lo_rb, hi_rb = S.hi_rb, tile = S.tile;
         if (lo_rb >= hi_rb) return;
         TileSrc ts;
@@ -2249,19 +2263,23 @@ nerve_hip_status launch_stream(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = NMAT * (A.lw + A.ls);
     size_t lds = (size_t)2 * A.slot_bytes + (size_t)NW * NMAT * NSUB * 64 * 16;
-    // The set-up tables and the staged address table share the ring's LDS
-    // (short rings are extended to hold them).
-    const size_t tables = (sizeof(FusedTables) + 15) / 16 * 16 + (size_t)A.T.n_records * 32;
-    if (FUSED && lds < tables) lds = tables;
-    A.addr_lds_records = FUSED ? (uint32_t)((lds - (sizeof(FusedTables) + 15) / 16 * 16) / 32) : 0u;
-    if (lds > 160 * 1024 || A.copies_per_item * 2 > 63) return NERVE_HIP_UNSUPPORTED;
     A.small_plan = FUSED && A.T.E <= 64 && A.T.batch_width * A.T.k <= 64 && ctx->cu_count >= 64 ? 1u : 0u;
+    // The set-up tables and the staged address table share the ring's LDS
+    // (short rings are extended to hold them, up to the LDS; the small plan
+    // reads a larger table from memory instead).
+    const size_t head = (sizeof(FusedTables) + 15) / 16 * 16;
+    size_t tables = head + (size_t)A.T.n_records * 32;
+    if (A.small_plan && tables > 160 * 1024) tables = head;
+    if (FUSED && lds < tables) lds = tables;
+    A.addr_lds_records = FUSED ? (uint32_t)((lds - head) / 32) : 0u;
+    if (lds > 160 * 1024 || A.copies_per_item * 2 > 63) return NERVE_HIP_UNSUPPORTED;
     if (FUSED) {
         // Every compacted slot needs a thread in the tables, and activation
         // rows are read in 16-byte pieces.
         const uint32_t cap = A.T.batch_width * A.T.k;
         if (cap > 64 * NW || cap > FUSED_MAX_SLOTS || A.T.E > FUSED_MAX_EXPERTS || A.T.E > 64 * NW || A.T.P > 4 ||
-            ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || A.x_seg % 8 || A.T.n_records > A.addr_lds_records ||
+            ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || A.x_seg % 8 ||
+            (A.T.n_records > A.addr_lds_records && !A.small_plan) ||   // the small plan reads a big table from memory
             ((uintptr_t)A.T.addr & 15))
             return NERVE_HIP_UNSUPPORTED;
     }
@@ -2336,6 +2354,9 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     // ---- wave 0's routing inputs and address table go to memory first, so
     // they are not queued behind the activation loads of the other waves.
     const uint32_t n16 = 2 * T.n_records;
+    // A table past TOK_MAX_RECORDS (a package-wide one) is not staged: the
+    // plan reads its experts' records from memory after the slot words.
+    const bool big_table = T.n_records > TOK_MAX_RECORDS;
     uint32_t sl[4] = {UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT, UNBOUND_SLOT};
     uint32_t r = 0, rt = 0, c2 = 0, c3 = 0;
     v4i tab[TOK_MAX_RECORDS * 2 / 64];
@@ -2353,7 +2374,7 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
 #pragma unroll
         for (uint32_t j = 0; j < TOK_MAX_RECORDS * 2 / 64; j++) {
             const uint32_t i = j * 64 + lane;
-            tab[j] = i < n16 ? src[i] : v4i{0, 0, 0, 0};
+            tab[j] = i < n16 && !big_table ? src[i] : v4i{0, 0, 0, 0};
         }
     }
     asm volatile("" ::: "memory");
@@ -2392,26 +2413,39 @@ __device__ __forceinline__ void mx_tokens_body(const StreamArgs& A) {
     uint32_t sa[CH];
     if (wave == 0) {
         // ---- the plan: the same validity rules as fused_tables.
-        {
+        if (!big_table) {
             v4i* dst = reinterpret_cast<v4i*>(addr_lds);
 #pragma unroll
             for (uint32_t j = 0; j < TOK_MAX_RECORDS * 2 / 64; j++) {
                 const uint32_t i = j * 64 + lane;
                 if (i < n16) dst[i] = tab[j];
             }
+        }
+        {
             v4i* mz = reinterpret_cast<v4i*>(&S.mask[0][0]);
 #pragma unroll
             for (uint32_t j = 0; j < TOK_MAX_EXPERTS * TOK_MAX_TOKENS / 4 / 64; j++) mz[j * 64 + lane] = v4i{0, 0, 0, 0};
             S.flag[lane] = 0;
         }
-        // Records of expert `lane` (a wave's LDS accesses complete in order).
+        // Records of expert `lane` (a wave's LDS accesses complete in order),
+        // or from memory for a table that was not staged.
         v4i lo[4], hi[4];
+        if (big_table) {
 #pragma unroll
-        for (uint32_t p = 0; p < 4; p++) {
-            const bool has = sl[p] != UNBOUND_SLOT && sl[p] < T.n_records;
-            const v4i* rp = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
-            lo[p] = rp[0];
-            hi[p] = rp[1];
+            for (uint32_t p = 0; p < 4; p++) {
+                const bool has = sl[p] != UNBOUND_SLOT && sl[p] < T.n_records;
+                const v4i* rp = reinterpret_cast<const v4i*>(T.addr + (uint64_t)(has ? sl[p] : 0u) * 8);
+                lo[p] = rp[0];
+                hi[p] = rp[1];
+            }
+        } else {
+#pragma unroll
+            for (uint32_t p = 0; p < 4; p++) {
+                const bool has = sl[p] != UNBOUND_SLOT && sl[p] < T.n_records;
+                const v4i* rp = reinterpret_cast<const v4i*>(addr_lds + (has ? sl[p] : 0u) * 8);
+                lo[p] = rp[0];
+                hi[p] = rp[1];
+            }
         }
         bool valid = lane < E;
         uint64_t ptr[4];
@@ -2703,7 +2737,7 @@ nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     constexpr uint32_t RI = 16, CH = 24 / NW;
     const uint32_t nch = (A.K + 127) / 128;
     if (A.T.batch_width > TOK_MAX_TOKENS || A.T.E > TOK_MAX_EXPERTS || A.T.batch_width * A.T.k > 64 || A.T.P != 4 ||
-        A.T.n_records > TOK_MAX_RECORDS || A.K % 32 || A.K > 4096 || (nch + NW - 1) / NW > CH || RI * (A.K / 32) < 256 || A.x_seg != 0 ||
+        A.K % 32 || A.K > 4096 || (nch + NW - 1) / NW > CH || RI * (A.K / 32) < 256 || A.x_seg != 0 ||
         ((uintptr_t)A.x16 & 15) || A.x_frame % 8 || ((uintptr_t)A.T.addr & 15) || A.T.k > 32 ||
         (uint32_t)ctx->cu_count < A.T.E)   // >= E blocks: a block's share spans at most two experts
         return NERVE_HIP_UNSUPPORTED;
@@ -2715,7 +2749,7 @@ nerve_hip_status launch_tokens(StreamArgs A, const nerve_hip_ctx* ctx, hipStream
     A.ls = (nps + NW - 1) / NW;
     A.copies_per_item = 2 * (A.lw + A.ls);
     const size_t lds = (size_t)2 * A.slot_bytes + (size_t)NW * 2 * 64 * 16;
-    const size_t plan = (sizeof(TokPlan) + 15) / 16 * 16 + (size_t)A.T.n_records * 32;
+    const size_t plan = (sizeof(TokPlan) + 15) / 16 * 16 + (A.T.n_records > TOK_MAX_RECORDS ? 0 : (size_t)A.T.n_records * 32);
     if (lds > 160 * 1024 || plan > lds || A.copies_per_item * 2 > 63) return NERVE_HIP_UNSUPPORTED;
     static bool attr_set = false;
     if (!attr_set) {

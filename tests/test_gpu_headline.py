@@ -92,6 +92,35 @@ def _dv(a, dev):
     return to_dev(np.ascontiguousarray(a), dev)
 
 
+@pytest.mark.parametrize("pad", [600, 6000])
+def test_moe_block_package_wide_address_table(ctx, dev, pad):
+    """A package-wide address table (pad unrelated records ahead of the
+    block's, slots rebased): past 512 records the token-form gate_up reads
+    its experts' records from memory instead of staging the table, past what
+    its LDS holds the down's small plan does the same; the block's outputs
+    are bit-identical to those with the block's own table."""
+    torch = _torch()
+    rng = np.random.default_rng(77 + pad)
+    E, k, B, H, I = 32, 4, 16, 512, 512
+    d = wl.moe_experts(rng, E, H, I)
+    router = _dv(wl.bf16_normal(rng, (E, H), 0.02), dev)
+    hidden = _dv(wl.bf16_normal(rng, (B, H)), dev)
+    bank = ExpertBank(*(_dv(d[n], dev) for n in ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")))
+    ref_block = MoEBlock(ctx, router, bank, k)
+    ref = to_np(ref_block.forward(hidden), np.uint16).copy()
+    ref_inter = to_np(ref_block.buffers(B)["inter"], np.uint32).copy()
+    big = ExpertBank(*(_dv(d[n], dev) for n in ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")))
+    junk = rng.integers(0, 2 ** 32, size=pad * 8, dtype=np.uint64).astype(np.uint32)
+    big.addresses = torch.cat([to_dev(junk, dev).view(torch.int32), big.addresses])
+    big.gate_slots = big.gate_slots + pad
+    big.down_slots = big.down_slots + pad
+    block = MoEBlock(ctx, router, big, k)
+    out = to_np(block.forward(hidden), np.uint16)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(block.buffers(B)["inter"], np.uint32), ref_inter)
+    assert np.array_equal(out, ref)
+
+
 def test_moe_block_forward_config2(ctx, dev):
     """MoEBlock.forward at config 2 (E = 32, k = 4, B = 16, H = I = 2880):
     fused routing (router partials + top-k + compaction), token-form gate_up,
